@@ -1,0 +1,347 @@
+"""Benchmark of the RAM-Net operator hot path on one MI355X.
+
+Headline (``value``): segment-parallel prefill tokens/s at config 2
+(B=8, H=16, T=4096, d_v=128, U=2, P=32 -> A=1024 slots, K=8, bf16
+activations, fp32 slot state, CAPE on half the heads). One step = the address
+decoder for write and read logits plus the segment scan (GSU + top-K read)
+over the whole batch, inputs resident in HBM, functional state
+(zeros in, new state out). The decode figure (config 3: B=64, 512 fused
+single-token steps on a persistent 64x16x1024x128 fp32 state, captured in a
+HIP graph) is reported beside it under ``decode``.
+
+``roofline`` is for the dominant kernel (the segment scan): algorithmic bytes
+of the event model per launch / the kernel's average duration measured with
+HIP events on the stream it runs on. ``cpu_baseline`` times the CPU
+restatement of the reference's dense PyTorch algorithm on a bounded sample of
+the same inputs (rank 0, N=1 only).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S]
+       [--no-cpu-baseline] [--only prefill|decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "ram-net_amd"), REPO, os.path.join(REPO, "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "prefill tokens/s (T=4096) + decode tokens/s (B=64); % HBM roofline"
+
+# config 2 (prefill) and config 3 (decode)
+C2 = dict(B=8, H=16, T=4096, C=128, U=2, P=32, K=8, d_k=128, seed=2)
+C3 = dict(B=64, H=16, C=128, U=2, P=32, K=8, steps=512, seed=3)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def event_model_bytes(U, P, C, K, H, s_a=2) -> dict:
+    """Algorithmic bytes per token-head of the event ("active state") model.
+
+    logits 2*U*P*s_a, x C*s_a, gamma s_a, y C*s_a, position 4/H, every write
+    a fp32 row + mass read-modify-write, every read a fp32 row read.
+    """
+    op = 2 * U * P * s_a + C * s_a + s_a + C * s_a + 4.0 / H + K * (2 * C * 4 + 2 * 4) + K * C * 4
+    # the segment scan itself: decoded (idx, val) pairs instead of logits
+    seg = op - 2 * U * P * s_a - 4.0 / H + 2 * K * 8
+    return {"op": op, "segment": seg}
+
+
+def make_prefill_inputs(dev):
+    from ram_cases import projected_logits
+    c = C2
+    B, H, T, C, U, P = c["B"], c["H"], c["T"], c["C"], c["U"], c["P"]
+    w, r = projected_logits(B, H, U, P, T, c["d_k"], seed=c["seed"], dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(c["seed"] + 100)
+    x = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16)
+    gamma = torch.sigmoid(torch.randn(B, H, T, generator=g) - 1).to(torch.bfloat16)
+    pos = torch.arange(T, dtype=torch.int32).view(1, T).expand(B, T).contiguous()
+    host = dict(w=w, r=r, x=x, gamma=gamma, pos=pos)
+    devd = {k: v.to(dev) for k, v in host.items()}
+    return host, devd
+
+
+def bench_prefill(steps, warmup, dev):
+    import ramnet_ops  # noqa: F401
+    ops = torch.ops.ramnet_ops
+    c = C2
+    B, H, T, C, U, P, K = c["B"], c["H"], c["T"], c["C"], c["U"], c["P"], c["K"]
+    A = P ** U
+    E = H // 2
+    host, d = make_prefill_inputs(dev)
+    slot0 = torch.zeros(B, H, A, C, device=dev)
+    mass0 = torch.full((B, H, A), 1.0 / A, device=dev)
+
+    def step(ev):
+        ev[0].record()
+        idx, val = ops.topk_addr_forward(d["w"], d["r"], E, A, d["pos"], K, K, 0.0, 0.0)
+        ev[1].record()
+        y, slot, mass = ops.topk_segment_forward(idx, val, d["x"], d["gamma"], slot0, mass0, None, K, K, False, 1e-12)
+        ev[2].record()
+        return y
+
+    def events(n):
+        return [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
+
+    for ev in events(warmup):
+        step(ev)
+    evs = events(steps)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for ev in evs:
+        step(ev)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = evs[0][0].elapsed_time(evs[-1][2])
+    ms_per_step = total_ms / steps
+    dec_ms = [ev[0].elapsed_time(ev[1]) for ev in evs]
+    seg_ms = [ev[1].elapsed_time(ev[2]) for ev in evs]
+    seg_avg = sum(seg_ms) / len(seg_ms)
+    dec_avg = sum(dec_ms) / len(dec_ms)
+    per = event_model_bytes(U, P, C, K, H)
+    state_io = 2 * B * H * A * (C + 1) * 4
+    n_th = B * H * T
+    seg_bytes = per["segment"] * n_th + state_io
+    op_bytes = per["op"] * n_th + state_io
+    tokens = B * T
+    return {
+        "host": host,
+        "ms_per_step": ms_per_step,
+        "wall_s": wall,
+        "tokens_per_s": tokens / (ms_per_step / 1e3),
+        "segment_ms": seg_avg,
+        "decoder_ms": dec_avg,
+        "segment_bytes": seg_bytes,
+        "op_bytes": op_bytes,
+        "op_roofline_frac": (op_bytes / (ms_per_step / 1e3)) / (HBM_PEAK_GBS * 1e9),
+        "bytes_per_token_head": per,
+    }
+
+
+def bench_decode(n_steps, dev, graph=True):
+    import ramnet_ops  # noqa: F401
+    ops = torch.ops.ramnet_ops
+    c = C3
+    B, H, C, U, P, K = c["B"], c["H"], c["C"], c["U"], c["P"], c["K"]
+    A = P ** U
+    E = H // 2
+    g = torch.Generator(device=dev).manual_seed(c["seed"])
+    slot = 0.5 * torch.randn(B, H, A, C, device=dev, generator=g)
+    mass = torch.full((B, H, A), 1.0 / A, device=dev)
+    d_k = 128
+    W = torch.randn(H, d_k, U * P, device=dev, generator=g) / d_k ** 0.5
+    q = torch.randn(n_steps, 2, B, H, d_k, device=dev, generator=g)
+    lg = (torch.einsum('sqbhd,hdn->sqbhn', q, W) / U ** 0.5).to(torch.bfloat16).view(n_steps, 2, B, H, U, P)
+    w_all, r_all = lg[:, 0].contiguous(), lg[:, 1].contiguous()
+    x_all = torch.randn(n_steps, B, H, C, device=dev, generator=g).to(torch.bfloat16)
+    g_all = torch.sigmoid(torch.randn(n_steps, B, H, device=dev, generator=g)).to(torch.bfloat16)
+    t0 = torch.randint(0, 8192, (B,), device=dev, generator=g)
+    pos_all = (t0.view(1, B) + torch.arange(n_steps, device=dev).view(n_steps, 1)).to(torch.int32).contiguous()
+    no_mask = torch.empty(0, dtype=torch.bool, device=dev)
+    keep = []
+
+    def run_all():
+        keep.clear()
+        for s in range(n_steps):
+            keep.append(ops.topk_autoregressive_(w_all[s], r_all[s], x_all[s], g_all[s], slot, mass, no_mask, E,
+                                                 pos_all[s], K, K, 0.0, 0.0, False, 1e-12))
+
+    # kernel duration on its stream, eager
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ops.topk_autoregressive_(w_all[0], r_all[0], x_all[0], g_all[0], slot, mass, no_mask, E, pos_all[0], K, K,
+                             0.0, 0.0, False, 1e-12)
+    torch.cuda.synchronize()
+    ks = []
+    for s in range(min(n_steps, 64)):
+        e0.record()
+        ops.topk_autoregressive_(w_all[s], r_all[s], x_all[s], g_all[s], slot, mass, no_mask, E, pos_all[s], K, K,
+                                 0.0, 0.0, False, 1e-12)
+        e1.record()
+        torch.cuda.synchronize()
+        ks.append(e0.elapsed_time(e1))
+    kernel_ms = sorted(ks)[len(ks) // 2]
+
+    mode = "eager"
+    if graph:
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                run_all()  # warm-up on the capture stream
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                run_all()
+            torch.cuda.synchronize()
+            gr.replay()
+            torch.cuda.synchronize()
+            runner = gr.replay
+            mode = "hip-graph"
+        except Exception as exc:  # capture unsupported: fall back to eager launches, reported as such
+            log(f"graph capture failed ({exc}); timing eager launches")
+            runner = run_all
+    else:
+        runner = run_all
+    runner()
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    s_ev.record()
+    for _ in range(reps):
+        runner()
+    e_ev.record()
+    torch.cuda.synchronize()
+    ms = s_ev.elapsed_time(e_ev) / reps
+    per_step_ms = ms / n_steps
+    bytes_step = event_model_bytes(U, P, C, K, H)["op"] * B * H
+    return {
+        "mode": mode,
+        "steps": n_steps,
+        "ms_per_step": per_step_ms,
+        "tokens_per_s": B / (per_step_ms / 1e3),
+        "kernel_ms": kernel_ms,
+        "bytes_per_step": bytes_step,
+        "roofline_frac": (bytes_step / (per_step_ms / 1e3)) / (HBM_PEAK_GBS * 1e9),
+        "kernel_roofline_frac": (bytes_step / (kernel_ms / 1e3)) / (HBM_PEAK_GBS * 1e9),
+    }
+
+
+def cpu_baseline(host, tokens=256, batch_rows=1):
+    """Dense reference algorithm (oracle restatement) on host cores over a bounded sample of the C2 inputs."""
+    import oracle
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    c = C2
+    H, C, U, P, K = c["H"], c["C"], c["U"], c["P"], c["K"]
+    A = P ** U
+    sl = (slice(0, batch_rows), slice(None))
+    w = host["w"][sl][..., :tokens]
+    r = host["r"][sl][..., :tokens]
+    x = host["x"][sl][:, :, :tokens]
+    gm = host["gamma"][sl][..., :tokens]
+    pos = host["pos"][:batch_rows, :tokens].long()
+    slot = torch.zeros(batch_rows, H, A, C)
+    mass = torch.full((batch_rows, H, A), 1.0 / A)
+    # warm-up on a few tokens
+    oracle.dense_ram_attn(w[..., :4], r[..., :4], x[:, :, :4], gm[..., :4], slot, mass, None, H // 2, pos[:, :4],
+                          (K, K), (0.0, 0.0), False, 1e-12, chunk=tokens)
+    t0 = time.perf_counter()
+    oracle.dense_ram_attn(w, r, x, gm, slot, mass, None, H // 2, pos, (K, K), (0.0, 0.0), False, 1e-12,
+                          chunk=tokens)
+    dt = time.perf_counter() - t0
+    return {
+        "value": batch_rows * tokens / dt,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"config 2 inputs, batch rows {batch_rows} of {c['B']}, first {tokens} of {c['T']} tokens, all "
+                  f"{H} heads; dense decode + per-step dense GSU (torch_impl.py algorithm) in {dt:.1f} s",
+        "cpu": platform.processor() or platform.machine(),
+        "seconds": dt,
+    }
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=C3["steps"])
+    ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--only", choices=("prefill", "decode"), default=None)
+    args = ap.parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU only: the operator shards over (batch, head) "
+                                   "with no communication, so a multi-GPU figure is N independent copies of the "
+                                   "one-GPU run; use --gpus 1"}), flush=True)
+        return 2
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device visible"}), flush=True)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    out = {"metric": METRIC}
+    pre = dec = None
+    if args.only in (None, "prefill"):
+        log("prefill: building config 2 inputs")
+        pre = bench_prefill(args.steps, args.warmup, dev)
+        log(f"prefill: {pre['ms_per_step']:.3f} ms/step, segment {pre['segment_ms']:.3f} ms, "
+            f"decoder {pre['decoder_ms']:.3f} ms")
+    if args.only in (None, "decode"):
+        log("decode: config 3, graph-captured steps")
+        dec = bench_decode(args.decode_steps, dev, graph=not args.no_graph)
+        log(f"decode: {dec['ms_per_step'] * 1e3:.2f} us/step ({dec['mode']}), kernel {dec['kernel_ms'] * 1e3:.2f} us")
+
+    if pre is not None:
+        seg_gbs = pre["segment_bytes"] / (pre["segment_ms"] / 1e3) / 1e9
+        out.update({
+            "value": pre["tokens_per_s"],
+            "unit": "tokens/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": pre["ms_per_step"],
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "f32",
+            "data": "synthetic",
+            "config": {
+                "workload": "config 2 segment-parallel prefill: B=8, H=16, T=4096, d_v=128, U=2, P=32 (A=1024), "
+                            "K=8 write + 8 read, CAPE on 8 of 16 heads, gamma=sigmoid(N(0,1)-1), zero initial "
+                            "state; logits = (q ~ N(0,1), d_k=128) @ W / sqrt(U)",
+                "activations": "bf16", "state": "f32", "tokens_per_step": C2["B"] * C2["T"],
+                "segment_length": 128,
+            },
+            "roofline": {
+                "bound": "hbm",
+                "kernel": "segment_forward_kernel",
+                "achieved": seg_gbs,
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": seg_gbs / HBM_PEAK_GBS,
+                "traffic": None,
+                "algorithmic_bytes": pre["segment_bytes"],
+                "kernel_ms": pre["segment_ms"],
+            },
+            "prefill": {
+                "tokens_per_s": pre["tokens_per_s"],
+                "op_roofline_frac": pre["op_roofline_frac"],
+                "decoder_ms": pre["decoder_ms"],
+                "segment_ms": pre["segment_ms"],
+                "op_bytes_per_step": pre["op_bytes"],
+                "bytes_per_token_head": pre["bytes_per_token_head"],
+            },
+        })
+    if dec is not None:
+        out["decode"] = dec
+        if pre is None:
+            out.update({"value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": dec["steps"],
+                        "warmup": 1, "ms_per_step": dec["ms_per_step"], "higher_is_better": True,
+                        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                        "config": {"workload": "config 3 decode: B=64, H=16, A=1024, d_v=128, K=8, 512 steps"}})
+    if pre is not None and not args.no_cpu_baseline:
+        log("cpu baseline: dense reference algorithm on host cores")
+        out["cpu_baseline"] = cpu_baseline(pre["host"], tokens=args.cpu_tokens)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,142 @@
+/*
+ * ramnet_hip.h - C ABI of the MI355X (gfx950) RAM-Net operator library.
+ *
+ * Each entry point replaces one native operator of the reference extension
+ * (packages/ramnet-ops/csrc/ram_attn_bind.cpp:22-113, implemented in
+ * ram_attn_ops.cpp). Arguments are raw device pointers, element counts and
+ * scalars; no framework types cross this boundary. All tensors are dense,
+ * row-major (C-contiguous) in the layouts given below, on the current HIP
+ * device. Work is enqueued on `stream` (a hipStream_t; NULL = default
+ * stream) and never synchronised; nothing is allocated or freed.
+ *
+ * Shape symbols: B batch, H heads, U address digits, P radix, A = P**U slots,
+ * K top-k, T tokens, C value channels.
+ *
+ * Return value: RAMNET_OK, or a nonzero RAMNET_E* code with a message
+ * available from ramnet_last_error() on the calling thread.
+ */
+#ifndef RAMNET_HIP_H
+#define RAMNET_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RAMNET_ABI_VERSION 1
+
+enum {
+    RAMNET_OK = 0,
+    RAMNET_EINVAL = 1,  /* bad argument: shape, range, dtype, null pointer, aliasing */
+    RAMNET_ELAUNCH = 2, /* the HIP runtime rejected the launch */
+};
+
+/* Activation dtypes (logits, values, gamma, y). Slot state is always fp32. */
+enum { RAMNET_F32 = 0, RAMNET_F16 = 1, RAMNET_BF16 = 2 };
+
+/* ABI revision of this header. */
+int ramnet_abi_version(void);
+
+/* Width of the index type used on device (32). Replaces the `_C.INT_BITS`
+ * module constant exported by the reference extension
+ * (ram_attn_bind.cpp:115-129; read by impl/_cuda_config.py:4). */
+int ramnet_int_bits(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *ramnet_last_error(void);
+
+/*
+ * Top-K address decoder for one address tensor.
+ * Replaces ramnet_ops::topk_addr_single_forward
+ * (ram_attn_bind.cpp:27-35, ram_attn_ops.cpp:63-95).
+ *   addr          (B, H, U, P, T) logits, `dtype`
+ *   position_ids  (B, T) int32, used by heads h < embed_num (CAPE)
+ *   idx_out       (B, H, top_k, T) int32: (b*H + h)*A + slot, or h*A + slot
+ *                 when encode_batch_idx == 0
+ *   val_out       (B, H, top_k, T) fp32 weights, negated if addr_val_neg
+ * Requires A == P**U, 0 < top_k <= A, 0 <= embed_num <= H,
+ * 0 <= top_k_re_norm <= 1.
+ */
+int ramnet_topk_addr_single_forward(const void *addr, int dtype, int64_t B, int64_t H, int64_t U, int64_t P,
+                                    int64_t T, int64_t embed_num, int64_t A, const int32_t *position_ids,
+                                    int64_t top_k, float top_k_re_norm, int addr_val_neg, int encode_batch_idx,
+                                    int32_t *idx_out, float *val_out, void *stream);
+
+/*
+ * Write and read address decoders in one launch.
+ * Replaces ramnet_ops::topk_addr_forward
+ * (ram_attn_bind.cpp:36-45, ram_attn_ops.cpp:137-172).
+ *   w_addr, r_addr  (B, H, U, P, T) logits, `dtype`
+ *   idx_out         (B, H, w_top_k + r_top_k, T) int32; write rows first
+ *   val_out         (B, H, w_top_k + r_top_k, T) fp32; write weights
+ *                   positive, read weights negated (the sign tells the
+ *                   segment scan which events read)
+ */
+int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, int64_t B, int64_t H, int64_t U,
+                             int64_t P, int64_t T, int64_t embed_num, int64_t A, const int32_t *position_ids,
+                             int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
+                             int encode_batch_idx, int32_t *idx_out, float *val_out, void *stream);
+
+/*
+ * Gated sparse update and top-K read over a whole sequence, returning a new
+ * state. Replaces ramnet_ops::topk_segment_forward
+ * (ram_attn_bind.cpp:65-73, ram_attn_ops.cpp:226-265). The reference op
+ * also takes event-grouping metadata built by a global sort; this library
+ * scans time in order and needs none.
+ *   addr_idx, addr_val  output of ramnet_topk_addr_forward with
+ *                       encode_batch_idx = 1
+ *   x                   (B, H, T, C) `dtype`;  gamma (B, H, T) `dtype`
+ *   mask                (B, T) uint8/bool (nonzero = valid) or NULL
+ *   init_slot/mass      (B, H, A, C) / (B, H, A) fp32
+ *   slot_out/mass_out   (B, H, A, C) / (B, H, A) fp32; slot_out may alias
+ *                       init_slot, mass_out must not alias init_mass
+ *   y                   (B, H, T, C) `dtype`; masked tokens get 0
+ */
+int ramnet_topk_segment_forward(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
+                                int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
+                                float *slot_out, float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A,
+                                int64_t C, int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *stream);
+
+/*
+ * In-place variant: updates slot and mass. Replaces
+ * ramnet_ops::topk_segment_forward_ (ram_attn_bind.cpp:83-91,
+ * ram_attn_ops.cpp:312-347). `mass_in` is a copy of the mass state taken
+ * before the call (B*H*A fp32, must not alias `mass`): channel slices of one
+ * head may start after another slice has already stored the new masses.
+ */
+int ramnet_topk_segment_forward_(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
+                                 int dtype, const uint8_t *mask, float *slot, float *mass, const float *mass_in,
+                                 void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
+                                 int64_t r_top_k, int mass_aware, float eps, void *stream);
+
+/*
+ * One fused decode step on a persistent state, updated in place.
+ * Replaces ramnet_ops::topk_autoregressive_ (ram_attn_bind.cpp:92-101,
+ * ram_attn_ops.cpp:349-394).
+ *   w_addr, r_addr  (B, H, U, P) `dtype`;  x (B, H, C);  gamma (B, H)
+ *   slot, mass      (B, H, A, C), (B, H, A) fp32, read-modify-write
+ *   mask            (B) uint8/bool or NULL: masked rows keep their state
+ *                   and get y = 0
+ *   position_ids    (B) int32
+ *   y               (B, H, C) `dtype`
+ */
+int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
+                                float *slot, float *mass, const uint8_t *mask, int64_t embed_num,
+                                const int32_t *position_ids, int64_t B, int64_t H, int64_t U, int64_t P, int64_t A,
+                                int64_t C, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
+                                int mass_aware, float eps, void *y, void *stream);
+
+/*
+ * Planning query (no device work): channel-slice width and LDS bytes per
+ * wave the segment scan uses for slot count A, C channels and top-k.
+ * Returns 1 if the shape is supported, else 0.
+ */
+int ramnet_segment_plan(int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int *slice_channels,
+                        int *lds_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RAMNET_HIP_H */

@@ -1,0 +1,300 @@
+"""CPU oracle for RAM-Net random-access memory attention -- TEST INFRASTRUCTURE ONLY.
+
+Never imported by the product package. Functions and what pins them
+(tests/test_oracle.py):
+
+* ``log_softmax_digits``, ``content_scores``: per-digit log-softmax and the
+  Kronecker sum of torch_impl.py:105-112,204,253. Pinned by the product-
+  distribution closed form (probabilities multiply; digit 0 least
+  significant), the reference's extreme-logit known-answer fixture
+  (tests/ops/test_address_numerics.py:83-102), and fp64 brute force.
+* ``dense_topk_addr``: torch_impl.py:152-214 with the deterministic tie rule
+  (score desc, content index asc). Pinned by the reference's closed-form
+  product-distribution test (test_address_numerics.py:20-56, values
+  q / sum(q)**r), the inactive (-inf) fixture (:58-71) and CAPE inverse.
+* ``dense_ram_attn``: torch_impl.py:7-75 (GSU) and :217-288 (composition):
+  dense decode of all A slots per token and the per-step dense GSU loop.
+  This is also the CPU baseline ``bench.py`` times. Pinned by GSU closed
+  forms (pure accumulation at gamma -> -inf is a weighted mean; gamma -> +inf
+  keeps the last write; constant w/gamma gives the geometric mass series),
+  agreement with the independent sparse fp64 loop, and the reference's
+  behavioural invariants (chunked == full, masked == compacted).
+* ``sparse_gsu_f64``: fp64 event loop over the selected slots only
+  (GPU conventions: masked tokens neither write nor read and get y = 0).
+  Pinned by the same closed forms and by agreement with ``dense_ram_attn``.
+* ``topk_f64`` / ``check_topk_indices``: fp64 brute-force top-K with the
+  tie rule, and the index comparator that exempts candidates whose fp64
+  score lies within ``tol`` of the K-th score.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+__all__ = [
+    "log_softmax_digits",
+    "content_scores",
+    "dense_topk_addr",
+    "dense_ram_attn",
+    "sparse_gsu_f64",
+    "split_events",
+    "topk_f64",
+    "check_topk_indices",
+    "rel_err",
+]
+
+
+# ---------------------------------------------------------------------------
+# address decoding
+
+def log_softmax_digits(addr: torch.Tensor, dtype=torch.float32) -> torch.Tensor:
+    """log_softmax over the radix axis of (..., U, P, T) logits (torch_impl.py:204,253)."""
+    return torch.log_softmax(addr.to(dtype), dim=-2)
+
+
+def content_scores(log_probs: torch.Tensor) -> torch.Tensor:
+    """(B, H, U, P, T) digit log-probabilities -> (B, H, T, A) content-slot scores.
+
+    score(c) = ((L_0[d_0] + L_1[d_1]) + L_2[d_2]) ..., c = sum_u d_u P**u
+    (digit 0 least significant), summed in digit order like the reference's
+    ``functools.reduce(torch.add, ...)`` (torch_impl.py:105-112).
+    """
+    lp = log_probs.permute(0, 1, 4, 2, 3)  # (B, H, T, U, P)
+    acc = lp[..., 0, :]
+    for u in range(1, lp.shape[-2]):
+        # new content index = d_u * P**u + previous index
+        acc = (acc.unsqueeze(-2) + lp[..., u, :].unsqueeze(-1)).flatten(-2)
+    return acc
+
+
+def _inactive(addr: torch.Tensor) -> torch.Tensor:
+    """(B, H, T): some digit has only -inf logits (torch_impl.py:199-201)."""
+    return torch.isneginf(addr).all(dim=-2).any(dim=-2)
+
+
+def dense_topk_addr(addr: torch.Tensor, embed_num: int, position_ids: torch.Tensor, top_k: int,
+                    top_k_re_norm: float = 0.0, addr_val_neg: bool = False, encode_batch_idx: bool = True,
+                    dtype=torch.float32) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense top-K decoder on (B, H, U, P, T) logits -> idx int32, val (B, H, K, T).
+
+    Restates torch_impl.py:152-214. Ties are broken by content index
+    ascending (a stable descending sort), where the reference's
+    ``torch.topk`` leaves them unspecified.
+    """
+    B, H, U, P, T = addr.shape
+    A = P ** U
+    logits = addr.to(dtype)
+    inactive = _inactive(logits)
+    logits = logits.masked_fill(inactive[:, :, None, None, :], 0)
+    scores = content_scores(log_softmax_digits(logits, dtype))  # (B, H, T, A)
+    order = torch.sort(scores, dim=-1, descending=True, stable=True).indices[..., :top_k]
+    val = scores.gather(-1, order)
+    if top_k_re_norm != 0:
+        val = val - float(top_k_re_norm) * val.logsumexp(dim=-1, keepdim=True)
+    val = val.exp().masked_fill(inactive[..., None], 0)
+    # CAPE: out slot o holds content (o + pos) mod A  (torch_impl.py:78-102)
+    heads = torch.arange(H).view(1, H, 1, 1)
+    shift = (heads < embed_num).long() * position_ids.long().view(B, 1, T, 1)
+    out = torch.remainder(order - shift, A)
+    base = (torch.arange(B * H).view(B, H, 1, 1) if encode_batch_idx else torch.arange(H).view(1, H, 1, 1)) * A
+    idx = (out + base).to(torch.int32).permute(0, 1, 3, 2).contiguous()
+    val = val.permute(0, 1, 3, 2).contiguous()
+    return idx, (-val if addr_val_neg else val)
+
+
+def _dense_weights(idx: torch.Tensor, val: torch.Tensor, A: int, H: int) -> torch.Tensor:
+    """Scatter (B, H, K, T) encoded indices/weights into dense (T, B, H, A) weights."""
+    B, _, K, T = idx.shape
+    base = torch.arange(B * H).view(B, H, 1, 1) * A
+    local = (idx.long() - base).permute(3, 0, 1, 2)  # (T, B, H, K)
+    dense = torch.zeros(T, B, H, A, dtype=val.dtype)
+    dense.scatter_(-1, local, val.permute(3, 0, 1, 2))
+    return dense
+
+
+# ---------------------------------------------------------------------------
+# dense GSU (the reference algorithm; CPU baseline)
+
+def _dense_gsu(ws, rs, xs, gamma, slot, mass, mass_aware, eps):
+    """Per-step dense gated sparse update over all A slots (torch_impl.py:7-75).
+
+    ws, rs: (T, B, H, A); xs: (T, B, H, C); gamma: (T, B, H); slot (B, H, A, C);
+    mass (B, H, A). Returns ys (T, B, H, C), slot, mass.
+    """
+    ys = []
+    m = mass.unsqueeze(-1)
+    for i in range(xs.shape[0]):
+        w = ws[i].unsqueeze(-1)
+        r = rs[i]
+        comp_w = 1 - w
+        alpha = comp_w / (comp_w + torch.exp(gamma[i][..., None, None]) * w)
+        m = alpha * m + w
+        gain = w / (m + eps)
+        slot = slot + gain * (xs[i].unsqueeze(-2) - slot)
+        if mass_aware:
+            mr = m.squeeze(-1) * r
+            r = r.sum(dim=-1, keepdim=True) * mr / (mr.sum(dim=-1, keepdim=True) + eps)
+        ys.append(torch.einsum('...ac,...a->...c', slot, r))
+    return torch.stack(ys, 0), slot, m.squeeze(-1)
+
+
+def dense_ram_attn(w_addr, r_addr, xs, gamma, init_slot, init_mass, mask=None, embed_num=0, position_ids=None,
+                   top_k=(8, 8), top_k_re_norm=(0.0, 0.0), mass_aware=False, eps=1e-12, chunk=256,
+                   decoded=None):
+    """Dense RAM attention on CPU (torch_impl.py:217-288), processed in time chunks.
+
+    Inputs in the backend layout: w/r_addr (B, H, U, P, T), xs (B, H, T, C),
+    gamma (B, H, T), init_slot (B, H, A, C), init_mass (B, H, A), mask (B, T),
+    position_ids (B, T). State is carried across chunks, so results do not
+    depend on ``chunk``. ``decoded`` optionally supplies (w_idx, w_val, r_idx,
+    r_val) decoder outputs to use instead of decoding the logits. Returns
+    y (B, H, T, C) in xs.dtype (reads on masked tokens are computed, as in
+    the reference), slot and mass in float32.
+    """
+    B, H, U, P, T = w_addr.shape
+    A = P ** U
+    acc = torch.float32 if xs.dtype in (torch.float16, torch.bfloat16) else xs.dtype
+    if position_ids is None:
+        position_ids = torch.arange(T).view(1, T).expand(B, T)
+    slot = init_slot.to(acc).clone()
+    mass = init_mass.to(acc).clone()
+    ys = []
+    for t0 in range(0, T, chunk):
+        t1 = min(T, t0 + chunk)
+        if decoded is None:
+            wi, wv = dense_topk_addr(w_addr[..., t0:t1], embed_num, position_ids[:, t0:t1], top_k[0], top_k_re_norm[0], dtype=acc)
+            ri, rv = dense_topk_addr(r_addr[..., t0:t1], embed_num, position_ids[:, t0:t1], top_k[1], top_k_re_norm[1], dtype=acc)
+        else:
+            wi, wv, ri, rv = (d[..., t0:t1] for d in decoded)
+        ws = _dense_weights(wi, wv.to(acc), A, H)
+        rs = _dense_weights(ri, rv.to(acc).abs(), A, H)
+        if mask is not None:
+            ws = ws * mask[:, t0:t1].to(acc).t()[:, :, None, None]
+        x = xs[:, :, t0:t1].to(acc).permute(2, 0, 1, 3)
+        g = gamma[:, :, t0:t1].to(acc).permute(2, 0, 1)
+        y, slot, mass = _dense_gsu(ws, rs, x, g, slot, mass, mass_aware, eps)
+        ys.append(y.permute(1, 2, 0, 3))
+    return torch.cat(ys, dim=2).to(xs.dtype), slot, mass
+
+
+# ---------------------------------------------------------------------------
+# sparse fp64 event loop (GPU conventions)
+
+def split_events(idx, val, w_top_k: int):
+    """Split a combined (B, H, Kw + Kr, T) decoder output into write/read parts (read weights made positive)."""
+    idx = np.asarray(idx)
+    val = np.asarray(val)
+    return idx[:, :, :w_top_k], val[:, :, :w_top_k], idx[:, :, w_top_k:], np.abs(val[:, :, w_top_k:])
+
+
+def sparse_gsu_f64(w_idx, w_val, r_idx, r_val, x, gamma, init_slot, init_mass, mask=None, mass_aware=False,
+                   eps=1e-12, encoded=True):
+    """fp64 gated sparse update over the selected slots only.
+
+    w_idx/w_val: (B, H, Kw, T); r_idx/r_val: (B, H, Kr, T) with positive read
+    weights; x (B, H, T, C); gamma (B, H, T); init_slot (B, H, A, C);
+    init_mass (B, H, A); mask (B, T) or None. Masked tokens neither write nor
+    read and get y = 0. Returns y (B, H, T, C), slot, mass as float64.
+    """
+    f = np.float64
+    x = np.asarray(x, dtype=f)
+    B, H, T, C = x.shape
+    S = np.array(init_slot, dtype=f).reshape(B * H, -1, C)
+    A = S.shape[1]
+    M = np.array(init_mass, dtype=f).reshape(B * H, A)
+    g = np.asarray(gamma, dtype=f).reshape(B * H, T)
+    xs = x.reshape(B * H, T, C)
+    wi = np.asarray(w_idx, dtype=np.int64).reshape(B * H, -1, T)
+    wv = np.asarray(w_val, dtype=f).reshape(B * H, -1, T)
+    ri = np.asarray(r_idx, dtype=np.int64).reshape(B * H, -1, T)
+    rv = np.asarray(r_val, dtype=f).reshape(B * H, -1, T)
+    if encoded:
+        base = (np.arange(B * H) * A)[:, None, None]
+        wi = wi - base
+        ri = ri - base
+    valid = np.ones((B, T), dtype=bool) if mask is None else np.asarray(mask, dtype=bool)
+    valid = np.repeat(valid, H, axis=0)  # (B*H, T)
+    rows = np.arange(B * H)
+    y = np.zeros((B * H, T, C), dtype=f)
+    for t in range(T):
+        v = valid[:, t]
+        eg = np.exp(g[:, t])
+        for k in range(wi.shape[1]):
+            a = wi[:, k, t]
+            w = np.where(v, wv[:, k, t], 0.0)
+            comp = 1.0 - w
+            with np.errstate(invalid="ignore", divide="ignore"):
+                alpha = np.where(w == 0.0, 1.0, comp / (comp + eg * w))
+            m = alpha * M[rows, a] + w
+            M[rows, a] = m
+            gain = w / (m + eps)
+            s = S[rows, a]
+            S[rows, a] = s + gain[:, None] * (xs[:, t] - s)
+        a = ri[:, :, t]
+        r = np.where(v[:, None], rv[:, :, t], 0.0)
+        if mass_aware:
+            rm = r * M[rows[:, None], a]
+            r = r.sum(axis=1, keepdims=True) * rm / (rm.sum(axis=1, keepdims=True) + eps)
+        y[:, t] = np.einsum('bk,bkc->bc', r, S[rows[:, None], a])
+        y[~v, t] = 0.0
+    return y.reshape(B, H, T, C), S.reshape(B, H, A, C), M.reshape(B, H, A)
+
+
+# ---------------------------------------------------------------------------
+# fp64 brute force and the tie-aware index comparator
+
+def topk_f64(addr, top_k: int):
+    """fp64 content scores (B, H, T, A) and the top-K content slots under (score desc, index asc)."""
+    logits = torch.as_tensor(addr).to(torch.float64)
+    inactive = _inactive(logits)
+    logits = logits.masked_fill(inactive[:, :, None, None, :], 0)
+    scores = content_scores(torch.log_softmax(logits, dim=-2))
+    order = torch.sort(scores, dim=-1, descending=True, stable=True).indices[..., :top_k]
+    return scores, order
+
+
+def check_topk_indices(idx, addr, embed_num: int, position_ids, top_k: int, encode_batch_idx: bool = True,
+                       tol: float = 1e-6) -> dict:
+    """Compare decoder indices (B, H, K, T) against the fp64 ranking of the same logits.
+
+    Per (b, h, t) the content-slot sets must be equal, except that a slot in
+    the symmetric difference is accepted when its fp64 score lies within
+    ``tol`` of the fp64 K-th score (a tie). Raises AssertionError on a
+    violation; returns counts of checked addresses and exempted differences.
+    """
+    idx = torch.as_tensor(idx).long()
+    B, H, K, T = idx.shape
+    assert K == top_k
+    scores, order = topk_f64(addr, top_k)
+    A = scores.shape[-1]
+    base = (torch.arange(B * H).view(B, H, 1, 1) if encode_batch_idx else torch.arange(H).view(1, H, 1, 1)) * A
+    heads = torch.arange(H).view(1, H, 1, 1)
+    shift = (heads < embed_num).long() * torch.as_tensor(position_ids).long().view(B, 1, 1, T)
+    local = idx - base
+    assert bool(((local >= 0) & (local < A)).all()), "decoder index out of its (b, h) slot range"
+    content = torch.remainder(local + shift, A).permute(0, 1, 3, 2)  # (B, H, T, K)
+    got = torch.zeros(B, H, T, A, dtype=torch.bool)
+    got.scatter_(-1, content, True)
+    assert bool((got.sum(-1) == K).all()), "decoder returned duplicate slots for one address"
+    want = torch.zeros_like(got)
+    want.scatter_(-1, order, True)
+    diff = got ^ want
+    kth = scores.gather(-1, order[..., -1:])
+    both_ninf = torch.isneginf(scores) & torch.isneginf(kth)
+    near = ((scores - kth).abs() <= tol) | both_ninf
+    bad = diff & ~near
+    if bool(bad.any()):
+        b, h, t, a = (int(v) for v in bad.nonzero()[0])
+        raise AssertionError(
+            f"top-K mismatch at (b={b}, h={h}, t={t}): slot {a} score {float(scores[b, h, t, a])!r} vs "
+            f"K-th {float(kth[b, h, t, 0])!r}")
+    return {"addresses": B * H * T, "exempt_slots": int(diff.sum())}
+
+
+def rel_err(actual, expected) -> float:
+    """max|a - b| / max|b| over a tensor (0 when both are all zero)."""
+    a = torch.as_tensor(actual).double()
+    b = torch.as_tensor(expected).double()
+    den = b.abs().max().item() if b.numel() else 0.0
+    num = (a - b).abs().max().item() if b.numel() else 0.0
+    return num / den if den > 0 else num

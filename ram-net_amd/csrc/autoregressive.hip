@@ -1,0 +1,344 @@
+// Fused single-token decode step against a persistent slot state.
+//
+// Semantics follow the reference decode step
+// (csrc/ram_attn_topk_autoregressive.cu:37-191 and the torch path
+// torch_impl.py:217-288 at T = 1): decode the write and read addresses,
+// apply the K gated-sparse-update writes (row + mass read-modify-write),
+// then read y = sum_k r_k s_{a_k} from the post-write state. A masked batch
+// row leaves the state untouched and gets y = 0.
+//
+// MI355X mapping: one 64-lane wave per (b, h).
+//  * Fast path (P <= 64, K <= 16, C <= 256): the two addresses are decoded
+//    cooperatively (one per half-wave when they fit, lane-parallel bitonic
+//    sorts), then every write row, every read row that is not also written,
+//    and their masses are requested in one batch so the step costs a single
+//    HBM round trip; reads of a just-written slot take the updated row from
+//    LDS instead of re-reading memory.
+//  * General path: exact LDS search for each address, then sequential row
+//    updates and reads.
+#include "ramnet_device.hpp"
+#include "ramnet_kernels.hpp"
+#include "ramnet_search.hpp"
+
+#include <algorithm>
+
+namespace ramnet {
+
+namespace {
+
+constexpr int kEv = 16;   // fast path: up to 16 write and 16 read slots
+constexpr int kCpl = 4;   // fast path: up to 4 channels per lane (C <= 256)
+
+__device__ __forceinline__ float gsu_gain(float w, float d) {
+    float r = __builtin_amdgcn_rcpf(d);
+    r = fmaf(r, fmaf(-d, r, 1.f), r);
+    return w * r;
+}
+
+// Turn a group's sorted top list into (slot after CAPE, weight) events.
+__device__ __forceinline__ void finalize_events(float v, int c, bool inactive, int K, float re_norm, int li, int g0,
+                                                int shift, int A, int *slots, float *vals) {
+    float lse = 0.f;
+    const float v0 = __shfl(v, g0);
+    if (re_norm != 0.f && !inactive && v0 > kNegInfF) {
+        const float e = expf(v - v0);
+        float sum = 0.f;
+        for (int k = K - 1; k >= 0; --k)
+            sum += __shfl(e, g0 + k);
+        lse = v0 + logf(sum);
+    }
+    if (li < K) {
+        const int content = inactive ? li : c;
+        int o = content - shift;
+        o = o < 0 ? o + A : o;
+        slots[li] = o;
+        vals[li] = inactive ? 0.f : expf(v - re_norm * lse);
+    }
+}
+
+template<typename T, int GW>
+__global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob job) {
+    __shared__ int s_ws[kEv], s_rs[kEv];
+    __shared__ float s_wv[kEv], s_rv[kEv];
+    __shared__ float s_row[kEv][kWave * kCpl];
+
+    const int bh = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int H = job.H, A = job.A, C = job.C, U = job.U, P = job.P, Kw = job.Kw, Kr = job.Kr;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    T *yrow = static_cast<T *>(job.y) + static_cast<int64_t>(bh) * C;
+    if (job.mask && !job.mask[b]) {
+        for (int c = lane; c < C; c += kWave)
+            store_f32(yrow + c, 0.f);
+        return;
+    }
+    const int shift = h < job.embed_num ? pos_mod(job.position_ids[b], A) : 0;
+    const T *wp = static_cast<const T *>(job.w_addr) + static_cast<int64_t>(bh) * U * P;
+    const T *rp = static_cast<const T *>(job.r_addr) + static_cast<int64_t>(bh) * U * P;
+
+    // ---- address decode
+    if constexpr (GW == 32) {
+        const int half = lane >> 5, li = lane & 31;
+        const int K = half ? Kr : Kw;
+        float v;
+        int c;
+        const bool inactive = group_search<T, 32>(half ? rp : wp, U, P, K, li, v, c);
+        finalize_events(v, c, inactive, K, half ? job.r_re_norm : job.w_re_norm, li, half * 32, shift, A,
+                        half ? s_rs : s_ws, half ? s_rv : s_wv);
+    } else {
+        float v;
+        int c;
+        bool inactive = group_search<T, 64>(wp, U, P, Kw, lane, v, c);
+        finalize_events(v, c, inactive, Kw, job.w_re_norm, lane, 0, shift, A, s_ws, s_wv);
+        inactive = group_search<T, 64>(rp, U, P, Kr, lane, v, c);
+        finalize_events(v, c, inactive, Kr, job.r_re_norm, lane, 0, shift, A, s_rs, s_rv);
+    }
+    __syncthreads();
+
+    // ---- one batch of row requests
+    float *slot = job.slot + static_cast<int64_t>(bh) * A * C;
+    float *mass = job.mass + static_cast<int64_t>(bh) * A;
+    int wa[kEv], ra[kEv], fwd[kEv];
+    float wv[kEv], rv[kEv], wm[kEv], rm[kEv];
+    float wrow[kEv][kCpl], rrow[kEv][kCpl];
+#pragma unroll
+    for (int k = 0; k < kEv; ++k) {
+        wa[k] = k < Kw ? s_ws[k] : 0;
+        wv[k] = k < Kw ? s_wv[k] : 0.f;
+        ra[k] = k < Kr ? s_rs[k] : 0;
+        rv[k] = k < Kr ? s_rv[k] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < kEv; ++k) {
+        wm[k] = 0.f;
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j)
+            wrow[k][j] = 0.f;
+        if (wv[k] != 0.f) {
+            const float *row = slot + static_cast<int64_t>(wa[k]) * C;
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) {
+                const int c = lane + j * kWave;
+                if (c < C)
+                    wrow[k][j] = row[c];
+            }
+            wm[k] = mass[wa[k]];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kEv; ++k) {
+        fwd[k] = -1;
+#pragma unroll
+        for (int j2 = 0; j2 < kEv; ++j2)
+            if (wv[j2] != 0.f && wa[j2] == ra[k])
+                fwd[k] = j2;
+        rm[k] = 0.f;
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j)
+            rrow[k][j] = 0.f;
+        if (rv[k] != 0.f && fwd[k] < 0) {
+            const float *row = slot + static_cast<int64_t>(ra[k]) * C;
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) {
+                const int c = lane + j * kWave;
+                if (c < C)
+                    rrow[k][j] = row[c];
+            }
+            rm[k] = mass[ra[k]];
+        }
+    }
+    const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
+    float xv[kCpl];
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j) {
+        const int c = lane + j * kWave;
+        xv[j] = c < C ? load_f32(xp + c) : 0.f;
+    }
+    const float gamma = load_f32(static_cast<const T *>(job.gamma) + bh);
+
+    // ---- writes
+#pragma unroll
+    for (int k = 0; k < kEv; ++k) {
+        const float w = wv[k];
+        if (w != 0.f) {
+            const float alpha = gsu_alpha(w, gamma);
+            const float m2 = fmaf(alpha, wm[k], w);
+            const float g = gsu_gain(w, m2 + job.eps);
+            float *row = slot + static_cast<int64_t>(wa[k]) * C;
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) {
+                const int c = lane + j * kWave;
+                const float s = fmaf(g, xv[j] - wrow[k][j], wrow[k][j]);
+                s_row[k][c] = s;  // each lane re-reads only what it wrote
+                if (c < C)
+                    row[c] = s;
+            }
+            if (lane == 0)
+                mass[wa[k]] = m2;
+            wm[k] = m2;
+        }
+    }
+
+    // ---- reads of the post-write state
+    float acc[kCpl];
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j)
+        acc[j] = 0.f;
+    float sr = 0.f, srm = 0.f;
+#pragma unroll
+    for (int k = 0; k < kEv; ++k) {
+        const float r = rv[k];
+        if (r != 0.f) {
+            const int f = fwd[k];
+            float m = rm[k];
+#pragma unroll
+            for (int j2 = 0; j2 < kEv; ++j2)
+                m = f == j2 ? wm[j2] : m;
+            const float wgt = job.mass_aware ? r * m : r;
+            sr += r;
+            srm += wgt;
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) {
+                const float s = f >= 0 ? s_row[f][lane + j * kWave] : rrow[k][j];
+                acc[j] = fmaf(wgt, s, acc[j]);
+            }
+        }
+    }
+    const float scale = job.mass_aware ? sr / (srm + job.eps) : 1.f;
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j) {
+        const int c = lane + j * kWave;
+        if (c < C)
+            store_f32(yrow + c, acc[j] * scale);
+    }
+}
+
+// General shapes: exact LDS search, then sequential row updates.
+template<typename T>
+__global__ __launch_bounds__(64) void autoregressive_general_kernel(const DecodeJob job, int NA, int NPD) {
+    extern __shared__ float smem[];
+    __shared__ int s_flag;
+    const int bh = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int H = job.H, A = job.A, C = job.C, U = job.U, P = job.P, Kw = job.Kw, Kr = job.Kr;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    T *yrow = static_cast<T *>(job.y) + static_cast<int64_t>(bh) * C;
+    if (job.mask && !job.mask[b]) {
+        for (int c = lane; c < C; c += kWave)
+            store_f32(yrow + c, 0.f);
+        return;
+    }
+    float *lg = smem;
+    float *ex = lg + U * P;
+    float *sv = ex + U * NPD;
+    int *si = reinterpret_cast<int *>(sv + NA);
+    int *ev_slot = si + NA;            // Kw + Kr
+    float *ev_val = reinterpret_cast<float *>(ev_slot + Kw + Kr);  // Kw + Kr
+    const int shift = h < job.embed_num ? pos_mod(job.position_ids[b], A) : 0;
+
+    for (int which = 0; which < 2; ++which) {
+        const T *ptr = static_cast<const T *>(which ? job.r_addr : job.w_addr) + static_cast<int64_t>(bh) * U * P;
+        const int K = which ? Kr : Kw;
+        const float re = which ? job.r_re_norm : job.w_re_norm;
+        const bool inactive = block_search_exact(ptr, 1, U, P, A, NA, NPD, lg, ex, sv, si, &s_flag);
+        const float lse = (re != 0.f && !inactive) ? topk_lse_serial(sv, K) : 0.f;
+        for (int k = lane; k < K; k += kWave) {
+            const int content = inactive ? k : si[k];
+            int o = content - shift;
+            o = o < 0 ? o + A : o;
+            ev_slot[which * Kw + k] = o;
+            ev_val[which * Kw + k] = inactive ? 0.f : expf(sv[k] - re * lse);
+        }
+        __syncthreads();
+    }
+
+    float *slot = job.slot + static_cast<int64_t>(bh) * A * C;
+    float *mass = job.mass + static_cast<int64_t>(bh) * A;
+    const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
+    const float gamma = load_f32(static_cast<const T *>(job.gamma) + bh);
+    for (int k = 0; k < Kw; ++k) {
+        const float w = ev_val[k];
+        if (w == 0.f)
+            continue;
+        const int a = ev_slot[k];
+        const float alpha = gsu_alpha(w, gamma);
+        const float m2 = fmaf(alpha, mass[a], w);
+        const float g = gsu_gain(w, m2 + job.eps);
+        float *row = slot + static_cast<int64_t>(a) * C;
+        for (int c = lane; c < C; c += kWave) {
+            const float s = row[c];
+            row[c] = fmaf(g, load_f32(xp + c) - s, s);
+        }
+        __syncthreads();
+        if (lane == 0)
+            mass[a] = m2;
+        __syncthreads();
+    }
+    __threadfence_block();
+    __syncthreads();
+    float sr = 0.f, srm = 0.f;
+    for (int k = 0; k < Kr; ++k) {
+        const float r = ev_val[Kw + k];
+        sr += r;
+        srm += job.mass_aware ? r * mass[ev_slot[Kw + k]] : r;
+    }
+    const float scale = job.mass_aware ? sr / (srm + job.eps) : 1.f;
+    for (int c = lane; c < C; c += kWave) {
+        float acc = 0.f;
+        for (int k = 0; k < Kr; ++k) {
+            const float r = ev_val[Kw + k];
+            if (r == 0.f)
+                continue;
+            const int a = ev_slot[Kw + k];
+            const float wgt = job.mass_aware ? r * mass[a] : r;
+            acc = fmaf(wgt, slot[static_cast<int64_t>(a) * C + c], acc);
+        }
+        store_f32(yrow + c, acc * scale);
+    }
+}
+
+int pow2_ceil(int x) {
+    int p = 1;
+    while (p < x)
+        p <<= 1;
+    return p;
+}
+
+template<typename T>
+hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **why) {
+    const int kmax = std::max(job.Kw, job.Kr);
+    const int stair = staircase_count(kmax);
+    const bool fast_ok = job.P <= 64 && kmax <= kEv && job.C <= kWave * kCpl && stair <= 64;
+    const unsigned grid = static_cast<unsigned>(job.B * job.H);
+    if (fast_ok) {
+        if (job.P <= 32 && stair <= 32)
+            hipLaunchKernelGGL((autoregressive_fast_kernel<T, 32>), dim3(grid), dim3(kWave), 0, stream, job);
+        else
+            hipLaunchKernelGGL((autoregressive_fast_kernel<T, 64>), dim3(grid), dim3(kWave), 0, stream, job);
+        return hipGetLastError();
+    }
+    const int NA = pow2_ceil(job.A), NPD = pow2_ceil(job.P);
+    const size_t lds = static_cast<size_t>(job.U) * job.P * 4 + static_cast<size_t>(job.U) * NPD * 4 +
+                       static_cast<size_t>(NA) * 8 + static_cast<size_t>(job.Kw + job.Kr) * 8;
+    if (lds > 96 * 1024) {
+        *why = "decode step: shape needs P <= 64, top_k <= 16 and C <= 256, or P**U small enough for the exact LDS search (A <= 8192)";
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(autoregressive_general_kernel<T>, dim3(grid), dim3(kWave), lds, stream, job, NA, NPD);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const char **why) {
+    if (job.B * job.H == 0)
+        return hipSuccess;
+    switch (job.dtype) {
+        case kF32: return launch_typed<float>(job, stream, why);
+        case kF16: return launch_typed<_Float16>(job, stream, why);
+        case kBF16: return launch_typed<bf16_t>(job, stream, why);
+        default: *why = "decode step: unsupported dtype"; return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace ramnet

@@ -1,0 +1,261 @@
+// C-ABI entry points: argument validation, then one launch on the caller's
+// stream. Errors never abort: they set a thread-local message and return a
+// nonzero code (the reference raises RuntimeError from the same checks,
+// csrc/cuda_utils.cuh:375-391 and ram_attn_topk_addr.cu:241-246).
+#include "ramnet_hip.h"
+#include "ramnet_kernels.hpp"
+#include "ramnet_search.hpp"
+
+#include <stdio.h>
+#include <string>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+constexpr int64_t kIntMax = 0x7fffffffLL;
+constexpr int64_t kAddressLimit = 1LL << 30;  // headroom bit for index arithmetic
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+#define RAMNET_REQUIRE(cond, msg)              \
+    do {                                       \
+        if (!(cond))                           \
+            return fail(RAMNET_EINVAL, (msg)); \
+    } while (0)
+
+bool valid_dtype(int d) { return d == RAMNET_F32 || d == RAMNET_F16 || d == RAMNET_BF16; }
+
+// A == P**U without overflow.
+bool is_power(int64_t P, int64_t U, int64_t A) {
+    int64_t v = 1;
+    for (int64_t u = 0; u < U; ++u) {
+        v *= P;
+        if (v > kAddressLimit)
+            return false;
+    }
+    return v == A;
+}
+
+bool fits_int(std::initializer_list<int64_t> prods) {
+    for (int64_t p : prods)
+        if (p < 0 || p >= kIntMax)
+            return false;
+    return true;
+}
+
+int finish(hipError_t err, const char *why, const char *what) {
+    if (err == hipSuccess) {
+        g_last_error.clear();
+        return RAMNET_OK;
+    }
+    if (why)
+        return fail(RAMNET_EINVAL, why);
+    return fail(RAMNET_ELAUNCH, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+int check_addr_shape(int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int64_t embed_num, int64_t A) {
+    RAMNET_REQUIRE(B >= 0 && H > 0 && U > 0 && P > 0 && T >= 0, "address shape must have B, T >= 0 and H, U, P > 0");
+    RAMNET_REQUIRE(A > 0 && A < kAddressLimit, "Address space overflow: A must be in (0, 2**30)");
+    RAMNET_REQUIRE(is_power(P, U, A), "A must equal P**U");
+    RAMNET_REQUIRE(embed_num >= 0 && embed_num <= H, "embed_num must be in [0, H]");
+    return RAMNET_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ramnet_abi_version(void) { return RAMNET_ABI_VERSION; }
+
+int ramnet_int_bits(void) { return 32; }
+
+const char *ramnet_last_error(void) { return g_last_error.c_str(); }
+
+int ramnet_topk_addr_single_forward(const void *addr, int dtype, int64_t B, int64_t H, int64_t U, int64_t P,
+                                    int64_t T, int64_t embed_num, int64_t A, const int32_t *position_ids,
+                                    int64_t top_k, float top_k_re_norm, int addr_val_neg, int encode_batch_idx,
+                                    int32_t *idx_out, float *val_out, void *stream) {
+    if (int rc = check_addr_shape(B, H, U, P, T, embed_num, A))
+        return rc;
+    RAMNET_REQUIRE(valid_dtype(dtype), "addr dtype must be float32, float16 or bfloat16");
+    RAMNET_REQUIRE(top_k > 0 && top_k <= A, "top_k must be in [1, A]");
+    RAMNET_REQUIRE(top_k_re_norm >= 0.f && top_k_re_norm <= 1.f, "top_k_re_norm must be in [0, 1]");
+    RAMNET_REQUIRE(fits_int({B * H * U * P * T, B * H * A, B * H * top_k * T}), "CUDA index overflow: sizes exceed int32");
+    if (B * T == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(addr && position_ids && idx_out && val_out, "null tensor pointer");
+    ramnet::AddrJob job{};
+    job.src[0] = {addr, static_cast<int>(top_k), top_k_re_norm, addr_val_neg ? -1.f : 1.f, 0};
+    job.n_src = 1;
+    job.dtype = dtype;
+    job.B = static_cast<int>(B);
+    job.H = static_cast<int>(H);
+    job.U = static_cast<int>(U);
+    job.P = static_cast<int>(P);
+    job.T = static_cast<int>(T);
+    job.A = static_cast<int>(A);
+    job.embed_num = static_cast<int>(embed_num);
+    job.encode_batch_idx = encode_batch_idx ? 1 : 0;
+    job.k_total = static_cast<int>(top_k);
+    job.position_ids = position_ids;
+    job.idx_out = idx_out;
+    job.val_out = val_out;
+    const char *why = nullptr;
+    const hipError_t err = ramnet::launch_topk_addr(job, static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, "topk_addr_single_forward launch");
+}
+
+int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, int64_t B, int64_t H, int64_t U,
+                             int64_t P, int64_t T, int64_t embed_num, int64_t A, const int32_t *position_ids,
+                             int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
+                             int encode_batch_idx, int32_t *idx_out, float *val_out, void *stream) {
+    if (int rc = check_addr_shape(B, H, U, P, T, embed_num, A))
+        return rc;
+    RAMNET_REQUIRE(valid_dtype(dtype), "addr dtype must be float32, float16 or bfloat16");
+    RAMNET_REQUIRE(w_top_k > 0 && w_top_k <= A && r_top_k > 0 && r_top_k <= A, "top_k values must be in [1, A]");
+    RAMNET_REQUIRE(w_re_norm >= 0.f && w_re_norm <= 1.f && r_re_norm >= 0.f && r_re_norm <= 1.f,
+                   "top_k_re_norm exponents must be in [0, 1]");
+    RAMNET_REQUIRE(fits_int({B * H * U * P * T, B * H * A, B * H * (w_top_k + r_top_k) * T}),
+                   "CUDA index overflow: sizes exceed int32");
+    if (B * T == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(w_addr && r_addr && position_ids && idx_out && val_out, "null tensor pointer");
+    ramnet::AddrJob job{};
+    job.src[0] = {w_addr, static_cast<int>(w_top_k), w_re_norm, 1.f, 0};
+    job.src[1] = {r_addr, static_cast<int>(r_top_k), r_re_norm, -1.f, static_cast<int>(w_top_k)};
+    job.n_src = 2;
+    job.dtype = dtype;
+    job.B = static_cast<int>(B);
+    job.H = static_cast<int>(H);
+    job.U = static_cast<int>(U);
+    job.P = static_cast<int>(P);
+    job.T = static_cast<int>(T);
+    job.A = static_cast<int>(A);
+    job.embed_num = static_cast<int>(embed_num);
+    job.encode_batch_idx = encode_batch_idx ? 1 : 0;
+    job.k_total = static_cast<int>(w_top_k + r_top_k);
+    job.position_ids = position_ids;
+    job.idx_out = idx_out;
+    job.val_out = val_out;
+    const char *why = nullptr;
+    const hipError_t err = ramnet::launch_topk_addr(job, static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, "topk_addr_forward launch");
+}
+
+static int segment_common(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma, int dtype,
+                          const uint8_t *mask, const float *init_slot, const float *init_mass, float *slot_out,
+                          float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                          int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *stream, const char *what) {
+    RAMNET_REQUIRE(B >= 0 && H > 0 && T >= 0 && C > 0, "segment shape must have B, T >= 0 and H, C > 0");
+    RAMNET_REQUIRE(A > 0 && A < kAddressLimit, "Address space overflow: A must be in (0, 2**30)");
+    RAMNET_REQUIRE(valid_dtype(dtype), "x dtype must be float32, float16 or bfloat16");
+    RAMNET_REQUIRE(w_top_k > 0 && w_top_k <= A && r_top_k > 0 && r_top_k <= A, "top_k values must be in [1, A]");
+    RAMNET_REQUIRE(eps > 0.f, "eps must be > 0");
+    RAMNET_REQUIRE(fits_int({B * H * A * C, B * H * A, B * H * T * C, B * H * T * (w_top_k + r_top_k)}),
+                   "CUDA index overflow: sizes exceed int32");
+    if (B == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(init_slot && init_mass && slot_out && mass_out, "null state pointer");
+    RAMNET_REQUIRE(static_cast<const void *>(init_mass) != static_cast<const void *>(mass_out),
+                   "mass_out must not alias init_mass");
+    RAMNET_REQUIRE(T == 0 || (addr_idx && addr_val && x && gamma && y), "null tensor pointer");
+    ramnet::SegmentJob job{};
+    job.addr_idx = addr_idx;
+    job.addr_val = addr_val;
+    job.x = x;
+    job.gamma = gamma;
+    job.mask = mask;
+    job.init_slot = init_slot;
+    job.init_mass = init_mass;
+    job.slot_out = slot_out;
+    job.mass_out = mass_out;
+    job.y = y;
+    job.dtype = dtype;
+    job.B = static_cast<int>(B);
+    job.H = static_cast<int>(H);
+    job.T = static_cast<int>(T);
+    job.A = static_cast<int>(A);
+    job.C = static_cast<int>(C);
+    job.Kw = static_cast<int>(w_top_k);
+    job.Kr = static_cast<int>(r_top_k);
+    job.mass_aware = mass_aware ? 1 : 0;
+    job.eps = eps;
+    const char *why = nullptr;
+    const hipError_t err = ramnet::launch_segment_forward(job, static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, what);
+}
+
+int ramnet_topk_segment_forward(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
+                                int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
+                                float *slot_out, float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A,
+                                int64_t C, int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *stream) {
+    return segment_common(addr_idx, addr_val, x, gamma, dtype, mask, init_slot, init_mass, slot_out, mass_out, y, B, H,
+                          T, A, C, w_top_k, r_top_k, mass_aware, eps, stream, "topk_segment_forward launch");
+}
+
+int ramnet_topk_segment_forward_(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
+                                 int dtype, const uint8_t *mask, float *slot, float *mass, const float *mass_in,
+                                 void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
+                                 int64_t r_top_k, int mass_aware, float eps, void *stream) {
+    return segment_common(addr_idx, addr_val, x, gamma, dtype, mask, slot, mass_in, slot, mass, y, B, H, T, A, C,
+                          w_top_k, r_top_k, mass_aware, eps, stream, "topk_segment_forward_ launch");
+}
+
+int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
+                                float *slot, float *mass, const uint8_t *mask, int64_t embed_num,
+                                const int32_t *position_ids, int64_t B, int64_t H, int64_t U, int64_t P, int64_t A,
+                                int64_t C, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
+                                int mass_aware, float eps, void *y, void *stream) {
+    if (int rc = check_addr_shape(B, H, U, P, 1, embed_num, A))
+        return rc;
+    RAMNET_REQUIRE(C > 0, "C must be > 0");
+    RAMNET_REQUIRE(valid_dtype(dtype), "x dtype must be float32, float16 or bfloat16");
+    RAMNET_REQUIRE(w_top_k > 0 && w_top_k <= A && r_top_k > 0 && r_top_k <= A, "top_k values must be in [1, A]");
+    RAMNET_REQUIRE(w_re_norm >= 0.f && w_re_norm <= 1.f && r_re_norm >= 0.f && r_re_norm <= 1.f,
+                   "top_k_re_norm exponents must be in [0, 1]");
+    RAMNET_REQUIRE(eps > 0.f, "eps must be > 0");
+    RAMNET_REQUIRE(fits_int({B * H * U * P, B * H * A * C, B * H * A, B * H * C}), "CUDA index overflow: sizes exceed int32");
+    if (B == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(w_addr && r_addr && x && gamma && slot && mass && position_ids && y, "null tensor pointer");
+    ramnet::DecodeJob job{};
+    job.w_addr = w_addr;
+    job.r_addr = r_addr;
+    job.x = x;
+    job.gamma = gamma;
+    job.mask = mask;
+    job.position_ids = position_ids;
+    job.slot = slot;
+    job.mass = mass;
+    job.y = y;
+    job.dtype = dtype;
+    job.B = static_cast<int>(B);
+    job.H = static_cast<int>(H);
+    job.U = static_cast<int>(U);
+    job.P = static_cast<int>(P);
+    job.A = static_cast<int>(A);
+    job.C = static_cast<int>(C);
+    job.Kw = static_cast<int>(w_top_k);
+    job.Kr = static_cast<int>(r_top_k);
+    job.embed_num = static_cast<int>(embed_num);
+    job.w_re_norm = w_re_norm;
+    job.r_re_norm = r_re_norm;
+    job.mass_aware = mass_aware ? 1 : 0;
+    job.eps = eps;
+    const char *why = nullptr;
+    const hipError_t err = ramnet::launch_autoregressive(job, static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, "topk_autoregressive_ launch");
+}
+
+int ramnet_segment_plan(int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int *slice_channels, int *lds_bytes) {
+    if (A <= 0 || A >= kAddressLimit || C <= 0 || w_top_k <= 0 || r_top_k <= 0)
+        return 0;
+    return ramnet::segment_plan(static_cast<int>(A), static_cast<int>(C), static_cast<int>(w_top_k),
+                                static_cast<int>(r_top_k), slice_channels, lds_bytes);
+}
+
+}  // extern "C"

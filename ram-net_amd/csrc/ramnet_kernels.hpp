@@ -1,0 +1,82 @@
+// Host-side launch interface shared by the kernel translation units and the
+// C-ABI layer. Everything here is plain data: raw device pointers, sizes and
+// scalars. Shapes are validated by the C-ABI layer before any launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ramnet {
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// One address tensor to decode: logits (B, H, U, P, T) in `dtype`.
+struct AddrSource {
+    const void *addr;
+    int top_k;
+    float re_norm;  // top_k_re_norm exponent r in [0, 1]
+    float sign;     // +1, or -1 when the weights are returned negated
+    int k_off;      // first row of this address in the (B, H, k_total, T) outputs
+};
+
+// Decode one or two address tensors (write and read) sharing a shape.
+struct AddrJob {
+    AddrSource src[2];
+    int n_src;
+    int dtype;
+    int B, H, U, P, T, A;
+    int embed_num;           // CAPE applies to heads h < embed_num
+    int encode_batch_idx;    // idx = (b*H + h)*A + a, else h*A + a
+    int k_total;
+    const int32_t *position_ids;  // (B, T)
+    int32_t *idx_out;             // (B, H, k_total, T)
+    float *val_out;               // (B, H, k_total, T)
+};
+
+// Time-sequential gated sparse update + top-K read over a whole sequence.
+struct SegmentJob {
+    const int32_t *addr_idx;  // (B, H, Kw + Kr, T), encoded (b*H + h)*A + a
+    const float *addr_val;    // (B, H, Kw + Kr, T); write weights > 0, read weights stored negated
+    const void *x;            // (B, H, T, C) in dtype
+    const void *gamma;        // (B, H, T) in dtype
+    const uint8_t *mask;      // (B, T) bool, or null
+    const float *init_slot;   // (B, H, A, C)
+    const float *init_mass;   // (B, H, A)
+    float *slot_out;          // (B, H, A, C); may alias init_slot
+    float *mass_out;          // (B, H, A); may alias init_mass
+    void *y;                  // (B, H, T, C) in dtype
+    int dtype;
+    int B, H, T, A, C, Kw, Kr;
+    int mass_aware;
+    float eps;
+};
+
+// One fused autoregressive step: decode, K writes, then K reads.
+struct DecodeJob {
+    const void *w_addr;       // (B, H, U, P)
+    const void *r_addr;       // (B, H, U, P)
+    const void *x;            // (B, H, C)
+    const void *gamma;        // (B, H)
+    const uint8_t *mask;      // (B) or null
+    const int32_t *position_ids;  // (B)
+    float *slot;              // (B, H, A, C), updated in place
+    float *mass;              // (B, H, A), updated in place
+    void *y;                  // (B, H, C)
+    int dtype;
+    int B, H, U, P, A, C, Kw, Kr;
+    int embed_num;
+    float w_re_norm, r_re_norm;
+    int mass_aware;
+    float eps;
+};
+
+// Launchers return hipSuccess or the launch error; `why` receives a static
+// message when the shape is outside what the kernels were built for.
+hipError_t launch_topk_addr(const AddrJob &job, hipStream_t stream, const char **why);
+hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, const char **why);
+hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const char **why);
+
+// Channel-slice width and dynamic LDS bytes the segment kernel would use.
+int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes);
+
+}  // namespace ramnet

@@ -1,0 +1,296 @@
+// Product-Softmax top-K address decoder for gfx950.
+//
+// Semantics follow the reference decoder
+// (packages/ramnet-ops/src/ramnet_ops/impl/torch_impl.py:152-214 and
+// csrc/ram_attn_topk_addr.cu:51-117):
+//   L_u = log_softmax(x_u) per digit (fp32),
+//   score(c) = ((L_0[d_0] + L_1[d_1]) + L_2[d_2]) ..., c = sum_u d_u P^u,
+//   top-K of score under (score desc, content index asc),
+//   val = exp(score - r * logsumexp_K(score)),
+//   CAPE: out = (c - pos) mod A for heads h < embed_num,
+//   an address with any all -inf digit is inactive: val = 0.
+//
+// Two kernels:
+//  * topk_addr_lane_kernel: one lane per (b, h, t) address. Per digit the P
+//    log-probabilities are sorted in registers with a bitonic network and the
+//    running top-K prefix list is merged column by column
+//    (prefix_i + digit_j for every j), so the search never materialises the
+//    A = P^U scores. Used for P <= 64, K <= 16.
+//  * topk_addr_bruteforce_kernel: one workgroup per address materialises all
+//    A scores in LDS and bitonic-sorts them; exact for every K <= A.
+//    Used for the shapes the lane kernel does not cover (A <= 8192).
+#include "ramnet_device.hpp"
+#include "ramnet_kernels.hpp"
+#include "ramnet_search.hpp"
+
+#include <math.h>
+
+namespace ramnet {
+
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// Sorted top-KM of one digit's NP (padded) log-probabilities.
+template<int NP, int KM, int G = 0>
+__device__ __forceinline__ void sort_groups(float (&v)[NP], int (&id)[NP]) {
+    if constexpr (G * KM < NP) {
+        bitonic_sort<KM, G * KM>(v, id);
+        sort_groups<NP, KM, G + 1>(v, id);
+    }
+}
+
+template<int NP, int KM>
+__device__ __forceinline__ void digit_topk(float (&v)[NP], int (&id)[NP], float (&dv)[KM], int (&di)[KM]) {
+    if constexpr (NP <= KM) {
+        bitonic_sort<NP, 0>(v, id);
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+            dv[k] = k < NP ? v[k < NP ? k : 0] : kNegInf;
+            di[k] = k < NP ? id[k < NP ? k : 0] : kNoIdx;
+        }
+    } else {
+        sort_groups<NP, KM>(v, id);
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+            dv[k] = v[k];
+            di[k] = id[k];
+        }
+#pragma unroll
+        for (int g = 1; g < NP / KM; ++g) {
+            float tv[KM];
+            int ti[KM];
+#pragma unroll
+            for (int k = 0; k < KM; ++k) {
+                tv[k] = v[g * KM + k];
+                ti[k] = id[g * KM + k];
+            }
+            merge_topk(dv, di, tv, ti);
+        }
+    }
+}
+
+// Column j of the prefix x digit candidate grid: prefix_i + digit_j, which is
+// sorted in i because the prefix list is.
+template<int KM>
+__device__ __forceinline__ void build_column(const float (&mv)[KM], const int (&mi)[KM], float dvj, int dij, int stride,
+                                             float (&cv)[KM], int (&ci)[KM]) {
+#pragma unroll
+    for (int i = 0; i < KM; ++i) {
+        const bool ok = mi[i] != kNoIdx && dij != kNoIdx;
+        cv[i] = ok ? mv[i] + dvj : kNegInf;
+        ci[i] = ok ? mi[i] + stride * dij : kNoIdx;
+    }
+}
+
+template<typename Scalar, int NP, int KM>
+__global__ __launch_bounds__(256) void topk_addr_lane_kernel(const AddrJob job) {
+    const AddrSource &src = job.src[blockIdx.y];
+    const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= n)
+        return;
+    const int T = job.T, H = job.H, U = job.U, P = job.P, A = job.A;
+    const int t = static_cast<int>(gid % T);
+    const int64_t bh = gid / T;
+    const int h = static_cast<int>(bh % H);
+    const int b = static_cast<int>(bh / H);
+    const Scalar *base = static_cast<const Scalar *>(src.addr) + bh * static_cast<int64_t>(U * P) * T + t;
+
+    float mv[KM];
+    int mi[KM];
+    bool inactive = false;
+    int stride = 1;
+    for (int u = 0; u < U; ++u) {
+        float v[NP];
+        int id[NP];
+        bool all_ninf = true;
+        float mx = kNegInf;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            v[p] = p < P ? load_f32(base + static_cast<int64_t>(u * P + p) * T) : kNegInf;
+            id[p] = p < P ? p : kNoIdx;
+            all_ninf = all_ninf && (p >= P || v[p] == kNegInf);
+            mx = fmaxf(mx, v[p]);
+        }
+        inactive = inactive || all_ninf;
+        // log-softmax; the exponentials are summed with a fixed pairwise tree
+        // (padding lanes contribute exact zeros).
+        float e[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            e[p] = p < P ? expf(v[p] - mx) : 0.f;
+#pragma unroll
+        for (int s = NP / 2; s >= 1; s >>= 1) {
+#pragma unroll
+            for (int p = 0; p < s; ++p)
+                e[p] += e[p + s];
+        }
+        const float ls = logf(e[0]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            v[p] = p < P ? (v[p] - mx) - ls : kNegInf;
+
+        float dv[KM];
+        int di[KM];
+        digit_topk<NP, KM>(v, id, dv, di);
+        if (u == 0) {
+#pragma unroll
+            for (int k = 0; k < KM; ++k) {
+                mv[k] = dv[k];
+                mi[k] = di[k];
+            }
+        } else {
+            float av[KM], cv[KM];
+            int ai[KM], ci[KM];
+            build_column(mv, mi, dv[0], di[0], stride, av, ai);
+#pragma unroll
+            for (int j = 1; j < KM; ++j) {
+                build_column(mv, mi, dv[j], di[j], stride, cv, ci);
+                merge_topk(av, ai, cv, ci);
+            }
+#pragma unroll
+            for (int k = 0; k < KM; ++k) {
+                mv[k] = av[k];
+                mi[k] = ai[k];
+            }
+        }
+        stride *= P;
+    }
+
+    const int K = src.top_k;
+    float lse = 0.f;
+    if (src.re_norm != 0.f && !inactive && mv[0] > kNegInf) {
+        float sum = 0.f;
+#pragma unroll
+        for (int k = KM - 1; k >= 0; --k)
+            if (k < K)
+                sum += expf(mv[k] - mv[0]);
+        lse = mv[0] + logf(sum);
+    }
+    const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + t], A) : 0;
+    const int idx_base = (job.encode_batch_idx ? static_cast<int>(bh) : h) * A;
+    const int64_t row0 = (bh * job.k_total + src.k_off) * static_cast<int64_t>(T) + t;
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+        if (k < K) {
+            const int c = inactive ? k : mi[k];
+            const float val = inactive ? 0.f : expf(mv[k] - src.re_norm * lse);
+            int o = c - shift;
+            o = o < 0 ? o + A : o;
+            job.idx_out[row0 + static_cast<int64_t>(k) * T] = idx_base + o;
+            job.val_out[row0 + static_cast<int64_t>(k) * T] = src.sign * val;
+        }
+    }
+}
+
+// Workgroup-per-address exact search (all A scores in LDS).
+template<typename Scalar>
+__global__ __launch_bounds__(256) void topk_addr_bruteforce_kernel(const AddrJob job, int NA, int NPD) {
+    extern __shared__ float smem[];
+    const AddrSource &src = job.src[blockIdx.y];
+    const int T = job.T, H = job.H, U = job.U, P = job.P, A = job.A;
+    const int64_t gid = blockIdx.x;  // (b, h, t)
+    const int t = static_cast<int>(gid % T);
+    const int64_t bh = gid / T;
+    const int h = static_cast<int>(bh % H);
+    const int b = static_cast<int>(bh / H);
+    const Scalar *base = static_cast<const Scalar *>(src.addr) + bh * static_cast<int64_t>(U * P) * T + t;
+
+    float *lg = smem;
+    float *ex = lg + U * P;
+    float *sv = ex + U * NPD;
+    int *si = reinterpret_cast<int *>(sv + NA);
+    __shared__ int s_flag;
+    __shared__ float s_lse;
+    const bool inactive = block_search_exact(base, static_cast<int64_t>(T), U, P, A, NA, NPD, lg, ex, sv, si, &s_flag);
+    const int K = src.top_k;
+    const int tid = threadIdx.x;
+    if (tid == 0)
+        s_lse = (src.re_norm != 0.f && !inactive) ? topk_lse_serial(sv, K) : 0.f;
+    __syncthreads();
+    const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + t], A) : 0;
+    const int idx_base = (job.encode_batch_idx ? static_cast<int>(bh) : h) * A;
+    const int64_t row0 = (bh * job.k_total + src.k_off) * static_cast<int64_t>(T) + t;
+    for (int k = tid; k < K; k += blockDim.x) {
+        const int c = inactive ? k : si[k];
+        const float val = inactive ? 0.f : expf(sv[k] - src.re_norm * s_lse);
+        int o = c - shift;
+        o = o < 0 ? o + A : o;
+        job.idx_out[row0 + static_cast<int64_t>(k) * T] = idx_base + o;
+        job.val_out[row0 + static_cast<int64_t>(k) * T] = src.sign * val;
+    }
+}
+
+int pow2_at_least(int x) {
+    int p = 1;
+    while (p < x)
+        p <<= 1;
+    return p;
+}
+
+template<typename T, int NP, int KM>
+hipError_t launch_lane(const AddrJob &job, hipStream_t stream) {
+    const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256), job.n_src);
+    hipLaunchKernelGGL((topk_addr_lane_kernel<T, NP, KM>), grid, dim3(256), 0, stream, job);
+    return hipGetLastError();
+}
+
+template<typename T, int NP>
+hipError_t launch_lane_k(const AddrJob &job, int km, hipStream_t stream) {
+    switch (km) {
+        case 4: return launch_lane<T, NP, 4>(job, stream);
+        case 8: return launch_lane<T, NP, 8>(job, stream);
+        default: return launch_lane<T, NP, 16>(job, stream);
+    }
+}
+
+template<typename T>
+hipError_t launch_typed(const AddrJob &job, hipStream_t stream, const char **why) {
+    int kmax = 0;
+    for (int s = 0; s < job.n_src; ++s)
+        kmax = job.src[s].top_k > kmax ? job.src[s].top_k : kmax;
+    const int np = pow2_at_least(job.P < 4 ? 4 : job.P);
+    const int km = pow2_at_least(kmax < 4 ? 4 : kmax);
+    const bool lane_ok = np <= 64 && km <= 16;
+    if (lane_ok) {
+        switch (np) {
+            case 4: return launch_lane_k<T, 4>(job, km, stream);
+            case 8: return launch_lane_k<T, 8>(job, km, stream);
+            case 16: return launch_lane_k<T, 16>(job, km, stream);
+            case 32: return launch_lane_k<T, 32>(job, km, stream);
+            default: return launch_lane_k<T, 64>(job, km, stream);
+        }
+    }
+    const int NA = pow2_at_least(job.A);
+    const int NPD = pow2_at_least(job.P);
+    const size_t lds = static_cast<size_t>(job.U) * job.P * 4 + static_cast<size_t>(job.U) * NPD * 4 + static_cast<size_t>(NA) * 8;
+    if (lds > 96 * 1024) {
+        *why = "address decoder: shape needs P <= 64 and top_k <= 16, or P**U small enough for the exact LDS search (A <= 8192)";
+        return hipErrorInvalidValue;
+    }
+    const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
+    if (n > 0x7fffffff) {
+        *why = "address decoder: B*H*T too large for the exact search grid";
+        return hipErrorInvalidValue;
+    }
+    const dim3 grid(static_cast<unsigned>(n), job.n_src);
+    hipLaunchKernelGGL(topk_addr_bruteforce_kernel<T>, grid, dim3(256), lds, stream, job, NA, NPD);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_topk_addr(const AddrJob &job, hipStream_t stream, const char **why) {
+    if (static_cast<int64_t>(job.B) * job.H * job.T == 0)
+        return hipSuccess;
+    switch (job.dtype) {
+        case kF32: return launch_typed<float>(job, stream, why);
+        case kF16: return launch_typed<_Float16>(job, stream, why);
+        case kBF16: return launch_typed<bf16_t>(job, stream, why);
+        default: *why = "address decoder: unsupported dtype"; return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace ramnet

@@ -1,0 +1,183 @@
+"""``torch.library`` operators backed by the gfx950 C ABI.
+
+Operator names follow the reference extension's dispatcher registrations
+(packages/ramnet-ops/csrc/ram_attn_bind.cpp:22-113) so that
+``torch.ops.ramnet_ops.<name>`` resolves to the MI355X kernels. Schemas of
+the decoder and decode-step ops are the reference's; the segment ops drop the
+event-grouping metadata (seg_idx/seg_off/seg_len/event_i) because the HIP
+scan walks time in order and needs no sort, and take the decoded indices
+instead. Every op allocates its outputs with torch and launches on the
+current stream of the input's device; fake (meta) implementations give
+output shapes for tracing.
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from .. import _native as nat
+
+_NS = "ramnet_ops"
+
+
+def _code(t: Tensor) -> int:
+    try:
+        return nat.DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise RuntimeError(f"ramnet_ops: unsupported dtype {t.dtype}; expected float32, float16 or bfloat16") from None
+
+
+def _require_gpu(name: str, *tensors: Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{name}: tensors must be on a GPU (HIP) device, got {t.device}")
+
+
+# --------------------------------------------------------------------------
+# address decoder
+
+@torch.library.custom_op(f"{_NS}::topk_addr_single_forward", mutates_args=(), device_types="cuda")
+def topk_addr_single_forward(addr: Tensor, embed_num: int, A: int, position_ids: Tensor, top_k: int,
+                             top_k_re_norm: float, addr_val_neg: bool = False,
+                             encode_batch_idx: bool = True) -> tuple[Tensor, Tensor]:
+    _require_gpu("topk_addr_single_forward", addr, position_ids)
+    B, H, U, P, T = addr.shape
+    addr = addr.contiguous()
+    pos = position_ids.to(device=addr.device, dtype=torch.int32).contiguous()
+    idx = torch.empty((B, H, top_k, T), dtype=torch.int32, device=addr.device)
+    val = torch.empty((B, H, top_k, T), dtype=torch.float32, device=addr.device)
+    with torch.cuda.device(addr.device):
+        nat.call("ramnet_topk_addr_single_forward", addr.data_ptr(), _code(addr), B, H, U, P, T, embed_num, A,
+                 pos.data_ptr(), top_k, float(top_k_re_norm), int(addr_val_neg), int(encode_batch_idx),
+                 idx.data_ptr(), val.data_ptr(), nat.stream_of(addr))
+    return idx, val
+
+
+@topk_addr_single_forward.register_fake
+def _(addr, embed_num, A, position_ids, top_k, top_k_re_norm, addr_val_neg=False, encode_batch_idx=True):
+    B, H, _, _, T = addr.shape
+    shape = (B, H, top_k, T)
+    return addr.new_empty(shape, dtype=torch.int32), addr.new_empty(shape, dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{_NS}::topk_addr_forward", mutates_args=(), device_types="cuda")
+def topk_addr_forward(w_addr: Tensor, r_addr: Tensor, embed_num: int, A: int, position_ids: Tensor, w_top_k: int,
+                      r_top_k: int, w_re_norm: float, r_re_norm: float,
+                      encode_batch_idx: bool = True) -> tuple[Tensor, Tensor]:
+    _require_gpu("topk_addr_forward", w_addr, r_addr, position_ids)
+    B, H, U, P, T = w_addr.shape
+    if r_addr.shape != w_addr.shape or r_addr.dtype != w_addr.dtype:
+        raise RuntimeError("topk_addr_forward: w_addr and r_addr must share shape and dtype")
+    w_addr, r_addr = w_addr.contiguous(), r_addr.contiguous()
+    pos = position_ids.to(device=w_addr.device, dtype=torch.int32).contiguous()
+    K = w_top_k + r_top_k
+    idx = torch.empty((B, H, K, T), dtype=torch.int32, device=w_addr.device)
+    val = torch.empty((B, H, K, T), dtype=torch.float32, device=w_addr.device)
+    with torch.cuda.device(w_addr.device):
+        nat.call("ramnet_topk_addr_forward", w_addr.data_ptr(), r_addr.data_ptr(), _code(w_addr), B, H, U, P, T,
+                 embed_num, A, pos.data_ptr(), w_top_k, r_top_k, float(w_re_norm), float(r_re_norm),
+                 int(encode_batch_idx), idx.data_ptr(), val.data_ptr(), nat.stream_of(w_addr))
+    return idx, val
+
+
+@topk_addr_forward.register_fake
+def _(w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re_norm, r_re_norm, encode_batch_idx=True):
+    B, H, _, _, T = w_addr.shape
+    shape = (B, H, w_top_k + r_top_k, T)
+    return w_addr.new_empty(shape, dtype=torch.int32), w_addr.new_empty(shape, dtype=torch.float32)
+
+
+# --------------------------------------------------------------------------
+# segment scan (prefill)
+
+def _segment_args(addr_idx, addr_val, x, gamma, mask):
+    B, H, T, C = x.shape
+    x = x.contiguous()
+    gamma = gamma.to(dtype=x.dtype).contiguous()
+    addr_idx = addr_idx.to(torch.int32).contiguous()
+    addr_val = addr_val.to(torch.float32).contiguous()
+    if mask is not None:
+        mask = mask.to(device=x.device, dtype=torch.bool).contiguous()
+    return B, H, T, C, addr_idx, addr_val, x, gamma, mask
+
+
+@torch.library.custom_op(f"{_NS}::topk_segment_forward", mutates_args=(), device_types="cuda")
+def topk_segment_forward(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, init_slot: Tensor,
+                         init_mass: Tensor, mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool,
+                         eps: float) -> tuple[Tensor, Tensor, Tensor]:
+    _require_gpu("topk_segment_forward", addr_idx, addr_val, x, gamma, init_slot, init_mass, mask)
+    B, H, T, C, addr_idx, addr_val, x, gamma, mask = _segment_args(addr_idx, addr_val, x, gamma, mask)
+    A = init_slot.shape[-2]
+    init_slot = init_slot.to(torch.float32).contiguous()
+    init_mass = init_mass.to(torch.float32).contiguous()
+    slot = torch.empty_like(init_slot)
+    mass = torch.empty_like(init_mass)
+    y = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        nat.call("ramnet_topk_segment_forward", addr_idx.data_ptr(), addr_val.data_ptr(), x.data_ptr(),
+                 gamma.data_ptr(), _code(x), nat.ptr(mask), init_slot.data_ptr(), init_mass.data_ptr(),
+                 slot.data_ptr(), mass.data_ptr(), y.data_ptr(), B, H, T, A, C, w_top_k, r_top_k, int(mass_aware),
+                 float(eps), nat.stream_of(x))
+    return y, slot, mass
+
+
+@topk_segment_forward.register_fake
+def _(addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps):
+    return (x.new_empty(x.shape), init_slot.new_empty(init_slot.shape, dtype=torch.float32),
+            init_mass.new_empty(init_mass.shape, dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{_NS}::topk_segment_forward_", mutates_args=("slot", "mass"), device_types="cuda")
+def topk_segment_forward_(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
+                          mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool, eps: float) -> Tensor:
+    _require_gpu("topk_segment_forward_", addr_idx, addr_val, x, gamma, slot, mass, mask)
+    if slot.dtype != torch.float32 or mass.dtype != torch.float32 or not (slot.is_contiguous() and mass.is_contiguous()):
+        raise RuntimeError("topk_segment_forward_: slot and mass must be contiguous float32 tensors")
+    B, H, T, C, addr_idx, addr_val, x, gamma, mask = _segment_args(addr_idx, addr_val, x, gamma, mask)
+    A = slot.shape[-2]
+    # channel slices of one head may start after another has stored the new
+    # masses, so every slice reads the masses from a snapshot
+    mass_in = mass.clone()
+    y = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        nat.call("ramnet_topk_segment_forward_", addr_idx.data_ptr(), addr_val.data_ptr(), x.data_ptr(),
+                 gamma.data_ptr(), _code(x), nat.ptr(mask), slot.data_ptr(), mass.data_ptr(), mass_in.data_ptr(),
+                 y.data_ptr(), B, H, T, A, C, w_top_k, r_top_k, int(mass_aware), float(eps), nat.stream_of(x))
+    return y
+
+
+@topk_segment_forward_.register_fake
+def _(addr_idx, addr_val, x, gamma, slot, mass, mask, w_top_k, r_top_k, mass_aware, eps):
+    return x.new_empty(x.shape)
+
+
+# --------------------------------------------------------------------------
+# fused decode step
+
+@torch.library.custom_op(f"{_NS}::topk_autoregressive_", mutates_args=("slot", "mass"), device_types="cuda")
+def topk_autoregressive_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
+                         mask: Tensor, embed_num: int, position_ids: Tensor, w_top_k: int, r_top_k: int,
+                         w_re_norm: float, r_re_norm: float, mass_aware: bool, eps: float) -> Tensor:
+    _require_gpu("topk_autoregressive_", w_addr, r_addr, x, gamma, slot, mass, position_ids)
+    if slot.dtype != torch.float32 or mass.dtype != torch.float32 or not (slot.is_contiguous() and mass.is_contiguous()):
+        raise RuntimeError("topk_autoregressive_: slot and mass must be contiguous float32 tensors")
+    B, H, U, P = w_addr.shape
+    C = x.shape[-1]
+    A = slot.shape[-2]
+    w_addr, r_addr, x = w_addr.contiguous(), r_addr.contiguous(), x.contiguous()
+    gamma = gamma.to(dtype=x.dtype).contiguous()
+    pos = position_ids.to(device=x.device, dtype=torch.int32).contiguous()
+    m = None if mask is None or mask.numel() == 0 else mask.to(device=x.device, dtype=torch.bool).contiguous()
+    y = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        nat.call("ramnet_topk_autoregressive_", w_addr.data_ptr(), r_addr.data_ptr(), x.data_ptr(), gamma.data_ptr(),
+                 _code(x), slot.data_ptr(), mass.data_ptr(), nat.ptr(m), embed_num, pos.data_ptr(), B, H, U, P, A, C,
+                 w_top_k, r_top_k, float(w_re_norm), float(r_re_norm), int(mass_aware), float(eps), y.data_ptr(),
+                 nat.stream_of(x))
+    return y
+
+
+@topk_autoregressive_.register_fake
+def _(w_addr, r_addr, x, gamma, slot, mass, mask, embed_num, position_ids, w_top_k, r_top_k, w_re_norm, r_re_norm,
+      mass_aware, eps):
+    return x.new_empty(x.shape)
