@@ -218,36 +218,45 @@ def bench_decode(n_steps, dev, graph=True):
     }
 
 
-def cpu_baseline(host, tokens=256, batch_rows=1):
-    """Dense reference algorithm (oracle restatement) on host cores over a bounded sample of the C2 inputs."""
+def cpu_baseline(host, target_s=12.0, batch_rows=None):
+    """Dense reference algorithm (oracle restatement) on host cores over a bounded sample of the C2 inputs.
+
+    A 16-token calibration run sizes the sample so that the timed run takes
+    about ``target_s`` seconds (capped at the full sequence).
+    """
     import oracle
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
     c = C2
-    H, C, U, P, K = c["H"], c["C"], c["U"], c["P"], c["K"]
+    H, C, U, P, K, T = c["H"], c["C"], c["U"], c["P"], c["K"], c["T"]
+    rows = c["B"] if batch_rows is None else batch_rows
     A = P ** U
-    sl = (slice(0, batch_rows), slice(None))
-    w = host["w"][sl][..., :tokens]
-    r = host["r"][sl][..., :tokens]
-    x = host["x"][sl][:, :, :tokens]
-    gm = host["gamma"][sl][..., :tokens]
-    pos = host["pos"][:batch_rows, :tokens].long()
-    slot = torch.zeros(batch_rows, H, A, C)
-    mass = torch.full((batch_rows, H, A), 1.0 / A)
-    # warm-up on a few tokens
-    oracle.dense_ram_attn(w[..., :4], r[..., :4], x[:, :, :4], gm[..., :4], slot, mass, None, H // 2, pos[:, :4],
-                          (K, K), (0.0, 0.0), False, 1e-12, chunk=tokens)
-    t0 = time.perf_counter()
-    oracle.dense_ram_attn(w, r, x, gm, slot, mass, None, H // 2, pos, (K, K), (0.0, 0.0), False, 1e-12,
-                          chunk=tokens)
-    dt = time.perf_counter() - t0
+
+    def run(tokens):
+        w = host["w"][:rows, ..., :tokens]
+        r = host["r"][:rows, ..., :tokens]
+        x = host["x"][:rows, :, :tokens]
+        gm = host["gamma"][:rows, :, :tokens]
+        pos = host["pos"][:rows, :tokens].long()
+        slot = torch.zeros(rows, H, A, C)
+        mass = torch.full((rows, H, A), 1.0 / A)
+        t0 = time.perf_counter()
+        oracle.dense_ram_attn(w, r, x, gm, slot, mass, None, H // 2, pos, (K, K), (0.0, 0.0), False, 1e-12,
+                              chunk=256)
+        return time.perf_counter() - t0
+
+    cal = run(16)
+    tokens = int(min(T, max(16, 16 * target_s / max(cal, 1e-3))))
+    tokens = max(16, (tokens // 16) * 16)
+    dt = run(tokens)
     return {
-        "value": batch_rows * tokens / dt,
+        "value": rows * tokens / dt,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"config 2 inputs, batch rows {batch_rows} of {c['B']}, first {tokens} of {c['T']} tokens, all "
-                  f"{H} heads; dense decode + per-step dense GSU (torch_impl.py algorithm) in {dt:.1f} s",
+        "sample": f"config 2 inputs: {rows} of {c['B']} batch rows x first {tokens} of {T} tokens, all {H} heads; "
+                  f"dense decode of all {A} slots + per-step dense GSU (the reference torch_impl.py algorithm), "
+                  f"{dt:.1f} s",
         "cpu": platform.processor() or platform.machine(),
         "seconds": dt,
     }
@@ -259,7 +268,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=C3["steps"])
-    ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only", choices=("prefill", "decode"), default=None)
@@ -338,7 +347,7 @@ def main(argv=None) -> int:
                         "config": {"workload": "config 3 decode: B=64, H=16, A=1024, d_v=128, K=8, 512 steps"}})
     if pre is not None and not args.no_cpu_baseline:
         log("cpu baseline: dense reference algorithm on host cores")
-        out["cpu_baseline"] = cpu_baseline(pre["host"], tokens=args.cpu_tokens)
+        out["cpu_baseline"] = cpu_baseline(pre["host"], target_s=args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -32,11 +32,12 @@ namespace {
 
 constexpr int kMetaPerLane = 16;  // staged (slot, weight) pairs per lane per chunk
 constexpr int kXPerLane = 16;     // staged x-slice values per lane per chunk
-constexpr int kMaxChunk = 64;     // tokens per chunk (<= one per lane for gamma/mask)
+constexpr int kMaxChunk = 64;     // tokens per chunk (one gamma per lane)
 
 struct SegGeom {
     int n_units, ns, cs, L, n_chunks;
-    int st_off, ms_off, ma_off, mv_off, al_off, xs_off, gm_off, mk_off;  // LDS offsets in 4-byte words
+    int lpe, epp;                  // lanes per event, events per pass (lpe * epp = 64)
+    int st_off, ms_off, ev_off, al_off, xs_off, gm_off, mk_off;  // LDS offsets in 4-byte words
 };
 
 // 1/d refined by one Newton step; gain = w / (m + eps) to ~1 ulp.
@@ -46,7 +47,37 @@ __device__ __forceinline__ float gsu_gain(float w, float d) {
     return w * r;
 }
 
-template<typename Scalar, int VEC, bool MASS_AWARE>
+template<int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the `epp` consecutive lanes of an event group; every lane of the
+// group receives the same value. Within a 16-lane row the exchange uses DPP
+// (quad permutes, half-row and row mirrors); wider groups add lane shuffles.
+__device__ __forceinline__ float group_sum(float v, int epp) {
+    if (epp >= 2) v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    if (epp >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    if (epp >= 8) v += dpp<0x141>(v);  // row_half_mirror
+    if (epp >= 16) v += dpp<0x140>(v); // row_mirror
+    if (epp >= 32) v += __shfl_xor(v, 16);
+    if (epp >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+// Token loop state of one lane: its write and read events (one per pass)
+// and its channels of the token's value.
+template<int VEC, int NP>
+struct TokenMeta {
+    int aw[NP];
+    float w[NP];
+    float al[NP];
+    int ar[NP];
+    float r[NP];
+    float x[VEC];
+};
+
+template<typename Scalar, int VEC, int NP>
 __global__ __launch_bounds__(64) void segment_forward_kernel(const SegmentJob job, const SegGeom geo) {
     extern __shared__ float lds[];
     // Workgroups are dealt round-robin to the 8 XCDs; give each XCD a
@@ -56,22 +87,22 @@ __global__ __launch_bounds__(64) void segment_forward_kernel(const SegmentJob jo
     if (unit >= geo.n_units)
         return;
     const int lane = threadIdx.x;
-    const int ns = geo.ns, CS = geo.cs, L = geo.L;
+    const int ns = geo.ns, CS = geo.cs, L = geo.L, EPP = geo.epp;
     const int bh = unit / ns;
     const int c0 = (unit % ns) * CS;
     const int b = bh / job.H;
     const int T = job.T, A = job.A, C = job.C, Kw = job.Kw, Kr = job.Kr;
     const int Kt = Kw + Kr;
     const float eps = job.eps;
+    const bool mass_aware = job.mass_aware != 0;
 
-    float *st = lds + geo.st_off;                                // A * CS
-    float *ms = lds + geo.ms_off;                                // A
-    int *ma = reinterpret_cast<int *>(lds + geo.ma_off);         // L * Kt
-    float *mv = lds + geo.mv_off;                                // L * Kt
-    float *al = lds + geo.al_off;                                // L * Kw
-    float *xs = lds + geo.xs_off;                                // L * CS
-    float *gm = lds + geo.gm_off;                                // L
-    int *mk = reinterpret_cast<int *>(lds + geo.mk_off);         // L
+    float *st = lds + geo.st_off;                              // A * CS   slot slice
+    float *ms = lds + geo.ms_off;                              // A        masses
+    int2 *evm = reinterpret_cast<int2 *>(lds + geo.ev_off);    // L * Kt   (slot, weight) per event
+    float *al = lds + geo.al_off;                              // L * Kw   forget coefficient per write
+    float *xs = lds + geo.xs_off;                              // L * CS   x slice
+    float *gm = lds + geo.gm_off;                              // L        gamma
+    int *mk = reinterpret_cast<int *>(lds + geo.mk_off);       // L        token valid
 
     // ---- state slice -> LDS
     {
@@ -92,13 +123,16 @@ __global__ __launch_bounds__(64) void segment_forward_kernel(const SegmentJob jo
     Scalar *gy = static_cast<Scalar *>(job.y) + static_cast<int64_t>(bh) * T * C;
     const int slot_base = bh * A;
 
-    // ---- chunk staging registers
+    // ---- chunk staging registers (next chunk's loads are in flight while
+    // the current chunk is processed)
     int r_idx[kMetaPerLane];
     float r_val[kMetaPerLane];
     float r_x[kXPerLane];
     float r_g = 0.f;
     int r_mk = 0;
 
+    // Staging writes masked tokens and out-of-range slots with weight 0,
+    // which makes every event of the token a no-op and its read sum 0.
     auto load_chunk = [&](int t0) {
 #pragma unroll
         for (int q = 0; q < kMetaPerLane; ++q) {
@@ -121,7 +155,73 @@ __global__ __launch_bounds__(64) void segment_forward_kernel(const SegmentJob jo
         r_mk = tok ? (job.mask ? static_cast<int>(job.mask[static_cast<int64_t>(b) * T + t0 + lane] != 0) : 1) : 0;
     };
 
-    auto store_chunk = [&]() {
+    const int ev = lane & (EPP - 1);   // event slot of this lane within a pass
+    const int cg = lane / EPP;         // channel group
+    const int cl = cg * VEC;           // first channel of this lane within the slice
+
+    auto fetch = [&](int tt, TokenMeta<VEC, NP> &m) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const int e = p * EPP + ev;
+            const bool okw = e < Kw, okr = e < Kr;
+            const int2 we = evm[tt * Kt + (okw ? e : 0)];
+            const int2 re = evm[tt * Kt + Kw + (okr ? e : 0)];
+            m.aw[p] = we.x;
+            m.w[p] = okw ? __int_as_float(we.y) : 0.f;
+            m.al[p] = okw ? al[tt * Kw + e] : 1.f;
+            m.ar[p] = re.x;
+            m.r[p] = okr ? __int_as_float(re.y) : 0.f;
+        }
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+            m.x[v] = xs[tt * CS + cl + v];
+    };
+
+    // deferred read of the previous token
+    bool pend = false;
+    int pend_t = 0;
+    float prs[NP][VEC], pr[NP], prm[NP];
+
+    auto flush = [&]() {
+        float acc[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+            acc[v] = 0.f;
+        float sr = 0.f, srm = 0.f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float wgt = mass_aware ? pr[p] * prm[p] : pr[p];
+            sr += pr[p];
+            srm += wgt;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+                acc[v] = fmaf(wgt, prs[p][v], acc[v]);
+        }
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+            acc[v] = group_sum(acc[v], EPP);
+        if (mass_aware) {
+            sr = group_sum(sr, EPP);
+            srm = group_sum(srm, EPP);
+            const float scale = sr / (srm + eps);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+                acc[v] *= scale;
+        }
+        if (ev == 0) {
+            Scalar *yrow = gy + static_cast<int64_t>(pend_t) * C + c0 + cl;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+                if (c0 + cl + v < C)
+                    store_f32(yrow + v, acc[v]);
+        }
+    };
+
+    load_chunk(0);
+    for (int ci = 0; ci < geo.n_chunks; ++ci) {
+        const int t0 = ci * L;
+        __syncthreads();
+        // ---- stage the chunk
 #pragma unroll
         for (int q = 0; q < kMetaPerLane; ++q) {
             const int j = lane + q * kWave;
@@ -129,9 +229,9 @@ __global__ __launch_bounds__(64) void segment_forward_kernel(const SegmentJob jo
                 const int kk = j / L, tt = j - kk * L;
                 const int a = r_idx[q] - slot_base;
                 const bool ok = a >= 0 && a < A;
-                ma[tt * Kt + kk] = ok ? a : 0;
                 // reads are stored negated by the decoder; keep positive weights
-                mv[tt * Kt + kk] = ok ? (kk < Kw ? r_val[q] : -r_val[q]) : 0.f;
+                const float wv = ok ? (kk < Kw ? r_val[q] : -r_val[q]) : 0.f;
+                evm[tt * Kt + kk] = make_int2(ok ? a : 0, __float_as_int(wv));
             }
         }
 #pragma unroll
@@ -144,117 +244,74 @@ __global__ __launch_bounds__(64) void segment_forward_kernel(const SegmentJob jo
             gm[lane] = r_g;
             mk[lane] = r_mk;
         }
-    };
-
-    const int LPE = CS / VEC;      // lanes per event
-    const int EPP = kWave / LPE;   // events per pass
-    const int ev = lane / LPE;     // event slot of this lane within a pass
-    const int cg = lane - ev * LPE;
-    const int cl = cg * VEC;       // first channel of this lane within the slice
-
-    load_chunk(0);
-    for (int ci = 0; ci < geo.n_chunks; ++ci) {
-        const int t0 = ci * L;
         __syncthreads();
-        store_chunk();
-        __syncthreads();
-        // forget coefficients of the chunk's write events
-        for (int j = lane; j < L * Kw; j += kWave) {
-            const int tt = j / Kw, e = j - tt * Kw;
-            al[j] = gsu_alpha(mv[tt * Kt + e], gm[tt]);
+        // forget coefficients; masked tokens lose all their events
+        for (int j = lane; j < L * Kt; j += kWave) {
+            const int tt = j / Kt, e = j - tt * Kt;
+            const float g = gm[tt];
+            const bool masked = mk[tt] == 0;
+            int2 evv = evm[j];
+            if (masked)
+                evv.y = __float_as_int(0.f);
+            if (e < Kw)
+                al[tt * Kw + e] = masked ? 1.f : gsu_alpha(__int_as_float(evv.y), g);
+            evm[j] = evv;
         }
         __syncthreads();
         if (ci + 1 < geo.n_chunks)
             load_chunk(t0 + L);
 
         const int n_tok = min(L, T - t0);
+        TokenMeta<VEC, NP> cur, nxt;
+        fetch(0, cur);
         for (int tt = 0; tt < n_tok; ++tt) {
-            const int t = t0 + tt;
-            Scalar *yrow = gy + static_cast<int64_t>(t) * C + c0 + cl;
-            if (!mk[tt]) {
-                if (lane < LPE) {
+            // state rows of this token's writes
+            float m[NP], s[NP][VEC];
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                m[p] = ms[cur.aw[p]];
+                const float *row = st + cur.aw[p] * CS + cl;
+#pragma unroll
+                for (int v = 0; v < VEC; ++v)
+                    s[p][v] = row[v];
+            }
+            // finish the previous token's read while those loads fly
+            if (pend)
+                flush();
+            if (tt + 1 < n_tok)
+                fetch(tt + 1, nxt);
+            // gated sparse update of the write slots
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const float w = cur.w[p];
+                const float m2 = fmaf(cur.al[p], m[p], w);
+                const float g = gsu_gain(w, m2 + eps);
+                if (w != 0.f) {
+                    float *row = st + cur.aw[p] * CS + cl;
 #pragma unroll
                     for (int v = 0; v < VEC; ++v)
-                        if (c0 + cl + v < C)
-                            store_f32(yrow + v, 0.f);
-                }
-                continue;
-            }
-            float xv[VEC];
-#pragma unroll
-            for (int v = 0; v < VEC; ++v)
-                xv[v] = xs[tt * CS + cl + v];
-            // writes (distinct slots within a token)
-            for (int e0 = 0; e0 < Kw; e0 += EPP) {
-                const int e = e0 + ev;
-                if (e < Kw) {
-                    const float w = mv[tt * Kt + e];
-                    if (w != 0.f) {
-                        const int a = ma[tt * Kt + e];
-                        const float alpha = al[tt * Kw + e];
-                        float *row = st + a * CS + cl;
-                        const float m2 = fmaf(alpha, ms[a], w);
-                        float s[VEC];
-#pragma unroll
-                        for (int v = 0; v < VEC; ++v)
-                            s[v] = row[v];
-                        const float g = gsu_gain(w, m2 + eps);
-#pragma unroll
-                        for (int v = 0; v < VEC; ++v)
-                            row[v] = fmaf(g, xv[v] - s[v], s[v]);
-                        if (cg == 0)
-                            ms[a] = m2;
-                    }
+                        row[v] = fmaf(g, cur.x[v] - s[p][v], s[p][v]);
+                    if (cg == 0)
+                        ms[cur.aw[p]] = m2;
                 }
             }
-            // reads of the post-write state
-            float acc[VEC];
+            // read rows of the post-write state (consumed next iteration)
 #pragma unroll
-            for (int v = 0; v < VEC; ++v)
-                acc[v] = 0.f;
-            float sr = 0.f, srm = 0.f;
-            for (int e0 = 0; e0 < Kr; e0 += EPP) {
-                const int e = e0 + ev;
-                if (e < Kr) {
-                    const float r = mv[tt * Kt + Kw + e];
-                    if (r != 0.f) {
-                        const int a = ma[tt * Kt + Kw + e];
-                        const float *row = st + a * CS + cl;
-                        float wgt = r;
-                        if constexpr (MASS_AWARE) {
-                            wgt = r * ms[a];
-                            sr += r;
-                            srm += wgt;
-                        }
-#pragma unroll
-                        for (int v = 0; v < VEC; ++v)
-                            acc[v] = fmaf(wgt, row[v], acc[v]);
-                    }
-                }
-            }
-            for (int off = LPE; off < kWave; off <<= 1) {
+            for (int p = 0; p < NP; ++p) {
+                const float *row = st + cur.ar[p] * CS + cl;
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
-                    acc[v] += __shfl_xor(acc[v], off);
-                if constexpr (MASS_AWARE) {
-                    sr += __shfl_xor(sr, off);
-                    srm += __shfl_xor(srm, off);
-                }
+                    prs[p][v] = row[v];
+                prm[p] = mass_aware ? ms[cur.ar[p]] : 1.f;
+                pr[p] = cur.r[p];
             }
-            if constexpr (MASS_AWARE) {
-                const float scale = sr / (srm + eps);
-#pragma unroll
-                for (int v = 0; v < VEC; ++v)
-                    acc[v] *= scale;
-            }
-            if (lane < LPE) {
-#pragma unroll
-                for (int v = 0; v < VEC; ++v)
-                    if (c0 + cl + v < C)
-                        store_f32(yrow + v, acc[v]);
-            }
+            pend = true;
+            pend_t = t0 + tt;
+            cur = nxt;
         }
     }
+    if (pend)
+        flush();
     __syncthreads();
 
     // ---- LDS -> post state. Every slice of a (b, h) computes identical
@@ -274,13 +331,6 @@ __global__ __launch_bounds__(64) void segment_forward_kernel(const SegmentJob jo
     }
 }
 
-int pow2_floor(int x) {
-    int p = 1;
-    while (p * 2 <= x)
-        p <<= 1;
-    return p;
-}
-
 int pow2_ceil(int x) {
     int p = 1;
     while (p < x)
@@ -291,71 +341,90 @@ int pow2_ceil(int x) {
 // LDS words for a given slice width and chunk length.
 int64_t lds_words(int A, int cs, int L, int Kw, int Kr) {
     const int Kt = Kw + Kr;
-    return static_cast<int64_t>(A) * cs + A + 2LL * L * Kt + static_cast<int64_t>(L) * Kw + static_cast<int64_t>(L) * cs + 2LL * L;
+    return static_cast<int64_t>(A) * cs + A + 2LL * L * Kt + static_cast<int64_t>(L) * Kw +
+           static_cast<int64_t>(L) * cs + 2LL * L + 1;
 }
 
-bool make_geom(const SegmentJob &job, SegGeom *g, int *vec) {
+// Choose the channel-slice width (LDS-resident state of A x CS fp32 per
+// wave, two waves per CU when possible), the chunk length, and the lane
+// layout: EPP events per pass x LPE lanes per event, VEC channels per lane.
+bool make_geom(const SegmentJob &job, SegGeom *g, int *vec, int *npass) {
     const int Kt = job.Kw + job.Kr;
+    const int kmax = std::max(job.Kw, job.Kr);
     const int64_t budget2 = 78 * 1024;   // two units per CU
     const int64_t budget1 = 150 * 1024;  // one unit per CU
     const int cs_max = job.C >= 32 ? 32 : pow2_ceil(job.C);
     for (int pass = 0; pass < 2; ++pass) {
         const int64_t budget = pass == 0 ? budget2 : budget1;
         for (int cs = cs_max; cs >= 1; cs >>= 1) {
+            // events per pass: enough for top-K in at most two passes, VEC <= 4
+            int epp = std::min(kWave, pow2_ceil(std::max(kmax, 1)));
+            int v = std::max(1, cs * epp / kWave);
+            if (v > 4)
+                continue;  // slice too wide for this K: try a narrower one
+            const int lpe = cs / v;
+            epp = kWave / lpe;
+            const int np = (kmax + epp - 1) / epp;
+            if (np > 2)
+                continue;
             int L = kMaxChunk;
             L = std::min(L, kMetaPerLane * kWave / Kt);
             L = std::min(L, kXPerLane * kWave / cs);
             if (L < 1)
                 return false;
-            // smaller chunks trade staging for LDS room
             while (L > 8 && lds_words(job.A, cs, L, job.Kw, job.Kr) * 4 > budget)
                 L >>= 1;
             if (lds_words(job.A, cs, L, job.Kw, job.Kr) * 4 > budget)
                 continue;
-            // lanes per event: as many events per pass as top-K needs
-            const int kmax = std::max(job.Kw, job.Kr);
-            const int epp_want = std::min(kWave, pow2_ceil(std::max(kmax, 1)));
-            int v = cs * epp_want / kWave;
-            v = std::max(1, std::min(v, 4));
-            v = std::min(v, cs);
             g->cs = cs;
             g->L = L;
+            g->lpe = lpe;
+            g->epp = epp;
             g->ns = (job.C + cs - 1) / cs;
             g->n_units = job.B * job.H * g->ns;
             g->n_chunks = (job.T + L - 1) / L;
             int off = 0;
             g->st_off = off; off += job.A * cs;
             g->ms_off = off; off += job.A;
-            g->ma_off = off; off += L * Kt;
-            g->mv_off = off; off += L * Kt;
+            off = (off + 1) & ~1;  // 8-byte alignment of the event pairs
+            g->ev_off = off; off += 2 * L * Kt;
             g->al_off = off; off += L * job.Kw;
             g->xs_off = off; off += L * cs;
             g->gm_off = off; off += L;
             g->mk_off = off; off += L;
             *vec = v;
+            *npass = np;
             return true;
         }
     }
     return false;
 }
 
-template<typename T, int VEC>
+size_t lds_bytes_of(const SegmentJob &job, const SegGeom &g) {
+    return static_cast<size_t>(g.mk_off + g.L) * 4;
+}
+
+template<typename T, int VEC, int NP>
 hipError_t launch_vec(const SegmentJob &job, const SegGeom &g, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(lds_words(job.A, g.cs, g.L, job.Kw, job.Kr)) * 4;
     const unsigned blocks = static_cast<unsigned>(((g.n_units + 7) / 8) * 8);
-    if (job.mass_aware)
-        hipLaunchKernelGGL((segment_forward_kernel<T, VEC, true>), dim3(blocks), dim3(kWave), lds, stream, job, g);
-    else
-        hipLaunchKernelGGL((segment_forward_kernel<T, VEC, false>), dim3(blocks), dim3(kWave), lds, stream, job, g);
+    hipLaunchKernelGGL((segment_forward_kernel<T, VEC, NP>), dim3(blocks), dim3(kWave), lds_bytes_of(job, g), stream,
+                       job, g);
     return hipGetLastError();
 }
 
 template<typename T>
-hipError_t launch_typed(const SegmentJob &job, const SegGeom &g, int vec, hipStream_t stream) {
+hipError_t launch_typed(const SegmentJob &job, const SegGeom &g, int vec, int np, hipStream_t stream) {
+    if (np == 1) {
+        switch (vec) {
+            case 1: return launch_vec<T, 1, 1>(job, g, stream);
+            case 2: return launch_vec<T, 2, 1>(job, g, stream);
+            default: return launch_vec<T, 4, 1>(job, g, stream);
+        }
+    }
     switch (vec) {
-        case 1: return launch_vec<T, 1>(job, g, stream);
-        case 2: return launch_vec<T, 2>(job, g, stream);
-        default: return launch_vec<T, 4>(job, g, stream);
+        case 1: return launch_vec<T, 1, 2>(job, g, stream);
+        case 2: return launch_vec<T, 2, 2>(job, g, stream);
+        default: return launch_vec<T, 4, 2>(job, g, stream);
     }
 }
 
@@ -369,13 +438,13 @@ int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes) {
     job.Kr = Kr;
     job.B = job.H = job.T = 1;
     SegGeom g{};
-    int vec = 0;
-    if (!make_geom(job, &g, &vec))
+    int vec = 0, np = 0;
+    if (!make_geom(job, &g, &vec, &np))
         return 0;
     if (cs)
         *cs = g.cs;
     if (lds_bytes)
-        *lds_bytes = static_cast<int>(lds_words(A, g.cs, g.L, Kw, Kr) * 4);
+        *lds_bytes = static_cast<int>(lds_bytes_of(job, g));
     return 1;
 }
 
@@ -383,19 +452,16 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     if (static_cast<int64_t>(job.B) * job.H == 0)
         return hipSuccess;
     SegGeom g{};
-    int vec = 0;
-    if (!make_geom(job, &g, &vec)) {
-        *why = "segment forward: slot count A too large for the LDS-resident state (needs A*2*4 bytes + staging <= 150 KiB)";
+    int vec = 0, np = 0;
+    if (!make_geom(job, &g, &vec, &np)) {
+        *why = "segment forward: shape outside the LDS-resident scan (needs A*2*4 bytes + staging <= 150 KiB and "
+               "top_k <= 128)";
         return hipErrorInvalidValue;
     }
-    if (job.T == 0) {
-        // nothing to scan: post state is the initial state
-        g.n_chunks = 0;
-    }
     switch (job.dtype) {
-        case kF32: return launch_typed<float>(job, g, vec, stream);
-        case kF16: return launch_typed<_Float16>(job, g, vec, stream);
-        case kBF16: return launch_typed<bf16_t>(job, g, vec, stream);
+        case kF32: return launch_typed<float>(job, g, vec, np, stream);
+        case kF16: return launch_typed<_Float16>(job, g, vec, np, stream);
+        case kBF16: return launch_typed<bf16_t>(job, g, vec, np, stream);
         default: *why = "segment forward: unsupported dtype"; return hipErrorInvalidValue;
     }
 }

@@ -80,7 +80,7 @@ def test_decoder_matches_oracle(case, dtype):
     ops = _ops()
     B, H, U, P, T, K, re_norm, E = case
     print(f"decoder case {case} {dtype}", flush=True)
-    g = torch.Generator().manual_seed(sum(case))
+    g = torch.Generator().manual_seed(int(sum(case) * 1000))
     addr = torch.randn(B, H, U, P, T, generator=g).to(dtype)
     pos = torch.randint(0, 10_000, (B, T), generator=g)
     idx, val = ops.topk_addr_single_forward(addr.to(DEV), E, P ** U, pos.to(DEV), K, re_norm, False, True)
@@ -244,13 +244,15 @@ def test_decode_step_matches_oracle(U, P, K, mass_aware, dtype):
     y = ops.topk_autoregressive_(w.to(DEV), r.to(DEV), x.to(DEV), gamma.to(DEV), s_gpu, m_gpu, mask.to(DEV), 2,
                                  pos.to(DEV), K, K, 0.0, 0.0, mass_aware, 1e-12)
     torch.cuda.synchronize()
-    # the same step through the oracle decoder + fp64 event loop
-    wi, wv = oracle.dense_topk_addr(w.unsqueeze(-1), 2, pos.view(B, 1), K, 0.0)
-    ri, rv = oracle.dense_topk_addr(r.unsqueeze(-1), 2, pos.view(B, 1), K, 0.0)
+    # the same step through the fp64 event loop, on the decoder's selection
+    # (checked against the fp64 ranking, ties exempt)
+    events = []
     for lg in (w, r):
-        idx, _ = ops.topk_addr_single_forward(lg.unsqueeze(-1).to(DEV), 2, A, pos.view(B, 1).to(DEV), K, 0.0, False, True)
-        st = oracle.check_topk_indices(idx.cpu(), lg.unsqueeze(-1), 2, pos.view(B, 1), K)
-        assert st["exempt_slots"] == 0, "near-tie selection in the decode test case"
+        idx, val = ops.topk_addr_single_forward(lg.unsqueeze(-1).to(DEV), 2, A, pos.view(B, 1).to(DEV), K, 0.0,
+                                                False, True)
+        oracle.check_topk_indices(idx.cpu(), lg.unsqueeze(-1), 2, pos.view(B, 1), K)
+        events += [idx.cpu(), val.cpu()]
+    wi, wv, ri, rv = events
     ry, rslot, rmass = oracle.sparse_gsu_f64(wi, wv, ri, rv, x.double().unsqueeze(2), gamma.double().unsqueeze(-1),
                                              slot, mass, mask.view(B, 1), mass_aware, 1e-12)
     assert bool((y.cpu()[2] == 0).all()), "masked batch row must read 0"
