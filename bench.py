@@ -73,8 +73,10 @@ def make_prefill_inputs(dev):
 
 
 def bench_prefill(steps, warmup, dev):
+    """Config 2 through the product path's two native stages (what the fused
+    ``ram_attn_forward`` op runs): record decoder, then the segment scan."""
     import ramnet_ops  # noqa: F401
-    ops = torch.ops.ramnet_ops
+    from ramnet_ops import _native as nat
     c = C2
     B, H, T, C, U, P, K = c["B"], c["H"], c["T"], c["C"], c["U"], c["P"], c["K"]
     A = P ** U
@@ -82,14 +84,21 @@ def bench_prefill(steps, warmup, dev):
     host, d = make_prefill_inputs(dev)
     slot0 = torch.zeros(B, H, A, C, device=dev)
     mass0 = torch.full((B, H, A), 1.0 / A, device=dev)
+    slot = torch.empty_like(slot0)
+    mass = torch.empty_like(mass0)
+    y = torch.empty_like(d["x"])
+    ws = torch.empty(nat.scan_workspace_bytes(B, H, T, K, K), dtype=torch.uint8, device=dev)
+    code = nat.DTYPE_CODES[d["x"].dtype]
+    stream = torch.cuda.current_stream(dev).cuda_stream
 
     def step(ev):
         ev[0].record()
-        idx, val = ops.topk_addr_forward(d["w"], d["r"], E, A, d["pos"], K, K, 0.0, 0.0)
+        nat.call("ramnet_topk_addr_records", d["w"].data_ptr(), d["r"].data_ptr(), d["gamma"].data_ptr(), code, None,
+                 E, d["pos"].data_ptr(), B, H, U, P, T, A, K, K, 0.0, 0.0, ws.data_ptr(), ws.numel(), stream)
         ev[1].record()
-        y, slot, mass = ops.topk_segment_forward(idx, val, d["x"], d["gamma"], slot0, mass0, None, K, K, False, 1e-12)
+        nat.call("ramnet_segment_scan", d["x"].data_ptr(), code, slot0.data_ptr(), mass0.data_ptr(), slot.data_ptr(),
+                 mass.data_ptr(), y.data_ptr(), B, H, T, A, C, K, K, 0, 1e-12, ws.data_ptr(), ws.numel(), stream)
         ev[2].record()
-        return y
 
     def events(n):
         return [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
@@ -320,7 +329,7 @@ def main(argv=None) -> int:
             },
             "roofline": {
                 "bound": "hbm",
-                "kernel": "segment_forward_kernel",
+                "kernel": "segment_scan_kernel",
                 "achieved": seg_gbs,
                 "peak": HBM_PEAK_GBS,
                 "unit": "GB/s",

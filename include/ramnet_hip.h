@@ -79,6 +79,14 @@ int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, 
                              int encode_batch_idx, int32_t *idx_out, float *val_out, void *stream);
 
 /*
+ * Bytes of device workspace the segment scan needs for B x H heads, T tokens
+ * and the given top-k (per-event records, T padded to 16). The 32-bit form
+ * returns -1 when the size does not fit an int.
+ */
+int ramnet_scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k);
+int64_t ramnet_scan_workspace_bytes64(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k);
+
+/*
  * Gated sparse update and top-K read over a whole sequence, returning a new
  * state. Replaces ramnet_ops::topk_segment_forward
  * (ram_attn_bind.cpp:65-73, ram_attn_ops.cpp:226-265). The reference op
@@ -92,11 +100,14 @@ int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, 
  *   slot_out/mass_out   (B, H, A, C) / (B, H, A) fp32; slot_out may alias
  *                       init_slot, mass_out must not alias init_mass
  *   y                   (B, H, T, C) `dtype`; masked tokens get 0
+ *   workspace           >= ramnet_scan_workspace_bytes(B, H, T, w, r) bytes
+ *                       of device memory, overwritten by the call
  */
 int ramnet_topk_segment_forward(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
                                 int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
                                 float *slot_out, float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A,
-                                int64_t C, int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *stream);
+                                int64_t C, int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps,
+                                void *workspace, int64_t workspace_bytes, void *stream);
 
 /*
  * In-place variant: updates slot and mass. Replaces
@@ -108,7 +119,44 @@ int ramnet_topk_segment_forward(const int32_t *addr_idx, const float *addr_val, 
 int ramnet_topk_segment_forward_(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
                                  int dtype, const uint8_t *mask, float *slot, float *mass, const float *mass_in,
                                  void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
-                                 int64_t r_top_k, int mass_aware, float eps, void *stream);
+                                 int64_t r_top_k, int mass_aware, float eps, void *workspace, int64_t workspace_bytes,
+                                 void *stream);
+
+/*
+ * The two stages of ramnet_ram_attn_forward, for callers that schedule or
+ * time them separately. ramnet_topk_addr_records runs both address decoders
+ * and writes the scan's per-event records into `workspace` (CAPE, mask,
+ * inactive addresses and the forget coefficients from gamma folded in);
+ * ramnet_segment_scan runs the scan from those records. Arguments as for
+ * ramnet_ram_attn_forward.
+ */
+int ramnet_topk_addr_records(const void *w_addr, const void *r_addr, const void *gamma, int dtype,
+                             const uint8_t *mask, int64_t embed_num, const int32_t *position_ids, int64_t B, int64_t H,
+                             int64_t U, int64_t P, int64_t T, int64_t A, int64_t w_top_k, int64_t r_top_k,
+                             float w_re_norm, float r_re_norm, void *workspace, int64_t workspace_bytes,
+                             void *stream);
+int ramnet_segment_scan(const void *x, int dtype, const float *init_slot, const float *init_mass, float *slot_out,
+                        float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                        int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *workspace,
+                        int64_t workspace_bytes, void *stream);
+
+/*
+ * Whole parallel (prefill) forward: both address decoders and the segment
+ * scan, with the decoder writing the scan's per-event records directly (no
+ * idx/val round trip). Replaces the parallel branch of the reference's
+ * _cuda_ram_attn (packages/ramnet-ops/src/ramnet_ops/impl/cuda_impl.py:
+ * 240-271: topk_addr_forward, gather_segment, topk_segment_forward).
+ *   w_addr, r_addr  (B, H, U, P, T) logits;  other arguments as for
+ *                   ramnet_topk_addr_forward and ramnet_topk_segment_forward
+ * For an in-place update pass slot_out == init_slot and a snapshot copy of
+ * the masses as init_mass (mass_out must not alias init_mass).
+ */
+int ramnet_ram_attn_forward(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
+                            const uint8_t *mask, int64_t embed_num, const int32_t *position_ids,
+                            const float *init_slot, const float *init_mass, float *slot_out, float *mass_out, void *y,
+                            int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int64_t A, int64_t C,
+                            int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm, int mass_aware,
+                            float eps, void *workspace, int64_t workspace_bytes, void *stream);
 
 /*
  * One fused decode step on a persistent state, updated in place.

@@ -26,8 +26,11 @@ namespace ramnet {
 
 namespace {
 
-constexpr int kEv = 16;   // fast path: up to 16 write and 16 read slots
-constexpr int kCpl = 4;   // fast path: up to 4 channels per lane (C <= 256)
+constexpr int kEv = 16;     // fast path: up to 16 write and 16 read slots
+constexpr int kMaxCpl = 4;  // fast path: up to 4 channels per lane (C <= 256)
+// The fast path issues its row loads unconditionally from clamped in-bounds
+// addresses: a guarded load would wait for its data inside the branch and
+// serialise the HBM round trips.
 
 __device__ __forceinline__ float gsu_gain(float w, float d) {
     float r = __builtin_amdgcn_rcpf(d);
@@ -56,25 +59,48 @@ __device__ __forceinline__ void finalize_events(float v, int c, bool inactive, i
     }
 }
 
-template<typename T, int GW>
+template<typename T, int GW, int KE, int kCpl>
 __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob job) {
-    __shared__ int s_ws[kEv], s_rs[kEv];
-    __shared__ float s_wv[kEv], s_rv[kEv];
-    __shared__ float s_row[kEv][kWave * kCpl];
+    __shared__ int s_ws[KE], s_rs[KE];
+    __shared__ float s_wv[KE], s_rv[KE];
+    __shared__ float s_row[KE][kWave * kCpl];
 
     const int bh = blockIdx.x;
     const int lane = threadIdx.x;
     const int H = job.H, A = job.A, C = job.C, U = job.U, P = job.P, Kw = job.Kw, Kr = job.Kr;
     const int b = bh / H, h = bh - (bh / H) * H;
     T *yrow = static_cast<T *>(job.y) + static_cast<int64_t>(bh) * C;
-    if (job.mask && !job.mask[b]) {
+
+    // ---- every input of the step in one batch of loads
+    const T *wp = static_cast<const T *>(job.w_addr) + static_cast<int64_t>(bh) * U * P;
+    const T *rp = static_cast<const T *>(job.r_addr) + static_cast<int64_t>(bh) * U * P;
+    GroupLogits<T> lw, lr;
+    if constexpr (GW == 32) {
+        lw.load((lane >> 5) ? rp : wp, U, P, lane & 31);
+    } else {
+        lw.load(wp, U, P, lane);
+        lr.load(rp, U, P, lane);
+    }
+    int cidx[kCpl];
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j) {
+        const int c = lane + j * kWave;
+        cidx[j] = c < C ? c : C - 1;
+    }
+    const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
+    float xv[kCpl];
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j)
+        xv[j] = load_f32(xp + cidx[j]);
+    const float gamma = load_f32(static_cast<const T *>(job.gamma) + bh);
+    const int pos = job.position_ids[b];
+    const uint8_t valid = job.mask ? job.mask[b] : 1;
+    if (!valid) {
         for (int c = lane; c < C; c += kWave)
             store_f32(yrow + c, 0.f);
         return;
     }
-    const int shift = h < job.embed_num ? pos_mod(job.position_ids[b], A) : 0;
-    const T *wp = static_cast<const T *>(job.w_addr) + static_cast<int64_t>(bh) * U * P;
-    const T *rp = static_cast<const T *>(job.r_addr) + static_cast<int64_t>(bh) * U * P;
+    const int shift = h < job.embed_num ? pos_mod(pos, A) : 0;
 
     // ---- address decode
     if constexpr (GW == 32) {
@@ -82,15 +108,15 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
         const int K = half ? Kr : Kw;
         float v;
         int c;
-        const bool inactive = group_search<T, 32>(half ? rp : wp, U, P, K, li, v, c);
+        const bool inactive = group_search<T, 32>(lw, U, P, K, li, v, c);
         finalize_events(v, c, inactive, K, half ? job.r_re_norm : job.w_re_norm, li, half * 32, shift, A,
                         half ? s_rs : s_ws, half ? s_rv : s_wv);
     } else {
         float v;
         int c;
-        bool inactive = group_search<T, 64>(wp, U, P, Kw, lane, v, c);
+        bool inactive = group_search<T, 64>(lw, U, P, Kw, lane, v, c);
         finalize_events(v, c, inactive, Kw, job.w_re_norm, lane, 0, shift, A, s_ws, s_wv);
-        inactive = group_search<T, 64>(rp, U, P, Kr, lane, v, c);
+        inactive = group_search<T, 64>(lr, U, P, Kr, lane, v, c);
         finalize_events(v, c, inactive, Kr, job.r_re_norm, lane, 0, shift, A, s_rs, s_rv);
     }
     __syncthreads();
@@ -98,67 +124,41 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
     // ---- one batch of row requests
     float *slot = job.slot + static_cast<int64_t>(bh) * A * C;
     float *mass = job.mass + static_cast<int64_t>(bh) * A;
-    int wa[kEv], ra[kEv], fwd[kEv];
-    float wv[kEv], rv[kEv], wm[kEv], rm[kEv];
-    float wrow[kEv][kCpl], rrow[kEv][kCpl];
+    int wa[KE], ra[KE], fwd[KE];
+    float wv[KE], rv[KE], wm[KE], rm[KE];
+    float wrow[KE][kCpl], rrow[KE][kCpl];
 #pragma unroll
-    for (int k = 0; k < kEv; ++k) {
+    for (int k = 0; k < KE; ++k) {
         wa[k] = k < Kw ? s_ws[k] : 0;
         wv[k] = k < Kw ? s_wv[k] : 0.f;
         ra[k] = k < Kr ? s_rs[k] : 0;
         rv[k] = k < Kr ? s_rv[k] : 0.f;
     }
 #pragma unroll
-    for (int k = 0; k < kEv; ++k) {
-        wm[k] = 0.f;
+    for (int k = 0; k < KE; ++k) {
+        const float *row = slot + static_cast<int64_t>(wa[k]) * C;
 #pragma unroll
         for (int j = 0; j < kCpl; ++j)
-            wrow[k][j] = 0.f;
-        if (wv[k] != 0.f) {
-            const float *row = slot + static_cast<int64_t>(wa[k]) * C;
-#pragma unroll
-            for (int j = 0; j < kCpl; ++j) {
-                const int c = lane + j * kWave;
-                if (c < C)
-                    wrow[k][j] = row[c];
-            }
-            wm[k] = mass[wa[k]];
-        }
+            wrow[k][j] = row[cidx[j]];
+        wm[k] = mass[wa[k]];
     }
 #pragma unroll
-    for (int k = 0; k < kEv; ++k) {
+    for (int k = 0; k < KE; ++k) {
         fwd[k] = -1;
 #pragma unroll
-        for (int j2 = 0; j2 < kEv; ++j2)
+        for (int j2 = 0; j2 < KE; ++j2)
             if (wv[j2] != 0.f && wa[j2] == ra[k])
                 fwd[k] = j2;
-        rm[k] = 0.f;
+        // a slot written this step is read from the updated copy in LDS
+        const float *row = slot + static_cast<int64_t>(ra[k]) * C;
 #pragma unroll
         for (int j = 0; j < kCpl; ++j)
-            rrow[k][j] = 0.f;
-        if (rv[k] != 0.f && fwd[k] < 0) {
-            const float *row = slot + static_cast<int64_t>(ra[k]) * C;
-#pragma unroll
-            for (int j = 0; j < kCpl; ++j) {
-                const int c = lane + j * kWave;
-                if (c < C)
-                    rrow[k][j] = row[c];
-            }
-            rm[k] = mass[ra[k]];
-        }
+            rrow[k][j] = row[cidx[j]];
+        rm[k] = mass[ra[k]];
     }
-    const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
-    float xv[kCpl];
-#pragma unroll
-    for (int j = 0; j < kCpl; ++j) {
-        const int c = lane + j * kWave;
-        xv[j] = c < C ? load_f32(xp + c) : 0.f;
-    }
-    const float gamma = load_f32(static_cast<const T *>(job.gamma) + bh);
-
     // ---- writes
 #pragma unroll
-    for (int k = 0; k < kEv; ++k) {
+    for (int k = 0; k < KE; ++k) {
         const float w = wv[k];
         if (w != 0.f) {
             const float alpha = gsu_alpha(w, gamma);
@@ -186,13 +186,13 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
         acc[j] = 0.f;
     float sr = 0.f, srm = 0.f;
 #pragma unroll
-    for (int k = 0; k < kEv; ++k) {
+    for (int k = 0; k < KE; ++k) {
         const float r = rv[k];
         if (r != 0.f) {
             const int f = fwd[k];
             float m = rm[k];
 #pragma unroll
-            for (int j2 = 0; j2 < kEv; ++j2)
+            for (int j2 = 0; j2 < KE; ++j2)
                 m = f == j2 ? wm[j2] : m;
             const float wgt = job.mass_aware ? r * m : r;
             sr += r;
@@ -308,13 +308,22 @@ template<typename T>
 hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **why) {
     const int kmax = std::max(job.Kw, job.Kr);
     const int stair = staircase_count(kmax);
-    const bool fast_ok = job.P <= 64 && kmax <= kEv && job.C <= kWave * kCpl && stair <= 64;
+    const bool fast_ok = job.P <= 64 && kmax <= kEv && job.C <= kWave * kMaxCpl && stair <= 64;
     const unsigned grid = static_cast<unsigned>(job.B * job.H);
     if (fast_ok) {
-        if (job.P <= 32 && stair <= 32)
-            hipLaunchKernelGGL((autoregressive_fast_kernel<T, 32>), dim3(grid), dim3(kWave), 0, stream, job);
-        else
-            hipLaunchKernelGGL((autoregressive_fast_kernel<T, 64>), dim3(grid), dim3(kWave), 0, stream, job);
+        const bool half = job.P <= 32 && stair <= 32;
+        const bool narrow = job.C <= 2 * kWave;
+        const bool few = kmax <= 8;
+        const dim3 g(grid), blk(kWave);
+#define RAMNET_AR_LAUNCH(GW, KE, CPL) hipLaunchKernelGGL((autoregressive_fast_kernel<T, GW, KE, CPL>), g, blk, 0, stream, job)
+        if (half) {
+            if (few) { if (narrow) RAMNET_AR_LAUNCH(32, 8, 2); else RAMNET_AR_LAUNCH(32, 8, 4); }
+            else { if (narrow) RAMNET_AR_LAUNCH(32, 16, 2); else RAMNET_AR_LAUNCH(32, 16, 4); }
+        } else {
+            if (few) { if (narrow) RAMNET_AR_LAUNCH(64, 8, 2); else RAMNET_AR_LAUNCH(64, 8, 4); }
+            else { if (narrow) RAMNET_AR_LAUNCH(64, 16, 2); else RAMNET_AR_LAUNCH(64, 16, 4); }
+        }
+#undef RAMNET_AR_LAUNCH
         return hipGetLastError();
     }
     const int NA = pow2_ceil(job.A), NPD = pow2_ceil(job.P);

@@ -146,29 +146,51 @@ int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, 
     return finish(err, why, "topk_addr_forward launch");
 }
 
-static int segment_common(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma, int dtype,
-                          const uint8_t *mask, const float *init_slot, const float *init_mass, float *slot_out,
-                          float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
-                          int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *stream, const char *what) {
+static int64_t scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t Kw, int64_t Kr) {
+    const int64_t t_pad = ramnet::scan_t_pad64(T);
+    return B * H * t_pad * (Kw * static_cast<int64_t>(sizeof(ramnet::WriteRec)) +
+                            Kr * static_cast<int64_t>(sizeof(ramnet::ReadRec))) +
+           ramnet::kScanChunk * static_cast<int64_t>(sizeof(ramnet::WriteRec) + sizeof(ramnet::ReadRec));
+}
+
+// Checks shared by the segment entry points; fills the scan job.
+static int segment_checks(const void *x, const void *gamma, int dtype, const float *init_slot, const float *init_mass,
+                          float *slot_out, float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A,
+                          int64_t C, int64_t w_top_k, int64_t r_top_k, float eps, void *workspace,
+                          int64_t workspace_bytes) {
     RAMNET_REQUIRE(B >= 0 && H > 0 && T >= 0 && C > 0, "segment shape must have B, T >= 0 and H, C > 0");
     RAMNET_REQUIRE(A > 0 && A < kAddressLimit, "Address space overflow: A must be in (0, 2**30)");
     RAMNET_REQUIRE(valid_dtype(dtype), "x dtype must be float32, float16 or bfloat16");
     RAMNET_REQUIRE(w_top_k > 0 && w_top_k <= A && r_top_k > 0 && r_top_k <= A, "top_k values must be in [1, A]");
     RAMNET_REQUIRE(eps > 0.f, "eps must be > 0");
-    RAMNET_REQUIRE(fits_int({B * H * A * C, B * H * A, B * H * T * C, B * H * T * (w_top_k + r_top_k)}),
+    RAMNET_REQUIRE(fits_int({B * H * A * C, B * H * (A + 2), B * H * T * C, B * H * (T + ramnet::kScanPad) * (w_top_k + r_top_k)}),
                    "CUDA index overflow: sizes exceed int32");
     if (B == 0)
         return RAMNET_OK;
     RAMNET_REQUIRE(init_slot && init_mass && slot_out && mass_out, "null state pointer");
     RAMNET_REQUIRE(static_cast<const void *>(init_mass) != static_cast<const void *>(mass_out),
                    "mass_out must not alias init_mass");
-    RAMNET_REQUIRE(T == 0 || (addr_idx && addr_val && x && gamma && y), "null tensor pointer");
+    RAMNET_REQUIRE(T == 0 || (x && gamma && y), "null tensor pointer");
+    RAMNET_REQUIRE(workspace_bytes >= scan_workspace_bytes(B, H, T, w_top_k, r_top_k) && (T == 0 || workspace),
+                   "workspace too small: see ramnet_scan_workspace_bytes");
+    return RAMNET_OK;
+}
+
+static ramnet::SegmentJob make_segment_job(const void *x, int dtype, const float *init_slot, const float *init_mass,
+                                           float *slot_out, float *mass_out, void *y, int64_t B, int64_t H,
+                                           int64_t T, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k,
+                                           int mass_aware, float eps, void *workspace) {
     ramnet::SegmentJob job{};
-    job.addr_idx = addr_idx;
-    job.addr_val = addr_val;
+    const int64_t t_pad = ramnet::scan_t_pad64(T);
+    job.wrec = static_cast<const ramnet::WriteRec *>(workspace);
+    const char *ws = static_cast<const char *>(workspace);
+    const int64_t w_bytes = B * H * t_pad * w_top_k * static_cast<int64_t>(sizeof(ramnet::WriteRec));
+    const int64_t r_bytes = B * H * t_pad * r_top_k * static_cast<int64_t>(sizeof(ramnet::ReadRec));
+    job.rrec = reinterpret_cast<const ramnet::ReadRec *>(ws + w_bytes);
+    job.noop_w = reinterpret_cast<const ramnet::WriteRec *>(ws + w_bytes + r_bytes);
+    job.noop_r = reinterpret_cast<const ramnet::ReadRec *>(ws + w_bytes + r_bytes +
+                                                            ramnet::kScanChunk * sizeof(ramnet::WriteRec));
     job.x = x;
-    job.gamma = gamma;
-    job.mask = mask;
     job.init_slot = init_slot;
     job.init_mass = init_mass;
     job.slot_out = slot_out;
@@ -184,25 +206,161 @@ static int segment_common(const int32_t *addr_idx, const float *addr_val, const 
     job.Kr = static_cast<int>(r_top_k);
     job.mass_aware = mass_aware ? 1 : 0;
     job.eps = eps;
+    return job;
+}
+
+static int segment_from_decoded(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
+                                int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
+                                float *slot_out, float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A,
+                                int64_t C, int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps,
+                                void *workspace, int64_t workspace_bytes, void *stream, const char *what) {
+    if (int rc = segment_checks(x, gamma, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k,
+                                r_top_k, eps, workspace, workspace_bytes))
+        return rc;
+    if (B == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(T == 0 || (addr_idx && addr_val), "null tensor pointer");
+    ramnet::SegmentJob job = make_segment_job(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C,
+                                              w_top_k, r_top_k, mass_aware, eps, workspace);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
     const char *why = nullptr;
-    const hipError_t err = ramnet::launch_segment_forward(job, static_cast<hipStream_t>(stream), &why);
+    if (T > 0) {
+        ramnet::PackJob pack{};
+        pack.addr_idx = addr_idx;
+        pack.addr_val = addr_val;
+        pack.gamma = gamma;
+        pack.mask = mask;
+        pack.wrec = const_cast<ramnet::WriteRec *>(job.wrec);
+        pack.rrec = const_cast<ramnet::ReadRec *>(job.rrec);
+        pack.noop_w = const_cast<ramnet::WriteRec *>(job.noop_w);
+        pack.noop_r = const_cast<ramnet::ReadRec *>(job.noop_r);
+        pack.dtype = dtype;
+        pack.B = job.B;
+        pack.H = job.H;
+        pack.T = job.T;
+        pack.A = job.A;
+        pack.Kw = job.Kw;
+        pack.Kr = job.Kr;
+        const hipError_t err = ramnet::launch_pack_records(pack, s, &why);
+        if (err != hipSuccess)
+            return finish(err, why, what);
+    }
+    const hipError_t err = ramnet::launch_segment_forward(job, s, &why);
     return finish(err, why, what);
+}
+
+int ramnet_scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k) {
+    if (B < 0 || H < 0 || T < 0 || w_top_k < 0 || r_top_k < 0)
+        return -1;
+    const int64_t n = scan_workspace_bytes(B, H, T, w_top_k, r_top_k);
+    return n > 0x7fffffffLL ? -1 : static_cast<int>(n);
+}
+
+int64_t ramnet_scan_workspace_bytes64(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k) {
+    if (B < 0 || H < 0 || T < 0 || w_top_k < 0 || r_top_k < 0)
+        return -1;
+    return scan_workspace_bytes(B, H, T, w_top_k, r_top_k);
 }
 
 int ramnet_topk_segment_forward(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
                                 int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
                                 float *slot_out, float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A,
-                                int64_t C, int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *stream) {
-    return segment_common(addr_idx, addr_val, x, gamma, dtype, mask, init_slot, init_mass, slot_out, mass_out, y, B, H,
-                          T, A, C, w_top_k, r_top_k, mass_aware, eps, stream, "topk_segment_forward launch");
+                                int64_t C, int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps,
+                                void *workspace, int64_t workspace_bytes, void *stream) {
+    return segment_from_decoded(addr_idx, addr_val, x, gamma, dtype, mask, init_slot, init_mass, slot_out, mass_out, y,
+                                B, H, T, A, C, w_top_k, r_top_k, mass_aware, eps, workspace, workspace_bytes, stream,
+                                "topk_segment_forward launch");
 }
 
 int ramnet_topk_segment_forward_(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
                                  int dtype, const uint8_t *mask, float *slot, float *mass, const float *mass_in,
                                  void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
-                                 int64_t r_top_k, int mass_aware, float eps, void *stream) {
-    return segment_common(addr_idx, addr_val, x, gamma, dtype, mask, slot, mass_in, slot, mass, y, B, H, T, A, C,
-                          w_top_k, r_top_k, mass_aware, eps, stream, "topk_segment_forward_ launch");
+                                 int64_t r_top_k, int mass_aware, float eps, void *workspace, int64_t workspace_bytes,
+                                 void *stream) {
+    return segment_from_decoded(addr_idx, addr_val, x, gamma, dtype, mask, slot, mass_in, slot, mass, y, B, H, T, A,
+                                C, w_top_k, r_top_k, mass_aware, eps, workspace, workspace_bytes, stream,
+                                "topk_segment_forward_ launch");
+}
+
+int ramnet_topk_addr_records(const void *w_addr, const void *r_addr, const void *gamma, int dtype,
+                              const uint8_t *mask, int64_t embed_num, const int32_t *position_ids, int64_t B,
+                              int64_t H, int64_t U, int64_t P, int64_t T, int64_t A, int64_t w_top_k, int64_t r_top_k,
+                              float w_re_norm, float r_re_norm, void *workspace, int64_t workspace_bytes,
+                              void *stream) {
+    if (int rc = check_addr_shape(B, H, U, P, T, embed_num, A))
+        return rc;
+    RAMNET_REQUIRE(valid_dtype(dtype), "addr dtype must be float32, float16 or bfloat16");
+    RAMNET_REQUIRE(w_top_k > 0 && w_top_k <= A && r_top_k > 0 && r_top_k <= A, "top_k values must be in [1, A]");
+    RAMNET_REQUIRE(w_re_norm >= 0.f && w_re_norm <= 1.f && r_re_norm >= 0.f && r_re_norm <= 1.f,
+                   "top_k_re_norm exponents must be in [0, 1]");
+    RAMNET_REQUIRE(fits_int({B * H * U * P * T, B * H * (T + ramnet::kScanPad) * (w_top_k + r_top_k)}),
+                   "CUDA index overflow: sizes exceed int32");
+    RAMNET_REQUIRE(workspace_bytes >= scan_workspace_bytes(B, H, T, w_top_k, r_top_k) && workspace,
+                   "workspace too small: see ramnet_scan_workspace_bytes");
+    if (B * T == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(w_addr && r_addr && gamma && position_ids, "null tensor pointer");
+    ramnet::SegmentJob lay = make_segment_job(nullptr, dtype, nullptr, nullptr, nullptr, nullptr, nullptr, B, H, T,
+                                              A, 1, w_top_k, r_top_k, 0, 1.f, workspace);
+    ramnet::AddrJob dec{};
+    dec.src[0] = {w_addr, static_cast<int>(w_top_k), w_re_norm, 1.f, 0};
+    dec.src[1] = {r_addr, static_cast<int>(r_top_k), r_re_norm, 1.f, 0};
+    dec.n_src = 2;
+    dec.dtype = dtype;
+    dec.B = static_cast<int>(B);
+    dec.H = static_cast<int>(H);
+    dec.U = static_cast<int>(U);
+    dec.P = static_cast<int>(P);
+    dec.T = static_cast<int>(T);
+    dec.A = static_cast<int>(A);
+    dec.embed_num = static_cast<int>(embed_num);
+    dec.encode_batch_idx = 1;
+    dec.k_total = static_cast<int>(w_top_k + r_top_k);
+    dec.position_ids = position_ids;
+    dec.wrec = const_cast<ramnet::WriteRec *>(lay.wrec);
+    dec.rrec = const_cast<ramnet::ReadRec *>(lay.rrec);
+    dec.noop_w = const_cast<ramnet::WriteRec *>(lay.noop_w);
+    dec.noop_r = const_cast<ramnet::ReadRec *>(lay.noop_r);
+    dec.gamma = gamma;
+    dec.mask = mask;
+    const char *why = nullptr;
+    const hipError_t err = ramnet::launch_topk_addr(dec, static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, "topk_addr_records launch");
+}
+
+int ramnet_segment_scan(const void *x, int dtype, const float *init_slot, const float *init_mass, float *slot_out,
+                        float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                        int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *workspace,
+                        int64_t workspace_bytes, void *stream) {
+    if (int rc = segment_checks(x, x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k,
+                                r_top_k, eps, workspace, workspace_bytes))
+        return rc;
+    if (B == 0)
+        return RAMNET_OK;
+    ramnet::SegmentJob job = make_segment_job(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C,
+                                              w_top_k, r_top_k, mass_aware, eps, workspace);
+    const char *why = nullptr;
+    const hipError_t err = ramnet::launch_segment_forward(job, static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, "segment_scan launch");
+}
+
+int ramnet_ram_attn_forward(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
+                            const uint8_t *mask, int64_t embed_num, const int32_t *position_ids,
+                            const float *init_slot, const float *init_mass, float *slot_out, float *mass_out, void *y,
+                            int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int64_t A, int64_t C,
+                            int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm, int mass_aware,
+                            float eps, void *workspace, int64_t workspace_bytes, void *stream) {
+    if (int rc = segment_checks(x, gamma, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k,
+                                r_top_k, eps, workspace, workspace_bytes))
+        return rc;
+    if (B > 0 && T > 0) {
+        if (int rc = ramnet_topk_addr_records(w_addr, r_addr, gamma, dtype, mask, embed_num, position_ids, B, H, U, P,
+                                              T, A, w_top_k, r_top_k, w_re_norm, r_re_norm, workspace,
+                                              workspace_bytes, stream))
+            return rc;
+    }
+    return ramnet_segment_scan(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k, r_top_k,
+                               mass_aware, eps, workspace, workspace_bytes, stream);
 }
 
 int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,

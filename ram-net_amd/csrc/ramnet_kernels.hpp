@@ -19,6 +19,40 @@ struct AddrSource {
     int k_off;      // first row of this address in the (B, H, k_total, T) outputs
 };
 
+// Per-event records consumed by the segment scan, laid out
+// [b*H + h][event][t] with t padded to a multiple of kScanPad (an even
+// number of kScanChunk-token chunks, so the scan's two prefetch buffers
+// alternate without a tail case). Slots are
+// local to the (b, h) head after CAPE. Events that must not act (masked or
+// padding tokens, inactive addresses, zero weights) point at dummy LDS rows
+// in front of the state: writes at slot -2 (weight 0, alpha 1), reads at
+// slot -1 (weight 0). The workspace holds, in order: write records
+// (B*H, Kw, T_pad), read records (B*H, Kr, T_pad), then one chunk of no-op
+// write records and one of no-op read records (read by lanes beyond top-K).
+constexpr int kScanChunk = 16;
+constexpr int kScanPad = 2 * kScanChunk;
+struct WriteRec {
+    int slot;
+    float w;
+    float alpha;
+    float pad;
+};
+struct ReadRec {
+    int slot;
+    float r;
+};
+
+__host__ __device__ inline int scan_t_pad(int T) { return (T + kScanPad - 1) / kScanPad * kScanPad; }
+inline int64_t scan_t_pad64(int64_t T) { return (T + kScanPad - 1) / kScanPad * kScanPad; }
+
+// Written by every record producer (the first kScanChunk threads of the grid).
+__device__ __forceinline__ void write_noop_chunk(WriteRec *w, ReadRec *r, int64_t tid) {
+    if (tid < kScanChunk) {
+        w[tid] = WriteRec{-2, 0.f, 1.f, 0.f};
+        r[tid] = ReadRec{-1, 0.f};
+    }
+}
+
 // Decode one or two address tensors (write and read) sharing a shape.
 struct AddrJob {
     AddrSource src[2];
@@ -31,15 +65,23 @@ struct AddrJob {
     const int32_t *position_ids;  // (B, T)
     int32_t *idx_out;             // (B, H, k_total, T)
     float *val_out;               // (B, H, k_total, T)
+    // Record mode (both set): instead of idx/val, write scan records for
+    // t < T_pad, source 0 as writes, source 1 as reads.
+    WriteRec *wrec;               // (B*H, Kw, T_pad)
+    ReadRec *rrec;                // (B*H, Kr, T_pad)
+    WriteRec *noop_w;             // kScanChunk no-op records (written too)
+    ReadRec *noop_r;
+    const void *gamma;            // (B, H, T) in dtype, for alpha
+    const uint8_t *mask;          // (B, T) or null
 };
 
 // Time-sequential gated sparse update + top-K read over a whole sequence.
 struct SegmentJob {
-    const int32_t *addr_idx;  // (B, H, Kw + Kr, T), encoded (b*H + h)*A + a
-    const float *addr_val;    // (B, H, Kw + Kr, T); write weights > 0, read weights stored negated
+    const WriteRec *wrec;     // (B*H, Kw, T_pad) scan records
+    const ReadRec *rrec;      // (B*H, Kr, T_pad)
+    const WriteRec *noop_w;   // kScanChunk no-op write records
+    const ReadRec *noop_r;    // kScanChunk no-op read records
     const void *x;            // (B, H, T, C) in dtype
-    const void *gamma;        // (B, H, T) in dtype
-    const uint8_t *mask;      // (B, T) bool, or null
     const float *init_slot;   // (B, H, A, C)
     const float *init_mass;   // (B, H, A)
     float *slot_out;          // (B, H, A, C); may alias init_slot
@@ -74,6 +116,21 @@ struct DecodeJob {
 // message when the shape is outside what the kernels were built for.
 hipError_t launch_topk_addr(const AddrJob &job, hipStream_t stream, const char **why);
 hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, const char **why);
+
+// Build scan records from decoder outputs idx/val (B, H, Kw + Kr, T).
+struct PackJob {
+    const int32_t *addr_idx;
+    const float *addr_val;
+    const void *gamma;        // (B, H, T) in dtype
+    const uint8_t *mask;      // (B, T) or null
+    WriteRec *wrec;
+    ReadRec *rrec;
+    WriteRec *noop_w;
+    ReadRec *noop_r;
+    int dtype;
+    int B, H, T, A, Kw, Kr;
+};
+hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const char **why);
 hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const char **why);
 
 // Channel-slice width and dynamic LDS bytes the segment kernel would use.

@@ -157,11 +157,43 @@ __host__ __device__ inline int staircase_count(int K) {
     return n;
 }
 
+// Logits of one address as seen by one lane of a GW-lane group: digit u,
+// radix li. The first kPreDigits digits are loaded up front in one batch
+// (unconditionally, from a clamped radix), later digits on demand.
+constexpr int kPreDigits = 4;
+
+template<typename T>
+struct GroupLogits {
+    float pre[kPreDigits];
+    const T *ptr;
+    int P;
+
+    __device__ __forceinline__ void load(const T *p, int U, int P_, int li) {
+        ptr = p;
+        P = P_;
+        const int r = li < P_ ? li : P_ - 1;
+#pragma unroll
+        for (int u = 0; u < kPreDigits; ++u)
+            pre[u] = load_f32(p + (u < U ? u : U - 1) * P_ + r);
+    }
+
+    __device__ __forceinline__ float get(int u, int li) const {
+        if (u < kPreDigits) {
+            float v = pre[0];
+#pragma unroll
+            for (int k = 1; k < kPreDigits; ++k)
+                v = u == k ? pre[k] : v;
+            return li < P ? v : kNegInfF;
+        }
+        return li < P ? load_f32(ptr + u * P + li) : kNegInfF;
+    }
+};
+
 // Decode one address with a group of GW lanes starting at lane g0. On return
 // lanes g0 .. g0+K-1 hold the sorted top entries (score, content slot).
 // Returns the inactive flag (uniform within the group).
 template<typename T, int GW>
-__device__ bool group_search(const T *ptr, int U, int P, int K, int li, float &out_v, int &out_i) {
+__device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int li, float &out_v, int &out_i) {
     float cv = kNegInfF;
     int ci = kNoIdx;
     bool inactive = false;
@@ -182,7 +214,7 @@ __device__ bool group_search(const T *ptr, int U, int P, int K, int li, float &o
     }
     const int g0 = (threadIdx.x & (kWave - 1)) & ~(GW - 1);
     for (int u = 0; u < U; ++u) {
-        const float x = li < P ? load_f32(ptr + u * P + li) : kNegInfF;
+        const float x = lg.get(u, li);
         const bool fin = li < P && x != kNegInfF;
         // any finite logit in this digit, within the group
         float any = fin ? 1.f : 0.f;

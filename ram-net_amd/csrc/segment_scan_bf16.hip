@@ -1,0 +1,11 @@
+// Segment scan kernels for bf16_t activations (one translation unit per dtype
+// so the lane-layout instantiations compile in parallel).
+#include "segment_scan.hpp"
+
+namespace ramnet {
+
+hipError_t launch_scan_bf16(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, hipStream_t stream) {
+    return scan_dispatch<bf16_t>(job, geo, vec, epp, np, stream);
+}
+
+}  // namespace ramnet

@@ -83,19 +83,67 @@ __device__ __forceinline__ void build_column(const float (&mv)[KM], const int (&
     }
 }
 
+__device__ const uint8_t kAddrAllValid = 1;
+
+// Record mode output of one address (source 0 = writes, 1 = reads). `get(k,
+// c, v)` yields the k-th selected content slot and its weight. Events of
+// masked or padding tokens, inactive addresses and zero weights become
+// no-ops pointing at the scan's dummy rows (slot -2 for writes, -1 for reads).
+// KM > 0 unrolls over a register list of that size; KM == 0 loops at run
+// time (list in LDS).
+template<typename Scalar, int KM, typename Get>
+__device__ __forceinline__ void write_records(const AddrJob &job, int which, int64_t bh, int b, int t, int tl,
+                                              bool inactive, Get get, int K, int shift) {
+    const int T = job.T, A = job.A;
+    const int Tp = scan_t_pad(T);
+    const uint8_t *mp = job.mask ? job.mask + static_cast<int64_t>(b) * T + tl : &kAddrAllValid;
+    const bool live = t < T && *mp != 0 && !inactive;
+    const float g = which == 0 ? load_f32(static_cast<const Scalar *>(job.gamma) + bh * T + tl) : 0.f;
+    auto one = [&](int k) {
+        int c;
+        float v;
+        get(k, c, v);
+        int o = c - shift;
+        o = o < 0 ? o + A : o;
+        const bool act = live && v != 0.f;
+        if (which == 0) {
+            WriteRec rec{-2, 0.f, 1.f, 0.f};
+            if (act)
+                rec = WriteRec{o, v, gsu_alpha(v, g), 0.f};
+            job.wrec[(bh * K + k) * Tp + t] = rec;
+        } else {
+            job.rrec[(bh * K + k) * Tp + t] = act ? ReadRec{o, v} : ReadRec{-1, 0.f};
+        }
+    };
+    if constexpr (KM > 0) {
+#pragma unroll
+        for (int k = 0; k < KM; ++k)
+            if (k < K)
+                one(k);
+    } else {
+        for (int k = 0; k < K; ++k)
+            one(k);
+    }
+}
+
 template<typename Scalar, int NP, int KM>
 __global__ __launch_bounds__(256) void topk_addr_lane_kernel(const AddrJob job) {
     const AddrSource &src = job.src[blockIdx.y];
-    const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
+    const int T = job.T, H = job.H, U = job.U, P = job.P, A = job.A;
+    const bool rec_mode = job.wrec != nullptr;
+    const int Tg = rec_mode ? scan_t_pad(T) : T;  // record mode also writes the padding tokens
+    const int64_t n = static_cast<int64_t>(job.B) * job.H * Tg;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (rec_mode && blockIdx.y == 0)
+        write_noop_chunk(job.noop_w, job.noop_r, gid);
     if (gid >= n)
         return;
-    const int T = job.T, H = job.H, U = job.U, P = job.P, A = job.A;
-    const int t = static_cast<int>(gid % T);
-    const int64_t bh = gid / T;
+    const int t = static_cast<int>(gid % Tg);
+    const int tl = t < T ? t : T - 1;
+    const int64_t bh = gid / Tg;
     const int h = static_cast<int>(bh % H);
     const int b = static_cast<int>(bh / H);
-    const Scalar *base = static_cast<const Scalar *>(src.addr) + bh * static_cast<int64_t>(U * P) * T + t;
+    const Scalar *base = static_cast<const Scalar *>(src.addr) + bh * static_cast<int64_t>(U * P) * T + tl;
 
     float mv[KM];
     int mi[KM];
@@ -108,7 +156,10 @@ __global__ __launch_bounds__(256) void topk_addr_lane_kernel(const AddrJob job) 
         float mx = kNegInf;
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            v[p] = p < P ? load_f32(base + static_cast<int64_t>(u * P + p) * T) : kNegInf;
+            // unconditional load from a clamped radix (a guarded load would
+            // wait for its data inside the branch)
+            const float raw = load_f32(base + static_cast<int64_t>(u * P + (p < P ? p : P - 1)) * T);
+            v[p] = p < P ? raw : kNegInf;
             id[p] = p < P ? p : kNoIdx;
             all_ninf = all_ninf && (p >= P || v[p] == kNegInf);
             mx = fmaxf(mx, v[p]);
@@ -168,7 +219,14 @@ __global__ __launch_bounds__(256) void topk_addr_lane_kernel(const AddrJob job) 
                 sum += expf(mv[k] - mv[0]);
         lse = mv[0] + logf(sum);
     }
-    const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + t], A) : 0;
+    const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + tl], A) : 0;
+    if (rec_mode) {
+        write_records<Scalar, KM>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
+            c = mi[k];
+            v = expf(mv[k] - src.re_norm * lse);
+        }, K, shift);
+        return;
+    }
     const int idx_base = (job.encode_batch_idx ? static_cast<int>(bh) : h) * A;
     const int64_t row0 = (bh * job.k_total + src.k_off) * static_cast<int64_t>(T) + t;
 #pragma unroll
@@ -190,12 +248,17 @@ __global__ __launch_bounds__(256) void topk_addr_bruteforce_kernel(const AddrJob
     extern __shared__ float smem[];
     const AddrSource &src = job.src[blockIdx.y];
     const int T = job.T, H = job.H, U = job.U, P = job.P, A = job.A;
+    const bool rec_mode = job.wrec != nullptr;
+    const int Tg = rec_mode ? scan_t_pad(T) : T;
+    if (rec_mode && blockIdx.x == 0 && blockIdx.y == 0)
+        write_noop_chunk(job.noop_w, job.noop_r, threadIdx.x);
     const int64_t gid = blockIdx.x;  // (b, h, t)
-    const int t = static_cast<int>(gid % T);
-    const int64_t bh = gid / T;
+    const int t = static_cast<int>(gid % Tg);
+    const int tl = t < T ? t : T - 1;
+    const int64_t bh = gid / Tg;
     const int h = static_cast<int>(bh % H);
     const int b = static_cast<int>(bh / H);
-    const Scalar *base = static_cast<const Scalar *>(src.addr) + bh * static_cast<int64_t>(U * P) * T + t;
+    const Scalar *base = static_cast<const Scalar *>(src.addr) + bh * static_cast<int64_t>(U * P) * T + tl;
 
     float *lg = smem;
     float *ex = lg + U * P;
@@ -209,7 +272,15 @@ __global__ __launch_bounds__(256) void topk_addr_bruteforce_kernel(const AddrJob
     if (tid == 0)
         s_lse = (src.re_norm != 0.f && !inactive) ? topk_lse_serial(sv, K) : 0.f;
     __syncthreads();
-    const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + t], A) : 0;
+    const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + tl], A) : 0;
+    if (rec_mode) {
+        if (tid == 0)
+            write_records<Scalar, 0>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
+                c = si[k];
+                v = expf(sv[k] - src.re_norm * s_lse);
+            }, K, shift);
+        return;
+    }
     const int idx_base = (job.encode_batch_idx ? static_cast<int>(bh) : h) * A;
     const int64_t row0 = (bh * job.k_total + src.k_off) * static_cast<int64_t>(T) + t;
     for (int k = tid; k < K; k += blockDim.x) {
@@ -229,9 +300,11 @@ int pow2_at_least(int x) {
     return p;
 }
 
+int grid_t(const AddrJob &job) { return job.wrec ? scan_t_pad(job.T) : job.T; }
+
 template<typename T, int NP, int KM>
 hipError_t launch_lane(const AddrJob &job, hipStream_t stream) {
-    const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
+    const int64_t n = static_cast<int64_t>(job.B) * job.H * grid_t(job);
     const dim3 grid(static_cast<unsigned>((n + 255) / 256), job.n_src);
     hipLaunchKernelGGL((topk_addr_lane_kernel<T, NP, KM>), grid, dim3(256), 0, stream, job);
     return hipGetLastError();
@@ -270,7 +343,7 @@ hipError_t launch_typed(const AddrJob &job, hipStream_t stream, const char **why
         *why = "address decoder: shape needs P <= 64 and top_k <= 16, or P**U small enough for the exact LDS search (A <= 8192)";
         return hipErrorInvalidValue;
     }
-    const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
+    const int64_t n = static_cast<int64_t>(job.B) * job.H * grid_t(job);
     if (n > 0x7fffffff) {
         *why = "address decoder: B*H*T too large for the exact search grid";
         return hipErrorInvalidValue;

@@ -43,12 +43,24 @@ SIGNATURES: dict[str, tuple[type, list]] = {
     "ramnet_topk_addr_forward": (_c_int, [
         _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr,
         _c_i64, _c_i64, _c_float, _c_float, _c_int, _c_ptr, _c_ptr, _c_ptr]),
+    "ramnet_scan_workspace_bytes64": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "ramnet_scan_workspace_bytes": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "ramnet_topk_segment_forward": (_c_int, [
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
-        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_float, _c_ptr]),
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_float, _c_ptr, _c_i64, _c_ptr]),
     "ramnet_topk_segment_forward_": (_c_int, [
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
-        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_float, _c_ptr]),
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_float, _c_ptr, _c_i64, _c_ptr]),
+    "ramnet_topk_addr_records": (_c_int, [
+        _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_i64, _c_i64, _c_float, _c_float, _c_ptr, _c_i64, _c_ptr]),
+    "ramnet_segment_scan": (_c_int, [
+        _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_i64, _c_int, _c_float, _c_ptr, _c_i64, _c_ptr]),
+    "ramnet_ram_attn_forward": (_c_int, [
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_float, _c_int,
+        _c_float, _c_ptr, _c_i64, _c_ptr]),
     "ramnet_topk_autoregressive_": (_c_int, [
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr,
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_float,
@@ -100,6 +112,11 @@ def segment_plan(A: int, C: int, w_top_k: int, r_top_k: int) -> tuple[int, int] 
     cs, lds = _c_int(0), _c_int(0)
     ok = lib().ramnet_segment_plan(A, C, w_top_k, r_top_k, ctypes.byref(cs), ctypes.byref(lds))
     return (cs.value, lds.value) if ok else None
+
+
+def scan_workspace_bytes(B: int, H: int, T: int, w_top_k: int, r_top_k: int) -> int:
+    """Device workspace (bytes) the segment scan needs for these sizes."""
+    return int(lib().ramnet_scan_workspace_bytes64(B, H, T, w_top_k, r_top_k))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

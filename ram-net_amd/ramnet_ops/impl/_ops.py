@@ -90,15 +90,18 @@ def _(w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re_norm, r
 # --------------------------------------------------------------------------
 # segment scan (prefill)
 
-def _segment_args(addr_idx, addr_val, x, gamma, mask):
-    B, H, T, C = x.shape
+def _segment_args(x, gamma, mask):
     x = x.contiguous()
     gamma = gamma.to(dtype=x.dtype).contiguous()
-    addr_idx = addr_idx.to(torch.int32).contiguous()
-    addr_val = addr_val.to(torch.float32).contiguous()
     if mask is not None:
         mask = mask.to(device=x.device, dtype=torch.bool).contiguous()
-    return B, H, T, C, addr_idx, addr_val, x, gamma, mask
+    return x, gamma, mask
+
+
+def _workspace(x: Tensor, B: int, H: int, T: int, w_top_k: int, r_top_k: int) -> Tensor:
+    """Per-call scan workspace (per-event records) from torch's caching allocator."""
+    return torch.empty(max(1, nat.scan_workspace_bytes(B, H, T, w_top_k, r_top_k)), dtype=torch.uint8,
+                       device=x.device)
 
 
 @torch.library.custom_op(f"{_NS}::topk_segment_forward", mutates_args=(), device_types="cuda")
@@ -106,18 +109,22 @@ def topk_segment_forward(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: T
                          init_mass: Tensor, mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool,
                          eps: float) -> tuple[Tensor, Tensor, Tensor]:
     _require_gpu("topk_segment_forward", addr_idx, addr_val, x, gamma, init_slot, init_mass, mask)
-    B, H, T, C, addr_idx, addr_val, x, gamma, mask = _segment_args(addr_idx, addr_val, x, gamma, mask)
+    B, H, T, C = x.shape
+    x, gamma, mask = _segment_args(x, gamma, mask)
+    addr_idx = addr_idx.to(torch.int32).contiguous()
+    addr_val = addr_val.to(torch.float32).contiguous()
     A = init_slot.shape[-2]
     init_slot = init_slot.to(torch.float32).contiguous()
     init_mass = init_mass.to(torch.float32).contiguous()
     slot = torch.empty_like(init_slot)
     mass = torch.empty_like(init_mass)
     y = torch.empty_like(x)
+    ws = _workspace(x, B, H, T, w_top_k, r_top_k)
     with torch.cuda.device(x.device):
         nat.call("ramnet_topk_segment_forward", addr_idx.data_ptr(), addr_val.data_ptr(), x.data_ptr(),
                  gamma.data_ptr(), _code(x), nat.ptr(mask), init_slot.data_ptr(), init_mass.data_ptr(),
                  slot.data_ptr(), mass.data_ptr(), y.data_ptr(), B, H, T, A, C, w_top_k, r_top_k, int(mass_aware),
-                 float(eps), nat.stream_of(x))
+                 float(eps), ws.data_ptr(), ws.numel(), nat.stream_of(x))
     return y, slot, mass
 
 
@@ -131,23 +138,94 @@ def _(addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k
 def topk_segment_forward_(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
                           mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool, eps: float) -> Tensor:
     _require_gpu("topk_segment_forward_", addr_idx, addr_val, x, gamma, slot, mass, mask)
-    if slot.dtype != torch.float32 or mass.dtype != torch.float32 or not (slot.is_contiguous() and mass.is_contiguous()):
-        raise RuntimeError("topk_segment_forward_: slot and mass must be contiguous float32 tensors")
-    B, H, T, C, addr_idx, addr_val, x, gamma, mask = _segment_args(addr_idx, addr_val, x, gamma, mask)
+    _require_state("topk_segment_forward_", slot, mass)
+    B, H, T, C = x.shape
+    x, gamma, mask = _segment_args(x, gamma, mask)
+    addr_idx = addr_idx.to(torch.int32).contiguous()
+    addr_val = addr_val.to(torch.float32).contiguous()
     A = slot.shape[-2]
     # channel slices of one head may start after another has stored the new
     # masses, so every slice reads the masses from a snapshot
     mass_in = mass.clone()
     y = torch.empty_like(x)
+    ws = _workspace(x, B, H, T, w_top_k, r_top_k)
     with torch.cuda.device(x.device):
         nat.call("ramnet_topk_segment_forward_", addr_idx.data_ptr(), addr_val.data_ptr(), x.data_ptr(),
                  gamma.data_ptr(), _code(x), nat.ptr(mask), slot.data_ptr(), mass.data_ptr(), mass_in.data_ptr(),
-                 y.data_ptr(), B, H, T, A, C, w_top_k, r_top_k, int(mass_aware), float(eps), nat.stream_of(x))
+                 y.data_ptr(), B, H, T, A, C, w_top_k, r_top_k, int(mass_aware), float(eps), ws.data_ptr(),
+                 ws.numel(), nat.stream_of(x))
     return y
 
 
 @topk_segment_forward_.register_fake
 def _(addr_idx, addr_val, x, gamma, slot, mass, mask, w_top_k, r_top_k, mass_aware, eps):
+    return x.new_empty(x.shape)
+
+
+def _require_state(name: str, slot: Tensor, mass: Tensor) -> None:
+    if slot.dtype != torch.float32 or mass.dtype != torch.float32 or not (slot.is_contiguous() and mass.is_contiguous()):
+        raise RuntimeError(f"{name}: slot and mass must be contiguous float32 tensors")
+
+
+def _ram_attn_call(w_addr, r_addr, x, gamma, mask, embed_num, position_ids, init_slot, init_mass, slot, mass,
+                   w_top_k, r_top_k, w_re_norm, r_re_norm, mass_aware, eps):
+    B, H, U, P, T = w_addr.shape
+    C = x.shape[-1]
+    A = P ** U
+    if r_addr.shape != w_addr.shape or r_addr.dtype != w_addr.dtype or x.dtype != w_addr.dtype:
+        raise RuntimeError("ram_attn_forward: w_addr, r_addr and x must share dtype and address shape")
+    w_addr, r_addr = w_addr.contiguous(), r_addr.contiguous()
+    x, gamma, mask = _segment_args(x, gamma, mask)
+    pos = position_ids.to(device=x.device, dtype=torch.int32).contiguous()
+    y = torch.empty_like(x)
+    ws = _workspace(x, B, H, T, w_top_k, r_top_k)
+    with torch.cuda.device(x.device):
+        nat.call("ramnet_ram_attn_forward", w_addr.data_ptr(), r_addr.data_ptr(), x.data_ptr(), gamma.data_ptr(),
+                 _code(x), nat.ptr(mask), embed_num, pos.data_ptr(), init_slot.data_ptr(), init_mass.data_ptr(),
+                 slot.data_ptr(), mass.data_ptr(), y.data_ptr(), B, H, U, P, T, A, C, w_top_k, r_top_k,
+                 float(w_re_norm), float(r_re_norm), int(mass_aware), float(eps), ws.data_ptr(), ws.numel(),
+                 nat.stream_of(x))
+    return y
+
+
+@torch.library.custom_op(f"{_NS}::ram_attn_forward", mutates_args=(), device_types="cuda")
+def ram_attn_forward(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tensor, init_slot: Tensor, init_mass: Tensor,
+                     mask: Tensor | None, embed_num: int, position_ids: Tensor, w_top_k: int, r_top_k: int,
+                     w_re_norm: float, r_re_norm: float, mass_aware: bool,
+                     eps: float) -> tuple[Tensor, Tensor, Tensor]:
+    """Whole parallel forward (decoders + segment scan) returning y, new slot and mass."""
+    _require_gpu("ram_attn_forward", w_addr, r_addr, x, gamma, init_slot, init_mass, position_ids, mask)
+    init_slot = init_slot.to(torch.float32).contiguous()
+    init_mass = init_mass.to(torch.float32).contiguous()
+    slot = torch.empty_like(init_slot)
+    mass = torch.empty_like(init_mass)
+    y = _ram_attn_call(w_addr, r_addr, x, gamma, mask, embed_num, position_ids, init_slot, init_mass, slot, mass,
+                       w_top_k, r_top_k, w_re_norm, r_re_norm, mass_aware, eps)
+    return y, slot, mass
+
+
+@ram_attn_forward.register_fake
+def _(w_addr, r_addr, x, gamma, init_slot, init_mass, mask, embed_num, position_ids, w_top_k, r_top_k, w_re_norm,
+      r_re_norm, mass_aware, eps):
+    return (x.new_empty(x.shape), init_slot.new_empty(init_slot.shape, dtype=torch.float32),
+            init_mass.new_empty(init_mass.shape, dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{_NS}::ram_attn_forward_", mutates_args=("slot", "mass"), device_types="cuda")
+def ram_attn_forward_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
+                      mask: Tensor | None, embed_num: int, position_ids: Tensor, w_top_k: int, r_top_k: int,
+                      w_re_norm: float, r_re_norm: float, mass_aware: bool, eps: float) -> Tensor:
+    """In-place whole parallel forward: updates slot and mass, returns y."""
+    _require_gpu("ram_attn_forward_", w_addr, r_addr, x, gamma, slot, mass, position_ids, mask)
+    _require_state("ram_attn_forward_", slot, mass)
+    mass_in = mass.clone()  # see topk_segment_forward_
+    return _ram_attn_call(w_addr, r_addr, x, gamma, mask, embed_num, position_ids, slot, mass_in, slot, mass,
+                          w_top_k, r_top_k, w_re_norm, r_re_norm, mass_aware, eps)
+
+
+@ram_attn_forward_.register_fake
+def _(w_addr, r_addr, x, gamma, slot, mass, mask, embed_num, position_ids, w_top_k, r_top_k, w_re_norm, r_re_norm,
+      mass_aware, eps):
     return x.new_empty(x.shape)
 
 
@@ -159,8 +237,7 @@ def topk_autoregressive_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tenso
                          mask: Tensor, embed_num: int, position_ids: Tensor, w_top_k: int, r_top_k: int,
                          w_re_norm: float, r_re_norm: float, mass_aware: bool, eps: float) -> Tensor:
     _require_gpu("topk_autoregressive_", w_addr, r_addr, x, gamma, slot, mass, position_ids)
-    if slot.dtype != torch.float32 or mass.dtype != torch.float32 or not (slot.is_contiguous() and mass.is_contiguous()):
-        raise RuntimeError("topk_autoregressive_: slot and mass must be contiguous float32 tensors")
+    _require_state("topk_autoregressive_", slot, mass)
     B, H, U, P = w_addr.shape
     C = x.shape[-1]
     A = slot.shape[-2]

@@ -134,14 +134,16 @@ def _cuda_ram_attn(
                 w_top_k, r_top_k, w_re, r_re, mass_aware, eps)
         return ys.unsqueeze(-2), post_slot, post_mass
 
-    addr_idx, addr_val = torch.ops.ramnet_ops.topk_addr_forward(
-        w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re, r_re)
+    # decoders + segment scan in one native call; the decoders hand the scan
+    # its per-event records directly
     if inplace:
-        ys = torch.ops.ramnet_ops.topk_segment_forward_(
-            addr_idx, addr_val, xs, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps)
+        ys = torch.ops.ramnet_ops.ram_attn_forward_(
+            w_addr, r_addr, xs, gamma, init_slot, init_mass, mask, embed_num, position_ids, w_top_k, r_top_k,
+            w_re, r_re, mass_aware, eps)
         return ys, init_slot, init_mass
-    ys, post_slot, post_mass = torch.ops.ramnet_ops.topk_segment_forward(
-        addr_idx, addr_val, xs, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps)
+    ys, post_slot, post_mass = torch.ops.ramnet_ops.ram_attn_forward(
+        w_addr, r_addr, xs, gamma, init_slot, init_mass, mask, embed_num, position_ids, w_top_k, r_top_k,
+        w_re, r_re, mass_aware, eps)
     return ys, post_slot, post_mass
 
 

@@ -125,7 +125,7 @@ def test_decoder_known_answer_fixtures(golden):
         idx, val = ops.topk_addr_single_forward(addr.float().to(DEV), 0, fx["A"], pos.to(DEV), K, r, False, True)
         torch.cuda.synchronize()
         got = _weight_map(idx, val, fx["A"], 1)[0, 0]
-        err = oracle.rel_err(got, torch.tensor(case["dense"]))
+        err = oracle.rel_err(got, torch.tensor(case["dense"], dtype=torch.float64))
         assert err <= FP32_TOL, f"extreme-logit weights rel err {err:.3e} (K={K}, r={r})"
     fx = golden("product_distribution.json")
     addr = torch.tensor(fx["addr"], dtype=torch.float64).view(fx["shape"])
@@ -137,7 +137,7 @@ def test_decoder_known_answer_fixtures(golden):
                                                 False, True)
         torch.cuda.synchronize()
         got = _weight_map(idx, val, fx["A"], H)
-        err = oracle.rel_err(got, torch.tensor(case["dense"]).view(got.shape))
+        err = oracle.rel_err(got, torch.tensor(case["dense"], dtype=torch.float64).view(got.shape))
         assert err <= FP32_TOL, f"product-distribution weights rel err {err:.3e} (K={K}, r={r})"
     fx = golden("inactive.json")
     addr = torch.tensor(fx["addr"]).view(fx["shape"]).float()

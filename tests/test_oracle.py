@@ -39,7 +39,7 @@ def test_decoder_matches_product_distribution_fixture(golden, dtype, tol):
     for case in fx["cases"]:
         idx, val = oracle.dense_topk_addr(addr, fx["embed_num"], pos, case["top_k"], case["re_norm"], dtype=dtype)
         got = _dense_map(idx, val, fx["A"], H)
-        assert oracle.rel_err(got, torch.tensor(case["dense"]).view(got.shape)) <= tol, case["top_k"]
+        assert oracle.rel_err(got, torch.tensor(case["dense"], dtype=torch.float64).view(got.shape)) <= tol, case["top_k"]
 
 
 def test_decoder_matches_extreme_logit_fixture(golden):
@@ -245,7 +245,8 @@ def test_dense_oracle_is_chunk_invariant():
     for chunk in (1, 7, 13):
         part = oracle.dense_ram_attn(*args, chunk=chunk)
         for a, b in zip(full, part):
-            assert torch.equal(a, b)
+            # torch's CPU kernels vectorise by shape, so only rounding may differ
+            assert oracle.rel_err(b, a) <= 1e-6
 
 
 def test_sparse_oracle_steps_match_one_call_and_masked_tokens_are_skipped():
