@@ -16,7 +16,11 @@ restatement of the reference's dense PyTorch algorithm on a bounded sample of
 the same inputs (rank 0, N=1 only).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S]
-       [--no-cpu-baseline] [--only prefill|decode]
+       [--no-cpu-baseline] [--only prefill|decode] [--copy-probe MIB]
+
+``--copy-probe MIB`` first runs one plain device-to-device copy of MIB MiB
+(torch ``copy_``, fp32): under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``
+it is the calibration kernel of known traffic for the byte counters.
 """
 from __future__ import annotations
 
@@ -281,6 +285,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only", choices=("prefill", "decode"), default=None)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -293,6 +298,16 @@ def main(argv=None) -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.copy_probe > 0:
+        n = args.copy_probe * (1 << 20) // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.copy_probe} MiB read + {args.copy_probe} MiB written")
+        del src, dst
 
     out = {"metric": METRIC}
     pre = dec = None

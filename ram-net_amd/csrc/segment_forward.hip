@@ -28,6 +28,8 @@
 #include "segment_scan.hpp"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 namespace ramnet {
 
@@ -57,38 +59,53 @@ int cu_count() {
 }
 
 struct Plan {
-    int vec, epp, np, cs;
+    int vec, epp, np, nw, cs;
     size_t lds;
 };
 
-// Fewest rounds of resident units wins; ties go to the wider slice.
+// Cost model of one layout, in cycles per token of one round of resident
+// workgroups: a wave's token loop is bound by its dependency chain (LDS
+// read -> update -> LDS write, ~kChainCycles) or by the issue of its VALU
+// work (~14 + 10 * VEC * NP instructions, 4 cycles each, shared by the waves
+// on one SIMD), whichever is longer. Total = rounds * per-token cycles.
+constexpr int64_t kChainCycles = 160;
+
 bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int n_cu, Plan *out) {
     const int kmax = std::max(Kw, Kr);
     if (kmax > 2 * kWave)
         return false;
     const int epp0 = std::min(kWave, std::max(4, pow2_ceil(kmax)));
-    const int np = (kmax + epp0 - 1) / epp0;
-    const int c_cap = pow2_ceil(C);
     bool found = false;
-    int64_t best_rounds = 0;
-    for (int epp = epp0; epp <= kWave; epp <<= 1) {
-        if (np > 1 && epp != kWave)
+    int64_t best = 0;
+    for (int epp = 4; epp <= kWave; epp <<= 1) {
+        const int np = (kmax + epp - 1) / epp;
+        if (np > 2 || (np == 2 && epp * 2 < epp0))
             continue;
-        for (int vec = 4; vec >= 1; vec >>= 1) {
-            const int cs = (kWave / epp) * vec;
-            if (cs > c_cap && vec > 1)
-                continue;
-            const size_t lds = scan_lds_bytes(A, vec, epp);
-            const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
-            if (gran > kLdsPerCu)
-                continue;
-            const int64_t per_cu = std::min<int64_t>(kLdsPerCu / gran, 8);
-            const int64_t units = static_cast<int64_t>(B) * H * ((C + cs - 1) / cs);
-            const int64_t rounds = (units + per_cu * n_cu - 1) / (per_cu * n_cu);
-            if (!found || rounds < best_rounds || (rounds == best_rounds && cs > out->cs)) {
-                *out = {vec, epp, np, cs, lds};
-                best_rounds = rounds;
-                found = true;
+        for (int nw = 4; nw >= 1; nw >>= 1) {
+            for (int vec = 4; vec >= 1; vec >>= 1) {
+                if (!scan_layout_compiled(vec, epp, np, nw))
+                    continue;
+                const int cs = nw * (kWave / epp) * vec;
+                const size_t lds = scan_lds_bytes(A, vec, epp, nw);
+                const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
+                if (gran > kLdsPerCu)
+                    continue;
+                const int64_t units = static_cast<int64_t>(B) * H * ((C + cs - 1) / cs);
+                const int64_t per_cu = std::min<int64_t>(kLdsPerCu / gran, std::max(1, 8 / nw));
+                const int64_t rounds = (units + per_cu * n_cu - 1) / (per_cu * n_cu);
+                const int64_t resident = std::min<int64_t>(per_cu, (units + n_cu - 1) / n_cu);
+                const int64_t waves_per_simd = (resident * nw + 3) / 4;
+                const int64_t issue = 4 * (14 + 10 * vec * np) * waves_per_simd;
+                int64_t cost = rounds * std::max(kChainCycles, issue);
+                if (C % cs != 0)
+                    cost = cost * 3 / 2;  // partial slices take the guarded path
+                const bool better = !found || cost < best ||
+                                    (cost == best && (nw > out->nw || (nw == out->nw && cs > out->cs)));
+                if (better) {
+                    *out = {vec, epp, np, nw, cs, lds};
+                    best = cost;
+                    found = true;
+                }
             }
         }
     }
@@ -159,11 +176,35 @@ int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes) {
     return 1;
 }
 
+// RAMNET_SCAN_LAYOUT="vec,epp,np,nw" replaces the planner's choice (tests
+// sweep every compiled layout with it; also a tuning knob). The layout must
+// be compiled, cover max(Kw, Kr) events and fit in LDS.
+static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
+    const char *env = std::getenv("RAMNET_SCAN_LAYOUT");
+    if (!env || !*env)
+        return 0;
+    int vec = 0, epp = 0, np = 0, nw = 0;
+    if (std::sscanf(env, "%d,%d,%d,%d", &vec, &epp, &np, &nw) != 4 || !scan_layout_compiled(vec, epp, np, nw)) {
+        *why = "RAMNET_SCAN_LAYOUT names no compiled layout (vec,epp,np,nw)";
+        return -1;
+    }
+    const size_t lds = scan_lds_bytes(job.A, vec, epp, nw);
+    if (epp * np < std::max(job.Kw, job.Kr) || static_cast<int64_t>(lds) > kLdsPerCu) {
+        *why = "RAMNET_SCAN_LAYOUT does not cover top_k or does not fit in LDS";
+        return -1;
+    }
+    *p = {vec, epp, np, nw, nw * (kWave / epp) * vec, lds};
+    return 1;
+}
+
 hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, const char **why) {
     if (static_cast<int64_t>(job.B) * job.H == 0)
         return hipSuccess;
     Plan p{};
-    if (!make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, cu_count(), &p)) {
+    const int forced = layout_override(job, &p, why);
+    if (forced < 0)
+        return hipErrorInvalidValue;
+    if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, cu_count(), &p)) {
         *why = "segment forward: shape outside the LDS-resident scan (needs (A*CS + A)*4 bytes <= 160 KiB for some "
                "slice width and top_k <= 128)";
         return hipErrorInvalidValue;
@@ -174,9 +215,9 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     geo.t_pad = scan_t_pad(job.T);
     geo.n_chunks = geo.t_pad / kChunk;
     switch (job.dtype) {
-        case kF32: return launch_scan_f32(job, geo, p.vec, p.epp, p.np, stream);
-        case kF16: return launch_scan_f16(job, geo, p.vec, p.epp, p.np, stream);
-        case kBF16: return launch_scan_bf16(job, geo, p.vec, p.epp, p.np, stream);
+        case kF32: return launch_scan_f32(job, geo, p.vec, p.epp, p.np, p.nw, stream);
+        case kF16: return launch_scan_f16(job, geo, p.vec, p.epp, p.np, p.nw, stream);
+        case kBF16: return launch_scan_bf16(job, geo, p.vec, p.epp, p.np, p.nw, stream);
         default: *why = "segment forward: unsupported dtype"; return hipErrorInvalidValue;
     }
 }

@@ -20,6 +20,8 @@
 #include "ramnet_device.hpp"
 #include "ramnet_kernels.hpp"
 
+#include <type_traits>
+
 namespace ramnet {
 
 constexpr int kChunk = kScanChunk;
@@ -192,18 +194,29 @@ __device__ __forceinline__ void store_act_vec(Scalar *p, const FVec<VEC> &r) {
 // Read in place of the mask when the caller passes none.
 __device__ const uint8_t kScanAllValid = 1;
 
-// Padded row stride of the LDS slot slice: spreads rows over banks and keeps
-// VEC-float alignment.
-template<int VEC, int CS>
-constexpr int scan_row_stride() {
-    return CS + (VEC == 1 ? 1 : VEC);
+// Row stride (floats) of the LDS slot slice: one pad float per row spreads
+// rows over banks; VEC-wide rows keep VEC-float alignment.
+constexpr int scan_row_stride(int vec, int cs) { return cs + (vec == 1 ? 1 : vec); }
+// Per-wave mass block: two dummy masses, A masses, then one sink float per
+// lane that takes the mass stores of lanes that do not own the event.
+constexpr int scan_mass_stride(int A) { return A + 2 + kWave; }
+
+// LDS bytes of a workgroup with NW waves of lane layout (vec, epp).
+inline size_t scan_lds_bytes(int A, int vec, int epp, int nw) {
+    const int cs = nw * (kWave / epp) * vec;
+    return (static_cast<size_t>(A + 2) * scan_row_stride(vec, cs) + static_cast<size_t>(nw) * scan_mass_stride(A)) * 4;
 }
 
-template<typename Scalar, int VEC, int EPP, int NP, bool MA, bool XV>
-__global__ __launch_bounds__(64) void segment_scan_kernel(const SegmentJob job, const ScanGeom geo) {
+// NW waves share one (b, h, CS-channel slice) unit: wave w owns channels
+// [w * CSW, (w + 1) * CSW) of the slice and walks the whole sequence on its
+// own (no barriers in the token loop), with its own copy of the slot masses.
+// FAST: C is a multiple of CS, so every lane owns VEC real channels.
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
+__global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJob job, const ScanGeom geo) {
     constexpr int LPE = kWave / EPP;
-    constexpr int CS = LPE * VEC;
-    constexpr int RS = scan_row_stride<VEC, CS>();
+    constexpr int CSW = LPE * VEC;
+    constexpr int CS = NW * CSW;
+    constexpr int RS = scan_row_stride(VEC, CS);
     extern __shared__ __align__(16) float lds[];
     // Workgroups are dealt round-robin to the 8 XCDs; give each XCD a
     // contiguous run of units so the slices of one (b, h) share an L2.
@@ -211,31 +224,34 @@ __global__ __launch_bounds__(64) void segment_scan_kernel(const SegmentJob job, 
     const int unit = static_cast<int>(blockIdx.x % 8) * per_xcd + static_cast<int>(blockIdx.x / 8);
     if (unit >= geo.n_units)
         return;
-    const int lane = threadIdx.x;
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
     const int bh = unit / geo.n_slices;
     const int c0 = (unit - bh * geo.n_slices) * CS;
     const int T = job.T, A = job.A, C = job.C, Kw = job.Kw, Kr = job.Kr, Tp = geo.t_pad;
+    const int MSW = scan_mass_stride(A);
     const float eps = job.eps;
 
-    // LDS: [dummy write row][dummy read row][A rows] x RS floats, then masses
-    // in the same order. st / ms point at slot 0.
+    // LDS: [dummy write row][dummy read row][A rows] x RS floats, then NW
+    // mass blocks. st points at slot 0; ms at this wave's mass of slot 0.
     float *st = lds + 2 * RS;
-    float *ms = lds + (A + 2) * RS + 2;
+    float *ms = lds + (A + 2) * RS + wave * MSW + 2;
 
-    const int ev = lane % EPP;  // event slot within a pass
-    const int cg = lane / EPP;  // channel group
-    const int cl = cg * VEC;    // first channel of this lane within the slice
+    const int ev = lane % EPP;                // event slot within a pass
+    const int cg = lane / EPP;                // channel group within the wave
+    const int cl = wave * CSW + cg * VEC;     // first channel of this lane within the slice
+    const int sink = A + lane;                // mass sink of this lane
 
-    // ---- state slice -> LDS
+    // ---- state slice -> LDS (whole workgroup), masses per wave
     {
         const float *src = job.init_slot + static_cast<int64_t>(bh) * A * C;
-        for (int i = lane; i < A * CS; i += kWave) {
+        for (int i = threadIdx.x; i < A * CS; i += kWave * NW) {
             const int a = i / CS, c = i - a * CS;
             const bool ok = c0 + c < C;
             const float v = src[static_cast<int64_t>(a) * C + (ok ? c0 + c : 0)];
             st[a * RS + c] = ok ? v : 0.f;
         }
-        for (int i = lane; i < 2 * RS; i += kWave)
+        for (int i = threadIdx.x; i < 2 * RS; i += kWave * NW)
             lds[i] = 0.f;
         const float *msrc = job.init_mass + static_cast<int64_t>(bh) * A;
         for (int a = lane; a < A; a += kWave)
@@ -259,9 +275,7 @@ __global__ __launch_bounds__(64) void segment_scan_kernel(const SegmentJob job, 
     }
     const Scalar *gx = static_cast<const Scalar *>(job.x) + static_cast<int64_t>(bh) * T * C;
     Scalar *gy = static_cast<Scalar *>(job.y) + static_cast<int64_t>(bh) * T * C;
-    const bool lane_ch = c0 + cl < C;                  // lane owns at least one real channel
-    const int xo = (XV ? (c0 + cl + VEC <= C) : lane_ch) ? c0 + cl : 0;  // clamped channel offset
-    const bool y_lane = ev == 0 && lane_ch;
+    const int xc = FAST ? c0 + cl : (c0 + cl < C ? c0 + cl : 0);  // clamped first channel
 
     struct Raw {
         int4 w[NP][kChunk];
@@ -284,11 +298,18 @@ __global__ __launch_bounds__(64) void segment_scan_kernel(const SegmentJob job, 
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
             const int t = t0 + j < T ? t0 + j : T - 1;
-            raw.x[j] = load_x_bits<Scalar, VEC, XV>(gx + static_cast<int64_t>(t) * C, XV ? xo : c0 + cl, C);
+            raw.x[j] = load_x_bits<Scalar, VEC, FAST>(gx + static_cast<int64_t>(t) * C, FAST ? xc : c0 + cl, C);
         }
     };
 
-    auto scan_chunk = [&](const Raw &cur, int t0) {
+    // One chunk of tokens. The body is one basic block when FAST and not
+    // TAIL: the mass store of lanes that do not own the event goes to their
+    // sink, and all EPP lanes of a channel group store the (bitwise equal)
+    // read sum to the same y elements, so no store is predicated and the
+    // scheduler can overlap one token's read phase with the next token's
+    // write phase.
+    auto scan_chunk = [&](const Raw &cur, int t0, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
             const FVec<VEC> xj = x_bits_to_f<Scalar, VEC>(cur.x[j]);
@@ -313,8 +334,7 @@ __global__ __launch_bounds__(64) void segment_scan_kernel(const SegmentJob job, 
                 for (int v = 0; v < VEC; ++v)
                     o.v[v] = fmaf(g, xj.v[v] - s[p].v[v], s[p].v[v]);
                 lds_store<VEC>(st + a * RS + cl, o);
-                if (cg == 0)
-                    ms[a] = m2;
+                ms[cg == 0 ? a : sink] = m2;
             }
             // reads of the post-write state
             FVec<VEC> acc;
@@ -349,16 +369,15 @@ __global__ __launch_bounds__(64) void segment_scan_kernel(const SegmentJob job, 
                     acc.v[v] *= scale;
             }
             const int t = t0 + j;
-            if (y_lane && t < T) {
-                Scalar *yp = gy + static_cast<int64_t>(t) * C + c0 + cl;
-                if constexpr (XV) {
+            Scalar *yp = gy + static_cast<int64_t>(t) * C + c0 + cl;
+            if constexpr (FAST) {
+                if (!TAIL || t < T)
                     store_act_vec<Scalar, VEC>(yp, acc);
-                } else {
+            } else if (t < T) {
 #pragma unroll
-                    for (int v = 0; v < VEC; ++v)
-                        if (c0 + cl + v < C)
-                            store_out(yp + v, acc.v[v]);
-                }
+                for (int v = 0; v < VEC; ++v)
+                    if (c0 + cl + v < C)
+                        store_out(yp + v, acc.v[v]);
             }
         }
     };
@@ -367,31 +386,41 @@ __global__ __launch_bounds__(64) void segment_scan_kernel(const SegmentJob job, 
     // flight while chunk ci runs, with no copy between the buffers. The chunk
     // count is even (T is padded to kScanPad), so every prefetch is issued
     // unconditionally -- a skipped prefetch would make the compiler's wait
-    // counts assume the worst at the join -- and the last one reloads the
-    // final chunk harmlessly.
+    // counts assume the worst at the join. Chunk pairs that lie wholly inside
+    // T run the branch-free body; the last pair, if it reaches past T, runs
+    // after the loop with guarded stores.
     const int nc = geo.n_chunks;
+    const int n_full = (T / kScanPad) * 2;  // chunks of whole pairs inside T
+    using Full = std::false_type;
+    using Tail = std::true_type;
     if (nc > 0) {
         Raw buf0, buf1;
         load(0, buf0);
-        for (int ci = 0; ci < nc; ci += 2) {
+        int ci = 0;
+        for (; ci < n_full; ci += 2) {
             load((ci + 1) * kChunk, buf1);
-            scan_chunk(buf0, ci * kChunk);
+            scan_chunk(buf0, ci * kChunk, Full{});
             load((ci + 2 < nc ? ci + 2 : nc - 1) * kChunk, buf0);
-            scan_chunk(buf1, (ci + 1) * kChunk);
+            scan_chunk(buf1, (ci + 1) * kChunk, Full{});
+        }
+        if (ci < nc) {
+            load((ci + 1) * kChunk, buf1);
+            scan_chunk(buf0, ci * kChunk, Tail{});
+            scan_chunk(buf1, (ci + 1) * kChunk, Tail{});
         }
     }
     __syncthreads();
 
-    // ---- LDS -> post state. Every slice of a (b, h) computes identical
-    // masses; slice 0 stores them.
+    // ---- LDS -> post state (whole workgroup). Every wave computes identical
+    // masses; wave 0 of slice 0 stores them.
     {
         float *dst = job.slot_out + static_cast<int64_t>(bh) * A * C;
-        for (int i = lane; i < A * CS; i += kWave) {
+        for (int i = threadIdx.x; i < A * CS; i += kWave * NW) {
             const int a = i / CS, c = i - a * CS;
             if (c0 + c < C)
                 dst[static_cast<int64_t>(a) * C + c0 + c] = st[a * RS + c];
         }
-        if (c0 == 0) {
+        if (c0 == 0 && wave == 0) {
             float *mdst = job.mass_out + static_cast<int64_t>(bh) * A;
             for (int a = lane; a < A; a += kWave)
                 mdst[a] = ms[a];
@@ -399,45 +428,50 @@ __global__ __launch_bounds__(64) void segment_scan_kernel(const SegmentJob job, 
     }
 }
 
-// LDS bytes of a unit with lane layout (vec, epp).
-inline size_t scan_lds_bytes(int A, int vec, int epp) {
-    const int cs = (kWave / epp) * vec;
-    const int rs = cs + (vec == 1 ? 1 : vec);
-    return (static_cast<size_t>(A + 2) * rs + A + 2) * 4;
-}
-
-template<typename Scalar, int VEC, int EPP, int NP, bool MA, bool XV>
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
 hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t stream) {
     const unsigned blocks = static_cast<unsigned>(((geo.n_units + 7) / 8) * 8);
-    hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, MA, XV>), dim3(blocks), dim3(kWave),
-                       scan_lds_bytes(job.A, VEC, EPP), stream, job, geo);
+    hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST>), dim3(blocks), dim3(kWave * NW),
+                       scan_lds_bytes(job.A, VEC, EPP, NW), stream, job, geo);
     return hipGetLastError();
 }
 
-// Lane layouts compiled for every activation dtype: (VEC, EPP, NP).
-#define RAMNET_SCAN_LAYOUTS(X) \
-    X(1, 4, 1) X(2, 4, 1) X(4, 4, 1) X(1, 8, 1) X(2, 8, 1) X(4, 8, 1) X(1, 16, 1) X(2, 16, 1) X(4, 16, 1) \
-    X(1, 32, 1) X(2, 32, 1) X(4, 32, 1) X(1, 64, 1) X(2, 64, 1) X(4, 64, 1) X(1, 64, 2) X(2, 64, 2) X(4, 64, 2)
+// Layouts compiled for every activation dtype: (VEC, EPP, NP, NW).
+#define RAMNET_SCAN_LAYOUTS(X)                                                                       \
+    X(1, 4, 1, 1) X(1, 8, 1, 1) X(1, 16, 1, 1) X(1, 32, 1, 1) X(1, 64, 1, 1) X(1, 64, 2, 1)         \
+    X(1, 8, 1, 2) X(1, 8, 1, 4) X(1, 8, 2, 1) X(1, 8, 2, 2) X(1, 8, 2, 4) X(1, 16, 1, 2) X(1, 16, 1, 4) \
+    X(2, 8, 1, 1) X(2, 8, 1, 2) X(2, 8, 1, 4) X(2, 16, 1, 1) X(2, 16, 1, 2)                          \
+    X(4, 8, 1, 1) X(4, 8, 1, 2) X(4, 16, 1, 1)
 
 template<typename Scalar>
-hipError_t scan_dispatch(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, hipStream_t stream) {
-    const bool xv = job.C % vec == 0;
-#define RAMNET_SCAN_CASE(V, E, N)                                                                   \
-    if (vec == V && epp == E && np == N) {                                                           \
+hipError_t scan_dispatch(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, int nw,
+                         hipStream_t stream) {
+    const int cs = nw * (kWave / epp) * vec;
+    const bool fast = job.C % cs == 0;
+#define RAMNET_SCAN_CASE(V, E, N, W)                                                                 \
+    if (vec == V && epp == E && np == N && nw == W) {                                                \
         if (job.mass_aware)                                                                          \
-            return xv ? launch_scan<Scalar, V, E, N, true, true>(job, geo, stream)                   \
-                      : launch_scan<Scalar, V, E, N, true, (V == 1)>(job, geo, stream);              \
-        return xv ? launch_scan<Scalar, V, E, N, false, true>(job, geo, stream)                      \
-                  : launch_scan<Scalar, V, E, N, false, (V == 1)>(job, geo, stream);                 \
+            return fast ? launch_scan<Scalar, V, E, N, W, true, true>(job, geo, stream)              \
+                        : launch_scan<Scalar, V, E, N, W, true, false>(job, geo, stream);            \
+        return fast ? launch_scan<Scalar, V, E, N, W, false, true>(job, geo, stream)                 \
+                    : launch_scan<Scalar, V, E, N, W, false, false>(job, geo, stream);               \
     }
     RAMNET_SCAN_LAYOUTS(RAMNET_SCAN_CASE)
 #undef RAMNET_SCAN_CASE
     return hipErrorInvalidValue;
 }
 
+// Whether (vec, epp, np, nw) is one of the compiled layouts.
+inline bool scan_layout_compiled(int vec, int epp, int np, int nw) {
+#define RAMNET_SCAN_HAS(V, E, N, W) if (vec == V && epp == E && np == N && nw == W) return true;
+    RAMNET_SCAN_LAYOUTS(RAMNET_SCAN_HAS)
+#undef RAMNET_SCAN_HAS
+    return false;
+}
+
 // One definition per activation dtype, each in its own translation unit.
-hipError_t launch_scan_f32(const SegmentJob &, const ScanGeom &, int, int, int, hipStream_t);
-hipError_t launch_scan_f16(const SegmentJob &, const ScanGeom &, int, int, int, hipStream_t);
-hipError_t launch_scan_bf16(const SegmentJob &, const ScanGeom &, int, int, int, hipStream_t);
+hipError_t launch_scan_f32(const SegmentJob &, const ScanGeom &, int, int, int, int, hipStream_t);
+hipError_t launch_scan_f16(const SegmentJob &, const ScanGeom &, int, int, int, int, hipStream_t);
+hipError_t launch_scan_bf16(const SegmentJob &, const ScanGeom &, int, int, int, int, hipStream_t);
 
 }  // namespace ramnet

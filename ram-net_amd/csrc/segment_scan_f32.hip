@@ -4,8 +4,9 @@
 
 namespace ramnet {
 
-hipError_t launch_scan_f32(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, hipStream_t stream) {
-    return scan_dispatch<float>(job, geo, vec, epp, np, stream);
+hipError_t launch_scan_f32(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, int nw,
+                          hipStream_t stream) {
+    return scan_dispatch<float>(job, geo, vec, epp, np, nw, stream);
 }
 
 }  // namespace ramnet

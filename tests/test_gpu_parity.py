@@ -197,6 +197,45 @@ def test_segment_scan_matches_oracle(case, dtype):
     assert err <= _out_tol(dtype), f"y rel err {err:.3e}"
 
 
+# Every compiled lane layout of the segment scan (vec, epp, np, nw), mirrored
+# from RAMNET_SCAN_LAYOUTS in segment_scan.hpp.
+SCAN_LAYOUTS = [
+    (1, 4, 1, 1), (1, 8, 1, 1), (1, 16, 1, 1), (1, 32, 1, 1), (1, 64, 1, 1), (1, 64, 2, 1),
+    (1, 8, 1, 2), (1, 8, 1, 4), (1, 8, 2, 1), (1, 8, 2, 2), (1, 8, 2, 4), (1, 16, 1, 2), (1, 16, 1, 4),
+    (2, 8, 1, 1), (2, 8, 1, 2), (2, 8, 1, 4), (2, 16, 1, 1), (2, 16, 1, 2),
+    (4, 8, 1, 1), (4, 8, 1, 2), (4, 16, 1, 1),
+]
+
+
+@pytest.mark.parametrize("partial", [False, True], ids=["full_slices", "partial_slice"])
+@pytest.mark.parametrize("layout", SCAN_LAYOUTS, ids=lambda l: "v{}e{}n{}w{}".format(*l))
+def test_segment_scan_every_layout(layout, partial, monkeypatch):
+    """Each layout, forced through RAMNET_SCAN_LAYOUT, against the fp64 sparse
+    oracle: top-K filling every event lane (writes) and all but one (reads),
+    a tail chunk pair (T = 45), and channel slices that are whole or end
+    inside C."""
+    vec, epp, np_, nw = layout
+    kmax = epp * np_
+    U, P = (4, 4) if kmax > 64 else (3, 4)
+    cs = nw * (64 // epp) * vec
+    C = 2 * cs + (0 if not partial else (-3 if cs > 3 else 1))  # partial: last slice ends inside C
+    Kw, Kr = kmax, max(1, kmax - 1)
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", ",".join(map(str, layout)))
+    for mass_aware, dtype, masked in ((False, torch.bfloat16, True), (True, torch.float32, False)):
+        print(f"layout {layout} C={C} K=({Kw},{Kr}) mass_aware={mass_aware} {dtype}", flush=True)
+        src, got, ref = _segment_case(2, 2, U, P, 45, C, Kw, Kr, dtype, masked, mass_aware, seed=sum(layout) + C)
+        y, slot, mass = got
+        ry, rslot, rmass = ref
+        ry = torch.as_tensor(ry)
+        if src.mask is not None:
+            assert bool((y[:, :, ~src.mask[0]] == 0).all()), "masked tokens must read 0"
+            y, ry = y[:, :, src.mask[0]], ry[:, :, src.mask[0]]
+        assert oracle.rel_err(slot, rslot) <= FP32_TOL, f"slot state, layout {layout}"
+        assert oracle.rel_err(mass, rmass) <= FP32_TOL, f"mass state, layout {layout}"
+        err = oracle.rel_err(y, ry)
+        assert err <= _out_tol(dtype), f"y rel err {err:.3e}, layout {layout}"
+
+
 @pytest.mark.parametrize("re_norm", [(0.0, 0.0), (1.0, 1.0), (0.25, 0.75)])
 def test_api_matches_dense_reference(re_norm):
     """random_access_memory_attention vs the dense restatement of the reference (config 1 shape)."""
