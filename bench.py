@@ -39,6 +39,9 @@ for _p in (os.path.join(REPO, "ram-net_amd"), REPO, os.path.join(REPO, "tests"))
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# Calibrated HBM bytes per segment-scan dispatch at config 2, from the
+# rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in profiles/.
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "segment_scan_traffic_c2.json")
 METRIC = "prefill tokens/s (T=4096) + decode tokens/s (B=64); % HBM roofline"
 
 # config 2 (prefill) and config 3 (decode)
@@ -323,6 +326,13 @@ def main(argv=None) -> int:
 
     if pre is not None:
         seg_gbs = pre["segment_bytes"] / (pre["segment_ms"] / 1e3) / 1e9
+        traffic = None
+        if os.path.exists(TRAFFIC_FILE):
+            with open(TRAFFIC_FILE) as f:
+                tr = json.load(f)
+            traffic = {"bytes": tr["traffic_bytes"], "kernel": tr["kernel"],
+                       "counter_gbs": tr["traffic_bytes"] / (pre["segment_ms"] / 1e3) / 1e9,
+                       "source": "profiles/segment_scan_traffic_c2.json"}
         out.update({
             "value": pre["tokens_per_s"],
             "unit": "tokens/s",
@@ -349,7 +359,8 @@ def main(argv=None) -> int:
                 "peak": HBM_PEAK_GBS,
                 "unit": "GB/s",
                 "frac": seg_gbs / HBM_PEAK_GBS,
-                "traffic": None,
+                "traffic": None if traffic is None else traffic["bytes"],
+                "traffic_detail": traffic,
                 "algorithmic_bytes": pre["segment_bytes"],
                 "kernel_ms": pre["segment_ms"],
             },

@@ -80,7 +80,7 @@ int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, 
 
 /*
  * Bytes of device workspace the segment scan needs for B x H heads, T tokens
- * and the given top-k (per-event records, T padded to 16). The 32-bit form
+ * and the given top-k (per-event records, T padded to 32). The 32-bit form
  * returns -1 when the size does not fit an int.
  */
 int ramnet_scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k);
