@@ -58,6 +58,8 @@ int cu_count() {
     return cached;
 }
 
+int dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
+
 struct Plan {
     int vec, epp, np, nw, cs;
     size_t lds;
@@ -70,7 +72,7 @@ struct Plan {
 // on one SIMD), whichever is longer. Total = rounds * per-token cycles.
 constexpr int64_t kChainCycles = 160;
 
-bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int n_cu, Plan *out) {
+bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, Plan *out) {
     const int kmax = std::max(Kw, Kr);
     if (kmax > 2 * kWave)
         return false;
@@ -86,7 +88,7 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int n_cu, Plan *out) 
                 if (!scan_layout_compiled(vec, epp, np, nw))
                     continue;
                 const int cs = nw * (kWave / epp) * vec;
-                const size_t lds = scan_lds_bytes(A, vec, epp, nw);
+                const size_t lds = scan_lds_bytes(A, vec, epp, np, nw, elem);
                 const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
                 if (gran > kLdsPerCu)
                     continue;
@@ -167,7 +169,7 @@ hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const cha
 
 int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes) {
     Plan p{};
-    if (!make_plan(8, 16, A, C, Kw, Kr, 256, &p))
+    if (!make_plan(8, 16, A, C, Kw, Kr, 2, 256, &p))
         return 0;
     if (cs)
         *cs = p.cs;
@@ -188,7 +190,7 @@ static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
         *why = "RAMNET_SCAN_LAYOUT names no compiled layout (vec,epp,np,nw)";
         return -1;
     }
-    const size_t lds = scan_lds_bytes(job.A, vec, epp, nw);
+    const size_t lds = scan_lds_bytes(job.A, vec, epp, np, nw, dtype_bytes(job.dtype));
     if (epp * np < std::max(job.Kw, job.Kr) || static_cast<int64_t>(lds) > kLdsPerCu) {
         *why = "RAMNET_SCAN_LAYOUT does not cover top_k or does not fit in LDS";
         return -1;
@@ -204,7 +206,7 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     const int forced = layout_override(job, &p, why);
     if (forced < 0)
         return hipErrorInvalidValue;
-    if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, cu_count(), &p)) {
+    if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, dtype_bytes(job.dtype), cu_count(), &p)) {
         *why = "segment forward: shape outside the LDS-resident scan (needs (A*CS + A)*4 bytes <= 160 KiB for some "
                "slice width and top_k <= 128)";
         return hipErrorInvalidValue;
@@ -213,7 +215,7 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     geo.n_slices = (job.C + p.cs - 1) / p.cs;
     geo.n_units = job.B * job.H * geo.n_slices;
     geo.t_pad = scan_t_pad(job.T);
-    geo.n_chunks = geo.t_pad / kChunk;
+    geo.n_chunks = (job.T + kChunk - 1) / kChunk;
     switch (job.dtype) {
         case kF32: return launch_scan_f32(job, geo, p.vec, p.epp, p.np, p.nw, stream);
         case kF16: return launch_scan_f16(job, geo, p.vec, p.epp, p.np, p.nw, stream);

@@ -1,20 +1,18 @@
 // Time-ordered segment scan kernel (gated sparse update + top-K read).
 //
-// One 64-lane wave owns one (b, h, channel slice) unit and walks the whole
-// sequence with the unit's A x CS slot slice and the slot masses resident in
-// LDS. The lane layout is fixed at compile time:
+// A workgroup of NW waves owns one (b, h, channel slice) unit and walks the
+// whole sequence with the unit's A x CS slot slice resident in LDS; each
+// wave owns CSW channels of the slice and keeps its own copy of the slot
+// masses. The lane layout is fixed at compile time:
 //   EPP events per pass (lane % EPP), LPE = 64 / EPP lanes per event,
-//   VEC channels per lane, CS = LPE * VEC channels per unit,
+//   VEC channels per lane, CSW = LPE * VEC channels per wave,
 //   NP passes cover up to NP * EPP write and NP * EPP read events per token.
 // Per-event records ({slot, w, alpha} for writes, {slot, r} for reads; see
-// ramnet_kernels.hpp) and the lane's x channels are loaded straight from
-// global memory into registers one kScanChunk-token chunk ahead of use, so
-// the token loop touches LDS only for the slot state. The chunk body is
-// fully unrolled and branch-free: events that must not act point at two
-// dummy LDS rows in front of the state (slot -2 for writes, -1 for reads),
-// so every load and store is unconditional. LDS executes a wave's accesses
-// in program order, which carries the read-modify-write dependency from one
-// token to the next.
+// ramnet_kernels.hpp) and x are staged per 16-token chunk through LDS.
+// Events that must not act point at two dummy LDS rows in front of the
+// state (slot -2 for writes, -1 for reads), so the token body is
+// branch-free. LDS executes a wave's accesses in program order, which
+// carries the read-modify-write dependency from one token to the next.
 #pragma once
 
 #include "ramnet_device.hpp"
@@ -29,8 +27,8 @@ constexpr int kChunk = kScanChunk;
 struct ScanGeom {
     int n_units;  // B * H * n_slices
     int n_slices; // ceil(C / CS)
-    int n_chunks; // T_pad / kChunk (even)
-    int t_pad;    // T rounded up to kScanPad
+    int n_chunks; // ceil(T / kChunk)
+    int t_pad;    // T rounded up to kScanPad (record row length)
 };
 
 // 1/d refined by one Newton step; gain = w / (m + eps) to ~1 ulp.
@@ -199,17 +197,33 @@ __device__ const uint8_t kScanAllValid = 1;
 constexpr int scan_row_stride(int vec, int cs) { return cs + (vec == 1 ? 1 : vec); }
 // Per-wave mass block: two dummy masses, A masses, then one sink float per
 // lane that takes the mass stores of lanes that do not own the event.
-constexpr int scan_mass_stride(int A) { return A + 2 + kWave; }
+__host__ __device__ constexpr int scan_mass_stride(int A) { return A + 2 + kWave; }
+// Staged x row of one channel: kChunk elements + 16 bytes of padding, which
+// keeps the 16-byte reads of neighbouring channels on disjoint banks.
+constexpr int scan_xrow_bytes(int elem) { return kChunk * elem + 16; }
 
-// LDS bytes of a workgroup with NW waves of lane layout (vec, epp).
-inline size_t scan_lds_bytes(int A, int vec, int epp, int nw) {
+// LDS bytes of a workgroup with NW waves of lane layout (vec, epp, np):
+// slot slice, NW mass blocks, then two chunk buffers of staged write
+// records, read records and x.
+__host__ __device__ constexpr size_t scan_stage_offset(int A, int rs, int nw) {
+    return ((static_cast<size_t>(A + 2) * rs + static_cast<size_t>(nw) * scan_mass_stride(A)) * 4 + 15) / 16 * 16;
+}
+inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem) {
     const int cs = nw * (kWave / epp) * vec;
-    return (static_cast<size_t>(A + 2) * scan_row_stride(vec, cs) + static_cast<size_t>(nw) * scan_mass_stride(A)) * 4;
+    const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs), nw);
+    const size_t stage = static_cast<size_t>(kChunk) * epp * np * (sizeof(WriteRec) + sizeof(ReadRec)) +
+                         static_cast<size_t>(cs) * scan_xrow_bytes(elem);
+    return state + 2 * stage;
 }
 
 // NW waves share one (b, h, CS-channel slice) unit: wave w owns channels
-// [w * CSW, (w + 1) * CSW) of the slice and walks the whole sequence on its
-// own (no barriers in the token loop), with its own copy of the slot masses.
+// [w * CSW, (w + 1) * CSW) of the slice and keeps its own copy of the slot
+// masses. Per 16-token chunk the workgroup loads the chunk's records and x
+// once -- each thread one or two unique elements -- into a double-buffered
+// LDS stage (one barrier per chunk), each lane then reads its event's
+// records and its channels' x from the stage in bulk, and the token loop
+// runs on registers and the LDS-resident state. Read sums are kept in
+// registers and stored once per chunk.
 // FAST: C is a multiple of CS, so every lane owns VEC real channels.
 template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
 __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJob job, const ScanGeom geo) {
@@ -217,6 +231,15 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
     constexpr int CSW = LPE * VEC;
     constexpr int CS = NW * CSW;
     constexpr int RS = scan_row_stride(VEC, CS);
+    constexpr int NT = kWave * NW;           // threads per workgroup
+    constexpr int E = EPP * NP;              // event lanes per token
+    constexpr int ES = static_cast<int>(sizeof(Scalar));
+    constexpr int XRB = scan_xrow_bytes(ES);  // staged x row bytes
+    constexpr int WI = (E * kChunk + NT - 1) / NT;   // staged write records per thread
+    constexpr int XI = (CS * kChunk + NT - 1) / NT;  // staged x elements per thread
+    constexpr int NSL = EPP <= kChunk ? kChunk / EPP : 1;  // tokens whose y a lane stores
+    using Bits = std::conditional_t<ES == 4, uint32_t, uint16_t>;
+
     extern __shared__ __align__(16) float lds[];
     // Workgroups are dealt round-robin to the 8 XCDs; give each XCD a
     // contiguous run of units so the slices of one (b, h) share an L2.
@@ -224,18 +247,28 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
     const int unit = static_cast<int>(blockIdx.x % 8) * per_xcd + static_cast<int>(blockIdx.x / 8);
     if (unit >= geo.n_units)
         return;
-    const int wave = static_cast<int>(threadIdx.x) / kWave;
-    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
     const int bh = unit / geo.n_slices;
     const int c0 = (unit - bh * geo.n_slices) * CS;
     const int T = job.T, A = job.A, C = job.C, Kw = job.Kw, Kr = job.Kr, Tp = geo.t_pad;
     const int MSW = scan_mass_stride(A);
     const float eps = job.eps;
 
-    // LDS: [dummy write row][dummy read row][A rows] x RS floats, then NW
-    // mass blocks. st points at slot 0; ms at this wave's mass of slot 0.
+    // LDS: [dummy write row][dummy read row][A rows] x RS floats, NW mass
+    // blocks, then the two stage buffers.
     float *st = lds + 2 * RS;
     float *ms = lds + (A + 2) * RS + wave * MSW + 2;
+    char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(A, RS, NW);
+    constexpr int kStageBytes = kChunk * E * static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec)) + CS * XRB;
+    auto stage_w = [&](int buf) { return reinterpret_cast<WriteRec *>(stage0 + buf * kStageBytes); };
+    auto stage_r = [&](int buf) {
+        return reinterpret_cast<ReadRec *>(stage0 + buf * kStageBytes + kChunk * E * sizeof(WriteRec));
+    };
+    auto stage_x = [&](int buf) {
+        return stage0 + buf * kStageBytes + kChunk * E * static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec));
+    };
 
     const int ev = lane % EPP;                // event slot within a pass
     const int cg = lane / EPP;                // channel group within the wave
@@ -245,13 +278,13 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
     // ---- state slice -> LDS (whole workgroup), masses per wave
     {
         const float *src = job.init_slot + static_cast<int64_t>(bh) * A * C;
-        for (int i = threadIdx.x; i < A * CS; i += kWave * NW) {
+        for (int i = tid; i < A * CS; i += NT) {
             const int a = i / CS, c = i - a * CS;
             const bool ok = c0 + c < C;
             const float v = src[static_cast<int64_t>(a) * C + (ok ? c0 + c : 0)];
             st[a * RS + c] = ok ? v : 0.f;
         }
-        for (int i = threadIdx.x; i < 2 * RS; i += kWave * NW)
+        for (int i = tid; i < 2 * RS; i += NT)
             lds[i] = 0.f;
         const float *msrc = job.init_mass + static_cast<int64_t>(bh) * A;
         for (int a = lane; a < A; a += kWave)
@@ -259,80 +292,125 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
         if (lane < 2)
             ms[lane - 2] = 1.f;
     }
-    __syncthreads();
 
-    // per-lane record rows; lanes beyond top-K read the no-op chunk
-    const WriteRec *wbase[NP];
-    const ReadRec *rbase[NP];
-    bool wreal[NP], rreal[NP];
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        const int e = p * EPP + ev;
-        wreal[p] = e < Kw;
-        rreal[p] = e < Kr;
-        wbase[p] = job.wrec + (static_cast<int64_t>(bh) * Kw + (wreal[p] ? e : 0)) * Tp;
-        rbase[p] = job.rrec + (static_cast<int64_t>(bh) * Kr + (rreal[p] ? e : 0)) * Tp;
-    }
+    // ---- chunk staging: global -> registers (start of the previous chunk),
+    // registers -> LDS (end of the previous chunk)
+    const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * Tp;
+    const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * Tp;
     const Scalar *gx = static_cast<const Scalar *>(job.x) + static_cast<int64_t>(bh) * T * C;
     Scalar *gy = static_cast<Scalar *>(job.y) + static_cast<int64_t>(bh) * T * C;
-    const int xc = FAST ? c0 + cl : (c0 + cl < C ? c0 + cl : 0);  // clamped first channel
-
-    struct Raw {
-        int4 w[NP][kChunk];
-        int2 r[NP][kChunk];
-        XBits<Scalar, VEC> x[kChunk];
+    struct Staged {
+        int4 w[WI];
+        int2 r[WI];
+        Bits x[XI];
     };
-    // Lanes beyond top-K read the no-op chunk at the end of the workspace;
-    // both candidates derive from kernel arguments, so the loads stay global.
-    auto load = [&](int t0, Raw &raw) {
+    // Items past the end are clamped to the last item, so the threads that
+    // hold them load and store identical data: fetch and deposit stay
+    // branch-free, which keeps the compiler's memory wait counts exact.
+    auto fetch = [&](int t0, Staged &sg) {
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const WriteRec *wp = wreal[p] ? wbase[p] + t0 : job.noop_w;
-            const ReadRec *rp = rreal[p] ? rbase[p] + t0 : job.noop_r;
+        for (int k = 0; k < WI; ++k) {
+            const int it = min(tid + k * NT, E * kChunk - 1);
+            const int e = it / kChunk, j = it % kChunk;
+            const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
+            sg.w[k] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ew) * Tp + t0 + j);
+            sg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
+        }
 #pragma unroll
-            for (int j = 0; j < kChunk; ++j) {
-                raw.w[p][j] = *reinterpret_cast<const int4 *>(wp + j);
-                raw.r[p][j] = *reinterpret_cast<const int2 *>(rp + j);
+        for (int k = 0; k < XI; ++k) {
+            const int it = min(tid + k * NT, CS * kChunk - 1);
+            const int j = it / CS, c = it % CS;
+            const int t = t0 + j < T ? t0 + j : T - 1;
+            const int ch = c0 + c < C ? c0 + c : C - 1;
+            sg.x[k] = *reinterpret_cast<const Bits *>(gx + static_cast<int64_t>(t) * C + ch);
+        }
+    };
+    auto deposit = [&](int buf, const Staged &sg) {
+        WriteRec *sw = stage_w(buf);
+        ReadRec *sr = stage_r(buf);
+        char *sx = stage_x(buf);
+#pragma unroll
+        for (int k = 0; k < WI; ++k) {
+            const int it = min(tid + k * NT, E * kChunk - 1);
+            const int e = it / kChunk, j = it % kChunk;
+            const bool wl = e < Kw, rl = e < Kr;  // events past top-K get no-op records
+            const int4 w = make_int4(wl ? sg.w[k].x : -2, wl ? sg.w[k].y : 0, wl ? sg.w[k].z : __float_as_int(1.f), 0);
+            const int2 r = make_int2(rl ? sg.r[k].x : -1, rl ? sg.r[k].y : 0);
+            *reinterpret_cast<int4 *>(sw + j * E + e) = w;
+            *reinterpret_cast<int2 *>(sr + j * E + e) = r;
+        }
+#pragma unroll
+        for (int k = 0; k < XI; ++k) {
+            const int it = min(tid + k * NT, CS * kChunk - 1);
+            const int j = it / CS, c = it % CS;
+            *reinterpret_cast<Bits *>(sx + c * XRB + j * ES) = sg.x[k];
+        }
+    };
+
+    // One chunk: bulk-read this lane's records and x from the stage, then
+    // the token loop. The token body is branch-free: the mass store of lanes
+    // that do not own the event goes to their sink, and each lane keeps the
+    // read sum of the tokens whose y it stores. TAIL guards tokens past T.
+    auto scan_chunk = [&](int buf, int t0, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        const WriteRec *sw = stage_w(buf);
+        const ReadRec *sr = stage_r(buf);
+        const char *sx = stage_x(buf);
+        int4 wrec[NP][kChunk];
+        int2 rrec[NP][kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                wrec[p][j] = *reinterpret_cast<const int4 *>(sw + j * E + p * EPP + ev);
+                rrec[p][j] = *reinterpret_cast<const int2 *>(sr + j * E + p * EPP + ev);
             }
         }
+        constexpr int XW = kChunk * ES / 16;  // 16-byte words per staged channel row
+        uint4 xr[VEC][XW];
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            const int t = t0 + j < T ? t0 + j : T - 1;
-            raw.x[j] = load_x_bits<Scalar, VEC, FAST>(gx + static_cast<int64_t>(t) * C, FAST ? xc : c0 + cl, C);
-        }
-    };
+        for (int v = 0; v < VEC; ++v)
+#pragma unroll
+            for (int q = 0; q < XW; ++q)
+                xr[v][q] = *reinterpret_cast<const uint4 *>(sx + (cl + v) * XRB + q * 16);
+        auto x_at = [&](int v, int j) -> float {
+            const uint4 q4 = xr[v][(j * ES) / 16];
+            const int wi = ((j * ES) % 16) / 4;
+            const uint32_t wd = wi == 0 ? q4.x : wi == 1 ? q4.y : wi == 2 ? q4.z : q4.w;
+            if constexpr (ES == 4)
+                return __uint_as_float(wd);
+            else
+                return half_bits_to_f<Scalar>((wd >> (16 * (j % 2))) & 0xffffu);
+        };
 
-    // One chunk of tokens. The body is one basic block when FAST and not
-    // TAIL: the mass store of lanes that do not own the event goes to their
-    // sink, and all EPP lanes of a channel group store the (bitwise equal)
-    // read sum to the same y elements, so no store is predicated and the
-    // scheduler can overlap one token's read phase with the next token's
-    // write phase.
-    auto scan_chunk = [&](const Raw &cur, int t0, auto tail_tag) {
-        constexpr bool TAIL = decltype(tail_tag)::value;
+        FVec<VEC> ykeep[NSL];
+#pragma unroll
+        for (int q = 0; q < NSL; ++q)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+                ykeep[q].v[v] = 0.f;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
-            const FVec<VEC> xj = x_bits_to_f<Scalar, VEC>(cur.x[j]);
             // writes: read-modify-write of the slot rows and masses
             float m[NP];
             FVec<VEC> s[NP];
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                const int a = cur.w[p][j].x;
+                const int a = wrec[p][j].x;
                 m[p] = ms[a];
                 s[p] = lds_load<VEC>(st + a * RS + cl);
             }
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                const int a = cur.w[p][j].x;
-                const float w = __int_as_float(cur.w[p][j].y);
-                const float al = __int_as_float(cur.w[p][j].z);
+                const int a = wrec[p][j].x;
+                const float w = __int_as_float(wrec[p][j].y);
+                const float al = __int_as_float(wrec[p][j].z);
                 const float m2 = fmaf(al, m[p], w);
                 const float g = scan_gain(w, m2 + eps);
                 FVec<VEC> o;
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
-                    o.v[v] = fmaf(g, xj.v[v] - s[p].v[v], s[p].v[v]);
+                    o.v[v] = fmaf(g, x_at(v, j) - s[p].v[v], s[p].v[v]);
                 lds_store<VEC>(st + a * RS + cl, o);
                 ms[cg == 0 ? a : sink] = m2;
             }
@@ -341,15 +419,15 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
                 acc.v[v] = 0.f;
-            float sr = 0.f, srm = 0.f;
+            float sr_ = 0.f, srm = 0.f;
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                const int a = cur.r[p][j].x;
-                const float r = __int_as_float(cur.r[p][j].y);
+                const int a = rrec[p][j].x;
+                const float r = __int_as_float(rrec[p][j].y);
                 float wgt = r;
                 if constexpr (MA) {
                     wgt = r * ms[a];
-                    sr += r;
+                    sr_ += r;
                     srm += wgt;
                 }
                 const FVec<VEC> rv = lds_load<VEC>(st + a * RS + cl);
@@ -361,61 +439,74 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
             for (int v = 0; v < VEC; ++v)
                 acc.v[v] = group_sum<EPP>(acc.v[v]);
             if constexpr (MA) {
-                sr = group_sum<EPP>(sr);
+                sr_ = group_sum<EPP>(sr_);
                 srm = group_sum<EPP>(srm);
-                const float scale = sr / (srm + eps);
+                const float scale = sr_ / (srm + eps);
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
                     acc.v[v] *= scale;
             }
+            // keep the sum in the lanes that store token j
+            const bool mine = EPP <= kChunk ? ev == j % EPP : ev % kChunk == j;
+            const int q = EPP <= kChunk ? j / EPP : 0;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+                ykeep[q].v[v] = mine ? acc.v[v] : ykeep[q].v[v];
+        }
+        // y of this chunk: lane stores tokens q * EPP + ev (or ev % 16)
+#pragma unroll
+        for (int q = 0; q < NSL; ++q) {
+            const int j = EPP <= kChunk ? q * EPP + ev : ev % kChunk;
             const int t = t0 + j;
             Scalar *yp = gy + static_cast<int64_t>(t) * C + c0 + cl;
             if constexpr (FAST) {
                 if (!TAIL || t < T)
-                    store_act_vec<Scalar, VEC>(yp, acc);
+                    store_act_vec<Scalar, VEC>(yp, ykeep[q]);
             } else if (t < T) {
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
                     if (c0 + cl + v < C)
-                        store_out(yp + v, acc.v[v]);
+                        store_out(yp + v, ykeep[q].v[v]);
             }
         }
     };
 
-    // Two register buffers in alternation: the loads of chunk ci + 1 are in
-    // flight while chunk ci runs, with no copy between the buffers. The chunk
-    // count is even (T is padded to kScanPad), so every prefetch is issued
-    // unconditionally -- a skipped prefetch would make the compiler's wait
-    // counts assume the worst at the join. Chunk pairs that lie wholly inside
-    // T run the branch-free body; the last pair, if it reaches past T, runs
-    // after the loop with guarded stores.
-    const int nc = geo.n_chunks;
-    const int n_full = (T / kScanPad) * 2;  // chunks of whole pairs inside T
+    // Chunks wholly inside T run the unguarded body; at most one chunk at
+    // the end reaches past T. The next chunk's loads are issued before the
+    // current chunk runs and deposited into the other stage buffer after it.
     using Full = std::false_type;
     using Tail = std::true_type;
+    const int nc = geo.n_chunks;
+    const int n_full = T / kChunk;
+    Staged sg;
     if (nc > 0) {
-        Raw buf0, buf1;
-        load(0, buf0);
-        int ci = 0;
-        for (; ci < n_full; ci += 2) {
-            load((ci + 1) * kChunk, buf1);
-            scan_chunk(buf0, ci * kChunk, Full{});
-            load((ci + 2 < nc ? ci + 2 : nc - 1) * kChunk, buf0);
-            scan_chunk(buf1, (ci + 1) * kChunk, Full{});
-        }
-        if (ci < nc) {
-            load((ci + 1) * kChunk, buf1);
-            scan_chunk(buf0, ci * kChunk, Tail{});
-            scan_chunk(buf1, (ci + 1) * kChunk, Tail{});
-        }
+        fetch(0, sg);
+        deposit(0, sg);
     }
     __syncthreads();
+    int ci = 0;
+    for (; ci < n_full; ++ci) {
+        // scheduling fences keep the loads at the top and their use at the
+        // bottom, so a whole chunk of work covers their latency
+        fetch((ci + 1 < nc ? ci + 1 : nc - 1) * kChunk, sg);
+        __builtin_amdgcn_sched_barrier(0);
+        scan_chunk(ci & 1, ci * kChunk, Full{});
+        __builtin_amdgcn_sched_barrier(0);
+        deposit((ci + 1) & 1, sg);
+        __syncthreads();
+    }
+    for (; ci < nc; ++ci) {
+        fetch((ci + 1 < nc ? ci + 1 : nc - 1) * kChunk, sg);
+        scan_chunk(ci & 1, ci * kChunk, Tail{});
+        deposit((ci + 1) & 1, sg);
+        __syncthreads();
+    }
 
     // ---- LDS -> post state (whole workgroup). Every wave computes identical
     // masses; wave 0 of slice 0 stores them.
     {
         float *dst = job.slot_out + static_cast<int64_t>(bh) * A * C;
-        for (int i = threadIdx.x; i < A * CS; i += kWave * NW) {
+        for (int i = tid; i < A * CS; i += NT) {
             const int a = i / CS, c = i - a * CS;
             if (c0 + c < C)
                 dst[static_cast<int64_t>(a) * C + c0 + c] = st[a * RS + c];
@@ -432,7 +523,7 @@ template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
 hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t stream) {
     const unsigned blocks = static_cast<unsigned>(((geo.n_units + 7) / 8) * 8);
     hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST>), dim3(blocks), dim3(kWave * NW),
-                       scan_lds_bytes(job.A, VEC, EPP, NW), stream, job, geo);
+                       scan_lds_bytes(job.A, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar))), stream, job, geo);
     return hipGetLastError();
 }
 
