@@ -1,0 +1,296 @@
+// Per-lane Product-Softmax top-K search on packed sort keys.
+//
+// One lane decodes one address. Candidates are ordered by (score desc,
+// content index asc); both parts are packed into one unsigned key so that a
+// compare-exchange is a max/min pair:
+//   digit keys      16-bit inputs: ord16(logit) << 16 | (0xFFFF - digit)
+//                   fp32 inputs:   ord32(logit) << 32 | (0xFFFFFFFF - digit)
+//   prefix keys     ord32(score) << 32 | (0xFFFFFFFF - content index)
+// where ord maps a float's bits to an unsigned integer with the same order
+// (-0 is folded onto +0 first so that equal values compare equal). Within a
+// digit, log_softmax is a monotone shift of the logits, so ordering by logit
+// orders by log-probability. Key 0 marks "no candidate".
+//
+// Search (U digits, top-KM lists): the sorted top-KM of each digit is
+// combined with the sorted top-KM prefix list over the staircase
+// (i + 1)(j + 1) <= KM of prefix i x digit j -- every element outside it has
+// at least KM elements before it in both orders -- and the top-KM of those
+// candidates becomes the next prefix.
+#pragma once
+
+#include "ramnet_device.hpp"
+
+#include <stdint.h>
+#include <type_traits>
+
+namespace ramnet {
+
+__device__ __forceinline__ uint32_t ord16(uint32_t h) {
+    h = h == 0x8000u ? 0u : h;
+    return (h & 0x8000u) ? (~h & 0xFFFFu) : (h | 0x8000u);
+}
+__device__ __forceinline__ uint32_t unord16(uint32_t o) { return (o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu); }
+__device__ __forceinline__ uint32_t ord32(uint32_t u) {
+    u = u == 0x80000000u ? 0u : u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ uint32_t unord32(uint32_t o) { return (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o; }
+
+// Descending compare-exchange: a gets the larger key.
+__device__ __forceinline__ void ce_desc(uint32_t &a, uint32_t &b) {
+    const uint32_t hi = a > b ? a : b;
+    const uint32_t lo = a > b ? b : a;
+    a = hi;
+    b = lo;
+}
+__device__ __forceinline__ void ce_desc(uint64_t &a, uint64_t &b) {
+    const bool sw = b > a;
+    const uint64_t t = a;
+    a = sw ? b : a;
+    b = sw ? t : b;
+}
+
+// Bitonic sort (descending) of keys [OFF, OFF + N); N a power of two.
+template<int N, int OFF, typename K, int M>
+__device__ __forceinline__ void sort_desc(K (&k)[M]) {
+#pragma unroll
+    for (int kk = 2; kk <= N; kk <<= 1) {
+#pragma unroll
+        for (int j = kk >> 1; j > 0; j >>= 1) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const int l = i ^ j;
+                if (l > i) {
+                    if ((i & kk) == 0)
+                        ce_desc(k[OFF + i], k[OFF + l]);
+                    else
+                        ce_desc(k[OFF + l], k[OFF + i]);
+                }
+            }
+        }
+    }
+}
+
+// a <- sorted top-KM of sorted a and the sorted group [OFF, OFF + KM) of b.
+template<int KM, int OFF, typename K, int M>
+__device__ __forceinline__ void merge_top(K (&a)[KM], const K (&b)[M]) {
+#pragma unroll
+    for (int i = 0; i < KM; ++i) {
+        const K x = b[OFF + KM - 1 - i];
+        a[i] = a[i] > x ? a[i] : x;
+    }
+#pragma unroll
+    for (int j = KM >> 1; j > 0; j >>= 1) {
+#pragma unroll
+        for (int i = 0; i < KM; ++i) {
+            const int l = i ^ j;
+            if (l > i)
+                ce_desc(a[i], a[l]);
+        }
+    }
+}
+
+template<int KM, int G, int NG, typename K, int N>
+__device__ __forceinline__ void sort_groups_desc(K (&k)[N]) {
+    if constexpr (G < NG) {
+        sort_desc<KM, G * KM>(k);
+        sort_groups_desc<KM, G + 1, NG>(k);
+    }
+}
+template<int KM, int G, int NG, typename K, int N>
+__device__ __forceinline__ void merge_groups(K (&top)[KM], const K (&k)[N]) {
+    if constexpr (G < NG) {
+        merge_top<KM, G * KM>(top, k);
+        merge_groups<KM, G + 1, NG>(top, k);
+    }
+}
+
+// Sorted top-KM of N keys (N a multiple of KM, or N <= KM).
+template<int KM, typename K, int N>
+__device__ __forceinline__ void top_keys(K (&k)[N], K (&top)[KM]) {
+    if constexpr (N <= KM) {
+        sort_desc<N, 0>(k);
+#pragma unroll
+        for (int i = 0; i < KM; ++i)
+            top[i] = i < N ? k[i < N ? i : 0] : K(0);
+    } else {
+        static_assert(N % KM == 0, "key count must be a multiple of KM");
+        sort_groups_desc<KM, 0, N / KM>(k);
+#pragma unroll
+        for (int i = 0; i < KM; ++i)
+            top[i] = k[i];
+        merge_groups<KM, 1, N / KM>(top, k);
+    }
+}
+
+// Staircase (i + 1)(j + 1) <= KM: candidate count and the (i, j) of entry n.
+template<int KM>
+constexpr int stair_count() {
+    int n = 0;
+    for (int i = 0; i < KM; ++i)
+        n += KM / (i + 1);
+    return n;
+}
+template<int KM>
+constexpr int stair_i(int n) {
+    for (int i = 0; i < KM; ++i) {
+        if (n < KM / (i + 1))
+            return i;
+        n -= KM / (i + 1);
+    }
+    return 0;
+}
+template<int KM>
+constexpr int stair_j(int n) {
+    for (int i = 0; i < KM; ++i) {
+        if (n < KM / (i + 1))
+            return n;
+        n -= KM / (i + 1);
+    }
+    return 0;
+}
+
+template<typename Scalar>
+using DigitKey = std::conditional_t<sizeof(Scalar) == 2, uint32_t, uint64_t>;
+
+template<typename Scalar>
+__device__ __forceinline__ uint32_t raw_bits(const Scalar *p) {
+    if constexpr (sizeof(Scalar) == 2)
+        return *reinterpret_cast<const uint16_t *>(p);
+    else
+        return *reinterpret_cast<const uint32_t *>(p);
+}
+template<typename Scalar>
+__device__ __forceinline__ float bits_value(uint32_t b) {
+    if constexpr (sizeof(Scalar) == 4)
+        return __uint_as_float(b);
+    else if constexpr (__is_same(Scalar, bf16_t))
+        return __uint_as_float(b << 16);
+    else
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+template<typename Scalar>
+__device__ __forceinline__ DigitKey<Scalar> digit_key(uint32_t bits, int p) {
+    if constexpr (sizeof(Scalar) == 2)
+        return (ord16(bits) << 16) | (0xFFFFu - static_cast<uint32_t>(p));
+    else
+        return (static_cast<uint64_t>(ord32(bits)) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(p));
+}
+template<typename Scalar>
+__device__ __forceinline__ void digit_unkey(DigitKey<Scalar> k, float &x, int &p) {
+    if constexpr (sizeof(Scalar) == 2) {
+        x = bits_value<Scalar>(unord16(k >> 16));
+        p = static_cast<int>(0xFFFFu - (k & 0xFFFFu));
+    } else {
+        x = __uint_as_float(unord32(static_cast<uint32_t>(k >> 32)));
+        p = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(k));
+    }
+}
+
+__device__ __forceinline__ uint64_t prefix_key(float s, int c) {
+    return (static_cast<uint64_t>(ord32(__float_as_uint(s))) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(c));
+}
+
+// One digit: sorted top-KM log-probabilities (lv) and digit values (dv),
+// valid flags; returns false when every logit of the digit is -inf.
+template<typename Scalar, int NP, int KM>
+__device__ __forceinline__ bool digit_top(const Scalar *row, int64_t stride, int P, float (&lv)[KM], int (&dv)[KM],
+                                          bool (&ok)[KM]) {
+    using K = DigitKey<Scalar>;
+    K keys[NP];
+    float x[NP];
+    // All loads first, unconditional: the pointer walks the P logits of the
+    // digit and stays on the last one for the padding. A guarded load or a
+    // branch on P would wait for each load's data before issuing the next.
+    const char *ptr = reinterpret_cast<const char *>(row);
+    const int64_t step = stride * static_cast<int64_t>(sizeof(Scalar));
+    uint32_t bits[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        bits[p] = raw_bits<Scalar>(reinterpret_cast<const Scalar *>(ptr));
+        ptr += p + 1 < P ? step : 0;
+    }
+    // padding keys are masked to 0 arithmetically (no branch)
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        x[p] = bits_value<Scalar>(bits[p]);
+        const K live = p < P ? ~K(0) : K(0);
+        keys[p] = digit_key<Scalar>(bits[p], p) & live;
+    }
+    K top[KM];
+    top_keys<KM>(keys, top);
+    float mx;
+    int p0;
+    digit_unkey<Scalar>(top[0], mx, p0);
+    const bool live = mx > -__builtin_huge_valf();
+    // log-sum-exp around the maximum; exp2 of a prescaled argument, summed
+    // with a fixed pairwise tree (padding contributes exact zeros)
+    constexpr float kLog2e = 1.4426950408889634f;
+    float e[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+            e[p] = __builtin_amdgcn_exp2f((x[p] - mx) * kLog2e) * (p < P ? 1.f : 0.f);
+#pragma unroll
+    for (int s = NP / 2; s >= 1; s >>= 1)
+#pragma unroll
+        for (int p = 0; p < s; ++p)
+            e[p] += e[p + s];
+    const float ls = logf(e[0]);
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+        float xv;
+        int p;
+        digit_unkey<Scalar>(top[k], xv, p);
+        ok[k] = top[k] != K(0);
+        lv[k] = (xv - mx) - ls;
+        dv[k] = p;
+    }
+    return live;
+}
+
+// Prefix (score sv, content cv) x digit (lv, dv) over the staircase ->
+// sorted top-KM new prefix. `stride` is P^u of the digit.
+template<int KM>
+__device__ __forceinline__ void combine_prefix(float (&sv)[KM], int (&cv)[KM], bool (&ok)[KM], const float (&lv)[KM],
+                                               const int (&dv)[KM], const bool (&dok)[KM], int stride) {
+    constexpr int NC = stair_count<KM>();
+    constexpr int NG = (NC + KM - 1) / KM * KM;
+    uint64_t cand[NG];
+#pragma unroll
+    for (int n = 0; n < NG; ++n) {
+        if (n < NC) {
+            const int i = stair_i<KM>(n), j = stair_j<KM>(n);
+            cand[n] = (ok[i] && dok[j]) ? prefix_key(sv[i] + lv[j], cv[i] + stride * dv[j]) : uint64_t(0);
+        } else {
+            cand[n] = 0;
+        }
+    }
+    uint64_t top[KM];
+    top_keys<KM>(cand, top);
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+        ok[k] = top[k] != 0;
+        sv[k] = __uint_as_float(unord32(static_cast<uint32_t>(top[k] >> 32)));
+        cv[k] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(top[k]));
+    }
+}
+
+// Full search of one address: sorted top-KM (score, content index, valid)
+// over all U digits. Returns false if any digit is all -inf (inactive).
+template<typename Scalar, int NP, int KM>
+__device__ __forceinline__ bool lane_search(const Scalar *base, int64_t T, int U, int P, float (&sv)[KM],
+                                            int (&cv)[KM], bool (&ok)[KM]) {
+    bool live = digit_top<Scalar, NP, KM>(base, T, P, sv, cv, ok);
+    int stride = P;
+    for (int u = 1; u < U; ++u) {
+        float lv[KM];
+        int dv[KM];
+        bool dok[KM];
+        live = digit_top<Scalar, NP, KM>(base + static_cast<int64_t>(u) * P * T, T, P, lv, dv, dok) && live;
+        combine_prefix<KM>(sv, cv, ok, lv, dv, dok, stride);
+        stride *= P;
+    }
+    return live;
+}
+
+}  // namespace ramnet

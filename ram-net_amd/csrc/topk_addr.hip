@@ -11,17 +11,18 @@
 //   an address with any all -inf digit is inactive: val = 0.
 //
 // Two kernels:
-//  * topk_addr_lane_kernel: one lane per (b, h, t) address. Per digit the P
-//    log-probabilities are sorted in registers with a bitonic network and the
-//    running top-K prefix list is merged column by column
-//    (prefix_i + digit_j for every j), so the search never materialises the
-//    A = P^U scores. Used for P <= 64, K <= 16.
+//  * topk_addr_lane_kernel: one lane per (b, h, t) address (lane_search.hpp):
+//    per digit the top-K logits are selected on packed (value, index) sort
+//    keys, and the running top-K prefix list is combined with each digit
+//    over the staircase of candidates that can reach the top K, so the
+//    search never materialises the A = P^U scores. Used for P <= 64, K <= 16.
 //  * topk_addr_bruteforce_kernel: one workgroup per address materialises all
 //    A scores in LDS and bitonic-sorts them; exact for every K <= A.
 //    Used for the shapes the lane kernel does not cover (A <= 8192).
 #include "ramnet_device.hpp"
 #include "ramnet_kernels.hpp"
 #include "ramnet_search.hpp"
+#include "lane_search.hpp"
 
 #include <math.h>
 
@@ -30,58 +31,6 @@ namespace ramnet {
 namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
-
-// Sorted top-KM of one digit's NP (padded) log-probabilities.
-template<int NP, int KM, int G = 0>
-__device__ __forceinline__ void sort_groups(float (&v)[NP], int (&id)[NP]) {
-    if constexpr (G * KM < NP) {
-        bitonic_sort<KM, G * KM>(v, id);
-        sort_groups<NP, KM, G + 1>(v, id);
-    }
-}
-
-template<int NP, int KM>
-__device__ __forceinline__ void digit_topk(float (&v)[NP], int (&id)[NP], float (&dv)[KM], int (&di)[KM]) {
-    if constexpr (NP <= KM) {
-        bitonic_sort<NP, 0>(v, id);
-#pragma unroll
-        for (int k = 0; k < KM; ++k) {
-            dv[k] = k < NP ? v[k < NP ? k : 0] : kNegInf;
-            di[k] = k < NP ? id[k < NP ? k : 0] : kNoIdx;
-        }
-    } else {
-        sort_groups<NP, KM>(v, id);
-#pragma unroll
-        for (int k = 0; k < KM; ++k) {
-            dv[k] = v[k];
-            di[k] = id[k];
-        }
-#pragma unroll
-        for (int g = 1; g < NP / KM; ++g) {
-            float tv[KM];
-            int ti[KM];
-#pragma unroll
-            for (int k = 0; k < KM; ++k) {
-                tv[k] = v[g * KM + k];
-                ti[k] = id[g * KM + k];
-            }
-            merge_topk(dv, di, tv, ti);
-        }
-    }
-}
-
-// Column j of the prefix x digit candidate grid: prefix_i + digit_j, which is
-// sorted in i because the prefix list is.
-template<int KM>
-__device__ __forceinline__ void build_column(const float (&mv)[KM], const int (&mi)[KM], float dvj, int dij, int stride,
-                                             float (&cv)[KM], int (&ci)[KM]) {
-#pragma unroll
-    for (int i = 0; i < KM; ++i) {
-        const bool ok = mi[i] != kNoIdx && dij != kNoIdx;
-        cv[i] = ok ? mv[i] + dvj : kNegInf;
-        ci[i] = ok ? mi[i] + stride * dij : kNoIdx;
-    }
-}
 
 __device__ const uint8_t kAddrAllValid = 1;
 
@@ -145,69 +94,10 @@ __global__ __launch_bounds__(256) void topk_addr_lane_kernel(const AddrJob job) 
     const int b = static_cast<int>(bh / H);
     const Scalar *base = static_cast<const Scalar *>(src.addr) + bh * static_cast<int64_t>(U * P) * T + tl;
 
-    float mv[KM];
-    int mi[KM];
-    bool inactive = false;
-    int stride = 1;
-    for (int u = 0; u < U; ++u) {
-        float v[NP];
-        int id[NP];
-        bool all_ninf = true;
-        float mx = kNegInf;
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            // unconditional load from a clamped radix (a guarded load would
-            // wait for its data inside the branch)
-            const float raw = load_f32(base + static_cast<int64_t>(u * P + (p < P ? p : P - 1)) * T);
-            v[p] = p < P ? raw : kNegInf;
-            id[p] = p < P ? p : kNoIdx;
-            all_ninf = all_ninf && (p >= P || v[p] == kNegInf);
-            mx = fmaxf(mx, v[p]);
-        }
-        inactive = inactive || all_ninf;
-        // log-softmax; the exponentials are summed with a fixed pairwise tree
-        // (padding lanes contribute exact zeros).
-        float e[NP];
-#pragma unroll
-        for (int p = 0; p < NP; ++p)
-            e[p] = p < P ? expf(v[p] - mx) : 0.f;
-#pragma unroll
-        for (int s = NP / 2; s >= 1; s >>= 1) {
-#pragma unroll
-            for (int p = 0; p < s; ++p)
-                e[p] += e[p + s];
-        }
-        const float ls = logf(e[0]);
-#pragma unroll
-        for (int p = 0; p < NP; ++p)
-            v[p] = p < P ? (v[p] - mx) - ls : kNegInf;
-
-        float dv[KM];
-        int di[KM];
-        digit_topk<NP, KM>(v, id, dv, di);
-        if (u == 0) {
-#pragma unroll
-            for (int k = 0; k < KM; ++k) {
-                mv[k] = dv[k];
-                mi[k] = di[k];
-            }
-        } else {
-            float av[KM], cv[KM];
-            int ai[KM], ci[KM];
-            build_column(mv, mi, dv[0], di[0], stride, av, ai);
-#pragma unroll
-            for (int j = 1; j < KM; ++j) {
-                build_column(mv, mi, dv[j], di[j], stride, cv, ci);
-                merge_topk(av, ai, cv, ci);
-            }
-#pragma unroll
-            for (int k = 0; k < KM; ++k) {
-                mv[k] = av[k];
-                mi[k] = ai[k];
-            }
-        }
-        stride *= P;
-    }
+    float mv[KM];  // sorted top-KM scores
+    int mi[KM];    // their content indices
+    bool ok[KM];
+    const bool inactive = !lane_search<Scalar, NP, KM>(base, static_cast<int64_t>(T), U, P, mv, mi, ok);
 
     const int K = src.top_k;
     float lse = 0.f;
