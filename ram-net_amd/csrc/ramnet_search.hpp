@@ -8,6 +8,7 @@
 #pragma once
 
 #include "ramnet_device.hpp"
+#include "lane_search.hpp"
 
 #include <math.h>
 
@@ -110,43 +111,89 @@ __device__ __forceinline__ float topk_lse_serial(const float *sv, int K) {
 // ---------------------------------------------------------------------------
 // Cooperative search by a group of GW lanes (GW = 32: two addresses per
 // wave, one per half; GW = 64: one address per wave). One digit value per
-// lane, bitonic sorts across lanes, and for each further digit the
-// prefix x digit candidates (i, j) with (i+1)(j+1) <= K: any other candidate
-// is preceded by at least K candidates that dominate it in both digits.
-// Requires P <= GW and the candidate count of K to fit in GW lanes.
+// lane; candidates are packed sort keys (see lane_search.hpp) sorted with a
+// bitonic network whose lane exchanges are single VALU moves (DPP within a
+// row, v_permlane16/32_swap across rows). For each further digit the
+// prefix x digit candidates (i, j) with (i+1)(j+1) <= K are formed: any other
+// candidate is preceded by at least K candidates that dominate it in both
+// digits. Requires P <= GW and the candidate count of K to fit in GW lanes.
 
+template<int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xf, 0xf,
+                                                             false));
+}
+
+// Value of lane (lane ^ J), J a power of two below 64.
+template<int J>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    if constexpr (J == 1) {
+        return dpp_u<0xB1>(v);  // quad_perm [1,0,3,2]
+    } else if constexpr (J == 2) {
+        return dpp_u<0x4E>(v);  // quad_perm [2,3,0,1]
+    } else if constexpr (J == 4) {
+        const uint32_t up = dpp_u<0x104>(v);  // row_shl:4 -> lane + 4
+        const uint32_t dn = dpp_u<0x114>(v);  // row_shr:4 -> lane - 4
+        return (lane & 4) ? dn : up;
+    } else if constexpr (J == 8) {
+        return dpp_u<0x128>(v);  // row_ror:8
+    } else if constexpr (J == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);  // {rows 0,0,2,2}, {rows 1,1,3,3}
+        return (lane & 16) ? r[0] : r[1];
+    } else {
+        static_assert(J == 32, "lane_xor distance");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // {low, low}, {high, high}
+        return (lane & 32) ? r[0] : r[1];
+    }
+}
+template<int J>
+__device__ __forceinline__ float lane_xor_f(float v) { return __uint_as_float(lane_xor<J>(__float_as_uint(v))); }
+template<int J>
+__device__ __forceinline__ uint64_t lane_xor(uint64_t v) {
+    return (static_cast<uint64_t>(lane_xor<J>(static_cast<uint32_t>(v >> 32))) << 32) |
+           lane_xor<J>(static_cast<uint32_t>(v));
+}
+
+// Butterfly reductions over GW lanes; every lane of the group ends with the
+// bitwise same result.
 template<int GW>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int s = GW / 2; s >= 1; s >>= 1)
-        v = fmaxf(v, __shfl_xor(v, s));
+    if constexpr (GW >= 2) v = fmaxf(v, lane_xor_f<1>(v));
+    if constexpr (GW >= 4) v = fmaxf(v, lane_xor_f<2>(v));
+    if constexpr (GW >= 8) v = fmaxf(v, lane_xor_f<4>(v));
+    if constexpr (GW >= 16) v = fmaxf(v, lane_xor_f<8>(v));
+    if constexpr (GW >= 32) v = fmaxf(v, lane_xor_f<16>(v));
+    if constexpr (GW >= 64) v = fmaxf(v, lane_xor_f<32>(v));
+    return v;
+}
+template<int GW>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (GW >= 2) v += lane_xor_f<1>(v);
+    if constexpr (GW >= 4) v += lane_xor_f<2>(v);
+    if constexpr (GW >= 8) v += lane_xor_f<4>(v);
+    if constexpr (GW >= 16) v += lane_xor_f<8>(v);
+    if constexpr (GW >= 32) v += lane_xor_f<16>(v);
+    if constexpr (GW >= 64) v += lane_xor_f<32>(v);
     return v;
 }
 
-// Sum with the same pairwise tree as e[p] += e[p + s], s = GW/2 .. 1.
-template<int GW>
-__device__ __forceinline__ float group_tree_sum(float v) {
-#pragma unroll
-    for (int s = GW / 2; s >= 1; s >>= 1)
-        v += __shfl_xor(v, s);
-    return v;
+// Descending bitonic sort of one key per lane over GW lanes.
+template<int GW, int K2, int J, typename Key>
+__device__ __forceinline__ void sort_step(Key &key, int li) {
+    const Key p = lane_xor<J>(key);
+    const bool keep_max = ((li & J) == 0) == ((li & K2) == 0);
+    const Key hi = key > p ? key : p;
+    const Key lo = key > p ? p : key;
+    key = keep_max ? hi : lo;
+    if constexpr (J > 1)
+        sort_step<GW, K2, J / 2>(key, li);
 }
-
-template<int GW>
-__device__ __forceinline__ void group_sort(float &v, int &id, int li) {
-#pragma unroll
-    for (int k = 2; k <= GW; k <<= 1) {
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const float pv = __shfl_xor(v, j);
-            const int pi = __shfl_xor(id, j);
-            const bool up = (li & k) == 0;
-            const bool lower = (li & j) == 0;
-            const bool take = (lower == up) ? before(pv, pi, v, id) : before(v, id, pv, pi);
-            v = take ? pv : v;
-            id = take ? pi : id;
-        }
-    }
+template<int GW, int K2 = 2, typename Key>
+__device__ __forceinline__ void group_sort_desc(Key &key, int li) {
+    sort_step<GW, K2, K2 / 2>(key, li);
+    if constexpr (K2 < GW)
+        group_sort_desc<GW, K2 * 2>(key, li);
 }
 
 // Number of staircase candidates (i+1)(j+1) <= K.
@@ -189,16 +236,40 @@ struct GroupLogits {
     }
 };
 
+// Digit sort key of a logit held as float: for 16-bit inputs the low
+// mantissa bits of the float are zero, so the radix index fits in the low 6
+// bits of a 32-bit key; fp32 inputs use 64-bit keys.
+template<typename T>
+using GroupKey = std::conditional_t<sizeof(T) == 2, uint32_t, uint64_t>;
+
+template<typename T>
+__device__ __forceinline__ GroupKey<T> group_digit_key(float x, int li) {
+    const uint32_t o = ord32(__float_as_uint(x));
+    if constexpr (sizeof(T) == 2)
+        return (o & ~63u) | static_cast<uint32_t>(63 - li);
+    else
+        return (static_cast<uint64_t>(o) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(li));
+}
+template<typename T>
+__device__ __forceinline__ void group_digit_unkey(GroupKey<T> k, float &x, int &li) {
+    if constexpr (sizeof(T) == 2) {
+        const uint32_t hi = k & ~63u;
+        x = __uint_as_float(unord32((hi & 0x80000000u) ? hi : (hi | 63u)));
+        li = 63 - static_cast<int>(k & 63u);
+    } else {
+        x = __uint_as_float(unord32(static_cast<uint32_t>(k >> 32)));
+        li = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(k));
+    }
+}
+
 // Decode one address with a group of GW lanes starting at lane g0. On return
 // lanes g0 .. g0+K-1 hold the sorted top entries (score, content slot).
 // Returns the inactive flag (uniform within the group).
 template<typename T, int GW>
 __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int li, float &out_v, int &out_i) {
-    float cv = kNegInfF;
-    int ci = kNoIdx;
-    bool inactive = false;
-    int stride = 1;
-    // staircase slot of this lane
+    using Key = GroupKey<T>;
+    constexpr float kLog2e = 1.4426950408889634f;
+    // staircase slot (si_, sj_) of this lane
     int si_ = -1, sj_ = -1;
     {
         int q = li;
@@ -212,25 +283,27 @@ __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int 
             q -= cnt;
         }
     }
-    const int g0 = (threadIdx.x & (kWave - 1)) & ~(GW - 1);
+    const int g0 = (static_cast<int>(threadIdx.x) & (kWave - 1)) & ~(GW - 1);
+    float cv = kNegInfF;  // prefix score of this lane's rank
+    int ci = -1;          // its content slot, -1 = none
+    bool inactive = false;
+    int stride = 1;
     for (int u = 0; u < U; ++u) {
-        const float x = lg.get(u, li);
-        const bool fin = li < P && x != kNegInfF;
-        // any finite logit in this digit, within the group
-        float any = fin ? 1.f : 0.f;
-        any = group_max<GW>(any);
-        inactive = inactive || any == 0.f;
+        const float x = lg.get(u, li);  // -inf for li >= P
         const float mx = group_max<GW>(x);
-        const float e = li < P ? expf(x - mx) : 0.f;
-        const float ssum = group_tree_sum<GW>(e);
-        const float ls = logf(ssum);
-        float dv = li < P ? (x - mx) - ls : kNegInfF;
-        int di = li < P ? li : kNoIdx;
-        group_sort<GW>(dv, di, li);
+        inactive = inactive || !(mx > kNegInfF);
+        const float e = li < P ? __builtin_amdgcn_exp2f((x - mx) * kLog2e) : 0.f;
+        const float ls = logf(group_sum<GW>(e));
+        Key key = li < P ? group_digit_key<T>(x, li) : Key(0);
+        group_sort_desc<GW>(key, li);
+        float xs;
+        int d;
+        group_digit_unkey<T>(key, xs, d);
+        const float dv = (xs - mx) - ls;  // this lane's rank of the digit
+        const int di = key != Key(0) ? d : -1;
         if (u == 0) {
-            const bool keep = li < K;
-            cv = keep ? dv : kNegInfF;
-            ci = keep ? di : kNoIdx;
+            cv = dv;
+            ci = di;
         } else {
             const int ii = si_ < 0 ? 0 : si_;
             const int jj = sj_ < 0 ? 0 : sj_;
@@ -238,18 +311,19 @@ __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int 
             const int pi = __shfl(ci, g0 + ii);
             const float qv = __shfl(dv, g0 + jj);
             const int qi = __shfl(di, g0 + jj);
-            const bool ok = si_ >= 0 && pi != kNoIdx && qi != kNoIdx;
-            float nv = ok ? pv + qv : kNegInfF;
-            int ni = ok ? pi + stride * qi : kNoIdx;
-            group_sort<GW>(nv, ni, li);
-            const bool keep = li < K;
-            cv = keep ? nv : kNegInfF;
-            ci = keep ? ni : kNoIdx;
+            const bool ok = si_ >= 0 && pi >= 0 && qi >= 0;
+            uint64_t ck = ok ? (static_cast<uint64_t>(ord32(__float_as_uint(pv + qv))) << 32) |
+                                   (0xFFFFFFFFu - static_cast<uint32_t>(pi + stride * qi))
+                             : uint64_t(0);
+            group_sort_desc<GW>(ck, li);
+            cv = __uint_as_float(unord32(static_cast<uint32_t>(ck >> 32)));
+            ci = ck != 0 ? static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck)) : -1;
         }
         stride *= P;
     }
-    out_v = cv;
-    out_i = ci;
+    const bool keep = li < K;
+    out_v = keep ? cv : kNegInfF;
+    out_i = keep && ci >= 0 ? ci : kNoIdx;
     return inactive;
 }
 
