@@ -59,7 +59,8 @@ __device__ __forceinline__ void finalize_events(float v, int c, bool inactive, i
     }
 }
 
-template<typename T, int GW, int KE, int kCpl>
+// FULLC: C == 64 * kCpl, so every lane owns kCpl real channels.
+template<typename T, int GW, int KE, int kCpl, bool FULLC>
 __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob job) {
     __shared__ int s_ws[KE], s_rs[KE];
     __shared__ float s_wv[KE], s_rv[KE];
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
 #pragma unroll
     for (int j = 0; j < kCpl; ++j) {
         const int c = lane + j * kWave;
-        cidx[j] = c < C ? c : C - 1;
+        cidx[j] = FULLC || c < C ? c : C - 1;
     }
     const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
     float xv[kCpl];
@@ -156,12 +157,21 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
             rrow[k][j] = row[cidx[j]];
         rm[k] = mass[ra[k]];
     }
-    // ---- writes
+    // every row and mass load is in flight before the first write (the
+    // fence stops the scheduler from sinking loads into the write branches,
+    // where each would wait for its own data)
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- writes. e^-|gamma| is shared by the events: alpha = num / den with
+    // the stable form of gsu_alpha, divided with one Newton-refined reciprocal.
+    const bool gpos = gamma >= 0.f;
+    const float eg = expf(gpos ? -gamma : gamma);
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
         const float w = wv[k];
         if (w != 0.f) {
-            const float alpha = gsu_alpha(w, gamma);
+            const float cw = 1.f - w;
+            const float den = gpos ? fmaf(eg, cw, w) : fmaf(eg, w, cw);
+            const float alpha = gsu_gain(gpos ? cw * eg : cw, den);
             const float m2 = fmaf(alpha, wm[k], w);
             const float g = gsu_gain(w, m2 + job.eps);
             float *row = slot + static_cast<int64_t>(wa[k]) * C;
@@ -170,7 +180,7 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
                 const int c = lane + j * kWave;
                 const float s = fmaf(g, xv[j] - wrow[k][j], wrow[k][j]);
                 s_row[k][c] = s;  // each lane re-reads only what it wrote
-                if (c < C)
+                if (FULLC || c < C)
                     row[c] = s;
             }
             if (lane == 0)
@@ -179,7 +189,34 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
         }
     }
 
-    // ---- reads of the post-write state
+    // ---- reads of the post-write state. The forwarded rows of every read
+    // are fetched from LDS in one batch (index clamped, value selected), so
+    // the reads cost one LDS round trip; events past top-K have r = 0.
+    float sval[KE][kCpl];
+#pragma unroll
+    for (int k = 0; k < KE; ++k) {
+        const int f = fwd[k];
+        const int fc = f < 0 ? 0 : f;
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j) {
+            const float lv = s_row[fc][lane + j * kWave];
+            sval[k][j] = f >= 0 ? lv : rrow[k][j];
+        }
+    }
+    float rw[KE];  // read weights (mass-aware: r * post-write mass)
+#pragma unroll
+    for (int k = 0; k < KE; ++k)
+        rw[k] = rv[k];
+    if (job.mass_aware) {
+#pragma unroll
+        for (int k = 0; k < KE; ++k) {
+            float m = rm[k];
+#pragma unroll
+            for (int j2 = 0; j2 < KE; ++j2)
+                m = fwd[k] == j2 ? wm[j2] : m;
+            rw[k] = rv[k] * m;
+        }
+    }
     float acc[kCpl];
 #pragma unroll
     for (int j = 0; j < kCpl; ++j)
@@ -187,28 +224,17 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
     float sr = 0.f, srm = 0.f;
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
-        const float r = rv[k];
-        if (r != 0.f) {
-            const int f = fwd[k];
-            float m = rm[k];
+        sr += rv[k];
+        srm += rw[k];
 #pragma unroll
-            for (int j2 = 0; j2 < KE; ++j2)
-                m = f == j2 ? wm[j2] : m;
-            const float wgt = job.mass_aware ? r * m : r;
-            sr += r;
-            srm += wgt;
-#pragma unroll
-            for (int j = 0; j < kCpl; ++j) {
-                const float s = f >= 0 ? s_row[f][lane + j * kWave] : rrow[k][j];
-                acc[j] = fmaf(wgt, s, acc[j]);
-            }
-        }
+        for (int j = 0; j < kCpl; ++j)
+            acc[j] = fmaf(rw[k], sval[k][j], acc[j]);
     }
     const float scale = job.mass_aware ? sr / (srm + job.eps) : 1.f;
 #pragma unroll
     for (int j = 0; j < kCpl; ++j) {
         const int c = lane + j * kWave;
-        if (c < C)
+        if (FULLC || c < C)
             store_f32(yrow + c, acc[j] * scale);
     }
 }
@@ -315,7 +341,13 @@ hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **w
         const bool narrow = job.C <= 2 * kWave;
         const bool few = kmax <= 8;
         const dim3 g(grid), blk(kWave);
-#define RAMNET_AR_LAUNCH(GW, KE, CPL) hipLaunchKernelGGL((autoregressive_fast_kernel<T, GW, KE, CPL>), g, blk, 0, stream, job)
+#define RAMNET_AR_LAUNCH(GW, KE, CPL)                                                                          \
+    do {                                                                                                        \
+        if (job.C == (CPL) * kWave)                                                                             \
+            hipLaunchKernelGGL((autoregressive_fast_kernel<T, GW, KE, CPL, true>), g, blk, 0, stream, job);    \
+        else                                                                                                    \
+            hipLaunchKernelGGL((autoregressive_fast_kernel<T, GW, KE, CPL, false>), g, blk, 0, stream, job);   \
+    } while (0)
         if (half) {
             if (few) { if (narrow) RAMNET_AR_LAUNCH(32, 8, 2); else RAMNET_AR_LAUNCH(32, 8, 4); }
             else { if (narrow) RAMNET_AR_LAUNCH(32, 16, 2); else RAMNET_AR_LAUNCH(32, 16, 4); }
