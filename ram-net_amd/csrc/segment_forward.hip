@@ -68,7 +68,7 @@ struct Plan {
 // Cost model of one layout, in cycles per token of one round of resident
 // workgroups: a wave's token loop is bound by its dependency chain (LDS
 // read -> update -> LDS write, ~kChainCycles) or by the issue of its VALU
-// work (~14 + 10 * VEC * NP instructions, 4 cycles each, shared by the waves
+// work (~10 + 6 * VEC * NP instructions, 4 cycles each, shared by the waves
 // on one SIMD), whichever is longer. Total = rounds * per-token cycles.
 constexpr int64_t kChainCycles = 160;
 
@@ -97,7 +97,7 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, P
                 const int64_t rounds = (units + per_cu * n_cu - 1) / (per_cu * n_cu);
                 const int64_t resident = std::min<int64_t>(per_cu, (units + n_cu - 1) / n_cu);
                 const int64_t waves_per_simd = (resident * nw + 3) / 4;
-                const int64_t issue = 4 * (14 + 10 * vec * np) * waves_per_simd;
+                const int64_t issue = 4 * (10 + 6 * vec * np) * waves_per_simd;
                 int64_t cost = rounds * std::max(kChainCycles, issue);
                 if (C % cs != 0)
                     cost = cost * 3 / 2;  // partial slices take the guarded path

@@ -46,7 +46,7 @@ __device__ __forceinline__ float dpp_f(float v) {
 // Sum over the EPP consecutive lanes of an event group; every lane of the
 // group receives the same value. DPP within a 16-lane row, shuffles across.
 template<int EPP>
-__device__ __forceinline__ float group_sum(float v) {
+__device__ __forceinline__ float event_sum(float v) {
     if constexpr (EPP >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
     if constexpr (EPP >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
     if constexpr (EPP >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
@@ -195,49 +195,57 @@ __device__ const uint8_t kScanAllValid = 1;
 // Row stride (floats) of the LDS slot slice: one pad float per row spreads
 // rows over banks; VEC-wide rows keep VEC-float alignment.
 constexpr int scan_row_stride(int vec, int cs) { return cs + (vec == 1 ? 1 : vec); }
-// Per-wave mass block: two dummy masses, A masses, then one sink float per
-// lane that takes the mass stores of lanes that do not own the event.
-__host__ __device__ constexpr int scan_mass_stride(int A) { return A + 2 + kWave; }
 // Staged x row of one channel: kChunk elements + 16 bytes of padding, which
 // keeps the 16-byte reads of neighbouring channels on disjoint banks.
 constexpr int scan_xrow_bytes(int elem) { return kChunk * elem + 16; }
+// Staged event: {write slot, gain, read slot, read weight}.
+struct StageRec {
+    int wslot;
+    float g;
+    int rslot;
+    float r;
+};
 
-// LDS bytes of a workgroup with NW waves of lane layout (vec, epp, np):
-// slot slice, NW mass blocks, then two chunk buffers of staged write
-// records, read records and x.
-__host__ __device__ constexpr size_t scan_stage_offset(int A, int rs, int nw) {
-    return ((static_cast<size_t>(A + 2) * rs + static_cast<size_t>(nw) * scan_mass_stride(A)) * 4 + 15) / 16 * 16;
+// LDS layout of a workgroup: slot slice (A + 2 rows: the dummy write row,
+// the dummy read row, A slots), the masses (2 dummies + A), then two chunk
+// buffers of staged events (kChunk x E) and x (CS rows), 16-byte aligned.
+__host__ __device__ constexpr size_t scan_stage_offset(int A, int rs) {
+    return ((static_cast<size_t>(A + 2) * rs + static_cast<size_t>(A + 2)) * 4 + 15) / 16 * 16;
 }
 inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem) {
     const int cs = nw * (kWave / epp) * vec;
-    const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs), nw);
-    const size_t stage = static_cast<size_t>(kChunk) * epp * np * (sizeof(WriteRec) + sizeof(ReadRec)) +
+    const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs));
+    const size_t stage = static_cast<size_t>(kChunk) * epp * np * sizeof(StageRec) +
                          static_cast<size_t>(cs) * scan_xrow_bytes(elem);
     return state + 2 * stage;
 }
 
-// NW waves share one (b, h, CS-channel slice) unit: wave w owns channels
-// [w * CSW, (w + 1) * CSW) of the slice and keeps its own copy of the slot
-// masses. Per 16-token chunk the workgroup loads the chunk's records and x
-// once -- each thread one or two unique elements -- into a double-buffered
-// LDS stage (one barrier per chunk), each lane then reads its event's
-// records and its channels' x from the stage in bulk, and the token loop
-// runs on registers and the LDS-resident state. Read sums are kept in
-// registers and stored once per chunk.
+// A workgroup owns one (b, h, CS-channel slice) unit: NW state waves, each
+// owning CSW channels of the slice, and one mass wave. Per 16-token chunk:
+//  * the mass wave replays the slot masses one chunk ahead of the state
+//    waves (m <- alpha m + w per write event, in token order) and stages
+//    each event's gain g = w / (m + eps) and effective read weight
+//    (mass-aware: (sum r) (m r) / (sum m r + eps), else r);
+//  * the state waves stage the chunk's x (one or two elements per thread),
+//    read their events and x from the stage in bulk, and run the token loop:
+//    s <- s + g (x - s) for the writes, then the weighted read sum -- the
+//    per-token dependency chain is one LDS row read-modify-write;
+//  * one barrier per chunk hands the double-buffered stage over.
 // FAST: C is a multiple of CS, so every lane owns VEC real channels.
 template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
-__global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJob job, const ScanGeom geo) {
+__global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const SegmentJob job, const ScanGeom geo) {
     constexpr int LPE = kWave / EPP;
     constexpr int CSW = LPE * VEC;
     constexpr int CS = NW * CSW;
     constexpr int RS = scan_row_stride(VEC, CS);
-    constexpr int NT = kWave * NW;           // threads per workgroup
-    constexpr int E = EPP * NP;              // event lanes per token
+    constexpr int NST = kWave * NW;           // state threads
+    constexpr int E = EPP * NP;               // event lanes per token
+    constexpr int MP = (E + 31) / 32;         // mass-wave passes (32 events each)
     constexpr int ES = static_cast<int>(sizeof(Scalar));
-    constexpr int XRB = scan_xrow_bytes(ES);  // staged x row bytes
-    constexpr int WI = (E * kChunk + NT - 1) / NT;   // staged write records per thread
-    constexpr int XI = (CS * kChunk + NT - 1) / NT;  // staged x elements per thread
+    constexpr int XRB = scan_xrow_bytes(ES);
+    constexpr int XI = (CS * kChunk + NST - 1) / NST;  // staged x elements per state thread
     constexpr int NSL = EPP <= kChunk ? kChunk / EPP : 1;  // tokens whose y a lane stores
+    constexpr int kStageBytes = kChunk * E * static_cast<int>(sizeof(StageRec)) + CS * XRB;
     using Bits = std::conditional_t<ES == 4, uint32_t, uint16_t>;
 
     extern __shared__ __align__(16) float lds[];
@@ -250,122 +258,153 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = tid / kWave;
     const int lane = tid % kWave;
+    const bool mass_wave = wave == NW;
     const int bh = unit / geo.n_slices;
     const int c0 = (unit - bh * geo.n_slices) * CS;
     const int T = job.T, A = job.A, C = job.C, Kw = job.Kw, Kr = job.Kr, Tp = geo.t_pad;
-    const int MSW = scan_mass_stride(A);
     const float eps = job.eps;
 
-    // LDS: [dummy write row][dummy read row][A rows] x RS floats, NW mass
-    // blocks, then the two stage buffers.
-    float *st = lds + 2 * RS;
-    float *ms = lds + (A + 2) * RS + wave * MSW + 2;
-    char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(A, RS, NW);
-    constexpr int kStageBytes = kChunk * E * static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec)) + CS * XRB;
-    auto stage_w = [&](int buf) { return reinterpret_cast<WriteRec *>(stage0 + buf * kStageBytes); };
-    auto stage_r = [&](int buf) {
-        return reinterpret_cast<ReadRec *>(stage0 + buf * kStageBytes + kChunk * E * sizeof(WriteRec));
-    };
-    auto stage_x = [&](int buf) {
-        return stage0 + buf * kStageBytes + kChunk * E * static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec));
-    };
+    float *st = lds + 2 * RS;              // slot 0 of the slice
+    float *ms = lds + (A + 2) * RS + 2;    // mass of slot 0
+    char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(A, RS);
+    auto stage_e = [&](int buf) { return reinterpret_cast<StageRec *>(stage0 + buf * kStageBytes); };
+    auto stage_x = [&](int buf) { return stage0 + buf * kStageBytes + kChunk * E * static_cast<int>(sizeof(StageRec)); };
 
-    const int ev = lane % EPP;                // event slot within a pass
-    const int cg = lane / EPP;                // channel group within the wave
-    const int cl = wave * CSW + cg * VEC;     // first channel of this lane within the slice
-    const int sink = A + lane;                // mass sink of this lane
-
-    // ---- state slice -> LDS (whole workgroup), masses per wave
+    // ---- state slice and masses -> LDS
     {
         const float *src = job.init_slot + static_cast<int64_t>(bh) * A * C;
-        for (int i = tid; i < A * CS; i += NT) {
+        for (int i = tid; i < A * CS; i += kWave * (NW + 1)) {
             const int a = i / CS, c = i - a * CS;
             const bool ok = c0 + c < C;
             const float v = src[static_cast<int64_t>(a) * C + (ok ? c0 + c : 0)];
             st[a * RS + c] = ok ? v : 0.f;
         }
-        for (int i = tid; i < 2 * RS; i += NT)
+        for (int i = tid; i < 2 * RS; i += kWave * (NW + 1))
             lds[i] = 0.f;
         const float *msrc = job.init_mass + static_cast<int64_t>(bh) * A;
-        for (int a = lane; a < A; a += kWave)
+        for (int a = tid; a < A; a += kWave * (NW + 1))
             ms[a] = msrc[a];
-        if (lane < 2)
-            ms[lane - 2] = 1.f;
+        if (tid < 2)
+            ms[tid - 2] = 1.f;
     }
 
-    // ---- chunk staging: global -> registers (start of the previous chunk),
-    // registers -> LDS (end of the previous chunk)
+    // ---- mass wave: raw records of one chunk in registers. Lanes 0..31
+    // hold write events p * 32 + lane, lanes 32..63 read events
+    // p * 32 + lane - 32, each for the chunk's kChunk tokens.
     const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * Tp;
     const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * Tp;
+    const int hl = lane & 31;
+    const bool wlane = lane < 32;
+    struct Raw {
+        int4 w[MP][kChunk];
+        int2 r[MP][kChunk];
+    };
+    auto mass_fetch = [&](int t0, Raw &raw) {
+#pragma unroll
+        for (int p = 0; p < MP; ++p) {
+            const int e = p * 32 + hl;
+            const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
+            const WriteRec *wp = gw + static_cast<int64_t>(ew) * Tp + t0;
+            const ReadRec *rp = gr + static_cast<int64_t>(er) * Tp + t0;
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) {
+                raw.w[p][j] = *reinterpret_cast<const int4 *>(wp + j);
+                raw.r[p][j] = *reinterpret_cast<const int2 *>(rp + j);
+            }
+        }
+    };
+    // Replays the chunk's mass updates and stages {slot, gain, slot, weight}.
+    auto mass_chunk = [&](int buf, const Raw &raw) {
+        StageRec *se = stage_e(buf);
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            int wa[MP];
+            float gg[MP];
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                const bool on = wlane && p * 32 + hl < Kw;
+                const int a = on ? raw.w[p][j].x : -2;
+                const float w = on ? __int_as_float(raw.w[p][j].y) : 0.f;
+                const float al = on ? __int_as_float(raw.w[p][j].z) : 1.f;
+                const float m2 = fmaf(al, ms[a], w);
+                ms[a] = m2;
+                wa[p] = a;
+                gg[p] = scan_gain(w, m2 + eps);
+            }
+            int rb[MP];
+            float rr[MP];
+            float sr = 0.f, srm = 0.f;
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                const bool on = !wlane && p * 32 + hl < Kr;
+                rb[p] = on ? raw.r[p][j].x : -1;
+                rr[p] = on ? __int_as_float(raw.r[p][j].y) : 0.f;
+                if constexpr (MA) {
+                    const float wm = rr[p] * ms[rb[p]];  // post-write mass
+                    sr += rr[p];
+                    srm += wm;
+                    rr[p] = wm;
+                }
+            }
+            if constexpr (MA) {
+                sr = event_sum<32>(sr);
+                srm = event_sum<32>(srm);
+                const float scale = sr / (srm + eps);
+#pragma unroll
+                for (int p = 0; p < MP; ++p)
+                    rr[p] *= scale;
+            }
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                const int e = p * 32 + hl;
+                if (e < E) {
+                    int2 *dst = reinterpret_cast<int2 *>(se + j * E + e) + (wlane ? 0 : 1);
+                    *dst = wlane ? make_int2(wa[p], __float_as_int(gg[p])) : make_int2(rb[p], __float_as_int(rr[p]));
+                }
+            }
+        }
+    };
+
+    // ---- state waves
+    const int ev = lane % EPP;                // event slot within a pass
+    const int cg = lane / EPP;                // channel group within the wave
+    const int cl = wave * CSW + cg * VEC;     // first channel of this lane within the slice
     const Scalar *gx = static_cast<const Scalar *>(job.x) + static_cast<int64_t>(bh) * T * C;
     Scalar *gy = static_cast<Scalar *>(job.y) + static_cast<int64_t>(bh) * T * C;
-    struct Staged {
-        int4 w[WI];
-        int2 r[WI];
-        Bits x[XI];
-    };
     // Items past the end are clamped to the last item, so the threads that
-    // hold them load and store identical data: fetch and deposit stay
-    // branch-free, which keeps the compiler's memory wait counts exact.
-    auto fetch = [&](int t0, Staged &sg) {
-#pragma unroll
-        for (int k = 0; k < WI; ++k) {
-            const int it = min(tid + k * NT, E * kChunk - 1);
-            const int e = it / kChunk, j = it % kChunk;
-            const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
-            sg.w[k] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ew) * Tp + t0 + j);
-            sg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
-        }
+    // hold them load and store identical data (no branch).
+    auto x_fetch = [&](int t0, Bits (&xb)[XI]) {
 #pragma unroll
         for (int k = 0; k < XI; ++k) {
-            const int it = min(tid + k * NT, CS * kChunk - 1);
+            const int it = min(tid + k * NST, CS * kChunk - 1);
             const int j = it / CS, c = it % CS;
             const int t = t0 + j < T ? t0 + j : T - 1;
             const int ch = c0 + c < C ? c0 + c : C - 1;
-            sg.x[k] = *reinterpret_cast<const Bits *>(gx + static_cast<int64_t>(t) * C + ch);
+            xb[k] = *reinterpret_cast<const Bits *>(gx + static_cast<int64_t>(t) * C + ch);
         }
     };
-    auto deposit = [&](int buf, const Staged &sg) {
-        WriteRec *sw = stage_w(buf);
-        ReadRec *sr = stage_r(buf);
+    auto x_deposit = [&](int buf, const Bits (&xb)[XI]) {
         char *sx = stage_x(buf);
 #pragma unroll
-        for (int k = 0; k < WI; ++k) {
-            const int it = min(tid + k * NT, E * kChunk - 1);
-            const int e = it / kChunk, j = it % kChunk;
-            const bool wl = e < Kw, rl = e < Kr;  // events past top-K get no-op records
-            const int4 w = make_int4(wl ? sg.w[k].x : -2, wl ? sg.w[k].y : 0, wl ? sg.w[k].z : __float_as_int(1.f), 0);
-            const int2 r = make_int2(rl ? sg.r[k].x : -1, rl ? sg.r[k].y : 0);
-            *reinterpret_cast<int4 *>(sw + j * E + e) = w;
-            *reinterpret_cast<int2 *>(sr + j * E + e) = r;
-        }
-#pragma unroll
         for (int k = 0; k < XI; ++k) {
-            const int it = min(tid + k * NT, CS * kChunk - 1);
+            const int it = min(tid + k * NST, CS * kChunk - 1);
             const int j = it / CS, c = it % CS;
-            *reinterpret_cast<Bits *>(sx + c * XRB + j * ES) = sg.x[k];
+            *reinterpret_cast<Bits *>(sx + c * XRB + j * ES) = xb[k];
         }
     };
-
-    // One chunk: bulk-read this lane's records and x from the stage, then
-    // the token loop. The token body is branch-free: the mass store of lanes
-    // that do not own the event goes to their sink, and each lane keeps the
-    // read sum of the tokens whose y it stores. TAIL guards tokens past T.
-    auto scan_chunk = [&](int buf, int t0, auto tail_tag) {
+    // One chunk of the state waves. The token body is branch-free; each lane
+    // keeps the read sum of the tokens whose y it stores. TAIL guards tokens
+    // past T.
+    auto state_chunk = [&](int buf, int t0, auto tail_tag) {
         constexpr bool TAIL = decltype(tail_tag)::value;
-        const WriteRec *sw = stage_w(buf);
-        const ReadRec *sr = stage_r(buf);
+        const StageRec *se = stage_e(buf);
         const char *sx = stage_x(buf);
-        int4 wrec[NP][kChunk];
-        int2 rrec[NP][kChunk];
+        int4 rec[NP][kChunk];
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
+        for (int j = 0; j < kChunk; ++j)
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                wrec[p][j] = *reinterpret_cast<const int4 *>(sw + j * E + p * EPP + ev);
-                rrec[p][j] = *reinterpret_cast<const int2 *>(sr + j * E + p * EPP + ev);
-            }
-        }
+            for (int p = 0; p < NP; ++p)
+                rec[p][j] = *reinterpret_cast<const int4 *>(se + j * E + p * EPP + ev);
         constexpr int XW = kChunk * ES / 16;  // 16-byte words per staged channel row
         uint4 xr[VEC][XW];
 #pragma unroll
@@ -391,61 +430,36 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
                 ykeep[q].v[v] = 0.f;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
-            // writes: read-modify-write of the slot rows and masses
-            float m[NP];
+            // writes: s <- s + g (x - s)
             FVec<VEC> s[NP];
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                const int a = wrec[p][j].x;
-                m[p] = ms[a];
-                s[p] = lds_load<VEC>(st + a * RS + cl);
-            }
+            for (int p = 0; p < NP; ++p)
+                s[p] = lds_load<VEC>(st + rec[p][j].x * RS + cl);
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                const int a = wrec[p][j].x;
-                const float w = __int_as_float(wrec[p][j].y);
-                const float al = __int_as_float(wrec[p][j].z);
-                const float m2 = fmaf(al, m[p], w);
-                const float g = scan_gain(w, m2 + eps);
+                const float g = __int_as_float(rec[p][j].y);
                 FVec<VEC> o;
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
                     o.v[v] = fmaf(g, x_at(v, j) - s[p].v[v], s[p].v[v]);
-                lds_store<VEC>(st + a * RS + cl, o);
-                ms[cg == 0 ? a : sink] = m2;
+                lds_store<VEC>(st + rec[p][j].x * RS + cl, o);
             }
             // reads of the post-write state
             FVec<VEC> acc;
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
                 acc.v[v] = 0.f;
-            float sr_ = 0.f, srm = 0.f;
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                const int a = rrec[p][j].x;
-                const float r = __int_as_float(rrec[p][j].y);
-                float wgt = r;
-                if constexpr (MA) {
-                    wgt = r * ms[a];
-                    sr_ += r;
-                    srm += wgt;
-                }
-                const FVec<VEC> rv = lds_load<VEC>(st + a * RS + cl);
+                const float wgt = __int_as_float(rec[p][j].w);
+                const FVec<VEC> rv = lds_load<VEC>(st + rec[p][j].z * RS + cl);
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
                     acc.v[v] = fmaf(wgt, rv.v[v], acc.v[v]);
             }
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
-                acc.v[v] = group_sum<EPP>(acc.v[v]);
-            if constexpr (MA) {
-                sr_ = group_sum<EPP>(sr_);
-                srm = group_sum<EPP>(srm);
-                const float scale = sr_ / (srm + eps);
-#pragma unroll
-                for (int v = 0; v < VEC; ++v)
-                    acc.v[v] *= scale;
-            }
+                acc.v[v] = event_sum<EPP>(acc.v[v]);
             // keep the sum in the lanes that store token j
             const bool mine = EPP <= kChunk ? ev == j % EPP : ev % kChunk == j;
             const int q = EPP <= kChunk ? j / EPP : 0;
@@ -471,49 +485,62 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
         }
     };
 
-    // Chunks wholly inside T run the unguarded body; at most one chunk at
-    // the end reaches past T. The next chunk's loads are issued before the
-    // current chunk runs and deposited into the other stage buffer after it.
+    // ---- pipeline. Iteration ci: the state waves run chunk ci (stage
+    // ci & 1) while the mass wave stages chunk ci + 1 (records fetched one
+    // iteration earlier) and fetches chunk ci + 2. Chunks wholly inside T
+    // run the unguarded state body; at most one chunk at the end reaches
+    // past T.
     using Full = std::false_type;
     using Tail = std::true_type;
     const int nc = geo.n_chunks;
     const int n_full = T / kChunk;
-    Staged sg;
+    Raw raw;
+    Bits xb[XI];
+    __syncthreads();  // masses initialised before the mass wave starts
     if (nc > 0) {
-        fetch(0, sg);
-        deposit(0, sg);
+        if (mass_wave) {
+            mass_fetch(0, raw);
+            mass_chunk(0, raw);
+            mass_fetch((1 < nc ? 1 : nc - 1) * kChunk, raw);
+        } else {
+            x_fetch(0, xb);
+            x_deposit(0, xb);
+        }
     }
     __syncthreads();
-    int ci = 0;
-    for (; ci < n_full; ++ci) {
-        // scheduling fences keep the loads at the top and their use at the
-        // bottom, so a whole chunk of work covers their latency
-        fetch((ci + 1 < nc ? ci + 1 : nc - 1) * kChunk, sg);
-        __builtin_amdgcn_sched_barrier(0);
-        scan_chunk(ci & 1, ci * kChunk, Full{});
-        __builtin_amdgcn_sched_barrier(0);
-        deposit((ci + 1) & 1, sg);
-        __syncthreads();
-    }
-    for (; ci < nc; ++ci) {
-        fetch((ci + 1 < nc ? ci + 1 : nc - 1) * kChunk, sg);
-        scan_chunk(ci & 1, ci * kChunk, Tail{});
-        deposit((ci + 1) & 1, sg);
+    for (int ci = 0; ci < nc; ++ci) {
+        const int nxt = ci + 1 < nc ? ci + 1 : nc - 1;
+        if (mass_wave) {
+            Raw cur = raw;
+            mass_fetch((ci + 2 < nc ? ci + 2 : nc - 1) * kChunk, raw);
+            if (ci + 1 < nc)
+                mass_chunk((ci + 1) & 1, cur);
+        } else {
+            // scheduling fences keep the x loads at the top and their use at
+            // the bottom, so a whole chunk of work covers their latency
+            x_fetch(nxt * kChunk, xb);
+            __builtin_amdgcn_sched_barrier(0);
+            if (ci < n_full)
+                state_chunk(ci & 1, ci * kChunk, Full{});
+            else
+                state_chunk(ci & 1, ci * kChunk, Tail{});
+            __builtin_amdgcn_sched_barrier(0);
+            x_deposit((ci + 1) & 1, xb);
+        }
         __syncthreads();
     }
 
-    // ---- LDS -> post state (whole workgroup). Every wave computes identical
-    // masses; wave 0 of slice 0 stores them.
+    // ---- LDS -> post state (whole workgroup); the masses from slice 0
     {
         float *dst = job.slot_out + static_cast<int64_t>(bh) * A * C;
-        for (int i = tid; i < A * CS; i += NT) {
+        for (int i = tid; i < A * CS; i += kWave * (NW + 1)) {
             const int a = i / CS, c = i - a * CS;
             if (c0 + c < C)
                 dst[static_cast<int64_t>(a) * C + c0 + c] = st[a * RS + c];
         }
-        if (c0 == 0 && wave == 0) {
+        if (c0 == 0) {
             float *mdst = job.mass_out + static_cast<int64_t>(bh) * A;
-            for (int a = lane; a < A; a += kWave)
+            for (int a = tid; a < A; a += kWave * (NW + 1))
                 mdst[a] = ms[a];
         }
     }
@@ -522,7 +549,7 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_kernel(const SegmentJ
 template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
 hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t stream) {
     const unsigned blocks = static_cast<unsigned>(((geo.n_units + 7) / 8) * 8);
-    hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST>), dim3(blocks), dim3(kWave * NW),
+    hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST>), dim3(blocks), dim3(kWave * (NW + 1)),
                        scan_lds_bytes(job.A, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar))), stream, job, geo);
     return hipGetLastError();
 }
