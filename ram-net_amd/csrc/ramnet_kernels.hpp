@@ -35,7 +35,7 @@ struct WriteRec {
     int slot;
     float w;
     float alpha;
-    float pad;
+    float overlap;  // int bits: 1 if a slot of this token is also written by token t - 1 (or unknown)
 };
 struct ReadRec {
     int slot;

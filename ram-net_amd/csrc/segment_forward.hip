@@ -139,9 +139,12 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
     const bool live = t < T && *mp != 0 && static_cast<unsigned>(a) < static_cast<unsigned>(A);
     if (k < job.Kw) {
         const bool act = live && v != 0.f;
-        WriteRec rec{-2, 0.f, 1.f, 0.f};
+        // overlap with token t - 1 is not computed here: assumed (the scan
+        // then orders the two tokens' row accesses strictly)
+        const float overlap = __int_as_float(1);
+        WriteRec rec{-2, 0.f, 1.f, overlap};
         if (act)
-            rec = WriteRec{a, v, gsu_alpha(v, g), 0.f};
+            rec = WriteRec{a, v, gsu_alpha(v, g), overlap};
         job.wrec[(static_cast<int64_t>(bh) * job.Kw + k) * t_pad + t] = rec;
     } else {
         const float r = -v;

@@ -195,9 +195,6 @@ __device__ const uint8_t kScanAllValid = 1;
 // Row stride (floats) of the LDS slot slice: one pad float per row spreads
 // rows over banks; VEC-wide rows keep VEC-float alignment.
 constexpr int scan_row_stride(int vec, int cs) { return cs + (vec == 1 ? 1 : vec); }
-// Staged x row of one channel: kChunk elements + 16 bytes of padding, which
-// keeps the 16-byte reads of neighbouring channels on disjoint banks.
-constexpr int scan_xrow_bytes(int elem) { return kChunk * elem + 16; }
 // Staged event: {write slot, gain, read slot, read weight}.
 struct StageRec {
     int wslot;
@@ -208,15 +205,22 @@ struct StageRec {
 
 // LDS layout of a workgroup: slot slice (A + 2 rows: the dummy write row,
 // the dummy read row, A slots), the masses (2 dummies + A), then two chunk
-// buffers of staged events (kChunk x E) and x (CS rows), 16-byte aligned.
+// buffers, 16-byte aligned, each holding the staged events (kChunk x E), x
+// (CS rows), the overlap flags and the raw records (kChunk x E) for the mass
+// wave.
 __host__ __device__ constexpr size_t scan_stage_offset(int A, int rs) {
     return ((static_cast<size_t>(A + 2) * rs + static_cast<size_t>(A + 2)) * 4 + 15) / 16 * 16;
 }
+// Tokens per chunk: 16, or 8 when more than 64 events per token would make
+// the double-buffered stage outgrow LDS.
+__host__ __device__ constexpr int scan_chunk_len(int events) { return events > 64 ? 8 : kChunk; }
+
 inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem) {
     const int cs = nw * (kWave / epp) * vec;
+    const int ch = scan_chunk_len(epp * np);
     const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs));
-    const size_t stage = static_cast<size_t>(kChunk) * epp * np * sizeof(StageRec) +
-                         static_cast<size_t>(cs) * scan_xrow_bytes(elem);
+    const size_t stage = static_cast<size_t>(ch) * epp * np * (sizeof(StageRec) + sizeof(WriteRec) + sizeof(ReadRec)) +
+                         static_cast<size_t>(cs) * (ch * elem + 16) + ch * sizeof(int);
     return state + 2 * stage;
 }
 
@@ -240,12 +244,15 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
     constexpr int RS = scan_row_stride(VEC, CS);
     constexpr int NST = kWave * NW;           // state threads
     constexpr int E = EPP * NP;               // event lanes per token
+    constexpr int CH = scan_chunk_len(E);     // tokens per chunk
     constexpr int MP = (E + 31) / 32;         // mass-wave passes (32 events each)
     constexpr int ES = static_cast<int>(sizeof(Scalar));
-    constexpr int XRB = scan_xrow_bytes(ES);
-    constexpr int XI = (CS * kChunk + NST - 1) / NST;  // staged x elements per state thread
-    constexpr int NSL = EPP <= kChunk ? kChunk / EPP : 1;  // tokens whose y a lane stores
-    constexpr int kStageBytes = kChunk * E * static_cast<int>(sizeof(StageRec)) + CS * XRB;
+    constexpr int XRB = CH * ES + 16;  // staged x row: CH elements + 16 bytes against bank conflicts
+    constexpr int XI = (CS * CH + NST - 1) / NST;  // staged x elements per state thread
+    constexpr int NSL = EPP <= CH ? CH / EPP : 1;  // tokens whose y a lane stores
+    constexpr int kStageBytes =
+        CH * E * static_cast<int>(sizeof(StageRec) + sizeof(WriteRec) + sizeof(ReadRec)) + CS * XRB + CH * 4;
+    constexpr int RI = (E * CH + NST - 1) / NST;  // raw records per state thread
     using Bits = std::conditional_t<ES == 4, uint32_t, uint16_t>;
 
     extern __shared__ __align__(16) float lds[];
@@ -268,7 +275,11 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
     float *ms = lds + (A + 2) * RS + 2;    // mass of slot 0
     char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(A, RS);
     auto stage_e = [&](int buf) { return reinterpret_cast<StageRec *>(stage0 + buf * kStageBytes); };
-    auto stage_x = [&](int buf) { return stage0 + buf * kStageBytes + kChunk * E * static_cast<int>(sizeof(StageRec)); };
+    auto stage_x = [&](int buf) { return stage0 + buf * kStageBytes + CH * E * static_cast<int>(sizeof(StageRec)); };
+    // per token: 1 if its writes may overlap the previous token's
+    auto stage_f = [&](int buf) { return reinterpret_cast<int *>(stage_x(buf) + CS * XRB); };
+    auto raw_w = [&](int buf) { return reinterpret_cast<WriteRec *>(stage_f(buf) + CH); };
+    auto raw_r = [&](int buf) { return reinterpret_cast<ReadRec *>(raw_w(buf) + CH * E); };
 
     // ---- state slice and masses -> LDS
     {
@@ -288,48 +299,82 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
             ms[tid - 2] = 1.f;
     }
 
-    // ---- mass wave: raw records of one chunk in registers. Lanes 0..31
-    // hold write events p * 32 + lane, lanes 32..63 read events
-    // p * 32 + lane - 32, each for the chunk's kChunk tokens.
+    // ---- raw records: fetched by the state threads two chunks ahead (one
+    // or two unique records per thread, clamped as for x) and deposited in
+    // LDS for the mass wave, whose lanes 0..31 take write events
+    // p * 32 + lane and lanes 32..63 read events p * 32 + lane - 32.
     const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * Tp;
     const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * Tp;
     const int hl = lane & 31;
     const bool wlane = lane < 32;
-    struct Raw {
-        int4 w[MP][kChunk];
-        int2 r[MP][kChunk];
+    struct RawRegs {
+        int4 w[RI];
+        int2 r[RI];
     };
-    auto mass_fetch = [&](int t0, Raw &raw) {
+    auto raw_fetch = [&](int t0, RawRegs &rg) {
+#pragma unroll
+        for (int k = 0; k < RI; ++k) {
+            const int it = min(tid + k * NST, E * CH - 1);
+            const int e = it / CH, j = it % CH;
+            const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
+            rg.w[k] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ew) * Tp + t0 + j);
+            rg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
+        }
+    };
+    auto raw_deposit = [&](int buf, const RawRegs &rg) {
+        WriteRec *rw = raw_w(buf);
+        ReadRec *rr = raw_r(buf);
+#pragma unroll
+        for (int k = 0; k < RI; ++k) {
+            const int it = min(tid + k * NST, E * CH - 1);
+            const int e = it / CH, j = it % CH;
+            *reinterpret_cast<int4 *>(rw + j * E + e) = rg.w[k];
+            *reinterpret_cast<int2 *>(rr + j * E + e) = rg.r[k];
+        }
+    };
+    struct Raw {
+        int4 w[MP][CH];
+        int2 r[MP][CH];
+    };
+    auto mass_load = [&](int buf, Raw &raw) {
+        const WriteRec *rw = raw_w(buf);
+        const ReadRec *rr = raw_r(buf);
 #pragma unroll
         for (int p = 0; p < MP; ++p) {
-            const int e = p * 32 + hl;
-            const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
-            const WriteRec *wp = gw + static_cast<int64_t>(ew) * Tp + t0;
-            const ReadRec *rp = gr + static_cast<int64_t>(er) * Tp + t0;
+            const int e = min(p * 32 + hl, E - 1);
 #pragma unroll
-            for (int j = 0; j < kChunk; ++j) {
-                raw.w[p][j] = *reinterpret_cast<const int4 *>(wp + j);
-                raw.r[p][j] = *reinterpret_cast<const int2 *>(rp + j);
+            for (int j = 0; j < CH; ++j) {
+                raw.w[p][j] = *reinterpret_cast<const int4 *>(rw + j * E + e);
+                raw.r[p][j] = *reinterpret_cast<const int2 *>(rr + j * E + e);
             }
         }
     };
-    // Replays the chunk's mass updates and stages {slot, gain, slot, weight}.
-    auto mass_chunk = [&](int buf, const Raw &raw) {
+    // Replays the chunk's mass updates and stages {slot, gain, slot, weight}
+    // and the overlap flags. Tokens go in pairs: the second token's masses
+    // are read before the first token's writes and read again only when the
+    // two tokens' write sets may overlap (flag of the second token).
+    auto mass_chunk = [&](int buf) {
+        Raw raw;
+        mass_load(buf, raw);
         StageRec *se = stage_e(buf);
-#pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            int wa[MP];
+        int *sf = stage_f(buf);
+        auto wev = [&](int p, int j, int &a, float &w, float &al) {
+            const bool on = wlane && p * 32 + hl < Kw;
+            a = on ? raw.w[p][j].x : -2;
+            w = on ? __int_as_float(raw.w[p][j].y) : 0.f;
+            al = on ? __int_as_float(raw.w[p][j].z) : 1.f;
+        };
+        // Stage entries are kept in registers and written after the chunk, so
+        // the LDS ops of the mass chain are only the mass reads and writes.
+        int2 out[MP][CH];
+        // writes of token j from masses m, then its reads
+        auto finish = [&](int j, const int (&a)[MP], const float (&w)[MP], const float (&al)[MP], float (&m)[MP]) {
             float gg[MP];
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
-                const bool on = wlane && p * 32 + hl < Kw;
-                const int a = on ? raw.w[p][j].x : -2;
-                const float w = on ? __int_as_float(raw.w[p][j].y) : 0.f;
-                const float al = on ? __int_as_float(raw.w[p][j].z) : 1.f;
-                const float m2 = fmaf(al, ms[a], w);
-                ms[a] = m2;
-                wa[p] = a;
-                gg[p] = scan_gain(w, m2 + eps);
+                const float m2 = fmaf(al[p], m[p], w[p]);
+                ms[a[p]] = m2;
+                gg[p] = scan_gain(w[p], m2 + eps);
             }
             int rb[MP];
             float rr[MP];
@@ -355,13 +400,44 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
                     rr[p] *= scale;
             }
 #pragma unroll
+            for (int p = 0; p < MP; ++p)
+                out[p][j] = wlane ? make_int2(a[p], __float_as_int(gg[p])) : make_int2(rb[p], __float_as_int(rr[p]));
+        };
+#pragma unroll
+        for (int j0 = 0; j0 < CH; j0 += 2) {
+            const int j1 = j0 + 1;
+            const int ov = __builtin_amdgcn_readfirstlane(raw.w[0][j1].w);
+            int a0[MP], a1[MP];
+            float w0[MP], w1[MP], al0[MP], al1[MP], m0[MP], m1[MP];
+#pragma unroll
             for (int p = 0; p < MP; ++p) {
-                const int e = p * 32 + hl;
-                if (e < E) {
-                    int2 *dst = reinterpret_cast<int2 *>(se + j * E + e) + (wlane ? 0 : 1);
-                    *dst = wlane ? make_int2(wa[p], __float_as_int(gg[p])) : make_int2(rb[p], __float_as_int(rr[p]));
-                }
+                wev(p, j0, a0[p], w0[p], al0[p]);
+                wev(p, j1, a1[p], w1[p], al1[p]);
+                m0[p] = ms[a0[p]];
+                m1[p] = ms[a1[p]];
             }
+            finish(j0, a0, w0, al0, m0);
+            if (ov) {
+#pragma unroll
+                for (int p = 0; p < MP; ++p)
+                    m1[p] = ms[a1[p]];
+            }
+            finish(j1, a1, w1, al1, m1);
+        }
+#pragma unroll
+        for (int p = 0; p < MP; ++p) {
+            const int e = p * 32 + hl;
+            if (e < E) {
+#pragma unroll
+                for (int j = 0; j < CH; ++j)
+                    *(reinterpret_cast<int2 *>(se + j * E + e) + (wlane ? 0 : 1)) = out[p][j];
+            }
+        }
+        if (lane == 0) {  // write event 0 carries every token's flag
+#pragma unroll
+            for (int q = 0; q < CH / 4; ++q)
+                reinterpret_cast<int4 *>(sf)[q] =
+                    make_int4(raw.w[0][4 * q].w, raw.w[0][4 * q + 1].w, raw.w[0][4 * q + 2].w, raw.w[0][4 * q + 3].w);
         }
     };
 
@@ -376,7 +452,7 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
     auto x_fetch = [&](int t0, Bits (&xb)[XI]) {
 #pragma unroll
         for (int k = 0; k < XI; ++k) {
-            const int it = min(tid + k * NST, CS * kChunk - 1);
+            const int it = min(tid + k * NST, CS * CH - 1);
             const int j = it / CS, c = it % CS;
             const int t = t0 + j < T ? t0 + j : T - 1;
             const int ch = c0 + c < C ? c0 + c : C - 1;
@@ -387,7 +463,7 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
         char *sx = stage_x(buf);
 #pragma unroll
         for (int k = 0; k < XI; ++k) {
-            const int it = min(tid + k * NST, CS * kChunk - 1);
+            const int it = min(tid + k * NST, CS * CH - 1);
             const int j = it / CS, c = it % CS;
             *reinterpret_cast<Bits *>(sx + c * XRB + j * ES) = xb[k];
         }
@@ -399,13 +475,13 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
         constexpr bool TAIL = decltype(tail_tag)::value;
         const StageRec *se = stage_e(buf);
         const char *sx = stage_x(buf);
-        int4 rec[NP][kChunk];
+        int4 rec[NP][CH];
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j)
+        for (int j = 0; j < CH; ++j)
 #pragma unroll
             for (int p = 0; p < NP; ++p)
                 rec[p][j] = *reinterpret_cast<const int4 *>(se + j * E + p * EPP + ev);
-        constexpr int XW = kChunk * ES / 16;  // 16-byte words per staged channel row
+        constexpr int XW = CH * ES / 16;  // 16-byte words per staged channel row
         uint4 xr[VEC][XW];
 #pragma unroll
         for (int v = 0; v < VEC; ++v)
@@ -428,13 +504,23 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
                 ykeep[q].v[v] = 0.f;
+        const int4 *sf4 = reinterpret_cast<const int4 *>(stage_f(buf));
+        int4 fl[CH / 4];
 #pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-            // writes: s <- s + g (x - s)
-            FVec<VEC> s[NP];
+        for (int q = 0; q < CH / 4; ++q)
+            fl[q] = sf4[q];
+        auto flag = [&](int j) {
+            const int4 q = fl[j / 4];
+            const int v = (j % 4) == 0 ? q.x : (j % 4) == 1 ? q.y : (j % 4) == 2 ? q.z : q.w;
+            return __builtin_amdgcn_readfirstlane(v);
+        };
+        auto load_rows = [&](int j, FVec<VEC> (&s)[NP]) {
 #pragma unroll
             for (int p = 0; p < NP; ++p)
                 s[p] = lds_load<VEC>(st + rec[p][j].x * RS + cl);
+        };
+        // writes s <- s + g (x - s) of token j, then its reads
+        auto token = [&](int j, const FVec<VEC> (&s)[NP]) {
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 const float g = __int_as_float(rec[p][j].y);
@@ -444,7 +530,6 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
                     o.v[v] = fmaf(g, x_at(v, j) - s[p].v[v], s[p].v[v]);
                 lds_store<VEC>(st + rec[p][j].x * RS + cl, o);
             }
-            // reads of the post-write state
             FVec<VEC> acc;
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
@@ -461,16 +546,28 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
             for (int v = 0; v < VEC; ++v)
                 acc.v[v] = event_sum<EPP>(acc.v[v]);
             // keep the sum in the lanes that store token j
-            const bool mine = EPP <= kChunk ? ev == j % EPP : ev % kChunk == j;
-            const int q = EPP <= kChunk ? j / EPP : 0;
+            const bool mine = EPP <= CH ? ev == j % EPP : ev % CH == j;
+            const int q = EPP <= CH ? j / EPP : 0;
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
                 ykeep[q].v[v] = mine ? acc.v[v] : ykeep[q].v[v];
+        };
+        // Token pairs: the second token's rows are read before the first
+        // token's writes, and read again if the write sets may overlap.
+#pragma unroll
+        for (int j0 = 0; j0 < CH; j0 += 2) {
+            FVec<VEC> s0[NP], s1[NP];
+            load_rows(j0, s0);
+            load_rows(j0 + 1, s1);
+            token(j0, s0);
+            if (flag(j0 + 1))
+                load_rows(j0 + 1, s1);
+            token(j0 + 1, s1);
         }
         // y of this chunk: lane stores tokens q * EPP + ev (or ev % 16)
 #pragma unroll
         for (int q = 0; q < NSL; ++q) {
-            const int j = EPP <= kChunk ? q * EPP + ev : ev % kChunk;
+            const int j = EPP <= CH ? q * EPP + ev : ev % CH;
             const int t = t0 + j;
             Scalar *yp = gy + static_cast<int64_t>(t) * C + c0 + cl;
             if constexpr (FAST) {
@@ -492,40 +589,46 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
     // past T.
     using Full = std::false_type;
     using Tail = std::true_type;
-    const int nc = geo.n_chunks;
-    const int n_full = T / kChunk;
-    Raw raw;
+    const int nc = (T + CH - 1) / CH;
+    const int n_full = T / CH;
+    auto clampc = [&](int c) { return (c < nc ? c : nc - 1) * CH; };
+    RawRegs rg;
     Bits xb[XI];
     __syncthreads();  // masses initialised before the mass wave starts
     if (nc > 0) {
-        if (mass_wave) {
-            mass_fetch(0, raw);
-            mass_chunk(0, raw);
-            mass_fetch((1 < nc ? 1 : nc - 1) * kChunk, raw);
-        } else {
+        if (!mass_wave) {
+            raw_fetch(0, rg);
+            raw_deposit(0, rg);
+            raw_fetch(clampc(1), rg);
+            raw_deposit(1, rg);
             x_fetch(0, xb);
             x_deposit(0, xb);
         }
+        __syncthreads();
+        if (mass_wave)
+            mass_chunk(0);
     }
     __syncthreads();
+    // Iteration ci: the state waves run chunk ci (stage ci & 1), fetch x of
+    // chunk ci + 1 and the raw records of chunk ci + 2; the mass wave stages
+    // chunk ci + 1 from the raw records deposited one iteration earlier.
     for (int ci = 0; ci < nc; ++ci) {
-        const int nxt = ci + 1 < nc ? ci + 1 : nc - 1;
         if (mass_wave) {
-            Raw cur = raw;
-            mass_fetch((ci + 2 < nc ? ci + 2 : nc - 1) * kChunk, raw);
             if (ci + 1 < nc)
-                mass_chunk((ci + 1) & 1, cur);
+                mass_chunk((ci + 1) & 1);
         } else {
-            // scheduling fences keep the x loads at the top and their use at
+            // scheduling fences keep the loads at the top and their use at
             // the bottom, so a whole chunk of work covers their latency
-            x_fetch(nxt * kChunk, xb);
+            x_fetch(clampc(ci + 1), xb);
+            raw_fetch(clampc(ci + 2), rg);
             __builtin_amdgcn_sched_barrier(0);
             if (ci < n_full)
-                state_chunk(ci & 1, ci * kChunk, Full{});
+                state_chunk(ci & 1, ci * CH, Full{});
             else
-                state_chunk(ci & 1, ci * kChunk, Tail{});
+                state_chunk(ci & 1, ci * CH, Tail{});
             __builtin_amdgcn_sched_barrier(0);
             x_deposit((ci + 1) & 1, xb);
+            raw_deposit(ci & 1, rg);
         }
         __syncthreads();
     }

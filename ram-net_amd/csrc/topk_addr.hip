@@ -42,7 +42,7 @@ __device__ const uint8_t kAddrAllValid = 1;
 // time (list in LDS).
 template<typename Scalar, int KM, typename Get>
 __device__ __forceinline__ void write_records(const AddrJob &job, int which, int64_t bh, int b, int t, int tl,
-                                              bool inactive, Get get, int K, int shift) {
+                                              bool inactive, Get get, int K, int shift, int overlap) {
     const int T = job.T, A = job.A;
     const int Tp = scan_t_pad(T);
     const uint8_t *mp = job.mask ? job.mask + static_cast<int64_t>(b) * T + tl : &kAddrAllValid;
@@ -56,9 +56,9 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
         o = o < 0 ? o + A : o;
         const bool act = live && v != 0.f;
         if (which == 0) {
-            WriteRec rec{-2, 0.f, 1.f, 0.f};
+            WriteRec rec{-2, 0.f, 1.f, __int_as_float(overlap)};
             if (act)
-                rec = WriteRec{o, v, gsu_alpha(v, g), 0.f};
+                rec = WriteRec{o, v, gsu_alpha(v, g), __int_as_float(overlap)};
             job.wrec[(bh * K + k) * Tp + t] = rec;
         } else {
             job.rrec[(bh * K + k) * Tp + t] = act ? ReadRec{o, v} : ReadRec{-1, 0.f};
@@ -111,10 +111,36 @@ __global__ __launch_bounds__(256) void topk_addr_lane_kernel(const AddrJob job) 
     }
     const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + tl], A) : 0;
     if (rec_mode) {
+        // Overlap flag of the write address: whether any written slot of this
+        // token is also written by token t - 1 (decoded by the previous lane;
+        // in another wave for lane 0, so assumed). The scan uses it to start a
+        // token's reads before the previous token's writes when they are
+        // disjoint.
+        int overlap = 0;
+        if (blockIdx.y == 0) {
+            const uint8_t *mp = job.mask ? job.mask + static_cast<int64_t>(b) * T + tl : &kAddrAllValid;
+            const bool live = t < T && *mp != 0 && !inactive;
+            int mine[KM], prev[KM];
+#pragma unroll
+            for (int k = 0; k < KM; ++k) {
+                int o = mi[k] - shift;
+                o = o < 0 ? o + A : o;
+                mine[k] = live && k < K ? o : -1;
+                prev[k] = __shfl_up(mine[k], 1);
+            }
+            bool hit = false;
+#pragma unroll
+            for (int k = 0; k < KM; ++k)
+#pragma unroll
+                for (int k2 = 0; k2 < KM; ++k2)
+                    hit = hit || (mine[k] >= 0 && mine[k] == prev[k2]);
+            const bool first_lane = (threadIdx.x & (kWave - 1)) == 0;
+            overlap = t > 0 && (hit || first_lane) ? 1 : 0;
+        }
         write_records<Scalar, KM>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
             c = mi[k];
             v = expf(mv[k] - src.re_norm * lse);
-        }, K, shift);
+        }, K, shift, overlap);
         return;
     }
     const int idx_base = (job.encode_batch_idx ? static_cast<int>(bh) : h) * A;
@@ -168,7 +194,7 @@ __global__ __launch_bounds__(256) void topk_addr_bruteforce_kernel(const AddrJob
             write_records<Scalar, 0>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
                 c = si[k];
                 v = expf(sv[k] - src.re_norm * s_lse);
-            }, K, shift);
+            }, K, shift, 1);  // overlap with token t - 1 not computed: assumed
         return;
     }
     const int idx_base = (job.encode_batch_idx ? static_cast<int>(bh) : h) * A;
