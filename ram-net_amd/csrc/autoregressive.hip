@@ -143,13 +143,38 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
             wrow[k][j] = row[cidx[j]];
         wm[k] = mass[wa[k]];
     }
+    // Forwarding: fwd[k] = the write event (nonzero weight) on read k's slot,
+    // or -1. One lane per (read, write) pair compares the slots; a ballot per
+    // 64 pairs collects the matches (top-K slots are distinct, so at most one
+    // write matches a read). The event tables are read unconditionally (both
+    // indices are below KE) and the conditions combined bitwise, so the
+    // comparison has no divergent branch.
+    static_assert((KE * KE) % kWave == 0, "forwarding rounds cover whole waves");
+#pragma unroll
+    for (int base = 0; base < KE * KE; base += kWave) {
+        const int l = base + lane;
+        const int k = (l / KE) % KE, j2 = l % KE;
+        const int ws = s_ws[j2], rs = s_rs[k];
+        const float wvj = s_wv[j2];
+        const bool match = (j2 < Kw) & (k < Kr) & (wvj != 0.f) & (ws == rs);
+        const uint64_t hits = __ballot(match);
+#pragma unroll
+        for (int k2 = 0; k2 < KE; ++k2) {
+            if (k2 * KE >= base && k2 * KE < base + kWave) {
+                const uint32_t bits =
+                    static_cast<uint32_t>(hits >> (k2 * KE - base)) & ((KE >= 32 ? 0u : (1u << KE)) - 1u);
+                // highest set bit, -1 when none, without a zero test:
+                // clz(2b + 1) = clz(b) - 1 for b != 0 and 31 for b = 0. (hipcc
+                // 7.2 turned `bits ? 31 - clz(bits) : -1` on the top field of
+                // the ballot into a 64-bit VALU compare and left the select
+                // reading a stale SCC, dropping those forwards.)
+                static_assert(KE <= 16, "2 * bits + 1 must fit 32 bits");
+                fwd[k2] = 30 - __builtin_clz(2u * bits + 1u);
+            }
+        }
+    }
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
-        fwd[k] = -1;
-#pragma unroll
-        for (int j2 = 0; j2 < KE; ++j2)
-            if (wv[j2] != 0.f && wa[j2] == ra[k])
-                fwd[k] = j2;
         // a slot written this step is read from the updated copy in LDS
         const float *row = slot + static_cast<int64_t>(ra[k]) * C;
 #pragma unroll

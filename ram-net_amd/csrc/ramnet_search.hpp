@@ -118,10 +118,12 @@ __device__ __forceinline__ float topk_lse_serial(const float *sv, int K) {
 // candidate is preceded by at least K candidates that dominate it in both
 // digits. Requires P <= GW and the candidate count of K to fit in GW lanes.
 
+// DPP move with bound_ctrl (lanes without a source read 0): every pattern
+// used here has a source in the same row for the lanes that keep the
+// result, and the form lets the compiler fold the move into its consumer.
 template<int CTRL>
 __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xf, 0xf,
-                                                             false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xf, 0xf, true));
 }
 
 // Value of lane (lane ^ J), J a power of two below 64.
@@ -157,15 +159,19 @@ __device__ __forceinline__ uint64_t lane_xor(uint64_t v) {
 
 // Butterfly reductions over GW lanes; every lane of the group ends with the
 // bitwise same result.
+// Maximum on order-preserving integer images of the floats (an integer max
+// folds the lane exchange into one instruction; fmaxf would canonicalise).
 template<int GW>
-__device__ __forceinline__ float group_max(float v) {
-    if constexpr (GW >= 2) v = fmaxf(v, lane_xor_f<1>(v));
-    if constexpr (GW >= 4) v = fmaxf(v, lane_xor_f<2>(v));
-    if constexpr (GW >= 8) v = fmaxf(v, lane_xor_f<4>(v));
-    if constexpr (GW >= 16) v = fmaxf(v, lane_xor_f<8>(v));
-    if constexpr (GW >= 32) v = fmaxf(v, lane_xor_f<16>(v));
-    if constexpr (GW >= 64) v = fmaxf(v, lane_xor_f<32>(v));
-    return v;
+__device__ __forceinline__ float group_max(float x) {
+    uint32_t v = ord32(__float_as_uint(x));
+    auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+    if constexpr (GW >= 2) v = mx(v, lane_xor<1>(v));
+    if constexpr (GW >= 4) v = mx(v, lane_xor<2>(v));
+    if constexpr (GW >= 8) v = mx(v, lane_xor<4>(v));
+    if constexpr (GW >= 16) v = mx(v, lane_xor<8>(v));
+    if constexpr (GW >= 32) v = mx(v, lane_xor<16>(v));
+    if constexpr (GW >= 64) v = mx(v, lane_xor<32>(v));
+    return __uint_as_float(unord32(v));
 }
 template<int GW>
 __device__ __forceinline__ float group_sum(float v) {
@@ -178,14 +184,28 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// Descending bitonic sort of one key per lane over GW lanes.
+// Descending bitonic sort of one key per lane over GW lanes. A 32-bit
+// compare-exchange is max, min and a lane-pattern select; a 64-bit one is
+// one 64-bit compare whose result is flipped on the lanes that keep the
+// smaller key.
+template<int J, int K2>
+__device__ __forceinline__ void ce_lane(uint32_t &key, int li) {
+    const uint32_t p = lane_xor<J>(key);
+    const bool keep_max = ((li & J) == 0) == ((li & K2) == 0);
+    const uint32_t hi = key > p ? key : p;
+    const uint32_t lo = key > p ? p : key;
+    key = keep_max ? hi : lo;
+}
+template<int J, int K2>
+__device__ __forceinline__ void ce_lane(uint64_t &key, int li) {
+    const uint64_t p = lane_xor<J>(key);
+    const bool keep_max = ((li & J) == 0) == ((li & K2) == 0);
+    const bool take = (p > key) == keep_max;
+    key = take ? p : key;
+}
 template<int GW, int K2, int J, typename Key>
 __device__ __forceinline__ void sort_step(Key &key, int li) {
-    const Key p = lane_xor<J>(key);
-    const bool keep_max = ((li & J) == 0) == ((li & K2) == 0);
-    const Key hi = key > p ? key : p;
-    const Key lo = key > p ? p : key;
-    key = keep_max ? hi : lo;
+    ce_lane<J, K2>(key, li);
     if constexpr (J > 1)
         sort_step<GW, K2, J / 2>(key, li);
 }
@@ -194,6 +214,21 @@ __device__ __forceinline__ void group_sort_desc(Key &key, int li) {
     sort_step<GW, K2, K2 / 2>(key, li);
     if constexpr (K2 < GW)
         group_sort_desc<GW, K2 * 2>(key, li);
+}
+// Two independent sorts interleaved stage by stage (each fills the other's
+// DPP wait states).
+template<int GW, int K2, int J, typename Key>
+__device__ __forceinline__ void sort_step2(Key &a, Key &b, int li) {
+    ce_lane<J, K2>(a, li);
+    ce_lane<J, K2>(b, li);
+    if constexpr (J > 1)
+        sort_step2<GW, K2, J / 2>(a, b, li);
+}
+template<int GW, int K2 = 2, typename Key>
+__device__ __forceinline__ void group_sort_desc2(Key &a, Key &b, int li) {
+    sort_step2<GW, K2, K2 / 2>(a, b, li);
+    if constexpr (K2 < GW)
+        group_sort_desc2<GW, K2 * 2>(a, b, li);
 }
 
 // Number of staircase candidates (i+1)(j+1) <= K.
@@ -284,42 +319,60 @@ __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int 
         }
     }
     const int g0 = (static_cast<int>(threadIdx.x) & (kWave - 1)) & ~(GW - 1);
+    const int ii = si_ < 0 ? 0 : si_;
+    const int jj = sj_ < 0 ? 0 : sj_;
     float cv = kNegInfF;  // prefix score of this lane's rank
     int ci = -1;          // its content slot, -1 = none
     bool inactive = false;
     int stride = 1;
-    for (int u = 0; u < U; ++u) {
-        const float x = lg.get(u, li);  // -inf for li >= P
-        const float mx = group_max<GW>(x);
-        inactive = inactive || !(mx > kNegInfF);
-        const float e = li < P ? __builtin_amdgcn_exp2f((x - mx) * kLog2e) : 0.f;
-        const float ls = logf(group_sum<GW>(e));
-        Key key = li < P ? group_digit_key<T>(x, li) : Key(0);
-        group_sort_desc<GW>(key, li);
+    // prefix x digit over the staircase -> new sorted prefix
+    auto combine = [&](float dv, int di) {
+        const float pv = __shfl(cv, g0 + ii);
+        const int pi = __shfl(ci, g0 + ii);
+        const float qv = __shfl(dv, g0 + jj);
+        const int qi = __shfl(di, g0 + jj);
+        const bool ok = si_ >= 0 && pi >= 0 && qi >= 0;
+        uint64_t ck = ok ? (static_cast<uint64_t>(ord32(__float_as_uint(pv + qv))) << 32) |
+                               (0xFFFFFFFFu - static_cast<uint32_t>(pi + stride * qi))
+                         : uint64_t(0);
+        group_sort_desc<GW>(ck, li);
+        cv = __uint_as_float(unord32(static_cast<uint32_t>(ck >> 32)));
+        ci = ck != 0 ? static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck)) : -1;
+    };
+    // digits two at a time: their statistics and sorts are independent
+    for (int u = 0; u < U; u += 2) {
+        const bool two = u + 1 < U;
+        const float xa = lg.get(u, li);  // -inf for li >= P
+        const float xb = two ? lg.get(u + 1, li) : kNegInfF;
+        const float mxa = group_max<GW>(xa);
+        const float mxb = group_max<GW>(xb);
+        inactive = inactive || !(mxa > kNegInfF) || (two && !(mxb > kNegInfF));
+        const float ea = li < P ? __builtin_amdgcn_exp2f((xa - mxa) * kLog2e) : 0.f;
+        const float eb = li < P ? __builtin_amdgcn_exp2f((xb - mxb) * kLog2e) : 0.f;
+        const float lsa = logf(group_sum<GW>(ea));
+        const float lsb = logf(group_sum<GW>(eb));
+        Key ka = li < P ? group_digit_key<T>(xa, li) : Key(0);
+        Key kb = li < P && two ? group_digit_key<T>(xb, li) : Key(0);
+        group_sort_desc2<GW>(ka, kb, li);
         float xs;
         int d;
-        group_digit_unkey<T>(key, xs, d);
-        const float dv = (xs - mx) - ls;  // this lane's rank of the digit
-        const int di = key != Key(0) ? d : -1;
+        group_digit_unkey<T>(ka, xs, d);
+        const float dva = (xs - mxa) - lsa;  // this lane's rank of digit u
+        const int dia = ka != Key(0) ? d : -1;
+        group_digit_unkey<T>(kb, xs, d);
+        const float dvb = (xs - mxb) - lsb;  // ... of digit u + 1
+        const int dib = kb != Key(0) ? d : -1;
         if (u == 0) {
-            cv = dv;
-            ci = di;
+            cv = dva;
+            ci = dia;
         } else {
-            const int ii = si_ < 0 ? 0 : si_;
-            const int jj = sj_ < 0 ? 0 : sj_;
-            const float pv = __shfl(cv, g0 + ii);
-            const int pi = __shfl(ci, g0 + ii);
-            const float qv = __shfl(dv, g0 + jj);
-            const int qi = __shfl(di, g0 + jj);
-            const bool ok = si_ >= 0 && pi >= 0 && qi >= 0;
-            uint64_t ck = ok ? (static_cast<uint64_t>(ord32(__float_as_uint(pv + qv))) << 32) |
-                                   (0xFFFFFFFFu - static_cast<uint32_t>(pi + stride * qi))
-                             : uint64_t(0);
-            group_sort_desc<GW>(ck, li);
-            cv = __uint_as_float(unord32(static_cast<uint32_t>(ck >> 32)));
-            ci = ck != 0 ? static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck)) : -1;
+            combine(dva, dia);
         }
         stride *= P;
+        if (two) {
+            combine(dvb, dib);
+            stride *= P;
+        }
     }
     const bool keep = li < K;
     out_v = keep ? cv : kNegInfF;
