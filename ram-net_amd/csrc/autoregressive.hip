@@ -48,7 +48,7 @@ __device__ __forceinline__ void finalize_events(float v, int c, bool inactive, i
         float sum = 0.f;
         for (int k = K - 1; k >= 0; --k)
             sum += __shfl(e, g0 + k);
-        lse = v0 + logf(sum);
+        lse = v0 + log_sum(sum);
     }
     if (li < K) {
         const int content = inactive ? li : c;

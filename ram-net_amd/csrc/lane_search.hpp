@@ -235,7 +235,7 @@ __device__ __forceinline__ bool digit_top(const Scalar *row, int64_t stride, int
 #pragma unroll
         for (int p = 0; p < s; ++p)
             e[p] += e[p + s];
-    const float ls = logf(e[0]);
+    const float ls = log_sum(e[0]);
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
         float xv;

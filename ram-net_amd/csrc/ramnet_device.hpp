@@ -34,6 +34,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
+// Natural logarithm as the hardware log2 (v_log_f32) times ln 2, for the
+// log-sum-exp terms of the address search. Its error (a few ulp) shifts every
+// candidate score of a digit, or every top-K value, by the same amount, so it
+// never changes a ranking; inputs are sums of exponentials >= 1.
+__device__ __forceinline__ float log_sum(float x) { return __builtin_amdgcn_logf(x) * 0.6931471805599453f; }
+
 __device__ __forceinline__ void store_f32(float *p, float v) { *p = v; }
 __device__ __forceinline__ void store_f32(_Float16 *p, float v) { *p = static_cast<_Float16>(v); }
 __device__ __forceinline__ void store_f32(bf16_t *p, float v) { p->bits = f32_to_bf16_bits(v); }

@@ -51,7 +51,7 @@ __device__ bool block_search_exact(const T *ptr, int64_t stride, int U, int P, i
         for (int s = NPD / 2; s >= 1; s >>= 1)
             for (int p = 0; p < s; ++p)
                 e[p] += e[p + s];
-        const float ls = logf(e[0]);
+        const float ls = log_sum(e[0]);
         for (int p = 0; p < P; ++p)
             lg[u * P + p] = (lg[u * P + p] - mx) - ls;
     }
@@ -105,7 +105,7 @@ __device__ __forceinline__ float topk_lse_serial(const float *sv, int K) {
     float sum = 0.f;
     for (int k = K - 1; k >= 0; --k)
         sum += expf(sv[k] - mx);
-    return mx + logf(sum);
+    return mx + log_sum(sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -157,30 +157,30 @@ __device__ __forceinline__ uint64_t lane_xor(uint64_t v) {
            lane_xor<J>(static_cast<uint32_t>(v));
 }
 
-// Butterfly reductions over GW lanes; every lane of the group ends with the
-// bitwise same result.
-// Maximum on order-preserving integer images of the floats (an integer max
-// folds the lane exchange into one instruction; fmaxf would canonicalise).
+// Value of the group's first lane (lane 0, or 32 for the upper half-wave).
 template<int GW>
-__device__ __forceinline__ float group_max(float x) {
-    uint32_t v = ord32(__float_as_uint(x));
-    auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
-    if constexpr (GW >= 2) v = mx(v, lane_xor<1>(v));
-    if constexpr (GW >= 4) v = mx(v, lane_xor<2>(v));
-    if constexpr (GW >= 8) v = mx(v, lane_xor<4>(v));
-    if constexpr (GW >= 16) v = mx(v, lane_xor<8>(v));
-    if constexpr (GW >= 32) v = mx(v, lane_xor<16>(v));
-    if constexpr (GW >= 64) v = mx(v, lane_xor<32>(v));
-    return __uint_as_float(unord32(v));
+__device__ __forceinline__ float group_first(float v) {
+    const int b = __float_as_int(v);
+    if constexpr (GW == 64) {
+        return __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    } else {
+        static_assert(GW == 32, "group_first: GW is 32 or 64");
+        const int lo = __builtin_amdgcn_readlane(b, 0), hi = __builtin_amdgcn_readlane(b, 32);
+        return __int_as_float((threadIdx.x & 32) ? hi : lo);
+    }
 }
+// Butterfly sum over GW lanes, widest exchange first; every lane of the group
+// ends with the bitwise same result. With zeros past the digit this is the
+// pairwise tree e[p] += e[p + s], s = NP/2 .. 1, of the per-lane decoder, so
+// both paths get the same log-sum-exp bit for bit.
 template<int GW>
 __device__ __forceinline__ float group_sum(float v) {
-    if constexpr (GW >= 2) v += lane_xor_f<1>(v);
-    if constexpr (GW >= 4) v += lane_xor_f<2>(v);
-    if constexpr (GW >= 8) v += lane_xor_f<4>(v);
-    if constexpr (GW >= 16) v += lane_xor_f<8>(v);
-    if constexpr (GW >= 32) v += lane_xor_f<16>(v);
     if constexpr (GW >= 64) v += lane_xor_f<32>(v);
+    if constexpr (GW >= 32) v += lane_xor_f<16>(v);
+    if constexpr (GW >= 16) v += lane_xor_f<8>(v);
+    if constexpr (GW >= 8) v += lane_xor_f<4>(v);
+    if constexpr (GW >= 4) v += lane_xor_f<2>(v);
+    if constexpr (GW >= 2) v += lane_xor_f<1>(v);
     return v;
 }
 
@@ -238,6 +238,30 @@ __host__ __device__ inline int staircase_count(int K) {
         n += K / i;
     return n;
 }
+
+// Staircase pairs of the prefix x digit combine for top-K (K = 1..16), in
+// (i, j) order: entry li of row K - 1 is (i << 4) | j of the li-th pair with
+// (i+1)(j+1) <= K, 0xFF past the last. A lookup replaces the per-lane search
+// with its integer divisions.
+constexpr int kStairMaxK = 16;
+struct StairTable {
+    uint8_t e[kStairMaxK][kWave];
+};
+constexpr StairTable make_stair_table() {
+    StairTable t{};
+    for (int K = 1; K <= kStairMaxK; ++K) {
+        int n = 0;
+        for (int i = 0; i < K; ++i)
+            for (int j = 0; (i + 1) * (j + 1) <= K; ++j)
+                t.e[K - 1][n++] = static_cast<uint8_t>((i << 4) | j);
+        for (; n < kWave; ++n)
+            t.e[K - 1][n] = 0xFF;
+    }
+    return t;
+}
+static_assert(make_stair_table().e[kStairMaxK - 1][49] != 0xFF && make_stair_table().e[kStairMaxK - 1][50] == 0xFF,
+              "50 staircase pairs for K = 16");
+__constant__ constexpr StairTable kStairTab = make_stair_table();
 
 // Logits of one address as seen by one lane of a GW-lane group: digit u,
 // radix li. The first kPreDigits digits are loaded up front in one batch
@@ -304,20 +328,10 @@ template<typename T, int GW>
 __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int li, float &out_v, int &out_i) {
     using Key = GroupKey<T>;
     constexpr float kLog2e = 1.4426950408889634f;
-    // staircase slot (si_, sj_) of this lane
-    int si_ = -1, sj_ = -1;
-    {
-        int q = li;
-        for (int i = 0; i < K; ++i) {
-            const int cnt = K / (i + 1);
-            if (q < cnt) {
-                si_ = i;
-                sj_ = q;
-                break;
-            }
-            q -= cnt;
-        }
-    }
+    // staircase slot (si_, sj_) of this lane (K <= 16 on this path)
+    const uint32_t st = kStairTab.e[(K < 1 ? 1 : K > kStairMaxK ? kStairMaxK : K) - 1][li];
+    const int si_ = st == 0xFFu ? -1 : static_cast<int>(st >> 4);
+    const int sj_ = st == 0xFFu ? -1 : static_cast<int>(st & 15u);
     const int g0 = (static_cast<int>(threadIdx.x) & (kWave - 1)) & ~(GW - 1);
     const int ii = si_ < 0 ? 0 : si_;
     const int jj = sj_ < 0 ? 0 : sj_;
@@ -344,24 +358,25 @@ __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int 
         const bool two = u + 1 < U;
         const float xa = lg.get(u, li);  // -inf for li >= P
         const float xb = two ? lg.get(u + 1, li) : kNegInfF;
-        const float mxa = group_max<GW>(xa);
-        const float mxb = group_max<GW>(xb);
-        inactive = inactive || !(mxa > kNegInfF) || (two && !(mxb > kNegInfF));
-        const float ea = li < P ? __builtin_amdgcn_exp2f((xa - mxa) * kLog2e) : 0.f;
-        const float eb = li < P ? __builtin_amdgcn_exp2f((xb - mxb) * kLog2e) : 0.f;
-        const float lsa = logf(group_sum<GW>(ea));
-        const float lsb = logf(group_sum<GW>(eb));
         Key ka = li < P ? group_digit_key<T>(xa, li) : Key(0);
         Key kb = li < P && two ? group_digit_key<T>(xb, li) : Key(0);
         group_sort_desc2<GW>(ka, kb, li);
-        float xs;
-        int d;
-        group_digit_unkey<T>(ka, xs, d);
-        const float dva = (xs - mxa) - lsa;  // this lane's rank of digit u
-        const int dia = ka != Key(0) ? d : -1;
-        group_digit_unkey<T>(kb, xs, d);
-        const float dvb = (xs - mxb) - lsb;  // ... of digit u + 1
-        const int dib = kb != Key(0) ? d : -1;
+        // the maxima are the group's first sorted entries
+        float xsa, xsb;
+        int da, db;
+        group_digit_unkey<T>(ka, xsa, da);
+        group_digit_unkey<T>(kb, xsb, db);
+        const float mxa = group_first<GW>(xsa);
+        const float mxb = two ? group_first<GW>(xsb) : kNegInfF;
+        inactive = inactive || !(mxa > kNegInfF) || (two && !(mxb > kNegInfF));
+        const float ea = li < P ? __builtin_amdgcn_exp2f((xa - mxa) * kLog2e) : 0.f;
+        const float eb = li < P ? __builtin_amdgcn_exp2f((xb - mxb) * kLog2e) : 0.f;
+        const float lsa = log_sum(group_sum<GW>(ea));
+        const float lsb = log_sum(group_sum<GW>(eb));
+        const float dva = (xsa - mxa) - lsa;  // this lane's rank of digit u
+        const int dia = ka != Key(0) ? da : -1;
+        const float dvb = (xsb - mxb) - lsb;  // ... of digit u + 1
+        const int dib = kb != Key(0) ? db : -1;
         if (u == 0) {
             cv = dva;
             ci = dia;

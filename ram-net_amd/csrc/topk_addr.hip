@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void topk_addr_lane_kernel(const AddrJob job) 
         for (int k = KM - 1; k >= 0; --k)
             if (k < K)
                 sum += expf(mv[k] - mv[0]);
-        lse = mv[0] + logf(sum);
+        lse = mv[0] + log_sum(sum);
     }
     const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + tl], A) : 0;
     if (rec_mode) {
