@@ -38,9 +38,21 @@ __device__ __forceinline__ float gsu_gain(float w, float d) {
     return w * r;
 }
 
-// Turn a group's sorted top list into (slot after CAPE, weight) events.
-__device__ __forceinline__ void finalize_events(float v, int c, bool inactive, int K, float re_norm, int li, int g0,
-                                                int shift, int A, int *slots, float *vals) {
+// Buffer resource word 3 for untyped 32-bit accesses on gfx9 parts.
+constexpr int kBufWord3 = 0x00020000;
+
+// 32-bit buffer accesses of fp32 data (the builtins move raw bits).
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buf_store_f32(float v, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff, 0);
+}
+
+// One event per lane from a group's sorted top list: (slot after CAPE,
+// weight), or (0, 0) on lanes past K.
+__device__ __forceinline__ void lane_event(float v, int c, bool inactive, int K, float re_norm, int li, int g0,
+                                           int shift, int A, int &slot, float &val) {
     float lse = 0.f;
     const float v0 = __shfl(v, g0);
     if (re_norm != 0.f && !inactive && v0 > kNegInfF) {
@@ -50,20 +62,32 @@ __device__ __forceinline__ void finalize_events(float v, int c, bool inactive, i
             sum += __shfl(e, g0 + k);
         lse = v0 + log_sum(sum);
     }
-    if (li < K) {
-        const int content = inactive ? li : c;
-        int o = content - shift;
-        o = o < 0 ? o + A : o;
-        slots[li] = o;
-        vals[li] = inactive ? 0.f : expf(v - re_norm * lse);
-    }
+    const int content = inactive ? li : c;
+    int o = content - shift;
+    o = o < 0 ? o + A : o;
+    slot = li < K ? o : 0;
+    val = li < K && !inactive ? expf(v - re_norm * lse) : 0.f;
 }
 
+// Value of `v` on lane L (L uniform; a constant after unrolling), as a
+// wave-uniform scalar.
+__device__ __forceinline__ float lane_f(float v, int L) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), L));
+}
+__device__ __forceinline__ int lane_i(int v, int L) { return __builtin_amdgcn_readlane(v, L); }
+
 // FULLC: C == 64 * kCpl, so every lane owns kCpl real channels.
+// Events live one per lane: write event k on lane k, read event k on lane
+// RB + k (RB = 32 when the two addresses share the wave as half-waves, else
+// 0 with separate registers). The event math (mass, alpha, gain) runs lane
+// parallel; each row's scalars are then broadcast with v_readlane. Rows and
+// masses of one (b, h) are addressed through buffer resources (32-bit
+// offsets; the launcher keeps A * C * 4 below 2^31).
 template<typename T, int GW, int KE, int kCpl, bool FULLC>
 __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob job) {
+    constexpr int RB = GW == 32 ? 32 : 0;
     __shared__ int s_ws[KE], s_rs[KE];
-    __shared__ float s_wv[KE], s_rv[KE];
+    __shared__ float s_wv[KE];
     __shared__ float s_row[KE][kWave * kCpl];
 
     const int bh = blockIdx.x;
@@ -82,17 +106,17 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
         lw.load(wp, U, P, lane);
         lr.load(rp, U, P, lane);
     }
-    int cidx[kCpl];
+    int coff[kCpl];  // byte offset of each owned channel (clamped into the row)
 #pragma unroll
     for (int j = 0; j < kCpl; ++j) {
         const int c = lane + j * kWave;
-        cidx[j] = FULLC || c < C ? c : C - 1;
+        coff[j] = (FULLC || c < C ? c : C - 1) * 4;
     }
     const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
     float xv[kCpl];
 #pragma unroll
     for (int j = 0; j < kCpl; ++j)
-        xv[j] = load_f32(xp + cidx[j]);
+        xv[j] = load_f32(xp + coff[j] / 4);
     const float gamma = load_f32(static_cast<const T *>(job.gamma) + bh);
     const int pos = job.position_ids[b];
     const uint8_t valid = job.mask ? job.mask[b] : 1;
@@ -102,47 +126,66 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
         return;
     }
     const int shift = h < job.embed_num ? pos_mod(pos, A) : 0;
+    const auto srs = __builtin_amdgcn_make_buffer_rsrc(job.slot + static_cast<int64_t>(bh) * A * C, 0, A * C * 4,
+                                                       kBufWord3);
+    const auto mrs = __builtin_amdgcn_make_buffer_rsrc(job.mass + static_cast<int64_t>(bh) * A, 0, A * 4, kBufWord3);
 
-    // ---- address decode
+    // ---- address decode: per-lane events, their masses, the slot tables
+    int ow, orr;      // write / read event slot of this lane
+    float vw, vr;     // their weights
+    float emw, emr;   // their pre-step masses
     if constexpr (GW == 32) {
         const int half = lane >> 5, li = lane & 31;
         const int K = half ? Kr : Kw;
         float v;
         int c;
         const bool inactive = group_search<T, 32>(lw, U, P, K, li, v, c);
-        finalize_events(v, c, inactive, K, half ? job.r_re_norm : job.w_re_norm, li, half * 32, shift, A,
-                        half ? s_rs : s_ws, half ? s_rv : s_wv);
+        lane_event(v, c, inactive, K, half ? job.r_re_norm : job.w_re_norm, li, half * 32, shift, A, ow, vw);
+        orr = ow;
+        vr = vw;
+        emw = buf_load_f32(mrs, ow * 4, 0);
+        emr = emw;
+        if (li < KE) {
+            (half ? s_rs : s_ws)[li] = ow;
+            if (!half)
+                s_wv[li] = vw;
+        }
     } else {
         float v;
         int c;
         bool inactive = group_search<T, 64>(lw, U, P, Kw, lane, v, c);
-        finalize_events(v, c, inactive, Kw, job.w_re_norm, lane, 0, shift, A, s_ws, s_wv);
+        lane_event(v, c, inactive, Kw, job.w_re_norm, lane, 0, shift, A, ow, vw);
+        emw = buf_load_f32(mrs, ow * 4, 0);
         inactive = group_search<T, 64>(lr, U, P, Kr, lane, v, c);
-        finalize_events(v, c, inactive, Kr, job.r_re_norm, lane, 0, shift, A, s_rs, s_rv);
+        lane_event(v, c, inactive, Kr, job.r_re_norm, lane, 0, shift, A, orr, vr);
+        emr = buf_load_f32(mrs, orr * 4, 0);
+        if (lane < KE) {
+            s_ws[lane] = ow;
+            s_wv[lane] = vw;
+            s_rs[lane] = orr;
+        }
     }
-    __syncthreads();
 
-    // ---- one batch of row requests
-    float *slot = job.slot + static_cast<int64_t>(bh) * A * C;
-    float *mass = job.mass + static_cast<int64_t>(bh) * A;
-    int wa[KE], ra[KE], fwd[KE];
-    float wv[KE], rv[KE], wm[KE], rm[KE];
+    // ---- one batch of row requests (row k's offset is a scalar)
+    const int rowb = C * 4;
     float wrow[KE][kCpl], rrow[KE][kCpl];
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
-        wa[k] = k < Kw ? s_ws[k] : 0;
-        wv[k] = k < Kw ? s_wv[k] : 0.f;
-        ra[k] = k < Kr ? s_rs[k] : 0;
-        rv[k] = k < Kr ? s_rv[k] : 0.f;
+        const int so = lane_i(ow, k) * rowb;
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j)
+            wrow[k][j] = buf_load_f32(srs, coff[j], so);
     }
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
-        const float *row = slot + static_cast<int64_t>(wa[k]) * C;
+        const int so = lane_i(orr, RB + k) * rowb;
 #pragma unroll
         for (int j = 0; j < kCpl; ++j)
-            wrow[k][j] = row[cidx[j]];
-        wm[k] = mass[wa[k]];
+            rrow[k][j] = buf_load_f32(srs, coff[j], so);
     }
+    // (one wave per workgroup: its LDS accesses complete in order, so the
+    // slot tables written above are visible to the reads below)
+    __builtin_amdgcn_wave_barrier();
     // Forwarding: fwd[k] = the write event (nonzero weight) on read k's slot,
     // or -1. One lane per (read, write) pair compares the slots; a ballot per
     // 64 pairs collects the matches (top-K slots are distinct, so at most one
@@ -150,6 +193,7 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
     // indices are below KE) and the conditions combined bitwise, so the
     // comparison has no divergent branch.
     static_assert((KE * KE) % kWave == 0, "forwarding rounds cover whole waves");
+    int fwd[KE];
 #pragma unroll
     for (int base = 0; base < KE * KE; base += kWave) {
         const int l = base + lane;
@@ -173,44 +217,37 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
             }
         }
     }
-#pragma unroll
-    for (int k = 0; k < KE; ++k) {
-        // a slot written this step is read from the updated copy in LDS
-        const float *row = slot + static_cast<int64_t>(ra[k]) * C;
-#pragma unroll
-        for (int j = 0; j < kCpl; ++j)
-            rrow[k][j] = row[cidx[j]];
-        rm[k] = mass[ra[k]];
-    }
-    // every row and mass load is in flight before the first write (the
-    // fence stops the scheduler from sinking loads into the write branches,
-    // where each would wait for its own data)
-    __builtin_amdgcn_sched_barrier(0);
-    // ---- writes. e^-|gamma| is shared by the events: alpha = num / den with
-    // the stable form of gsu_alpha, divided with one Newton-refined reciprocal.
+    // ---- write math, one write event per lane. e^-|gamma| is shared by the
+    // events: alpha = num / den with the stable form of gsu_alpha, divided
+    // with one Newton-refined reciprocal.
     const bool gpos = gamma >= 0.f;
     const float eg = expf(gpos ? -gamma : gamma);
+    const float cw = 1.f - vw;
+    const float den = gpos ? fmaf(eg, cw, vw) : fmaf(eg, vw, cw);
+    const float alpha = gsu_gain(gpos ? cw * eg : cw, den);
+    const float m2 = fmaf(alpha, emw, vw);
+    const float gain = gsu_gain(vw, m2 + job.eps);
+    const bool wlane = GW == 32 ? lane < 32 : true;
+    if (wlane && lane < Kw && vw != 0.f)
+        buf_store_f32(m2, mrs, ow * 4, 0);
+    // every row load is in flight before the first update (the fence stops
+    // the scheduler from sinking loads into the update branches, where each
+    // would wait for its own data)
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- row updates
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
-        const float w = wv[k];
-        if (w != 0.f) {
-            const float cw = 1.f - w;
-            const float den = gpos ? fmaf(eg, cw, w) : fmaf(eg, w, cw);
-            const float alpha = gsu_gain(gpos ? cw * eg : cw, den);
-            const float m2 = fmaf(alpha, wm[k], w);
-            const float g = gsu_gain(w, m2 + job.eps);
-            float *row = slot + static_cast<int64_t>(wa[k]) * C;
+        if (lane_f(vw, k) != 0.f) {
+            const float g = lane_f(gain, k);
+            const int so = lane_i(ow, k) * rowb;
 #pragma unroll
             for (int j = 0; j < kCpl; ++j) {
                 const int c = lane + j * kWave;
-                const float s = fmaf(g, xv[j] - wrow[k][j], wrow[k][j]);
-                s_row[k][c] = s;  // each lane re-reads only what it wrote
+                const float sv = fmaf(g, xv[j] - wrow[k][j], wrow[k][j]);
+                s_row[k][c] = sv;  // each lane re-reads only what it wrote
                 if (FULLC || c < C)
-                    row[c] = s;
+                    buf_store_f32(sv, srs, coff[j], so);
             }
-            if (lane == 0)
-                mass[wa[k]] = m2;
-            wm[k] = m2;
         }
     }
 
@@ -228,14 +265,20 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
             sval[k][j] = f >= 0 ? lv : rrow[k][j];
         }
     }
-    float rw[KE];  // read weights (mass-aware: r * post-write mass)
+    float rv[KE], rw[KE];  // read weights (mass-aware: r * post-write mass)
 #pragma unroll
-    for (int k = 0; k < KE; ++k)
+    for (int k = 0; k < KE; ++k) {
+        rv[k] = lane_f(vr, RB + k);
         rw[k] = rv[k];
+    }
     if (job.mass_aware) {
+        float wm[KE];
+#pragma unroll
+        for (int k = 0; k < KE; ++k)
+            wm[k] = lane_f(m2, k);
 #pragma unroll
         for (int k = 0; k < KE; ++k) {
-            float m = rm[k];
+            float m = lane_f(emr, RB + k);
 #pragma unroll
             for (int j2 = 0; j2 < KE; ++j2)
                 m = fwd[k] == j2 ? wm[j2] : m;
@@ -359,7 +402,8 @@ template<typename T>
 hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **why) {
     const int kmax = std::max(job.Kw, job.Kr);
     const int stair = staircase_count(kmax);
-    const bool fast_ok = job.P <= 64 && kmax <= kEv && job.C <= kWave * kMaxCpl && stair <= 64;
+    const bool fast_ok = job.P <= 64 && kmax <= kEv && job.C <= kWave * kMaxCpl && stair <= 64 &&
+                         static_cast<int64_t>(job.A) * job.C * 4 <= INT32_MAX;
     const unsigned grid = static_cast<unsigned>(job.B * job.H);
     if (fast_ok) {
         const bool half = job.P <= 32 && stair <= 32;
