@@ -431,7 +431,7 @@ hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **w
     const size_t lds = static_cast<size_t>(job.U) * job.P * 4 + static_cast<size_t>(job.U) * NPD * 4 +
                        static_cast<size_t>(NA) * 8 + static_cast<size_t>(job.Kw + job.Kr) * 8;
     if (lds > 96 * 1024) {
-        *why = "decode step: shape needs P <= 64, top_k <= 16 and C <= 256, or P**U small enough for the exact LDS search (A <= 8192)";
+        *why = "decode step: shape needs P <= 64, top_k <= 16, C <= 256 and A*C*4 < 2^31, or P**U small enough for the exact LDS search (A <= 8192)";
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(autoregressive_general_kernel<T>, dim3(grid), dim3(kWave), lds, stream, job, NA, NPD);
