@@ -16,7 +16,12 @@ restatement of the reference's dense PyTorch algorithm on a bounded sample of
 the same inputs (rank 0, N=1 only).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S]
-       [--no-cpu-baseline] [--only prefill|decode] [--copy-probe MIB]
+       [--no-cpu-baseline] [--no-stress] [--only prefill|decode|stress]
+       [--copy-probe MIB]
+
+Config 4 (B=4, H=8, T=8192, U=3, P=16 -> A=4096, K=16) and its tie-heavy
+variant (decoder logits quantised to multiples of 0.25) are timed the same
+way and reported under ``stress``.
 
 ``--copy-probe MIB`` first runs one plain device-to-device copy of MIB MiB
 (torch ``copy_``, fp32): under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``
@@ -44,9 +49,12 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "segment_scan_traffic_c2.json")
 METRIC = "prefill tokens/s (T=4096) + decode tokens/s (B=64); % HBM roofline"
 
-# config 2 (prefill) and config 3 (decode)
-C2 = dict(B=8, H=16, T=4096, C=128, U=2, P=32, K=8, d_k=128, seed=2)
+# config 2 (prefill), config 3 (decode), config 4 (stress prefill; tie-heavy
+# variant: decoder logits quantised to multiples of 0.25)
+C2 = dict(B=8, H=16, T=4096, C=128, U=2, P=32, K=8, d_k=128, seed=2, embed=8, gamma_shift=-1.0, quant=None)
 C3 = dict(B=64, H=16, C=128, U=2, P=32, K=8, steps=512, seed=3)
+C4 = dict(B=4, H=8, T=8192, C=128, U=3, P=16, K=16, d_k=128, seed=4, embed=4, gamma_shift=0.0, quant=None)
+C4_TIES = dict(C4, quant=0.25)
 
 
 def log(msg: str) -> None:
@@ -65,30 +73,31 @@ def event_model_bytes(U, P, C, K, H, s_a=2) -> dict:
     return {"op": op, "segment": seg}
 
 
-def make_prefill_inputs(dev):
+def make_prefill_inputs(dev, c=C2):
     from ram_cases import projected_logits
-    c = C2
     B, H, T, C, U, P = c["B"], c["H"], c["T"], c["C"], c["U"], c["P"]
-    w, r = projected_logits(B, H, U, P, T, c["d_k"], seed=c["seed"], dtype=torch.bfloat16)
+    w, r = projected_logits(B, H, U, P, T, c["d_k"], seed=c["seed"], dtype=torch.float32)
+    if c["quant"]:
+        w, r = (torch.round(v / c["quant"]) * c["quant"] for v in (w, r))
+    w, r = w.to(torch.bfloat16), r.to(torch.bfloat16)
     g = torch.Generator().manual_seed(c["seed"] + 100)
     x = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16)
-    gamma = torch.sigmoid(torch.randn(B, H, T, generator=g) - 1).to(torch.bfloat16)
+    gamma = torch.sigmoid(torch.randn(B, H, T, generator=g) + c["gamma_shift"]).to(torch.bfloat16)
     pos = torch.arange(T, dtype=torch.int32).view(1, T).expand(B, T).contiguous()
     host = dict(w=w, r=r, x=x, gamma=gamma, pos=pos)
     devd = {k: v.to(dev) for k, v in host.items()}
     return host, devd
 
 
-def bench_prefill(steps, warmup, dev):
-    """Config 2 through the product path's two native stages (what the fused
-    ``ram_attn_forward`` op runs): record decoder, then the segment scan."""
+def bench_prefill(steps, warmup, dev, c=C2):
+    """A prefill config through the product path's two native stages (what the
+    fused ``ram_attn_forward`` op runs): record decoder, then the segment scan."""
     import ramnet_ops  # noqa: F401
     from ramnet_ops import _native as nat
-    c = C2
     B, H, T, C, U, P, K = c["B"], c["H"], c["T"], c["C"], c["U"], c["P"], c["K"]
     A = P ** U
-    E = H // 2
-    host, d = make_prefill_inputs(dev)
+    E = c["embed"]
+    host, d = make_prefill_inputs(dev, c)
     slot0 = torch.zeros(B, H, A, C, device=dev)
     mass0 = torch.full((B, H, A), 1.0 / A, device=dev)
     slot = torch.empty_like(slot0)
@@ -287,7 +296,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--only", choices=("prefill", "decode"), default=None)
+    ap.add_argument("--only", choices=("prefill", "decode", "stress"), default=None)
+    ap.add_argument("--no-stress", action="store_true", help="skip the config-4 stress prefill lines")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -319,6 +329,26 @@ def main(argv=None) -> int:
         pre = bench_prefill(args.steps, args.warmup, dev)
         log(f"prefill: {pre['ms_per_step']:.3f} ms/step, segment {pre['segment_ms']:.3f} ms, "
             f"decoder {pre['decoder_ms']:.3f} ms")
+    stress = {}
+    if args.only == "stress" or (args.only is None and not args.no_stress):
+        for name, c in (("config4", C4), ("config4_tie_heavy", C4_TIES)):
+            log(f"stress: {name} prefill")
+            st = bench_prefill(max(3, args.steps // 4), 1, dev, c)
+            st.pop("host")
+            seg_gbs = st["segment_bytes"] / (st["segment_ms"] / 1e3) / 1e9
+            stress[name] = {
+                "workload": f"B={c['B']}, H={c['H']}, T={c['T']}, d_v={c['C']}, U={c['U']}, P={c['P']} "
+                            f"(A={c['P'] ** c['U']}), K={c['K']}, CAPE on {c['embed']} heads, "
+                            f"gamma=sigmoid(N(0,1)), logits quantised to {c['quant']}" if c["quant"] else
+                            f"B={c['B']}, H={c['H']}, T={c['T']}, d_v={c['C']}, U={c['U']}, P={c['P']} "
+                            f"(A={c['P'] ** c['U']}), K={c['K']}, CAPE on {c['embed']} heads, gamma=sigmoid(N(0,1))",
+                "tokens_per_s": st["tokens_per_s"], "ms_per_step": st["ms_per_step"],
+                "decoder_ms": st["decoder_ms"], "segment_ms": st["segment_ms"],
+                "op_roofline_frac": st["op_roofline_frac"],
+                "segment_roofline_frac": seg_gbs / HBM_PEAK_GBS, "op_bytes_per_step": st["op_bytes"],
+            }
+            log(f"stress: {name} {st['ms_per_step']:.3f} ms/step = {st['tokens_per_s'] / 1e6:.1f} M tokens/s, "
+                f"segment {st['segment_ms']:.3f} ms, decoder {st['decoder_ms']:.3f} ms")
     if args.only in (None, "decode"):
         log("decode: config 3, graph-captured steps")
         dec = bench_decode(args.decode_steps, dev, graph=not args.no_graph)
@@ -380,6 +410,14 @@ def main(argv=None) -> int:
                         "warmup": 1, "ms_per_step": dec["ms_per_step"], "higher_is_better": True,
                         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
                         "config": {"workload": "config 3 decode: B=64, H=16, A=1024, d_v=128, K=8, 512 steps"}})
+    if stress:
+        out["stress"] = stress
+        if pre is None and dec is None:
+            st = stress["config4"]
+            out.update({"value": st["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": max(3, args.steps // 4),
+                        "warmup": 1, "ms_per_step": st["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+                        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                        "config": {"workload": "config 4 stress prefill: " + st["workload"]}})
     if pre is not None and not args.no_cpu_baseline:
         log("cpu baseline: dense reference algorithm on host cores")
         out["cpu_baseline"] = cpu_baseline(pre["host"], target_s=args.cpu_seconds)

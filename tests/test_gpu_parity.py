@@ -430,3 +430,46 @@ def test_config2_full_size_subset():
         assert oracle.rel_err(slot.cpu()[sl], rslot) <= FP32_TOL, f"slot (b={b}, h={h})"
         assert oracle.rel_err(mass.cpu()[sl], rmass) <= FP32_TOL, f"mass (b={b}, h={h})"
         assert oracle.rel_err(y.cpu()[sl], ry) <= LOW_TOL, f"y (b={b}, h={h})"
+
+
+@pytest.mark.parametrize("tie_heavy", [False, True])
+def test_config4_full_size_subset(tie_heavy):
+    """Config 4 at full size (B=4, H=8, T=8192, U=3, P=16 -> A=4096, K=16, bf16).
+
+    Indices on a token subset against the fp64 ranking (near ties exempt),
+    outputs and state on two heads against the fp64 event loop on the GPU's
+    selection. The tie-heavy variant quantises the decoder logits to
+    multiples of 0.25, so exact score ties are everywhere.
+    """
+    ops = _ops()
+    B, H, U, P, T, C, K, E = 4, 8, 3, 16, 8192, 128, 16, 4
+    A = P ** U
+    print(f"config 4 full size, tie_heavy={tie_heavy}", flush=True)
+    w, r = projected_logits(B, H, U, P, T, 128, seed=4, dtype=torch.float32)
+    if tie_heavy:
+        w, r = (torch.round(v / 0.25) * 0.25 for v in (w, r))
+    w, r = w.to(torch.bfloat16), r.to(torch.bfloat16)
+    g = torch.Generator().manual_seed(40)
+    x = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16)
+    gamma = torch.sigmoid(torch.randn(B, H, T, generator=g)).to(torch.bfloat16)
+    pos = torch.arange(T).view(1, T).expand(B, T)
+    idx, val = ops.topk_addr_forward(w.to(DEV), r.to(DEV), E, A, pos.to(DEV), K, K, 0.0, 0.0)
+    slot0 = torch.zeros(B, H, A, C, device=DEV)
+    mass0 = torch.full((B, H, A), 1.0 / A, device=DEV)
+    y, slot, mass = ops.topk_segment_forward(idx, val, x.to(DEV), gamma.to(DEV), slot0, mass0, None, K, K, False, 1e-12)
+    torch.cuda.synchronize()
+    idx_c, val_c = idx.cpu(), val.cpu()
+    ts = slice(0, T, 127)
+    for lg, rows in ((w, slice(0, K)), (r, slice(K, 2 * K))):
+        stats = oracle.check_topk_indices(idx_c[:, :, rows, ts], lg[..., ts], E, pos[:, ts], K)
+        print("index check", stats, flush=True)
+    for b, h in ((0, 0), (3, 7)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        base = (b * H + h) * A
+        wi, wv, ri, rv = oracle.split_events(idx_c[sl] - base, val_c[sl], K)
+        ry, rslot, rmass = oracle.sparse_gsu_f64(wi, wv, ri, rv, x[sl].double(), gamma[sl].double(),
+                                                 torch.zeros(1, 1, A, C), torch.full((1, 1, A), 1.0 / A),
+                                                 None, False, 1e-12, encoded=False)
+        assert oracle.rel_err(slot.cpu()[sl], rslot) <= FP32_TOL, f"slot (b={b}, h={h})"
+        assert oracle.rel_err(mass.cpu()[sl], rmass) <= FP32_TOL, f"mass (b={b}, h={h})"
+        assert oracle.rel_err(y.cpu()[sl], ry) <= LOW_TOL, f"y (b={b}, h={h})"
