@@ -16,12 +16,14 @@ restatement of the reference's dense PyTorch algorithm on a bounded sample of
 the same inputs (rank 0, N=1 only).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S]
-       [--no-cpu-baseline] [--no-stress] [--only prefill|decode|stress]
-       [--copy-probe MIB]
+       [--no-cpu-baseline] [--no-stress] [--no-lm] [--lm-tokens N]
+       [--only prefill|decode|stress|lm] [--copy-probe MIB]
 
 Config 4 (B=4, H=8, T=8192, U=3, P=16 -> A=4096, K=16) and its tie-heavy
 variant (decoder logits quantised to multiples of 0.25) are timed the same
-way and reported under ``stress``.
+way and reported under ``stress``. Config 5 (the caller harness: a 24-block
+RAM-Net LM, prompt 16 x 2048, greedy in-place decode) is reported under
+``lm``.
 
 ``--copy-probe MIB`` first runs one plain device-to-device copy of MIB MiB
 (torch ``copy_``, fp32): under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``
@@ -55,6 +57,10 @@ C2 = dict(B=8, H=16, T=4096, C=128, U=2, P=32, K=8, d_k=128, seed=2, embed=8, ga
 C3 = dict(B=64, H=16, C=128, U=2, P=32, K=8, steps=512, seed=3)
 C4 = dict(B=4, H=8, T=8192, C=128, U=3, P=16, K=16, d_k=128, seed=4, embed=4, gamma_shift=0.0, quant=None)
 C4_TIES = dict(C4, quant=0.25)
+# config 5 (caller harness): a 24-block RAM-Net LM, prompt 16 x 2048, then
+# greedy single-token steps with in-place per-layer state
+C5 = dict(layers=24, d_model=1024, heads=8, C=128, U=2, P=32, K=8, vocab=32000, embed=4, mlp=2816, B=16, T=2048,
+          new=256, seed=5)
 
 
 def log(msg: str) -> None:
@@ -243,6 +249,72 @@ def bench_decode(n_steps, dev, graph=True):
     }
 
 
+def bench_lm(dev, new_tokens):
+    """Config 5 through the caller harness (``ramnet_harness``): one prefill of
+    the prompt with fresh states, then greedy decode steps captured as one HIP
+    graph per step (model forward + in-place state update + argmax), replayed."""
+    from ramnet_harness import HarnessConfig, RamLM
+    c = C5
+    cfg = HarnessConfig(vocab=c["vocab"], layers=c["layers"], d_model=c["d_model"], heads=c["heads"],
+                        value_chs=c["C"], addr_order=c["U"], addr_radix=c["P"], top_k=c["K"], embed_num=c["embed"],
+                        mlp_width=c["mlp"], dtype=torch.bfloat16)
+    torch.manual_seed(c["seed"])
+    model = RamLM(cfg)
+    model.init_weights()
+    model = model.to(device=dev, dtype=torch.bfloat16).eval()
+    B, T = c["B"], c["T"]
+    g = torch.Generator(device=dev).manual_seed(c["seed"])
+    prompt = torch.randint(0, c["vocab"], (B, T), device=dev, generator=g)
+    pos = torch.arange(T, device=dev).view(1, T).expand(B, T)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.no_grad():
+        model(prompt[:, :256], model.fresh_state(B, dev), pos[:, :256], inplace=False)  # library warm-up
+        states = model.fresh_state(B, dev)
+        torch.cuda.synchronize()
+        e0.record()
+        logits, states = model(prompt, states, pos, inplace=False)
+        e1.record()
+        torch.cuda.synchronize()
+        prefill_ms = e0.elapsed_time(e1)
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        p = torch.full((B, 1), T, device=dev, dtype=torch.long)
+
+        def step():
+            lg, _ = model(tok, states, p, inplace=True)
+            tok.copy_(lg[:, -1].argmax(-1, keepdim=True))
+            p.add_(1)
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()  # warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        n = max(1, new_tokens - 2)
+        e0.record()
+        for _ in range(n):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        step_ms = e0.elapsed_time(e1) / n
+    finite = all(bool(torch.isfinite(sl).all()) for sl, _ in states)
+    return {
+        "workload": f"config 5 harness: {c['layers']} blocks, d_model={c['d_model']}, H={c['heads']}, d_v={c['C']}, "
+                    f"A={c['P'] ** c['U']} (U={c['U']}, P={c['P']}), K={c['K']}, vocab={c['vocab']}, SwiGLU width "
+                    f"{c['mlp']}, bf16 weights (random init), prompt {B} x {T}, {new_tokens} greedy tokens",
+        "prefill_ms": prefill_ms,
+        "prefill_tokens_per_s": B * T / (prefill_ms / 1e3),
+        "decode_ms_per_step": step_ms,
+        "decode_tokens_per_s": B / (step_ms / 1e3),
+        "decode_mode": "hip-graph per step",
+        "state_finite": finite,
+    }
+
+
 def cpu_baseline(host, target_s=12.0, batch_rows=None):
     """Dense reference algorithm (oracle restatement) on host cores over a bounded sample of the C2 inputs.
 
@@ -296,7 +368,9 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--only", choices=("prefill", "decode", "stress"), default=None)
+    ap.add_argument("--only", choices=("prefill", "decode", "stress", "lm"), default=None)
+    ap.add_argument("--no-lm", action="store_true", help="skip the config-5 model harness line")
+    ap.add_argument("--lm-tokens", type=int, default=C5["new"])
     ap.add_argument("--no-stress", action="store_true", help="skip the config-4 stress prefill lines")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
     args = ap.parse_args(argv)
@@ -410,6 +484,18 @@ def main(argv=None) -> int:
                         "warmup": 1, "ms_per_step": dec["ms_per_step"], "higher_is_better": True,
                         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
                         "config": {"workload": "config 3 decode: B=64, H=16, A=1024, d_v=128, K=8, 512 steps"}})
+    lm = None
+    if args.only == "lm" or (args.only is None and not args.no_lm):
+        log("lm: config 5 harness (prefill, then graph-captured greedy steps)")
+        lm = bench_lm(dev, args.lm_tokens)
+        log(f"lm: prefill {lm['prefill_ms']:.1f} ms = {lm['prefill_tokens_per_s'] / 1e6:.2f} M tokens/s, "
+            f"decode {lm['decode_ms_per_step']:.3f} ms/step = {lm['decode_tokens_per_s']:.0f} tokens/s")
+        out["lm"] = lm
+        if args.only == "lm":
+            out.update({"value": lm["prefill_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": 1,
+                        "warmup": 1, "ms_per_step": lm["prefill_ms"], "higher_is_better": True, "scaling": "weak",
+                        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+                        "config": {"workload": lm["workload"]}})
     if stress:
         out["stress"] = stress
         if pre is None and dec is None:
