@@ -22,7 +22,10 @@
 //
 // This file holds the planner: it picks the lane layout (events per pass,
 // channels per lane) for top-K and the slice width that lets the most units
-// share a CU's LDS, then dispatches to the per-dtype kernels.
+// share a CU's LDS, then dispatches to the per-dtype kernels. For wide slot
+// spaces it can first run the mass pre-pass (segment_mass_kernel): the mass
+// recurrence once per (b, h) instead of once per channel slice, which frees
+// the LDS mass column so each slice holds twice the channels.
 #include "ramnet_device.hpp"
 #include "ramnet_kernels.hpp"
 #include "segment_scan.hpp"
@@ -63,6 +66,7 @@ int dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 struct Plan {
     int vec, epp, np, nw, cs;
     size_t lds;
+    bool pre;  // mass pre-pass + precomputed-gain scan
 };
 
 // Cost model of one layout, in cycles per token of one round of resident
@@ -71,6 +75,10 @@ struct Plan {
 // work (~10 + 6 * VEC * NP instructions, 4 cycles each, shared by the waves
 // on one SIMD), whichever is longer. Total = rounds * per-token cycles.
 constexpr int64_t kChainCycles = 160;
+// The mass pre-pass: one wave per (b, h) walks the sequence with the masses
+// in LDS; its token chain is one LDS read-modify-write (~kMassChainCycles).
+constexpr int64_t kMassChainCycles = 120;
+constexpr int64_t kMassPassLds = 64 * 1024;  // A <= 16382
 
 bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, Plan *out) {
     const int kmax = std::max(Kw, Kr);
@@ -79,34 +87,39 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, P
     const int epp0 = std::min(kWave, std::max(4, pow2_ceil(kmax)));
     bool found = false;
     int64_t best = 0;
-    for (int epp = 4; epp <= kWave; epp <<= 1) {
-        const int np = (kmax + epp - 1) / epp;
-        if (np > 2 || (np == 2 && epp * 2 < epp0))
-            continue;
-        for (int nw = 4; nw >= 1; nw >>= 1) {
-            for (int vec = 4; vec >= 1; vec >>= 1) {
-                if (!scan_layout_compiled(vec, epp, np, nw))
-                    continue;
-                const int cs = nw * (kWave / epp) * vec;
-                const size_t lds = scan_lds_bytes(A, vec, epp, np, nw, elem);
-                const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
-                if (gran > kLdsPerCu)
-                    continue;
-                const int64_t units = static_cast<int64_t>(B) * H * ((C + cs - 1) / cs);
-                const int64_t per_cu = std::min<int64_t>(kLdsPerCu / gran, std::max(1, 8 / nw));
-                const int64_t rounds = (units + per_cu * n_cu - 1) / (per_cu * n_cu);
-                const int64_t resident = std::min<int64_t>(per_cu, (units + n_cu - 1) / n_cu);
-                const int64_t waves_per_simd = (resident * nw + 3) / 4;
-                const int64_t issue = 4 * (10 + 6 * vec * np) * waves_per_simd;
-                int64_t cost = rounds * std::max(kChainCycles, issue);
-                if (C % cs != 0)
-                    cost = cost * 3 / 2;  // partial slices take the guarded path
-                const bool better = !found || cost < best ||
-                                    (cost == best && (nw > out->nw || (nw == out->nw && cs > out->cs)));
-                if (better) {
-                    *out = {vec, epp, np, nw, cs, lds};
-                    best = cost;
-                    found = true;
+    const bool pre_ok = static_cast<int64_t>(A + 2) * 4 <= kMassPassLds;
+    for (int pre = 0; pre <= (pre_ok ? 1 : 0); ++pre) {
+        for (int epp = 4; epp <= kWave; epp <<= 1) {
+            const int np = (kmax + epp - 1) / epp;
+            if (np > 2 || (np == 2 && epp * 2 < epp0))
+                continue;
+            for (int nw = 4; nw >= 1; nw >>= 1) {
+                for (int vec = 4; vec >= 1; vec >>= 1) {
+                    if (!scan_layout_compiled(vec, epp, np, nw, pre))
+                        continue;
+                    const int cs = nw * (kWave / epp) * vec;
+                    const size_t lds = scan_lds_bytes(A, vec, epp, np, nw, elem, pre);
+                    const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
+                    if (gran > kLdsPerCu)
+                        continue;
+                    const int64_t units = static_cast<int64_t>(B) * H * ((C + cs - 1) / cs);
+                    const int64_t per_cu = std::min<int64_t>(kLdsPerCu / gran, std::max(1, 8 / nw));
+                    const int64_t rounds = (units + per_cu * n_cu - 1) / (per_cu * n_cu);
+                    const int64_t resident = std::min<int64_t>(per_cu, (units + n_cu - 1) / n_cu);
+                    const int64_t waves_per_simd = (resident * nw + 3) / 4;
+                    const int64_t issue = 4 * (10 + 6 * vec * np) * waves_per_simd;
+                    int64_t cost = rounds * std::max(kChainCycles, issue);
+                    if (C % cs != 0)
+                        cost = cost * 3 / 2;  // partial slices take the guarded path
+                    if (pre)  // one wave per (b, h); several fit a CU
+                        cost += (static_cast<int64_t>(B) * H + 4 * n_cu - 1) / (4 * n_cu) * kMassChainCycles;
+                    const bool better = !found || cost < best ||
+                                        (cost == best && (nw > out->nw || (nw == out->nw && cs > out->cs)));
+                    if (better) {
+                        *out = {vec, epp, np, nw, cs, lds, pre != 0};
+                        best = cost;
+                        found = true;
+                    }
                 }
             }
         }
@@ -153,6 +166,155 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
     }
 }
 
+// Mass pre-pass: the slot-mass recurrence of one (b, h) over the whole
+// sequence (m <- alpha m + w per write event, in token order), once per
+// head. Each write record's alpha field is replaced by its gain
+// g = w / (m + eps); mass-aware, each read record's weight by its effective
+// weight (sum r) (m r) / (sum m r + eps) on the post-write masses. The masses
+// live in LDS; lanes 0..31 take write events p * 32 + lane and lanes 32..63
+// read events p * 32 + lane - 32. Tokens go in pairs like the scan's mass
+// wave: the second token's masses are read before the first token's writes
+// and again only when the two write sets may overlap. Records of the next
+// chunk are fetched while the current one is processed.
+template<bool MA, int MP>
+__global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, WriteRec *wrec, ReadRec *rrec,
+                                                            int t_pad) {
+    constexpr int CH = MP <= 1 ? 16 : MP == 2 ? 8 : 4;  // tokens per fetch
+    extern __shared__ __align__(16) float lds[];
+    const int bh = blockIdx.x;
+    const int lane = static_cast<int>(threadIdx.x);
+    const int hl = lane & 31;
+    const bool wlane = lane < 32;
+    const int A = job.A, T = job.T, Kw = job.Kw, Kr = job.Kr;
+    const float eps = job.eps;
+    float *ms = lds + 2;  // ms[-2], ms[-1]: the no-op slots of padding records
+    const float *msrc = job.init_mass + static_cast<int64_t>(bh) * A;
+    for (int a = lane; a < A; a += kWave)
+        ms[a] = msrc[a];
+    if (lane < 2)
+        lds[lane] = 1.f;
+    __syncthreads();
+
+    WriteRec *gw = wrec + static_cast<int64_t>(bh) * Kw * t_pad;
+    ReadRec *gr = rrec + static_cast<int64_t>(bh) * Kr * t_pad;
+    int ev[MP];     // this lane's event (clamped for loads)
+    bool on[MP];    // whether it is a real event
+#pragma unroll
+    for (int p = 0; p < MP; ++p) {
+        const int e = p * 32 + hl;
+        on[p] = wlane ? e < Kw : e < Kr;
+        ev[p] = wlane ? min(e, Kw - 1) : min(e, Kr - 1);
+    }
+    struct Chunk {
+        int4 w[MP][CH];
+        int2 r[MP][CH];
+    };
+    auto fetch = [&](int t0, Chunk &c) {
+#pragma unroll
+        for (int p = 0; p < MP; ++p)
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int t = min(t0 + j, t_pad - 1);
+                if (wlane)
+                    c.w[p][j] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ev[p]) * t_pad + t);
+                else
+                    c.r[p][j] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(ev[p]) * t_pad + t);
+            }
+    };
+    auto run = [&](int t0, const Chunk &c) {
+        auto wev = [&](int p, int j, int &a, float &w, float &al) {
+            const bool act = wlane && on[p];
+            a = act ? c.w[p][j].x : -2;
+            w = act ? __int_as_float(c.w[p][j].y) : 0.f;
+            al = act ? __int_as_float(c.w[p][j].z) : 1.f;
+        };
+        auto finish = [&](int j, const int (&a)[MP], const float (&w)[MP], const float (&al)[MP], float (&m)[MP]) {
+            const int t = t0 + j;
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                const float m2 = fmaf(al[p], m[p], w[p]);
+                ms[a[p]] = m2;
+                if (wlane && on[p] && t < t_pad)
+                    gw[static_cast<int64_t>(ev[p]) * t_pad + t].alpha = scan_gain(w[p], m2 + eps);
+            }
+            if constexpr (MA) {
+                int rb[MP];
+                float rr[MP];
+                float sr = 0.f, srm = 0.f;
+#pragma unroll
+                for (int p = 0; p < MP; ++p) {
+                    const bool act = !wlane && on[p];
+                    rb[p] = act ? c.r[p][j].x : -1;
+                    rr[p] = act ? __int_as_float(c.r[p][j].y) : 0.f;
+                    const float wm = rr[p] * ms[rb[p]];  // post-write mass
+                    sr += rr[p];
+                    srm += wm;
+                    rr[p] = wm;
+                }
+                sr = event_sum<32>(sr);
+                srm = event_sum<32>(srm);
+                const float scale = sr / (srm + eps);
+#pragma unroll
+                for (int p = 0; p < MP; ++p)
+                    if (!wlane && on[p] && t < t_pad)
+                        gr[static_cast<int64_t>(ev[p]) * t_pad + t].r = rr[p] * scale;
+            }
+        };
+#pragma unroll
+        for (int j0 = 0; j0 < CH; j0 += 2) {
+            const int j1 = j0 + 1;
+            const int ov = __builtin_amdgcn_readfirstlane(c.w[0][j1].w);
+            int a0[MP], a1[MP];
+            float w0[MP], w1[MP], al0[MP], al1[MP], m0[MP], m1[MP];
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                wev(p, j0, a0[p], w0[p], al0[p]);
+                wev(p, j1, a1[p], w1[p], al1[p]);
+                m0[p] = ms[a0[p]];
+                m1[p] = ms[a1[p]];
+            }
+            finish(j0, a0, w0, al0, m0);
+            if (ov) {
+#pragma unroll
+                for (int p = 0; p < MP; ++p)
+                    m1[p] = ms[a1[p]];
+            }
+            finish(j1, a1, w1, al1, m1);
+        }
+    };
+    const int nc = (T + CH - 1) / CH;
+    Chunk cur, nxt;
+    fetch(0, cur);
+    for (int ci = 0; ci < nc; ++ci) {
+        // the next chunk's loads stay ahead of this chunk's mass chain
+        fetch(min(ci + 1, nc - 1) * CH, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        run(ci * CH, cur);
+        __builtin_amdgcn_sched_barrier(0);
+        cur = nxt;
+    }
+    __syncthreads();
+    float *mdst = job.mass_out + static_cast<int64_t>(bh) * A;
+    for (int a = lane; a < A; a += kWave)
+        mdst[a] = ms[a];
+}
+
+template<bool MA>
+hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, hipStream_t stream) {
+    const int kmax = std::max(job.Kw, job.Kr);
+    const dim3 grid(static_cast<unsigned>(job.B * job.H)), blk(kWave);
+    const size_t lds = static_cast<size_t>(job.A + 2) * 4;
+    auto *w = const_cast<WriteRec *>(job.wrec);  // the records are the caller's workspace
+    auto *r = const_cast<ReadRec *>(job.rrec);
+    if (kmax <= 32)
+        hipLaunchKernelGGL((segment_mass_kernel<MA, 1>), grid, blk, lds, stream, job, w, r, t_pad);
+    else if (kmax <= 64)
+        hipLaunchKernelGGL((segment_mass_kernel<MA, 2>), grid, blk, lds, stream, job, w, r, t_pad);
+    else
+        hipLaunchKernelGGL((segment_mass_kernel<MA, 4>), grid, blk, lds, stream, job, w, r, t_pad);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const char **why) {
@@ -181,24 +343,26 @@ int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes) {
     return 1;
 }
 
-// RAMNET_SCAN_LAYOUT="vec,epp,np,nw" replaces the planner's choice (tests
+// RAMNET_SCAN_LAYOUT="vec,epp,np,nw[,pre]" replaces the planner's choice (tests
 // sweep every compiled layout with it; also a tuning knob). The layout must
 // be compiled, cover max(Kw, Kr) events and fit in LDS.
 static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
     const char *env = std::getenv("RAMNET_SCAN_LAYOUT");
     if (!env || !*env)
         return 0;
-    int vec = 0, epp = 0, np = 0, nw = 0;
-    if (std::sscanf(env, "%d,%d,%d,%d", &vec, &epp, &np, &nw) != 4 || !scan_layout_compiled(vec, epp, np, nw)) {
-        *why = "RAMNET_SCAN_LAYOUT names no compiled layout (vec,epp,np,nw)";
+    int vec = 0, epp = 0, np = 0, nw = 0, pre = 0;
+    const int n = std::sscanf(env, "%d,%d,%d,%d,%d", &vec, &epp, &np, &nw, &pre);
+    if ((n != 4 && n != 5) || (pre != 0 && pre != 1) || !scan_layout_compiled(vec, epp, np, nw, pre != 0)) {
+        *why = "RAMNET_SCAN_LAYOUT names no compiled layout (vec,epp,np,nw[,pre])";
         return -1;
     }
-    const size_t lds = scan_lds_bytes(job.A, vec, epp, np, nw, dtype_bytes(job.dtype));
-    if (epp * np < std::max(job.Kw, job.Kr) || static_cast<int64_t>(lds) > kLdsPerCu) {
+    const size_t lds = scan_lds_bytes(job.A, vec, epp, np, nw, dtype_bytes(job.dtype), pre != 0);
+    if (epp * np < std::max(job.Kw, job.Kr) || static_cast<int64_t>(lds) > kLdsPerCu ||
+        (pre && static_cast<int64_t>(job.A + 2) * 4 > kMassPassLds)) {
         *why = "RAMNET_SCAN_LAYOUT does not cover top_k or does not fit in LDS";
         return -1;
     }
-    *p = {vec, epp, np, nw, nw * (kWave / epp) * vec, lds};
+    *p = {vec, epp, np, nw, nw * (kWave / epp) * vec, lds, pre != 0};
     return 1;
 }
 
@@ -219,11 +383,20 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     geo.n_units = job.B * job.H * geo.n_slices;
     geo.t_pad = scan_t_pad(job.T);
     geo.n_chunks = (job.T + kChunk - 1) / kChunk;
+    if (job.dtype != kF32 && job.dtype != kF16 && job.dtype != kBF16) {
+        *why = "segment forward: unsupported dtype";
+        return hipErrorInvalidValue;
+    }
+    if (p.pre) {
+        const hipError_t err = job.mass_aware ? launch_mass_pass<true>(job, geo.t_pad, stream)
+                                              : launch_mass_pass<false>(job, geo.t_pad, stream);
+        if (err != hipSuccess)
+            return err;
+    }
     switch (job.dtype) {
-        case kF32: return launch_scan_f32(job, geo, p.vec, p.epp, p.np, p.nw, stream);
-        case kF16: return launch_scan_f16(job, geo, p.vec, p.epp, p.np, p.nw, stream);
-        case kBF16: return launch_scan_bf16(job, geo, p.vec, p.epp, p.np, p.nw, stream);
-        default: *why = "segment forward: unsupported dtype"; return hipErrorInvalidValue;
+        case kF32: return launch_scan_f32(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream);
+        case kF16: return launch_scan_f16(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream);
+        default: return launch_scan_bf16(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream);
     }
 }
 

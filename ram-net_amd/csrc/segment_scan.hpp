@@ -208,19 +208,22 @@ struct StageRec {
 // buffers, 16-byte aligned, each holding the staged events (kChunk x E), x
 // (CS rows), the overlap flags and the raw records (kChunk x E) for the mass
 // wave.
-__host__ __device__ constexpr size_t scan_stage_offset(int A, int rs) {
-    return ((static_cast<size_t>(A + 2) * rs + static_cast<size_t>(A + 2)) * 4 + 15) / 16 * 16;
+__host__ __device__ constexpr size_t scan_stage_offset(int A, int rs, bool pre = false) {
+    return ((static_cast<size_t>(A + 2) * rs + (pre ? 0 : static_cast<size_t>(A + 2))) * 4 + 15) / 16 * 16;
 }
 // Tokens per chunk: 16, or 8 when more than 64 events per token would make
 // the double-buffered stage outgrow LDS.
 __host__ __device__ constexpr int scan_chunk_len(int events) { return events > 64 ? 8 : kChunk; }
 
-inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem) {
+// PRE: gains precomputed by the mass pre-pass (no mass column, no staged
+// StageRec: the state waves read the records themselves).
+inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem, bool pre = false) {
     const int cs = nw * (kWave / epp) * vec;
     const int ch = scan_chunk_len(epp * np);
-    const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs));
-    const size_t stage = static_cast<size_t>(ch) * epp * np * (sizeof(StageRec) + sizeof(WriteRec) + sizeof(ReadRec)) +
-                         static_cast<size_t>(cs) * (ch * elem + 16) + ch * sizeof(int);
+    const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs), pre);
+    const size_t rec = (pre ? 0 : sizeof(StageRec)) + sizeof(WriteRec) + sizeof(ReadRec);
+    const size_t stage = static_cast<size_t>(ch) * epp * np * rec + static_cast<size_t>(cs) * (ch * elem + 16) +
+                         ch * sizeof(int);
     return state + 2 * stage;
 }
 
@@ -236,8 +239,14 @@ inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem) 
 //    per-token dependency chain is one LDS row read-modify-write;
 //  * one barrier per chunk hands the double-buffered stage over.
 // FAST: C is a multiple of CS, so every lane owns VEC real channels.
-template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
-__global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const SegmentJob job, const ScanGeom geo) {
+// PRE: the mass pre-pass (segment_mass_kernel) has already replaced each
+// write record's alpha by its gain and, mass-aware, each read weight by its
+// effective weight; there is no mass wave and no mass column, and the state
+// waves stage the records of the next chunk themselves.
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
+__global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_kernel(const SegmentJob job,
+                                                                                     const ScanGeom geo) {
+    constexpr int NWT = NW + (PRE ? 0 : 1);  // waves of the workgroup
     constexpr int LPE = kWave / EPP;
     constexpr int CSW = LPE * VEC;
     constexpr int CS = NW * CSW;
@@ -250,8 +259,9 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
     constexpr int XRB = CH * ES + 16;  // staged x row: CH elements + 16 bytes against bank conflicts
     constexpr int XI = (CS * CH + NST - 1) / NST;  // staged x elements per state thread
     constexpr int NSL = EPP <= CH ? CH / EPP : 1;  // tokens whose y a lane stores
+    constexpr int kStageRecBytes = PRE ? 0 : static_cast<int>(sizeof(StageRec));
     constexpr int kStageBytes =
-        CH * E * static_cast<int>(sizeof(StageRec) + sizeof(WriteRec) + sizeof(ReadRec)) + CS * XRB + CH * 4;
+        CH * E * (kStageRecBytes + static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec))) + CS * XRB + CH * 4;
     constexpr int RI = (E * CH + NST - 1) / NST;  // raw records per state thread
     using Bits = std::conditional_t<ES == 4, uint32_t, uint16_t>;
 
@@ -265,7 +275,7 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = tid / kWave;
     const int lane = tid % kWave;
-    const bool mass_wave = wave == NW;
+    const bool mass_wave = !PRE && wave == NW;
     const int bh = unit / geo.n_slices;
     const int c0 = (unit - bh * geo.n_slices) * CS;
     const int T = job.T, A = job.A, C = job.C, Kw = job.Kw, Kr = job.Kr, Tp = geo.t_pad;
@@ -273,9 +283,9 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
 
     float *st = lds + 2 * RS;              // slot 0 of the slice
     float *ms = lds + (A + 2) * RS + 2;    // mass of slot 0
-    char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(A, RS);
+    char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(A, RS, PRE);
     auto stage_e = [&](int buf) { return reinterpret_cast<StageRec *>(stage0 + buf * kStageBytes); };
-    auto stage_x = [&](int buf) { return stage0 + buf * kStageBytes + CH * E * static_cast<int>(sizeof(StageRec)); };
+    auto stage_x = [&](int buf) { return stage0 + buf * kStageBytes + CH * E * kStageRecBytes; };
     // per token: 1 if its writes may overlap the previous token's
     auto stage_f = [&](int buf) { return reinterpret_cast<int *>(stage_x(buf) + CS * XRB); };
     auto raw_w = [&](int buf) { return reinterpret_cast<WriteRec *>(stage_f(buf) + CH); };
@@ -284,19 +294,21 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
     // ---- state slice and masses -> LDS
     {
         const float *src = job.init_slot + static_cast<int64_t>(bh) * A * C;
-        for (int i = tid; i < A * CS; i += kWave * (NW + 1)) {
+        for (int i = tid; i < A * CS; i += kWave * NWT) {
             const int a = i / CS, c = i - a * CS;
             const bool ok = c0 + c < C;
             const float v = src[static_cast<int64_t>(a) * C + (ok ? c0 + c : 0)];
             st[a * RS + c] = ok ? v : 0.f;
         }
-        for (int i = tid; i < 2 * RS; i += kWave * (NW + 1))
+        for (int i = tid; i < 2 * RS; i += kWave * NWT)
             lds[i] = 0.f;
-        const float *msrc = job.init_mass + static_cast<int64_t>(bh) * A;
-        for (int a = tid; a < A; a += kWave * (NW + 1))
-            ms[a] = msrc[a];
-        if (tid < 2)
-            ms[tid - 2] = 1.f;
+        if constexpr (!PRE) {
+            const float *msrc = job.init_mass + static_cast<int64_t>(bh) * A;
+            for (int a = tid; a < A; a += kWave * NWT)
+                ms[a] = msrc[a];
+            if (tid < 2)
+                ms[tid - 2] = 1.f;
+        }
     }
 
     // ---- raw records: fetched by the state threads two chunks ahead (one
@@ -321,6 +333,8 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
             rg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
         }
     };
+    // PRE: events past top-K become no-ops here (the state waves read the
+    // records directly), and event 0 carries the token's overlap flag.
     auto raw_deposit = [&](int buf, const RawRegs &rg) {
         WriteRec *rw = raw_w(buf);
         ReadRec *rr = raw_r(buf);
@@ -328,8 +342,16 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
         for (int k = 0; k < RI; ++k) {
             const int it = min(tid + k * NST, E * CH - 1);
             const int e = it / CH, j = it % CH;
-            *reinterpret_cast<int4 *>(rw + j * E + e) = rg.w[k];
-            *reinterpret_cast<int2 *>(rr + j * E + e) = rg.r[k];
+            int4 w = rg.w[k];
+            int2 r = rg.r[k];
+            if constexpr (PRE) {
+                w = e < Kw ? w : make_int4(-2, 0, 0, w.w);
+                r = e < Kr ? r : make_int2(-1, 0);
+                if (e == 0)
+                    stage_f(buf)[j] = w.w;
+            }
+            *reinterpret_cast<int4 *>(rw + j * E + e) = w;
+            *reinterpret_cast<int2 *>(rr + j * E + e) = r;
         }
     };
     struct Raw {
@@ -475,12 +497,19 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
         constexpr bool TAIL = decltype(tail_tag)::value;
         const StageRec *se = stage_e(buf);
         const char *sx = stage_x(buf);
-        int4 rec[NP][CH];
+        int4 rec[NP][CH];  // {write slot, gain, read slot, read weight}
 #pragma unroll
         for (int j = 0; j < CH; ++j)
 #pragma unroll
-            for (int p = 0; p < NP; ++p)
-                rec[p][j] = *reinterpret_cast<const int4 *>(se + j * E + p * EPP + ev);
+            for (int p = 0; p < NP; ++p) {
+                if constexpr (PRE) {
+                    const int4 w4 = *reinterpret_cast<const int4 *>(raw_w(buf) + j * E + p * EPP + ev);
+                    const int2 r2 = *reinterpret_cast<const int2 *>(raw_r(buf) + j * E + p * EPP + ev);
+                    rec[p][j] = make_int4(w4.x, w4.z, r2.x, r2.y);
+                } else {
+                    rec[p][j] = *reinterpret_cast<const int4 *>(se + j * E + p * EPP + ev);
+                }
+            }
         constexpr int XW = CH * ES / 16;  // 16-byte words per staged channel row
         uint4 xr[VEC][XW];
 #pragma unroll
@@ -594,33 +623,19 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
     auto clampc = [&](int c) { return (c < nc ? c : nc - 1) * CH; };
     RawRegs rg;
     Bits xb[XI];
-    __syncthreads();  // masses initialised before the mass wave starts
-    if (nc > 0) {
-        if (!mass_wave) {
+    if constexpr (PRE) {
+        // Iteration ci: run chunk ci (stage ci & 1) while the records and x
+        // of chunk ci + 1 are in flight; deposit them after the chunk.
+        if (nc > 0) {
             raw_fetch(0, rg);
-            raw_deposit(0, rg);
-            raw_fetch(clampc(1), rg);
-            raw_deposit(1, rg);
             x_fetch(0, xb);
+            raw_deposit(0, rg);
             x_deposit(0, xb);
         }
         __syncthreads();
-        if (mass_wave)
-            mass_chunk(0);
-    }
-    __syncthreads();
-    // Iteration ci: the state waves run chunk ci (stage ci & 1), fetch x of
-    // chunk ci + 1 and the raw records of chunk ci + 2; the mass wave stages
-    // chunk ci + 1 from the raw records deposited one iteration earlier.
-    for (int ci = 0; ci < nc; ++ci) {
-        if (mass_wave) {
-            if (ci + 1 < nc)
-                mass_chunk((ci + 1) & 1);
-        } else {
-            // scheduling fences keep the loads at the top and their use at
-            // the bottom, so a whole chunk of work covers their latency
+        for (int ci = 0; ci < nc; ++ci) {
             x_fetch(clampc(ci + 1), xb);
-            raw_fetch(clampc(ci + 2), rg);
+            raw_fetch(clampc(ci + 1), rg);
             __builtin_amdgcn_sched_barrier(0);
             if (ci < n_full)
                 state_chunk(ci & 1, ci * CH, Full{});
@@ -628,32 +643,73 @@ __global__ __launch_bounds__(kWave * (NW + 1)) void segment_scan_kernel(const Se
                 state_chunk(ci & 1, ci * CH, Tail{});
             __builtin_amdgcn_sched_barrier(0);
             x_deposit((ci + 1) & 1, xb);
-            raw_deposit(ci & 1, rg);
+            raw_deposit((ci + 1) & 1, rg);
+            __syncthreads();
+        }
+    } else {
+        __syncthreads();  // masses initialised before the mass wave starts
+        if (nc > 0) {
+            if (!mass_wave) {
+                raw_fetch(0, rg);
+                raw_deposit(0, rg);
+                raw_fetch(clampc(1), rg);
+                raw_deposit(1, rg);
+                x_fetch(0, xb);
+                x_deposit(0, xb);
+            }
+            __syncthreads();
+            if (mass_wave)
+                mass_chunk(0);
         }
         __syncthreads();
+        // Iteration ci: the state waves run chunk ci (stage ci & 1), fetch x of
+        // chunk ci + 1 and the raw records of chunk ci + 2; the mass wave stages
+        // chunk ci + 1 from the raw records deposited one iteration earlier.
+        for (int ci = 0; ci < nc; ++ci) {
+            if (mass_wave) {
+                if (ci + 1 < nc)
+                    mass_chunk((ci + 1) & 1);
+            } else {
+                // scheduling fences keep the loads at the top and their use at
+                // the bottom, so a whole chunk of work covers their latency
+                x_fetch(clampc(ci + 1), xb);
+                raw_fetch(clampc(ci + 2), rg);
+                __builtin_amdgcn_sched_barrier(0);
+                if (ci < n_full)
+                    state_chunk(ci & 1, ci * CH, Full{});
+                else
+                    state_chunk(ci & 1, ci * CH, Tail{});
+                __builtin_amdgcn_sched_barrier(0);
+                x_deposit((ci + 1) & 1, xb);
+                raw_deposit(ci & 1, rg);
+            }
+            __syncthreads();
+        }
     }
 
     // ---- LDS -> post state (whole workgroup); the masses from slice 0
     {
         float *dst = job.slot_out + static_cast<int64_t>(bh) * A * C;
-        for (int i = tid; i < A * CS; i += kWave * (NW + 1)) {
+        for (int i = tid; i < A * CS; i += kWave * NWT) {
             const int a = i / CS, c = i - a * CS;
             if (c0 + c < C)
                 dst[static_cast<int64_t>(a) * C + c0 + c] = st[a * RS + c];
         }
-        if (c0 == 0) {
+        if (!PRE && c0 == 0) {
             float *mdst = job.mass_out + static_cast<int64_t>(bh) * A;
-            for (int a = tid; a < A; a += kWave * (NW + 1))
+            for (int a = tid; a < A; a += kWave * NWT)
                 mdst[a] = ms[a];
         }
     }
 }
 
-template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
 hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t stream) {
     const unsigned blocks = static_cast<unsigned>(((geo.n_units + 7) / 8) * 8);
-    hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST>), dim3(blocks), dim3(kWave * (NW + 1)),
-                       scan_lds_bytes(job.A, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar))), stream, job, geo);
+    hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST, PRE>), dim3(blocks),
+                       dim3(kWave * (NW + (PRE ? 0 : 1))),
+                       scan_lds_bytes(job.A, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar)), PRE), stream, job,
+                       geo);
     return hipGetLastError();
 }
 
@@ -663,36 +719,50 @@ hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t s
     X(1, 8, 1, 2) X(1, 8, 1, 4) X(1, 8, 2, 1) X(1, 8, 2, 2) X(1, 8, 2, 4) X(1, 16, 1, 2) X(1, 16, 1, 4) \
     X(2, 8, 1, 1) X(2, 8, 1, 2) X(2, 8, 1, 4) X(2, 16, 1, 1) X(2, 16, 1, 2)                          \
     X(4, 8, 1, 1) X(4, 8, 1, 2) X(4, 16, 1, 1)
+// Layouts also compiled in the precomputed-gain (PRE) form: the wide
+// slot spaces, where dropping the mass column lets a slice hold twice the
+// channels.
+#define RAMNET_SCAN_PRE_LAYOUTS(X)                                                                   \
+    X(1, 8, 1, 2) X(1, 8, 1, 4) X(1, 16, 1, 2) X(1, 16, 1, 4) X(1, 32, 1, 2) X(1, 64, 1, 2) X(1, 64, 2, 1)
 
 template<typename Scalar>
-hipError_t scan_dispatch(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, int nw,
+hipError_t scan_dispatch(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, int nw, bool pre,
                          hipStream_t stream) {
     const int cs = nw * (kWave / epp) * vec;
     const bool fast = job.C % cs == 0;
-#define RAMNET_SCAN_CASE(V, E, N, W)                                                                 \
-    if (vec == V && epp == E && np == N && nw == W) {                                                \
+#define RAMNET_SCAN_CASE(V, E, N, W, P)                                                              \
+    if (pre == P && vec == V && epp == E && np == N && nw == W) {                                    \
         if (job.mass_aware)                                                                          \
-            return fast ? launch_scan<Scalar, V, E, N, W, true, true>(job, geo, stream)              \
-                        : launch_scan<Scalar, V, E, N, W, true, false>(job, geo, stream);            \
-        return fast ? launch_scan<Scalar, V, E, N, W, false, true>(job, geo, stream)                 \
-                    : launch_scan<Scalar, V, E, N, W, false, false>(job, geo, stream);               \
+            return fast ? launch_scan<Scalar, V, E, N, W, true, true, P>(job, geo, stream)           \
+                        : launch_scan<Scalar, V, E, N, W, true, false, P>(job, geo, stream);         \
+        return fast ? launch_scan<Scalar, V, E, N, W, false, true, P>(job, geo, stream)              \
+                    : launch_scan<Scalar, V, E, N, W, false, false, P>(job, geo, stream);            \
     }
-    RAMNET_SCAN_LAYOUTS(RAMNET_SCAN_CASE)
+#define RAMNET_SCAN_CASE_MASS(V, E, N, W) RAMNET_SCAN_CASE(V, E, N, W, false)
+#define RAMNET_SCAN_CASE_PRE(V, E, N, W) RAMNET_SCAN_CASE(V, E, N, W, true)
+    RAMNET_SCAN_LAYOUTS(RAMNET_SCAN_CASE_MASS)
+    RAMNET_SCAN_PRE_LAYOUTS(RAMNET_SCAN_CASE_PRE)
+#undef RAMNET_SCAN_CASE_PRE
+#undef RAMNET_SCAN_CASE_MASS
 #undef RAMNET_SCAN_CASE
     return hipErrorInvalidValue;
 }
 
-// Whether (vec, epp, np, nw) is one of the compiled layouts.
-inline bool scan_layout_compiled(int vec, int epp, int np, int nw) {
+// Whether (vec, epp, np, nw) is one of the compiled layouts (in PRE form if pre).
+inline bool scan_layout_compiled(int vec, int epp, int np, int nw, bool pre = false) {
 #define RAMNET_SCAN_HAS(V, E, N, W) if (vec == V && epp == E && np == N && nw == W) return true;
-    RAMNET_SCAN_LAYOUTS(RAMNET_SCAN_HAS)
+    if (pre) {
+        RAMNET_SCAN_PRE_LAYOUTS(RAMNET_SCAN_HAS)
+    } else {
+        RAMNET_SCAN_LAYOUTS(RAMNET_SCAN_HAS)
+    }
 #undef RAMNET_SCAN_HAS
     return false;
 }
 
 // One definition per activation dtype, each in its own translation unit.
-hipError_t launch_scan_f32(const SegmentJob &, const ScanGeom &, int, int, int, int, hipStream_t);
-hipError_t launch_scan_f16(const SegmentJob &, const ScanGeom &, int, int, int, int, hipStream_t);
-hipError_t launch_scan_bf16(const SegmentJob &, const ScanGeom &, int, int, int, int, hipStream_t);
+hipError_t launch_scan_f32(const SegmentJob &, const ScanGeom &, int, int, int, int, bool, hipStream_t);
+hipError_t launch_scan_f16(const SegmentJob &, const ScanGeom &, int, int, int, int, bool, hipStream_t);
+hipError_t launch_scan_bf16(const SegmentJob &, const ScanGeom &, int, int, int, int, bool, hipStream_t);
 
 }  // namespace ramnet

@@ -4,9 +4,9 @@
 
 namespace ramnet {
 
-hipError_t launch_scan_f16(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, int nw,
+hipError_t launch_scan_f16(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, int nw, bool pre,
                           hipStream_t stream) {
-    return scan_dispatch<_Float16>(job, geo, vec, epp, np, nw, stream);
+    return scan_dispatch<_Float16>(job, geo, vec, epp, np, nw, pre, stream);
 }
 
 }  // namespace ramnet

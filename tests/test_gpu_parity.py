@@ -204,17 +204,20 @@ SCAN_LAYOUTS = [
     (1, 8, 1, 2), (1, 8, 1, 4), (1, 8, 2, 1), (1, 8, 2, 2), (1, 8, 2, 4), (1, 16, 1, 2), (1, 16, 1, 4),
     (2, 8, 1, 1), (2, 8, 1, 2), (2, 8, 1, 4), (2, 16, 1, 1), (2, 16, 1, 2),
     (4, 8, 1, 1), (4, 8, 1, 2), (4, 16, 1, 1),
+] + [  # precomputed-gain form (mass pre-pass), from RAMNET_SCAN_PRE_LAYOUTS
+    (1, 8, 1, 2, 1), (1, 8, 1, 4, 1), (1, 16, 1, 2, 1), (1, 16, 1, 4, 1), (1, 32, 1, 2, 1), (1, 64, 1, 2, 1),
+    (1, 64, 2, 1, 1),
 ]
 
 
 @pytest.mark.parametrize("partial", [False, True], ids=["full_slices", "partial_slice"])
-@pytest.mark.parametrize("layout", SCAN_LAYOUTS, ids=lambda l: "v{}e{}n{}w{}".format(*l))
+@pytest.mark.parametrize("layout", SCAN_LAYOUTS, ids=lambda l: "v{}e{}n{}w{}".format(*l) + ("p" if len(l) > 4 else ""))
 def test_segment_scan_every_layout(layout, partial, monkeypatch):
     """Each layout, forced through RAMNET_SCAN_LAYOUT, against the fp64 sparse
     oracle: top-K filling every event lane (writes) and all but one (reads),
     a tail chunk pair (T = 45), and channel slices that are whole or end
     inside C."""
-    vec, epp, np_, nw = layout
+    vec, epp, np_, nw = layout[:4]
     kmax = epp * np_
     U, P = (4, 4) if kmax > 64 else (3, 4)
     cs = nw * (64 // epp) * vec
