@@ -78,7 +78,7 @@ constexpr int64_t kChainCycles = 160;
 // The mass pre-pass: one wave per (b, h) walks the sequence with the masses
 // in LDS; its token chain is one LDS read-modify-write (~kMassChainCycles).
 constexpr int64_t kMassChainCycles = 120;
-constexpr int64_t kMassPassLds = 64 * 1024;  // A <= 16382
+constexpr int64_t kMassPassLds = 64 * 1024;  // chunk maps (A + 2) * 8 bytes: A <= 8190
 
 bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, Plan *out) {
     const int kmax = std::max(Kw, Kr);
@@ -87,7 +87,7 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, P
     const int epp0 = std::min(kWave, std::max(4, pow2_ceil(kmax)));
     bool found = false;
     int64_t best = 0;
-    const bool pre_ok = static_cast<int64_t>(A + 2) * 4 <= kMassPassLds;
+    const bool pre_ok = static_cast<int64_t>(A + 2) * 8 <= kMassPassLds;
     for (int pre = 0; pre <= (pre_ok ? 1 : 0); ++pre) {
         for (int epp = 4; epp <= kWave; epp <<= 1) {
             const int np = (kmax + epp - 1) / epp;
@@ -111,8 +111,8 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, P
                     int64_t cost = rounds * std::max(kChainCycles, issue);
                     if (C % cs != 0)
                         cost = cost * 3 / 2;  // partial slices take the guarded path
-                    if (pre)  // one wave per (b, h); several fit a CU
-                        cost += (static_cast<int64_t>(B) * H + 4 * n_cu - 1) / (4 * n_cu) * kMassChainCycles;
+                    if (pre)  // chunked over time: a few chunk replays of tokens
+                        cost += 2 * kMassChainCycles;
                     const bool better = !found || cost < best ||
                                         (cost == best && (nw > out->nw || (nw == out->nw && cs > out->cs)));
                     if (better) {
@@ -166,76 +166,177 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
     }
 }
 
-// Mass pre-pass: the slot-mass recurrence of one (b, h) over the whole
-// sequence (m <- alpha m + w per write event, in token order), once per
-// head. Each write record's alpha field is replaced by its gain
+// Mass pre-pass: the slot-mass recurrence (m <- alpha m + w per write
+// event, in token order), once per (b, h) instead of once per channel
+// slice. Each write record's alpha field is replaced by its gain
 // g = w / (m + eps); mass-aware, each read record's weight by its effective
-// weight (sum r) (m r) / (sum m r + eps) on the post-write masses. The masses
-// live in LDS; lanes 0..31 take write events p * 32 + lane and lanes 32..63
-// read events p * 32 + lane - 32. Tokens go in pairs like the scan's mass
-// wave: the second token's masses are read before the first token's writes
-// and again only when the two write sets may overlap. Records of the next
-// chunk are fetched while the current one is processed.
+// weight (sum r) (m r) / (sum m r + eps) on the post-write masses.
+//
+// The sequence is cut into NC time chunks run in parallel. The recurrence is
+// affine in m with coefficients independent of m, so:
+//   1. mass_chunk_map_kernel: per (b, h, chunk), each slot's composed map
+//      m_end = a m_start + b over the chunk (slots it does not touch: 1, 0);
+//   2. mass_chunk_scan_kernel: per (b, h, slot), m_start of every chunk from
+//      the initial mass and the maps in chunk order, and the final mass;
+//   3. segment_mass_kernel: per (b, h, chunk), the chunk replayed from its
+//      m_start, writing the gains.
+// The maps live in a caller buffer (the scan's output y, which the scan
+// overwrites afterwards); with NC = 1 step 3 alone runs, from the initial
+// mass.
+//
+// Lanes 0..31 take write events p * 32 + lane, lanes 32..63 read events
+// p * 32 + lane - 32; the masses (or maps) live in LDS, whose in-order
+// accesses carry the slot dependency from token to token. Tokens go in pairs
+// like the scan's mass wave: the second token's masses are read before the
+// first token's writes and again only when the two write sets may overlap.
+template<int MP>
+struct MassLanes {
+    static constexpr int CH = MP <= 1 ? 16 : MP == 2 ? 8 : 4;  // tokens per fetch
+    int ev[MP];   // this lane's event (clamped for loads)
+    bool on[MP];  // whether it is a real event
+    __device__ MassLanes(int lane, int Kw, int Kr) {
+        const int hl = lane & 31;
+#pragma unroll
+        for (int p = 0; p < MP; ++p) {
+            const int e = p * 32 + hl;
+            on[p] = lane < 32 ? e < Kw : e < Kr;
+            ev[p] = lane < 32 ? min(e, Kw - 1) : min(e, Kr - 1);
+        }
+    }
+};
+template<int MP, int CH>
+struct MassRecs {
+    int4 w[MP][CH];
+    int2 r[MP][CH];
+};
+template<int MP, int CH>
+__device__ __forceinline__ void mass_fetch(const MassLanes<MP> &ln, const WriteRec *gw, const ReadRec *gr, int t_pad,
+                                           int t0, bool wlane, MassRecs<MP, CH> &c) {
+#pragma unroll
+    for (int p = 0; p < MP; ++p)
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int t = min(t0 + j, t_pad - 1);
+            if (wlane)
+                c.w[p][j] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ln.ev[p]) * t_pad + t);
+            else
+                c.r[p][j] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(ln.ev[p]) * t_pad + t);
+        }
+}
+
+// Step 1: one wave per (b, h, chunk); LDS holds (a, b) per slot.
+template<int MP>
+__global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob job, float2 *maps, int t_pad,
+                                                              int chunk_len) {
+    using L = MassLanes<MP>;
+    constexpr int CH = L::CH;
+    extern __shared__ __align__(16) float2 cm[];
+    const int bh = blockIdx.x, ck = blockIdx.y, nck = gridDim.y;
+    const int lane = static_cast<int>(threadIdx.x);
+    const bool wlane = lane < 32;
+    const int A = job.A, Kw = job.Kw, Kr = job.Kr;
+    float2 *mp = cm + 2;  // mp[-2]: the no-op slot of padding records
+    for (int a = lane - 2; a < A; a += kWave)
+        mp[a] = make_float2(1.f, 0.f);
+    __syncthreads();
+    const L ln(lane, Kw, Kr);
+    const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * t_pad;
+    const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad;
+    const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
+    const int nc = (t_end - t_begin + CH - 1) / CH;
+    MassRecs<MP, CH> cur, nxt;  // read lanes fetch (unused) read records: in bounds for Kr > Kw
+    mass_fetch(ln, gw, gr, t_pad, t_begin, wlane, cur);
+    for (int ci = 0; ci < nc; ++ci) {
+        mass_fetch(ln, gw, gr, t_pad, t_begin + min(ci + 1, nc - 1) * CH, wlane, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                const bool act = wlane && ln.on[p] && t_begin + ci * CH + j < t_end;
+                const int a = act ? cur.w[p][j].x : -2;
+                const float w = act ? __int_as_float(cur.w[p][j].y) : 0.f;
+                const float al = act ? __int_as_float(cur.w[p][j].z) : 1.f;
+                const float2 m = mp[a];
+                mp[a] = make_float2(al * m.x, fmaf(al, m.y, w));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        cur = nxt;
+    }
+    __syncthreads();
+    float2 *dst = maps + (static_cast<int64_t>(bh) * nck + ck) * A;
+    for (int a = lane; a < A; a += kWave)
+        dst[a] = mp[a];
+}
+
+// Step 2: one thread per (b, h, slot); the map of chunk c is replaced by
+// (m_start of chunk c, unused).
+__global__ __launch_bounds__(256) void mass_chunk_scan_kernel(const SegmentJob job, float2 *maps, int nck) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int A = job.A;
+    if (i >= static_cast<int64_t>(job.B) * job.H * A)
+        return;
+    const int64_t bh = i / A;
+    const int a = static_cast<int>(i - bh * A);
+    float m = job.init_mass[i];
+    float2 *mp = maps + bh * nck * A + a;
+    for (int c = 0; c < nck; ++c) {
+        const float2 ab = mp[static_cast<int64_t>(c) * A];
+        mp[static_cast<int64_t>(c) * A] = make_float2(m, 0.f);
+        m = fmaf(ab.x, m, ab.y);
+    }
+    job.mass_out[i] = m;
+}
+
+// Step 3: one wave per (b, h, chunk), from m_start (the maps after step 2,
+// or the initial mass when there is one chunk).
 template<bool MA, int MP>
 __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, WriteRec *wrec, ReadRec *rrec,
-                                                            int t_pad) {
-    constexpr int CH = MP <= 1 ? 16 : MP == 2 ? 8 : 4;  // tokens per fetch
+                                                            int t_pad, int chunk_len, const float2 *starts) {
+    using L = MassLanes<MP>;
+    constexpr int CH = L::CH;
     extern __shared__ __align__(16) float lds[];
-    const int bh = blockIdx.x;
+    const int bh = blockIdx.x, ck = blockIdx.y, nck = gridDim.y;
     const int lane = static_cast<int>(threadIdx.x);
     const int hl = lane & 31;
     const bool wlane = lane < 32;
-    const int A = job.A, T = job.T, Kw = job.Kw, Kr = job.Kr;
+    const int A = job.A, Kw = job.Kw, Kr = job.Kr;
     const float eps = job.eps;
     float *ms = lds + 2;  // ms[-2], ms[-1]: the no-op slots of padding records
-    const float *msrc = job.init_mass + static_cast<int64_t>(bh) * A;
-    for (int a = lane; a < A; a += kWave)
-        ms[a] = msrc[a];
+    if (starts) {
+        const float2 *src = starts + (static_cast<int64_t>(bh) * nck + ck) * A;
+        for (int a = lane; a < A; a += kWave)
+            ms[a] = src[a].x;
+    } else {
+        const float *src = job.init_mass + static_cast<int64_t>(bh) * A;
+        for (int a = lane; a < A; a += kWave)
+            ms[a] = src[a];
+    }
     if (lane < 2)
         lds[lane] = 1.f;
     __syncthreads();
 
+    const L ln(lane, Kw, Kr);
     WriteRec *gw = wrec + static_cast<int64_t>(bh) * Kw * t_pad;
     ReadRec *gr = rrec + static_cast<int64_t>(bh) * Kr * t_pad;
-    int ev[MP];     // this lane's event (clamped for loads)
-    bool on[MP];    // whether it is a real event
-#pragma unroll
-    for (int p = 0; p < MP; ++p) {
-        const int e = p * 32 + hl;
-        on[p] = wlane ? e < Kw : e < Kr;
-        ev[p] = wlane ? min(e, Kw - 1) : min(e, Kr - 1);
-    }
-    struct Chunk {
-        int4 w[MP][CH];
-        int2 r[MP][CH];
-    };
-    auto fetch = [&](int t0, Chunk &c) {
-#pragma unroll
-        for (int p = 0; p < MP; ++p)
-#pragma unroll
-            for (int j = 0; j < CH; ++j) {
-                const int t = min(t0 + j, t_pad - 1);
-                if (wlane)
-                    c.w[p][j] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ev[p]) * t_pad + t);
-                else
-                    c.r[p][j] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(ev[p]) * t_pad + t);
-            }
-    };
-    auto run = [&](int t0, const Chunk &c) {
+    const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
+    auto run = [&](int t0, const MassRecs<MP, CH> &c) {
         auto wev = [&](int p, int j, int &a, float &w, float &al) {
-            const bool act = wlane && on[p];
+            const bool act = wlane && ln.on[p] && t0 + j < t_end;
             a = act ? c.w[p][j].x : -2;
             w = act ? __int_as_float(c.w[p][j].y) : 0.f;
             al = act ? __int_as_float(c.w[p][j].z) : 1.f;
         };
         auto finish = [&](int j, const int (&a)[MP], const float (&w)[MP], const float (&al)[MP], float (&m)[MP]) {
             const int t = t0 + j;
+            const bool live = t < t_end;
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
                 const float m2 = fmaf(al[p], m[p], w[p]);
                 ms[a[p]] = m2;
-                if (wlane && on[p] && t < t_pad)
-                    gw[static_cast<int64_t>(ev[p]) * t_pad + t].alpha = scan_gain(w[p], m2 + eps);
+                if (wlane && ln.on[p] && live)
+                    gw[static_cast<int64_t>(ln.ev[p]) * t_pad + t].alpha = scan_gain(w[p], m2 + eps);
             }
             if constexpr (MA) {
                 int rb[MP];
@@ -243,7 +344,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 float sr = 0.f, srm = 0.f;
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
-                    const bool act = !wlane && on[p];
+                    const bool act = !wlane && ln.on[p] && live;
                     rb[p] = act ? c.r[p][j].x : -1;
                     rr[p] = act ? __int_as_float(c.r[p][j].y) : 0.f;
                     const float wm = rr[p] * ms[rb[p]];  // post-write mass
@@ -256,8 +357,8 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 const float scale = sr / (srm + eps);
 #pragma unroll
                 for (int p = 0; p < MP; ++p)
-                    if (!wlane && on[p] && t < t_pad)
-                        gr[static_cast<int64_t>(ev[p]) * t_pad + t].r = rr[p] * scale;
+                    if (!wlane && ln.on[p] && live)
+                        gr[static_cast<int64_t>(ln.ev[p]) * t_pad + t].r = rr[p] * scale;
             }
         };
 #pragma unroll
@@ -282,37 +383,70 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
             finish(j1, a1, w1, al1, m1);
         }
     };
-    const int nc = (T + CH - 1) / CH;
-    Chunk cur, nxt;
-    fetch(0, cur);
+    const int nc = (t_end - t_begin + CH - 1) / CH;
+    MassRecs<MP, CH> cur, nxt;
+    mass_fetch(ln, gw, gr, t_pad, t_begin, wlane, cur);
     for (int ci = 0; ci < nc; ++ci) {
-        // the next chunk's loads stay ahead of this chunk's mass chain
-        fetch(min(ci + 1, nc - 1) * CH, nxt);
+        // the next loads stay ahead of this part's mass chain
+        mass_fetch(ln, gw, gr, t_pad, t_begin + min(ci + 1, nc - 1) * CH, wlane, nxt);
         __builtin_amdgcn_sched_barrier(0);
-        run(ci * CH, cur);
+        run(t_begin + ci * CH, cur);
         __builtin_amdgcn_sched_barrier(0);
         cur = nxt;
     }
-    __syncthreads();
-    float *mdst = job.mass_out + static_cast<int64_t>(bh) * A;
-    for (int a = lane; a < A; a += kWave)
-        mdst[a] = ms[a];
+    if (!starts) {
+        __syncthreads();
+        float *mdst = job.mass_out + static_cast<int64_t>(bh) * A;
+        for (int a = lane; a < A; a += kWave)
+            mdst[a] = ms[a];
+    }
+}
+
+// Chunks of the mass pre-pass: enough (b, h, chunk) waves to fill the GPU,
+// chunks a multiple of 16 tokens, and maps that fit the scratch buffer.
+int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chunk_len) {
+    const int64_t bh = static_cast<int64_t>(job.B) * job.H;
+    int nck = static_cast<int>(std::max<int64_t>(1, (4 * n_cu + bh - 1) / bh));
+    nck = std::min(nck, std::max(1, job.T / 64));  // chunks of >= 64 tokens
+    while (nck > 1 && static_cast<size_t>(bh) * nck * job.A * sizeof(float2) > scratch_bytes)
+        nck /= 2;
+    const int len = ((job.T + nck - 1) / nck + 15) / 16 * 16;
+    *chunk_len = std::max(16, len);
+    return (job.T + *chunk_len - 1) / *chunk_len;
+}
+
+template<bool MA, int MP>
+hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, hipStream_t stream) {
+    auto *w = const_cast<WriteRec *>(job.wrec);  // the records are the caller's workspace
+    auto *r = const_cast<ReadRec *>(job.rrec);
+    const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);
+    int len = 0;
+    const int nck = mass_chunks(job, y_bytes, n_cu, &len);
+    const unsigned bh = static_cast<unsigned>(job.B * job.H);
+    if (nck <= 1) {
+        hipLaunchKernelGGL((segment_mass_kernel<MA, MP>), dim3(bh, 1), dim3(kWave), static_cast<size_t>(job.A + 2) * 4,
+                           stream, job, w, r, t_pad, job.T, nullptr);
+        return hipGetLastError();
+    }
+    auto *maps = static_cast<float2 *>(job.y);  // scratch: the scan overwrites y afterwards
+    hipLaunchKernelGGL((mass_chunk_map_kernel<MP>), dim3(bh, nck), dim3(kWave), static_cast<size_t>(job.A + 2) * 8,
+                       stream, job, maps, t_pad, len);
+    const int64_t n = static_cast<int64_t>(bh) * job.A;
+    hipLaunchKernelGGL(mass_chunk_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, job,
+                       maps, nck);
+    hipLaunchKernelGGL((segment_mass_kernel<MA, MP>), dim3(bh, nck), dim3(kWave), static_cast<size_t>(job.A + 2) * 4,
+                       stream, job, w, r, t_pad, len, maps);
+    return hipGetLastError();
 }
 
 template<bool MA>
-hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, hipStream_t stream) {
+hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, int n_cu, hipStream_t stream) {
     const int kmax = std::max(job.Kw, job.Kr);
-    const dim3 grid(static_cast<unsigned>(job.B * job.H)), blk(kWave);
-    const size_t lds = static_cast<size_t>(job.A + 2) * 4;
-    auto *w = const_cast<WriteRec *>(job.wrec);  // the records are the caller's workspace
-    auto *r = const_cast<ReadRec *>(job.rrec);
     if (kmax <= 32)
-        hipLaunchKernelGGL((segment_mass_kernel<MA, 1>), grid, blk, lds, stream, job, w, r, t_pad);
-    else if (kmax <= 64)
-        hipLaunchKernelGGL((segment_mass_kernel<MA, 2>), grid, blk, lds, stream, job, w, r, t_pad);
-    else
-        hipLaunchKernelGGL((segment_mass_kernel<MA, 4>), grid, blk, lds, stream, job, w, r, t_pad);
-    return hipGetLastError();
+        return launch_mass_pass_mp<MA, 1>(job, t_pad, n_cu, stream);
+    if (kmax <= 64)
+        return launch_mass_pass_mp<MA, 2>(job, t_pad, n_cu, stream);
+    return launch_mass_pass_mp<MA, 4>(job, t_pad, n_cu, stream);
 }
 
 }  // namespace
@@ -358,7 +492,7 @@ static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
     }
     const size_t lds = scan_lds_bytes(job.A, vec, epp, np, nw, dtype_bytes(job.dtype), pre != 0);
     if (epp * np < std::max(job.Kw, job.Kr) || static_cast<int64_t>(lds) > kLdsPerCu ||
-        (pre && static_cast<int64_t>(job.A + 2) * 4 > kMassPassLds)) {
+        (pre && static_cast<int64_t>(job.A + 2) * 8 > kMassPassLds)) {
         *why = "RAMNET_SCAN_LAYOUT does not cover top_k or does not fit in LDS";
         return -1;
     }
@@ -388,8 +522,8 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
         return hipErrorInvalidValue;
     }
     if (p.pre) {
-        const hipError_t err = job.mass_aware ? launch_mass_pass<true>(job, geo.t_pad, stream)
-                                              : launch_mass_pass<false>(job, geo.t_pad, stream);
+        const hipError_t err = job.mass_aware ? launch_mass_pass<true>(job, geo.t_pad, cu_count(), stream)
+                                              : launch_mass_pass<false>(job, geo.t_pad, cu_count(), stream);
         if (err != hipSuccess)
             return err;
     }

@@ -239,6 +239,23 @@ def test_segment_scan_every_layout(layout, partial, monkeypatch):
         assert err <= _out_tol(dtype), f"y rel err {err:.3e}, layout {layout}"
 
 
+@pytest.mark.parametrize("mass_aware", [False, True])
+def test_mass_prepass_time_chunks(mass_aware, monkeypatch):
+    """The precomputed-gain scan with its mass pre-pass cut into time chunks
+    (affine chunk maps, a scan over chunks, chunk replays) against the fp64
+    oracle: A = 4096, T = 700 (several chunks and a ragged last one)."""
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", "1,16,1,2,1")
+    print(f"mass pre-pass chunks, mass_aware={mass_aware}", flush=True)
+    src, got, ref = _segment_case(1, 2, 3, 16, 700, 64, 8, 8, torch.float32, True, mass_aware, seed=31)
+    y, slot, mass = got
+    ry, rslot, rmass = ref
+    ry = torch.as_tensor(ry)
+    assert oracle.rel_err(slot, rslot) <= FP32_TOL
+    assert oracle.rel_err(mass, rmass) <= FP32_TOL
+    keep = src.mask[0]
+    assert oracle.rel_err(y[:, :, keep], ry[:, :, keep]) <= FP32_TOL
+
+
 @pytest.mark.parametrize("re_norm", [(0.0, 0.0), (1.0, 1.0), (0.25, 0.75)])
 def test_api_matches_dense_reference(re_norm):
     """random_access_memory_attention vs the dense restatement of the reference (config 1 shape)."""
