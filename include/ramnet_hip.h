@@ -79,6 +79,34 @@ int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, 
                              int encode_batch_idx, int32_t *idx_out, float *val_out, void *stream);
 
 /*
+ * Gradient of one address decoder with respect to its logits (the selection
+ * carries none). Replaces ramnet_ops::topk_addr_single_backward
+ * (ram_attn_bind.cpp:36-45, ram_attn_ops.cpp:97-135).
+ *   idx, val    (B, H, top_k, T): the forward's outputs (either index
+ *               encoding; val negated when addr_val_neg)
+ *   addr        (B, H, U, P, T) logits, `dtype`
+ *   grad_val    (B, H, top_k, T) fp32: gradient with respect to the positive
+ *               weights
+ *   grad_addr   (B, H, U, P, T) `dtype`, written in full
+ */
+int ramnet_topk_addr_single_backward(const int32_t *idx, const float *val, const void *addr, const float *grad_val,
+                                     int dtype, int64_t B, int64_t H, int64_t U, int64_t P, int64_t T,
+                                     int64_t embed_num, int64_t A, const int32_t *position_ids, int64_t top_k,
+                                     float top_k_re_norm, int addr_val_neg, void *grad_addr, void *stream);
+
+/*
+ * Gradients of both decoders of ramnet_topk_addr_forward (write rows first;
+ * read weights stored negated, their gradients with respect to the positive
+ * weights). Replaces ramnet_ops::topk_addr_backward
+ * (ram_attn_bind.cpp:55-64, ram_attn_ops.cpp:177-224).
+ */
+int ramnet_topk_addr_backward(const int32_t *idx, const float *val, const void *w_addr, const void *r_addr,
+                              const float *grad_val, int dtype, int64_t B, int64_t H, int64_t U, int64_t P, int64_t T,
+                              int64_t embed_num, int64_t A, const int32_t *position_ids, int64_t w_top_k,
+                              int64_t r_top_k, float w_re_norm, float r_re_norm, void *grad_w_addr,
+                              void *grad_r_addr, void *stream);
+
+/*
  * Bytes of device workspace the segment scan needs for B x H heads, T tokens
  * and the given top-k (per-event records, T padded to 32). The 32-bit form
  * returns -1 when the size does not fit an int.

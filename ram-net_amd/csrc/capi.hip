@@ -65,6 +65,37 @@ int check_addr_shape(int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int6
     return RAMNET_OK;
 }
 
+
+// One decoder source of a backward call (the k rows k_off .. k_off + top_k).
+int addr_backward(const int32_t *idx, const float *val, const void *addr, const float *grad_val, int dtype,
+                  int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int64_t embed_num, int64_t A,
+                  const int32_t *position_ids, int64_t k_total, int64_t k_off, int64_t top_k, float re_norm,
+                  float sign, void *grad_addr, void *stream) {
+    ramnet::AddrBwdJob job{};
+    job.addr = addr;
+    job.idx = idx;
+    job.val = val;
+    job.grad_val = grad_val;
+    job.grad_addr = grad_addr;
+    job.position_ids = position_ids;
+    job.dtype = dtype;
+    job.B = static_cast<int>(B);
+    job.H = static_cast<int>(H);
+    job.U = static_cast<int>(U);
+    job.P = static_cast<int>(P);
+    job.T = static_cast<int>(T);
+    job.A = static_cast<int>(A);
+    job.embed_num = static_cast<int>(embed_num);
+    job.k_total = static_cast<int>(k_total);
+    job.k_off = static_cast<int>(k_off);
+    job.K = static_cast<int>(top_k);
+    job.re_norm = re_norm;
+    job.sign = sign;
+    const char *why = nullptr;
+    const hipError_t err = ramnet::launch_topk_addr_backward(job, static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, "topk_addr backward launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -107,6 +138,48 @@ int ramnet_topk_addr_single_forward(const void *addr, int dtype, int64_t B, int6
     const char *why = nullptr;
     const hipError_t err = ramnet::launch_topk_addr(job, static_cast<hipStream_t>(stream), &why);
     return finish(err, why, "topk_addr_single_forward launch");
+}
+
+int ramnet_topk_addr_single_backward(const int32_t *idx, const float *val, const void *addr, const float *grad_val,
+                                     int dtype, int64_t B, int64_t H, int64_t U, int64_t P, int64_t T,
+                                     int64_t embed_num, int64_t A, const int32_t *position_ids, int64_t top_k,
+                                     float top_k_re_norm, int addr_val_neg, void *grad_addr, void *stream) {
+    if (int rc = check_addr_shape(B, H, U, P, T, embed_num, A))
+        return rc;
+    RAMNET_REQUIRE(valid_dtype(dtype), "addr dtype must be float32, float16 or bfloat16");
+    RAMNET_REQUIRE(top_k > 0 && top_k <= A, "top_k must be in [1, A]");
+    RAMNET_REQUIRE(top_k_re_norm >= 0.f && top_k_re_norm <= 1.f, "top_k_re_norm must be in [0, 1]");
+    RAMNET_REQUIRE(fits_int({B * H * U * P * T, B * H * A, B * H * top_k * T}), "CUDA index overflow: sizes exceed int32");
+    if (B * H * T == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(idx && val && addr && grad_val && position_ids && grad_addr, "null tensor pointer");
+    return addr_backward(idx, val, addr, grad_val, dtype, B, H, U, P, T, embed_num, A, position_ids, top_k, 0, top_k,
+                         top_k_re_norm, addr_val_neg ? -1.f : 1.f, grad_addr, stream);
+}
+
+int ramnet_topk_addr_backward(const int32_t *idx, const float *val, const void *w_addr, const void *r_addr,
+                              const float *grad_val, int dtype, int64_t B, int64_t H, int64_t U, int64_t P, int64_t T,
+                              int64_t embed_num, int64_t A, const int32_t *position_ids, int64_t w_top_k,
+                              int64_t r_top_k, float w_re_norm, float r_re_norm, void *grad_w_addr,
+                              void *grad_r_addr, void *stream) {
+    if (int rc = check_addr_shape(B, H, U, P, T, embed_num, A))
+        return rc;
+    RAMNET_REQUIRE(valid_dtype(dtype), "addr dtype must be float32, float16 or bfloat16");
+    RAMNET_REQUIRE(w_top_k > 0 && w_top_k <= A && r_top_k > 0 && r_top_k <= A, "top_k values must be in [1, A]");
+    RAMNET_REQUIRE(w_re_norm >= 0.f && w_re_norm <= 1.f && r_re_norm >= 0.f && r_re_norm <= 1.f,
+                   "top_k_re_norm exponents must be in [0, 1]");
+    RAMNET_REQUIRE(fits_int({B * H * U * P * T, B * H * A, B * H * (w_top_k + r_top_k) * T}),
+                   "CUDA index overflow: sizes exceed int32");
+    if (B * H * T == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(idx && val && w_addr && r_addr && grad_val && position_ids && grad_w_addr && grad_r_addr,
+                   "null tensor pointer");
+    const int64_t kt = w_top_k + r_top_k;
+    if (int rc = addr_backward(idx, val, w_addr, grad_val, dtype, B, H, U, P, T, embed_num, A, position_ids, kt, 0,
+                               w_top_k, w_re_norm, 1.f, grad_w_addr, stream))
+        return rc;
+    return addr_backward(idx, val, r_addr, grad_val, dtype, B, H, U, P, T, embed_num, A, position_ids, kt, w_top_k,
+                         r_top_k, r_re_norm, -1.f, grad_r_addr, stream);
 }
 
 int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, int64_t B, int64_t H, int64_t U,

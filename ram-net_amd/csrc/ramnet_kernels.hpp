@@ -75,6 +75,23 @@ struct AddrJob {
     const uint8_t *mask;          // (B, T) or null
 };
 
+// Decoder backward for one address source: gradient of the top-K weights
+// (positive-weight convention) -> gradient of the logits.
+struct AddrBwdJob {
+    const void *addr;             // (B, H, U, P, T) logits in dtype
+    const int32_t *idx;           // (B, H, k_total, T), this source at k_off .. k_off + K
+    const float *val;             // (B, H, k_total, T), stored weights (negated when sign < 0)
+    const float *grad_val;        // (B, H, k_total, T), gradient of the positive weights
+    void *grad_addr;              // (B, H, U, P, T) in dtype
+    const int32_t *position_ids;  // (B, T)
+    int dtype;
+    int B, H, U, P, T, A;
+    int embed_num;
+    int k_total, k_off, K;
+    float re_norm;
+    float sign;
+};
+
 // Time-sequential gated sparse update + top-K read over a whole sequence.
 struct SegmentJob {
     const WriteRec *wrec;     // (B*H, Kw, T_pad) scan records
@@ -115,6 +132,7 @@ struct DecodeJob {
 // Launchers return hipSuccess or the launch error; `why` receives a static
 // message when the shape is outside what the kernels were built for.
 hipError_t launch_topk_addr(const AddrJob &job, hipStream_t stream, const char **why);
+hipError_t launch_topk_addr_backward(const AddrBwdJob &job, hipStream_t stream, const char **why);
 hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, const char **why);
 
 // Build scan records from decoder outputs idx/val (B, H, Kw + Kr, T).

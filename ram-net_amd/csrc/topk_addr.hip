@@ -274,7 +274,131 @@ hipError_t launch_typed(const AddrJob &job, hipStream_t stream, const char **why
     return hipGetLastError();
 }
 
+// ---- backward (reference: csrc/ram_attn_topk_addr.cu:119-226)
+//
+// With v_k the selected weights, D_k = dL/dv_k * v_k is the gradient of the
+// score s_k = sum_u L_u[d_u(k)] when re_norm = 0; re-normalisation
+// v_k = exp(s_k - r LSE) subtracts r p_k sum_j D_j with p_k = v_k / sum v.
+// Through the per-digit log-softmax L_u = x_u - logsumexp(x_u):
+//     dL/dx_u[q] = sum_{k: d_u(k) = q} D_k - softmax(x_u)[q] (1 - r) sum_k D_k,
+// since the p_k sum to one. The selection itself carries no gradient, and an
+// inactive address (all weights 0) gets none. One lane per (b, h, t); the
+// logits of a digit are read in three passes (max, sum, gradient), coalesced
+// across the lanes' consecutive t. KM > 0 keeps the K terms in registers;
+// KM = 0 streams them for any K.
+template<typename Scalar, int KM>
+__global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJob job) {
+    const int T = job.T, H = job.H, A = job.A, P = job.P, U = job.U, K = job.K;
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= static_cast<int64_t>(job.B) * H * T)
+        return;
+    const int t = static_cast<int>(gid % T);
+    const int64_t bh = gid / T;
+    const int b = static_cast<int>(bh / H), h = static_cast<int>(bh % H);
+    const int64_t row0 = (bh * job.k_total + job.k_off) * T + t;  // event k at row0 + k * T
+    const float re = job.re_norm;
+    const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + t], A) : 0;
+    auto weight = [&](int k) { return job.sign * job.val[row0 + static_cast<int64_t>(k) * T]; };
+    auto dscore = [&](int k) { return job.grad_val[row0 + static_cast<int64_t>(k) * T] * weight(k); };
+    auto content = [&](int k) {
+        const int o = job.idx[row0 + static_cast<int64_t>(k) * T] % A;  // drops a (b*H + h)*A encoding
+        const int c = o + shift;
+        return c >= A ? c - A : c;
+    };
+    float dsum = 0.f, vsum = 0.f;
+    float D[KM > 0 ? KM : 1];
+    int c[KM > 0 ? KM : 1];
+    if constexpr (KM > 0) {
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+            const bool on = k < K;
+            D[k] = on ? dscore(on ? k : 0) : 0.f;
+            c[k] = on ? content(on ? k : 0) : -1;
+            dsum += D[k];
+            vsum += on ? weight(k) : 0.f;
+        }
+    } else {
+        for (int k = 0; k < K; ++k) {
+            dsum += dscore(k);
+            vsum += weight(k);
+        }
+    }
+    const bool renorm = re != 0.f && vsum > 0.f;
+    auto dk = [&](int k) {  // the re-normalised D_k (streaming form)
+        const float d = dscore(k);
+        return renorm ? d - re * (weight(k) / vsum) * dsum : d;
+    };
+    if constexpr (KM > 0) {
+        if (renorm) {
+#pragma unroll
+            for (int k = 0; k < KM; ++k)
+                D[k] = k < K ? D[k] - re * (weight(k) / vsum) * dsum : 0.f;
+        }
+    }
+    const float dsoft = (1.f - re) * dsum;
+    const Scalar *xp = static_cast<const Scalar *>(job.addr) + bh * U * P * static_cast<int64_t>(T) + t;
+    Scalar *gp = static_cast<Scalar *>(job.grad_addr) + bh * U * P * static_cast<int64_t>(T) + t;
+    int stride = 1;
+    for (int u = 0; u < U; ++u, stride *= P) {
+        const Scalar *xu = xp + static_cast<int64_t>(u) * P * T;
+        Scalar *gu = gp + static_cast<int64_t>(u) * P * T;
+        float mx = -__builtin_huge_valf();
+        for (int q = 0; q < P; ++q)
+            mx = fmaxf(mx, load_f32(xu + static_cast<int64_t>(q) * T));
+        const bool live = mx > -__builtin_huge_valf();
+        float se = 0.f;
+        for (int q = 0; q < P; ++q)
+            se += live ? expf(load_f32(xu + static_cast<int64_t>(q) * T) - mx) : 0.f;
+        const float scale = live ? dsoft / se : 0.f;
+        int du[KM > 0 ? KM : 1];
+        if constexpr (KM > 0) {
+#pragma unroll
+            for (int k = 0; k < KM; ++k)
+                du[k] = c[k] < 0 ? -1 : (c[k] / stride) % P;
+        }
+        for (int q = 0; q < P; ++q) {
+            float g = 0.f;
+            if constexpr (KM > 0) {
+#pragma unroll
+                for (int k = 0; k < KM; ++k)
+                    g += du[k] == q ? D[k] : 0.f;
+            } else {
+                for (int k = 0; k < K; ++k)
+                    g += (content(k) / stride) % P == q ? dk(k) : 0.f;
+            }
+            const float sm = live ? expf(load_f32(xu + static_cast<int64_t>(q) * T) - mx) : 0.f;
+            store_f32(gu + static_cast<int64_t>(q) * T, g - sm * scale);
+        }
+    }
+}
+
+template<typename T>
+hipError_t launch_backward_typed(const AddrBwdJob &job, hipStream_t stream) {
+    const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256)), blk(256);
+    if (job.K <= 8)
+        hipLaunchKernelGGL((topk_addr_backward_kernel<T, 8>), grid, blk, 0, stream, job);
+    else if (job.K <= 16)
+        hipLaunchKernelGGL((topk_addr_backward_kernel<T, 16>), grid, blk, 0, stream, job);
+    else if (job.K <= 32)
+        hipLaunchKernelGGL((topk_addr_backward_kernel<T, 32>), grid, blk, 0, stream, job);
+    else
+        hipLaunchKernelGGL((topk_addr_backward_kernel<T, 0>), grid, blk, 0, stream, job);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_topk_addr_backward(const AddrBwdJob &job, hipStream_t stream, const char **why) {
+    if (static_cast<int64_t>(job.B) * job.H * job.T == 0)
+        return hipSuccess;
+    switch (job.dtype) {
+        case kF32: return launch_backward_typed<float>(job, stream);
+        case kF16: return launch_backward_typed<_Float16>(job, stream);
+        case kBF16: return launch_backward_typed<bf16_t>(job, stream);
+        default: *why = "address decoder backward: unsupported dtype"; return hipErrorInvalidValue;
+    }
+}
 
 hipError_t launch_topk_addr(const AddrJob &job, hipStream_t stream, const char **why) {
     if (static_cast<int64_t>(job.B) * job.H * job.T == 0)

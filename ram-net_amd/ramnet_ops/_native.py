@@ -43,6 +43,12 @@ SIGNATURES: dict[str, tuple[type, list]] = {
     "ramnet_topk_addr_forward": (_c_int, [
         _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr,
         _c_i64, _c_i64, _c_float, _c_float, _c_int, _c_ptr, _c_ptr, _c_ptr]),
+    "ramnet_topk_addr_single_backward": (_c_int, [
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr,
+        _c_i64, _c_float, _c_int, _c_ptr, _c_ptr]),
+    "ramnet_topk_addr_backward": (_c_int, [
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_ptr, _c_i64, _c_i64, _c_float, _c_float, _c_ptr, _c_ptr, _c_ptr]),
     "ramnet_scan_workspace_bytes64": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "ramnet_scan_workspace_bytes": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "ramnet_topk_segment_forward": (_c_int, [

@@ -88,6 +88,106 @@ def _(w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re_norm, r
 
 
 # --------------------------------------------------------------------------
+# address decoder backward (reference: ram_attn_bind.cpp:36-64 schemas,
+# _cuda_autograd.py:4-180 wiring)
+
+@torch.library.custom_op(f"{_NS}::topk_addr_single_backward", mutates_args=(), device_types="cuda")
+def topk_addr_single_backward(idx: Tensor, val: Tensor, addr: Tensor, D_val: Tensor, embed_num: int,
+                              position_ids: Tensor, top_k: int, top_k_re_norm: float, addr_val_neg: bool,
+                              shape: list[int], dtype: torch.dtype) -> Tensor:
+    _require_gpu("topk_addr_single_backward", idx, val, addr, D_val, position_ids)
+    B, H, U, P, A, T = shape
+    addr = addr.to(dtype).contiguous()
+    pos = position_ids.to(device=addr.device, dtype=torch.int32).contiguous()
+    grad = torch.empty((B, H, U, P, T), dtype=dtype, device=addr.device)
+    with torch.cuda.device(addr.device):
+        nat.call("ramnet_topk_addr_single_backward", idx.to(torch.int32).contiguous().data_ptr(),
+                 val.to(torch.float32).contiguous().data_ptr(), addr.data_ptr(),
+                 D_val.to(torch.float32).contiguous().data_ptr(), _code(addr), B, H, U, P, T, embed_num, A,
+                 pos.data_ptr(), top_k, float(top_k_re_norm), int(addr_val_neg), grad.data_ptr(),
+                 nat.stream_of(addr))
+    return grad
+
+
+@topk_addr_single_backward.register_fake
+def _(idx, val, addr, D_val, embed_num, position_ids, top_k, top_k_re_norm, addr_val_neg, shape, dtype):
+    B, H, U, P, _, T = shape
+    return val.new_empty((B, H, U, P, T), dtype=dtype)
+
+
+@torch.library.custom_op(f"{_NS}::topk_addr_backward", mutates_args=(), device_types="cuda")
+def topk_addr_backward(idx: Tensor, val: Tensor, w_addr: Tensor, r_addr: Tensor, D_val: Tensor, embed_num: int,
+                       position_ids: Tensor, w_top_k: int, r_top_k: int, w_re_norm: float, r_re_norm: float,
+                       shape: list[int], dtype: torch.dtype) -> tuple[Tensor, Tensor]:
+    _require_gpu("topk_addr_backward", idx, val, w_addr, r_addr, D_val, position_ids)
+    B, H, U, P, A, T = shape
+    w_addr, r_addr = w_addr.to(dtype).contiguous(), r_addr.to(dtype).contiguous()
+    pos = position_ids.to(device=w_addr.device, dtype=torch.int32).contiguous()
+    gw = torch.empty((B, H, U, P, T), dtype=dtype, device=w_addr.device)
+    gr = torch.empty_like(gw)
+    with torch.cuda.device(w_addr.device):
+        nat.call("ramnet_topk_addr_backward", idx.to(torch.int32).contiguous().data_ptr(),
+                 val.to(torch.float32).contiguous().data_ptr(), w_addr.data_ptr(), r_addr.data_ptr(),
+                 D_val.to(torch.float32).contiguous().data_ptr(), _code(w_addr), B, H, U, P, T, embed_num, A,
+                 pos.data_ptr(), w_top_k, r_top_k, float(w_re_norm), float(r_re_norm), gw.data_ptr(), gr.data_ptr(),
+                 nat.stream_of(w_addr))
+    return gw, gr
+
+
+@topk_addr_backward.register_fake
+def _(idx, val, w_addr, r_addr, D_val, embed_num, position_ids, w_top_k, r_top_k, w_re_norm, r_re_norm, shape,
+      dtype):
+    B, H, U, P, _, T = shape
+    return val.new_empty((B, H, U, P, T), dtype=dtype), val.new_empty((B, H, U, P, T), dtype=dtype)
+
+
+def _single_setup(ctx, inputs, output):
+    addr, embed_num, A, position_ids, top_k, top_k_re_norm, addr_val_neg, _ = inputs
+    idx, val = output
+    B, H, U, P, T = addr.shape
+    ctx.args = (embed_num, top_k, float(top_k_re_norm), bool(addr_val_neg), [B, H, U, P, A, T], addr.dtype)
+    ctx.save_for_backward(idx, val, position_ids, addr)
+    ctx.mark_non_differentiable(idx)
+    ctx.set_materialize_grads(False)
+
+
+def _single_backward(ctx, D_idx, D_val):
+    if D_val is None:
+        return (None,) * 8
+    idx, val, position_ids, addr = ctx.saved_tensors
+    embed_num, top_k, re_norm, neg, shape, dtype = ctx.args
+    grad = topk_addr_single_backward(idx, val, addr, D_val, embed_num, position_ids, top_k, re_norm, neg, shape,
+                                     dtype)
+    return (grad,) + (None,) * 7
+
+
+topk_addr_single_forward.register_autograd(_single_backward, setup_context=_single_setup)
+
+
+def _pair_setup(ctx, inputs, output):
+    w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re_norm, r_re_norm, _ = inputs
+    idx, val = output
+    B, H, U, P, T = w_addr.shape
+    ctx.args = (embed_num, w_top_k, r_top_k, float(w_re_norm), float(r_re_norm), [B, H, U, P, A, T], w_addr.dtype)
+    ctx.save_for_backward(idx, val, position_ids, w_addr, r_addr)
+    ctx.mark_non_differentiable(idx)
+    ctx.set_materialize_grads(False)
+
+
+def _pair_backward(ctx, D_idx, D_val):
+    if D_val is None:
+        return (None,) * 10
+    idx, val, position_ids, w_addr, r_addr = ctx.saved_tensors
+    embed_num, w_top_k, r_top_k, w_re, r_re, shape, dtype = ctx.args
+    gw, gr = topk_addr_backward(idx, val, w_addr, r_addr, D_val, embed_num, position_ids, w_top_k, r_top_k, w_re,
+                                r_re, shape, dtype)
+    return (gw, gr) + (None,) * 8
+
+
+topk_addr_forward.register_autograd(_pair_backward, setup_context=_pair_setup)
+
+
+# --------------------------------------------------------------------------
 # segment scan (prefill)
 
 def _segment_args(x, gamma, mask):

@@ -9,8 +9,11 @@ time-ordered segment scan. Differences by design:
 * no padding of T to a multiple of 32 (the HIP kernels take any T);
 * no event grouping (``gather_segment``'s global sort): the segment scan walks
   tokens in order with the slot state resident in LDS;
-* forward only. Backward kernels are not built yet, so inputs that require
-  grad raise ``NotImplementedError`` instead of silently dropping gradients.
+* the address decoder is differentiable (its backward kernel is registered
+  as the autograd formula of ``topk_addr_single_forward`` and
+  ``topk_addr_forward``); the segment scan and the decode step are forward
+  only, so ``random_access_memory_attention`` on inputs that require grad
+  raises ``NotImplementedError`` instead of silently dropping gradients.
 """
 from __future__ import annotations
 
@@ -25,7 +28,8 @@ ops = _ops  # the registered torch.ops.ramnet_ops.* operators
 def _no_grad_support(tensors) -> None:
     if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
         raise NotImplementedError(
-            "ramnet_ops on MI355X implements the forward pass only; backward kernels are not built yet. "
+            "ramnet_ops on MI355X: random_access_memory_attention is forward only (the segment-scan backward is "
+            "not built yet; topk_addr is differentiable). "
             "Run under torch.no_grad() or detach the inputs.")
 
 
@@ -174,7 +178,6 @@ def _cuda_topk_addr(
     assert isinstance(encode_batch_idx, bool), f"Expected boolean encode_batch_idx, got {encode_batch_idx!r}."
     assert tuple(position_ids.shape) == (B, T), f"Expected position_ids.shape={(B, T)}, got {tuple(position_ids.shape)}."
     check_int_capacity(B, H, U, P, A, T, embed_num, top_k, B * H * U * P * T, B * H * A, B * H * top_k * T)
-    _no_grad_support([addr])
     position_ids = position_ids.to(device=addr.device, dtype=torch.int32)
     return torch.ops.ramnet_ops.topk_addr_single_forward(
         addr, embed_num, A, position_ids, top_k, float(top_k_re_norm), addr_val_neg, encode_batch_idx)
