@@ -151,6 +151,36 @@ int ramnet_topk_segment_forward_(const int32_t *addr_idx, const float *addr_val,
                                  void *stream);
 
 /*
+ * Gradients of ramnet_topk_segment_forward. Replaces
+ * ramnet_ops::topk_segment_backward (ram_attn_bind.cpp:74-82,
+ * ram_attn_ops.cpp:267-310); like the forward it takes the decoder outputs
+ * instead of event-grouping metadata.
+ *   addr_idx, addr_val, x, gamma, mask, init_slot, init_mass
+ *                       the forward's inputs
+ *   grad_y              (B, H, T, C) `dtype` (the reference casts it to x's
+ *                       dtype too); masked tokens' entries are ignored
+ *   grad_slot/mass      (B, H, A, C) / (B, H, A) fp32 gradients of the final
+ *                       state, or NULL for zero
+ *   grad_addr_val       (B, H, Kw + Kr, T) fp32: gradients of the positive
+ *                       write and read weights (0 for events that do not act)
+ *   grad_x              (B, H, T, C) fp32;  grad_gamma (B, H, T) fp32
+ *   grad_init_slot/mass (B, H, A, C) / (B, H, A) fp32
+ *   workspace           >= ramnet_segment_backward_workspace_bytes(...) bytes
+ * Deterministic: no atomics.
+ */
+int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
+                                 int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
+                                 const void *grad_y, const float *grad_slot, const float *grad_mass,
+                                 float *grad_addr_val, float *grad_x, float *grad_gamma, float *grad_init_slot,
+                                 float *grad_init_mass, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                                 int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *workspace,
+                                 int64_t workspace_bytes, void *stream);
+
+/* Device workspace bytes of ramnet_topk_segment_backward; -1 for shapes it does not take. */
+int64_t ramnet_segment_backward_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                                                int64_t w_top_k, int64_t r_top_k);
+
+/*
  * The two stages of ramnet_ram_attn_forward, for callers that schedule or
  * time them separately. ramnet_topk_addr_records runs both address decoders
  * and writes the scan's per-event records into `workspace` (CAPE, mask,

@@ -24,7 +24,7 @@ LIB_DIR = os.path.join(HERE, "ramnet_ops", "_lib")
 LIB = os.path.join(LIB_DIR, "libramnet_hip.so")
 
 SOURCES = ("topk_addr.hip", "segment_forward.hip", "segment_scan_f32.hip", "segment_scan_f16.hip",
-           "segment_scan_bf16.hip", "autoregressive.hip", "capi.hip")
+           "segment_scan_bf16.hip", "segment_backward.hip", "autoregressive.hip", "capi.hip")
 ARCH = "gfx950"
 
 

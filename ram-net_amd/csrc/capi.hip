@@ -282,6 +282,28 @@ static ramnet::SegmentJob make_segment_job(const void *x, int dtype, const float
     return job;
 }
 
+// Scan records from decoder outputs, into the job's workspace.
+static hipError_t pack_decoded(const ramnet::SegmentJob &job, const int32_t *addr_idx, const float *addr_val,
+                               const void *gamma, const uint8_t *mask, hipStream_t s, const char **why) {
+    ramnet::PackJob pack{};
+    pack.addr_idx = addr_idx;
+    pack.addr_val = addr_val;
+    pack.gamma = gamma;
+    pack.mask = mask;
+    pack.wrec = const_cast<ramnet::WriteRec *>(job.wrec);
+    pack.rrec = const_cast<ramnet::ReadRec *>(job.rrec);
+    pack.noop_w = const_cast<ramnet::WriteRec *>(job.noop_w);
+    pack.noop_r = const_cast<ramnet::ReadRec *>(job.noop_r);
+    pack.dtype = job.dtype;
+    pack.B = job.B;
+    pack.H = job.H;
+    pack.T = job.T;
+    pack.A = job.A;
+    pack.Kw = job.Kw;
+    pack.Kr = job.Kr;
+    return ramnet::launch_pack_records(pack, s, why);
+}
+
 static int segment_from_decoded(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
                                 int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
                                 float *slot_out, float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A,
@@ -298,23 +320,7 @@ static int segment_from_decoded(const int32_t *addr_idx, const float *addr_val, 
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const char *why = nullptr;
     if (T > 0) {
-        ramnet::PackJob pack{};
-        pack.addr_idx = addr_idx;
-        pack.addr_val = addr_val;
-        pack.gamma = gamma;
-        pack.mask = mask;
-        pack.wrec = const_cast<ramnet::WriteRec *>(job.wrec);
-        pack.rrec = const_cast<ramnet::ReadRec *>(job.rrec);
-        pack.noop_w = const_cast<ramnet::WriteRec *>(job.noop_w);
-        pack.noop_r = const_cast<ramnet::ReadRec *>(job.noop_r);
-        pack.dtype = dtype;
-        pack.B = job.B;
-        pack.H = job.H;
-        pack.T = job.T;
-        pack.A = job.A;
-        pack.Kw = job.Kw;
-        pack.Kr = job.Kr;
-        const hipError_t err = ramnet::launch_pack_records(pack, s, &why);
+        const hipError_t err = pack_decoded(job, addr_idx, addr_val, gamma, mask, s, &why);
         if (err != hipSuccess)
             return finish(err, why, what);
     }
@@ -434,6 +440,70 @@ int ramnet_ram_attn_forward(const void *w_addr, const void *r_addr, const void *
     }
     return ramnet_segment_scan(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k, r_top_k,
                                mass_aware, eps, workspace, workspace_bytes, stream);
+}
+
+static int64_t backward_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t Kw,
+                                        int64_t Kr) {
+    if (B < 0 || H <= 0 || T < 0 || A <= 0 || C <= 0 || Kw <= 0 || Kr <= 0 || A >= kAddressLimit ||
+        !fits_int({B * H * A * C, B * H * (A + 2), B * H * T * C, B * H * (T + ramnet::kScanPad) * (Kw + Kr)}))
+        return -1;
+    const int64_t rec = (scan_workspace_bytes(B, H, T, Kw, Kr) + 255) / 256 * 256;
+    const int64_t extra = ramnet::segment_backward_layout(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T),
+                                                          static_cast<int>(A), static_cast<int>(C), static_cast<int>(Kw),
+                                                          static_cast<int>(Kr), nullptr, nullptr);
+    return extra < 0 ? -1 : rec + extra;
+}
+
+int64_t ramnet_segment_backward_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                                                int64_t w_top_k, int64_t r_top_k) {
+    return backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k);
+}
+
+int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
+                                 int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
+                                 const void *grad_y, const float *grad_slot, const float *grad_mass,
+                                 float *grad_addr_val, float *grad_x, float *grad_gamma, float *grad_init_slot,
+                                 float *grad_init_mass, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                                 int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *workspace,
+                                 int64_t workspace_bytes, void *stream) {
+    if (int rc = segment_checks(x, gamma, dtype, init_slot, init_mass, grad_init_slot, grad_init_mass, grad_x, B, H,
+                                T, A, C, w_top_k, r_top_k, eps, workspace, workspace_bytes))
+        return rc;
+    if (B == 0)
+        return RAMNET_OK;
+    const int64_t need = backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k);
+    RAMNET_REQUIRE(need >= 0, "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A small "
+                              "enough for an (A + 2) x slice-channels fp32 slice in 160 KiB of LDS)");
+    RAMNET_REQUIRE(workspace_bytes >= need && workspace,
+                   "workspace too small: see ramnet_segment_backward_workspace_bytes");
+    RAMNET_REQUIRE(T == 0 || (addr_idx && addr_val && grad_y && grad_addr_val && grad_gamma), "null tensor pointer");
+    ramnet::SegmentJob fj = make_segment_job(x, dtype, init_slot, init_mass, nullptr, nullptr, nullptr, B, H, T, A, C,
+                                             w_top_k, r_top_k, mass_aware, eps, workspace);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const char *why = nullptr;
+    if (T > 0) {
+        const hipError_t err = pack_decoded(fj, addr_idx, addr_val, gamma, mask, s, &why);
+        if (err != hipSuccess)
+            return finish(err, why, "topk_segment_backward launch");
+    }
+    ramnet::SegmentBwdJob job{};
+    job.fwd = fj;
+    job.addr_val = addr_val;
+    job.gamma = gamma;
+    job.grad_y = grad_y;
+    job.grad_slot = grad_slot;
+    job.grad_mass = grad_mass;
+    job.grad_val = grad_addr_val;
+    job.grad_x = grad_x;
+    job.grad_gamma = grad_gamma;
+    job.grad_init_slot = grad_init_slot;
+    job.grad_init_mass = grad_init_mass;
+    const int64_t rec = (scan_workspace_bytes(B, H, T, w_top_k, r_top_k) + 255) / 256 * 256;
+    ramnet::segment_backward_layout(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T), static_cast<int>(A),
+                                    static_cast<int>(C), static_cast<int>(w_top_k), static_cast<int>(r_top_k),
+                                    static_cast<char *>(workspace) + rec, &job);
+    const hipError_t err = ramnet::launch_segment_backward(job, s, &why);
+    return finish(err, why, "topk_segment_backward launch");
 }
 
 int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,

@@ -110,6 +110,37 @@ struct SegmentJob {
     float eps;
 };
 
+// Per-event forward quantities of the segment backward, written by the mass
+// pre-pass in its record-keeping mode. Token-major: (B*H, T, K).
+struct MassAux {
+    int2 *wev;   // (B*H, T, Kw) {slot, or -2 for a no-op; gain g = w / (m + eps) as bits}
+    float *wm;   // (B*H, T, Kw) slot mass before the write
+    int2 *rev;   // (B*H, T, Kr) {slot, or -1 for a no-op; effective read weight as bits}
+    float *rm;   // (B*H, T, Kr) post-write mass of the read slot
+};
+
+// Segment backward (gradients of ramnet_topk_segment_forward).
+struct SegmentBwdJob {
+    SegmentJob fwd;           // records, x, init state, shapes (y, slot_out unused)
+    MassAux aux;
+    const float *addr_val;    // (B, H, Kw + Kr, T) decoder weights (reads negated)
+    const void *gamma;        // (B, H, T) in dtype
+    const void *grad_y;       // (B, H, T, C) in dtype
+    const float *grad_slot;   // (B, H, A, C) or null (zero)
+    const float *grad_mass;   // (B, H, A) or null (zero)
+    float *grad_val;          // (B, H, Kw + Kr, T): positive-weight gradients
+    float *grad_x;            // (B, H, T, C)
+    float *grad_gamma;        // (B, H, T)
+    float *grad_init_slot;    // (B, H, A, C)
+    float *grad_init_mass;    // (B, H, A)
+    float *delta;             // (B*H*n_sub, T, Kw, CSW) x - s before each write
+    float *dr_part;           // (n_sub, B*H, T, Kr) per-slice read dot products
+    float *dg_part;           // (n_sub, B*H, T, Kw) per-slice gain gradients
+    float *mass_scratch;      // (B*H*A)
+    void *maps;               // chunk maps of the mass replay
+    size_t maps_bytes;
+};
+
 // One fused autoregressive step: decode, K writes, then K reads.
 struct DecodeJob {
     const void *w_addr;       // (B, H, U, P)
@@ -153,5 +184,20 @@ hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const
 
 // Channel-slice width and dynamic LDS bytes the segment kernel would use.
 int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes);
+
+// Mass pre-pass in record-keeping mode: the records stay as they are and
+// `aux` receives the per-event quantities. `maps` holds the chunk maps
+// (mass_replay_scratch_bytes of it); the final masses go to job.mass_out.
+int64_t mass_replay_scratch_bytes(int B, int H, int T, int A);
+hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *maps, size_t maps_bytes,
+                              hipStream_t stream);
+
+// Segment backward. segment_backward_layout places the backward's buffers
+// (everything in SegmentBwdJob past `fwd` and the inputs/outputs) in `base`
+// and returns their total size in bytes (-1: shape not supported); with a
+// null `base` it only sizes. The launch expects the scan records already
+// packed into job.fwd's workspace.
+int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int Kr, char *base, SegmentBwdJob *job);
+hipError_t launch_segment_backward(const SegmentBwdJob &job, hipStream_t stream, const char **why);
 
 }  // namespace ramnet

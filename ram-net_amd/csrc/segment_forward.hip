@@ -290,10 +290,13 @@ __global__ __launch_bounds__(256) void mass_chunk_scan_kernel(const SegmentJob j
 }
 
 // Step 3: one wave per (b, h, chunk), from m_start (the maps after step 2,
-// or the initial mass when there is one chunk).
-template<bool MA, int MP>
+// or the initial mass when there is one chunk). With AUX the records stay
+// as they are and the per-event quantities go to `aux` instead (the forward
+// replay of the segment backward).
+template<bool MA, int MP, bool AUX = false>
 __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, WriteRec *wrec, ReadRec *rrec,
-                                                            int t_pad, int chunk_len, const float2 *starts) {
+                                                            int t_pad, int chunk_len, const float2 *starts,
+                                                            const MassAux aux) {
     using L = MassLanes<MP>;
     constexpr int CH = L::CH;
     extern __shared__ __align__(16) float lds[];
@@ -335,30 +338,49 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
             for (int p = 0; p < MP; ++p) {
                 const float m2 = fmaf(al[p], m[p], w[p]);
                 ms[a[p]] = m2;
-                if (wlane && ln.on[p] && live)
-                    gw[static_cast<int64_t>(ln.ev[p]) * t_pad + t].alpha = scan_gain(w[p], m2 + eps);
+                if (wlane && ln.on[p] && live) {
+                    const float gn = scan_gain(w[p], m2 + eps);
+                    if constexpr (AUX) {
+                        const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kw + ln.ev[p];
+                        aux.wev[o] = make_int2(a[p], __float_as_int(gn));
+                        aux.wm[o] = m[p];
+                    } else {
+                        gw[static_cast<int64_t>(ln.ev[p]) * t_pad + t].alpha = gn;
+                    }
+                }
             }
-            if constexpr (MA) {
+            if constexpr (MA || AUX) {
                 int rb[MP];
-                float rr[MP];
+                float rr[MP], mm[MP];
                 float sr = 0.f, srm = 0.f;
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
                     const bool act = !wlane && ln.on[p] && live;
                     rb[p] = act ? c.r[p][j].x : -1;
                     rr[p] = act ? __int_as_float(c.r[p][j].y) : 0.f;
-                    const float wm = rr[p] * ms[rb[p]];  // post-write mass
+                    mm[p] = ms[rb[p]];  // post-write mass
                     sr += rr[p];
-                    srm += wm;
-                    rr[p] = wm;
+                    srm += rr[p] * mm[p];
                 }
-                sr = event_sum<32>(sr);
-                srm = event_sum<32>(srm);
-                const float scale = sr / (srm + eps);
+                float scale = 1.f;
+                if constexpr (MA) {
+                    sr = event_sum<32>(sr);
+                    srm = event_sum<32>(srm);
+                    scale = sr / (srm + eps);
+                }
 #pragma unroll
-                for (int p = 0; p < MP; ++p)
-                    if (!wlane && ln.on[p] && live)
-                        gr[static_cast<int64_t>(ln.ev[p]) * t_pad + t].r = rr[p] * scale;
+                for (int p = 0; p < MP; ++p) {
+                    if (!wlane && ln.on[p] && live) {
+                        const float re = MA ? rr[p] * mm[p] * scale : rr[p];
+                        if constexpr (AUX) {
+                            const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kr + ln.ev[p];
+                            aux.rev[o] = make_int2(rb[p], __float_as_int(re));
+                            aux.rm[o] = mm[p];
+                        } else {
+                            gr[static_cast<int64_t>(ln.ev[p]) * t_pad + t].r = re;
+                        }
+                    }
+                }
             }
         };
 #pragma unroll
@@ -415,41 +437,64 @@ int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chun
     return (job.T + *chunk_len - 1) / *chunk_len;
 }
 
-template<bool MA, int MP>
-hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, hipStream_t stream) {
+// `maps` is scratch for the chunk maps (maps_bytes of it); the final masses
+// go to job.mass_out.
+template<bool MA, int MP, bool AUX>
+hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void *maps_buf, size_t maps_bytes,
+                               const MassAux &aux, hipStream_t stream) {
     auto *w = const_cast<WriteRec *>(job.wrec);  // the records are the caller's workspace
     auto *r = const_cast<ReadRec *>(job.rrec);
-    const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);
     int len = 0;
-    const int nck = mass_chunks(job, y_bytes, n_cu, &len);
+    const int nck = mass_chunks(job, maps_bytes, n_cu, &len);
     const unsigned bh = static_cast<unsigned>(job.B * job.H);
     if (nck <= 1) {
-        hipLaunchKernelGGL((segment_mass_kernel<MA, MP>), dim3(bh, 1), dim3(kWave), static_cast<size_t>(job.A + 2) * 4,
-                           stream, job, w, r, t_pad, job.T, nullptr);
+        hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, 1), dim3(kWave),
+                           static_cast<size_t>(job.A + 2) * 4, stream, job, w, r, t_pad, job.T, nullptr, aux);
         return hipGetLastError();
     }
-    auto *maps = static_cast<float2 *>(job.y);  // scratch: the scan overwrites y afterwards
+    auto *maps = static_cast<float2 *>(maps_buf);
     hipLaunchKernelGGL((mass_chunk_map_kernel<MP>), dim3(bh, nck), dim3(kWave), static_cast<size_t>(job.A + 2) * 8,
                        stream, job, maps, t_pad, len);
     const int64_t n = static_cast<int64_t>(bh) * job.A;
     hipLaunchKernelGGL(mass_chunk_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, job,
                        maps, nck);
-    hipLaunchKernelGGL((segment_mass_kernel<MA, MP>), dim3(bh, nck), dim3(kWave), static_cast<size_t>(job.A + 2) * 4,
-                       stream, job, w, r, t_pad, len, maps);
+    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, nck), dim3(kWave),
+                       static_cast<size_t>(job.A + 2) * 4, stream, job, w, r, t_pad, len, maps, aux);
     return hipGetLastError();
 }
 
-template<bool MA>
-hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, int n_cu, hipStream_t stream) {
+template<bool MA, bool AUX>
+hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, int n_cu, void *maps, size_t maps_bytes,
+                            const MassAux &aux, hipStream_t stream) {
     const int kmax = std::max(job.Kw, job.Kr);
     if (kmax <= 32)
-        return launch_mass_pass_mp<MA, 1>(job, t_pad, n_cu, stream);
+        return launch_mass_pass_mp<MA, 1, AUX>(job, t_pad, n_cu, maps, maps_bytes, aux, stream);
     if (kmax <= 64)
-        return launch_mass_pass_mp<MA, 2>(job, t_pad, n_cu, stream);
-    return launch_mass_pass_mp<MA, 4>(job, t_pad, n_cu, stream);
+        return launch_mass_pass_mp<MA, 2, AUX>(job, t_pad, n_cu, maps, maps_bytes, aux, stream);
+    return launch_mass_pass_mp<MA, 4, AUX>(job, t_pad, n_cu, maps, maps_bytes, aux, stream);
 }
 
 }  // namespace
+
+int64_t mass_replay_scratch_bytes(int B, int H, int T, int A) {
+    SegmentJob job{};
+    job.B = B;
+    job.H = H;
+    job.T = T;
+    job.A = A;
+    int len = 0;
+    const int nck = mass_chunks(job, static_cast<size_t>(1) << 62, cu_count(), &len);
+    return nck <= 1 ? 0 : static_cast<int64_t>(B) * H * nck * A * static_cast<int64_t>(sizeof(float2));
+}
+
+hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *maps, size_t maps_bytes,
+                              hipStream_t stream) {
+    if (static_cast<int64_t>(job.B) * job.H * job.T == 0)
+        return hipSuccess;
+    const int t_pad = scan_t_pad(job.T);
+    return job.mass_aware ? launch_mass_pass<true, true>(job, t_pad, cu_count(), maps, maps_bytes, aux, stream)
+                          : launch_mass_pass<false, true>(job, t_pad, cu_count(), maps, maps_bytes, aux, stream);
+}
 
 hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const char **why) {
     const int t_pad = scan_t_pad(job.T);
@@ -522,8 +567,12 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
         return hipErrorInvalidValue;
     }
     if (p.pre) {
-        const hipError_t err = job.mass_aware ? launch_mass_pass<true>(job, geo.t_pad, cu_count(), stream)
-                                              : launch_mass_pass<false>(job, geo.t_pad, cu_count(), stream);
+        // the chunk maps use y as scratch: the scan overwrites it afterwards
+        const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);
+        const MassAux none{};
+        const hipError_t err =
+            job.mass_aware ? launch_mass_pass<true, false>(job, geo.t_pad, cu_count(), job.y, y_bytes, none, stream)
+                           : launch_mass_pass<false, false>(job, geo.t_pad, cu_count(), job.y, y_bytes, none, stream);
         if (err != hipSuccess)
             return err;
     }

@@ -71,6 +71,11 @@ SIGNATURES: dict[str, tuple[type, list]] = {
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr,
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_float,
         _c_int, _c_float, _c_ptr, _c_ptr]),
+    "ramnet_topk_segment_backward": (_c_int, [
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_int, _c_float, _c_ptr, _c_i64, _c_ptr]),
+    "ramnet_segment_backward_workspace_bytes": (_c_i64, [_c_i64] * 7),
     "ramnet_segment_plan": (_c_int, [
         _c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
 }
@@ -123,6 +128,11 @@ def segment_plan(A: int, C: int, w_top_k: int, r_top_k: int) -> tuple[int, int] 
 def scan_workspace_bytes(B: int, H: int, T: int, w_top_k: int, r_top_k: int) -> int:
     """Device workspace (bytes) the segment scan needs for these sizes."""
     return int(lib().ramnet_scan_workspace_bytes64(B, H, T, w_top_k, r_top_k))
+
+
+def segment_backward_workspace_bytes(B: int, H: int, T: int, A: int, C: int, w_top_k: int, r_top_k: int) -> int:
+    """Device workspace (bytes) of the segment backward; -1 for shapes it does not take."""
+    return int(lib().ramnet_segment_backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

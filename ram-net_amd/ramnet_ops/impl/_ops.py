@@ -234,6 +234,90 @@ def _(addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k
             init_mass.new_empty(init_mass.shape, dtype=torch.float32))
 
 
+@torch.library.custom_op(f"{_NS}::topk_segment_backward", mutates_args=(), device_types="cuda")
+def topk_segment_backward(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, init_slot: Tensor,
+                          init_mass: Tensor, mask: Tensor | None, D_y: Tensor, D_post_slot: Tensor | None,
+                          D_post_mass: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool,
+                          eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of ``topk_segment_forward`` (reference op: ram_attn_ops.cpp:267-310).
+
+    Returns (D_addr_val (B, H, Kw + Kr, T), D_x (B, H, T, C), D_gamma (B, H, T),
+    D_init_slot, D_init_mass), all float32. Read rows of D_addr_val are
+    gradients with respect to the positive read weights, the contract
+    ``topk_addr_backward`` expects; events that do not act get 0.
+    """
+    _require_gpu("topk_segment_backward", addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, D_y,
+                 D_post_slot, D_post_mass)
+    B, H, T, C = x.shape
+    x, gamma, mask = _segment_args(x, gamma, mask)
+    addr_idx = addr_idx.to(torch.int32).contiguous()
+    addr_val = addr_val.to(torch.float32).contiguous()
+    A = init_slot.shape[-2]
+    init_slot = init_slot.to(torch.float32).contiguous()
+    init_mass = init_mass.to(torch.float32).contiguous()
+    D_y = D_y.to(dtype=x.dtype).contiguous()  # as the reference, the output gradient is taken in x's dtype
+    if D_post_slot is not None:
+        D_post_slot = D_post_slot.to(torch.float32).contiguous()
+    if D_post_mass is not None:
+        D_post_mass = D_post_mass.to(torch.float32).contiguous()
+    f32 = dict(dtype=torch.float32, device=x.device)
+    D_addr = torch.empty((B, H, w_top_k + r_top_k, T), **f32)
+    D_x = torch.empty((B, H, T, C), **f32)
+    D_gamma = torch.empty((B, H, T), **f32)
+    D_slot = torch.empty_like(init_slot)
+    D_mass = torch.empty_like(init_mass)
+    nbytes = nat.segment_backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k)
+    if nbytes < 0:
+        raise RuntimeError(f"topk_segment_backward: shape not supported (A={A}, C={C}, top_k=({w_top_k}, {r_top_k}))")
+    ws = torch.empty(max(1, nbytes), dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        nat.call("ramnet_topk_segment_backward", addr_idx.data_ptr(), addr_val.data_ptr(), x.data_ptr(),
+                 gamma.data_ptr(), _code(x), nat.ptr(mask), init_slot.data_ptr(), init_mass.data_ptr(),
+                 D_y.data_ptr(), nat.ptr(D_post_slot), nat.ptr(D_post_mass), D_addr.data_ptr(), D_x.data_ptr(),
+                 D_gamma.data_ptr(), D_slot.data_ptr(), D_mass.data_ptr(), B, H, T, A, C, w_top_k, r_top_k,
+                 int(mass_aware), float(eps), ws.data_ptr(), ws.numel(), nat.stream_of(x))
+    return D_addr, D_x, D_gamma, D_slot, D_mass
+
+
+@topk_segment_backward.register_fake
+def _(addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, D_y, D_post_slot, D_post_mass, w_top_k, r_top_k,
+      mass_aware, eps):
+    B, H, T, C = x.shape
+    f32 = torch.float32
+    return (x.new_empty((B, H, w_top_k + r_top_k, T), dtype=f32), x.new_empty(x.shape, dtype=f32),
+            x.new_empty((B, H, T), dtype=f32), init_slot.new_empty(init_slot.shape, dtype=f32),
+            init_mass.new_empty(init_mass.shape, dtype=f32))
+
+
+def _segment_setup(ctx, inputs, output):
+    addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps = inputs
+    ctx.args = (w_top_k, r_top_k, bool(mass_aware), float(eps))
+    ctx.dtypes = (x.dtype, gamma.dtype, init_slot.dtype, init_mass.dtype)
+    ctx.save_for_backward(addr_idx, addr_val, x, gamma, init_slot, init_mass, mask)
+    ctx.set_materialize_grads(False)
+
+
+def _segment_backward(ctx, D_y, D_slot, D_mass):
+    """Autograd formula of ``topk_segment_forward`` (reference: _cuda_autograd.py:239-287)."""
+    addr_idx, addr_val, x, gamma, init_slot, init_mass, mask = ctx.saved_tensors
+    w_top_k, r_top_k, mass_aware, eps = ctx.args
+    x_dt, g_dt, s_dt, m_dt = ctx.dtypes
+    if D_y is None:
+        D_y = torch.zeros_like(x)
+    D_addr, D_x, D_gamma, D_s, D_m = topk_segment_backward(addr_idx, addr_val, x, gamma, init_slot, init_mass, mask,
+                                                           D_y, D_slot, D_mass, w_top_k, r_top_k, mass_aware, eps)
+    need = ctx.needs_input_grad
+    return (None,
+            D_addr if need[1] else None,
+            D_x.to(x_dt) if need[2] else None,
+            D_gamma.to(g_dt) if need[3] else None,
+            D_s.to(s_dt) if need[4] else None,
+            D_m.to(m_dt) if need[5] else None) + (None,) * 5
+
+
+topk_segment_forward.register_autograd(_segment_backward, setup_context=_segment_setup)
+
+
 @torch.library.custom_op(f"{_NS}::topk_segment_forward_", mutates_args=("slot", "mass"), device_types="cuda")
 def topk_segment_forward_(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
                           mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool, eps: float) -> Tensor:

@@ -9,11 +9,11 @@ time-ordered segment scan. Differences by design:
 * no padding of T to a multiple of 32 (the HIP kernels take any T);
 * no event grouping (``gather_segment``'s global sort): the segment scan walks
   tokens in order with the slot state resident in LDS;
-* the address decoder is differentiable (its backward kernel is registered
-  as the autograd formula of ``topk_addr_single_forward`` and
-  ``topk_addr_forward``); the segment scan and the decode step are forward
-  only, so ``random_access_memory_attention`` on inputs that require grad
-  raises ``NotImplementedError`` instead of silently dropping gradients.
+* with inputs that require grad (and grad mode on) the forward runs the two
+  autograd-registered ops ``topk_addr_forward`` and ``topk_segment_forward``,
+  as the reference does, so their backward kernels
+  (``topk_addr_backward``, ``topk_segment_backward``) give the gradients;
+  without gradients it runs the fused decoder + scan op.
 """
 from __future__ import annotations
 
@@ -23,14 +23,6 @@ from . import _ops
 from ._cuda_config import ADDRESS_LIMIT, check_int_capacity
 
 ops = _ops  # the registered torch.ops.ramnet_ops.* operators
-
-
-def _no_grad_support(tensors) -> None:
-    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
-        raise NotImplementedError(
-            "ramnet_ops on MI355X: random_access_memory_attention is forward only (the segment-scan backward is "
-            "not built yet; topk_addr is differentiable). "
-            "Run under torch.no_grad() or detach the inputs.")
 
 
 def _cuda_topk_autoregressive_(
@@ -98,7 +90,8 @@ def _cuda_ram_attn(
     check_int_capacity(B, H, U, P, A, C, T, embed_num, w_top_k, r_top_k,
                        B * H * U * P * T, B * H * A * C, B * H * T * C, B * H * T * (w_top_k + r_top_k))
 
-    _no_grad_support([w_addr, r_addr, xs, gamma, init_slot, init_mass])
+    requires_grad = torch.is_grad_enabled() and any(
+        t.requires_grad for t in (w_addr, r_addr, xs, gamma, init_slot, init_mass))
     position_ids = position_ids.to(device=xs.device, dtype=torch.int32)
     if mask is not None:
         mask = mask.to(device=xs.device, dtype=torch.bool)
@@ -124,9 +117,17 @@ def _cuda_ram_attn(
     if acc_type != torch.float32:
         raise RuntimeError(f"ramnet_ops on MI355X supports float32, float16 and bfloat16 inputs, got {xs.dtype}.")
     if inplace:
+        assert not requires_grad, "inplace=True does not support backward."
         assert init_slot.dtype == init_mass.dtype == acc_type, \
             f"Expected inplace state dtype={acc_type}, got slot={init_slot.dtype}, mass={init_mass.dtype}."
         assert init_slot.is_contiguous() and init_mass.is_contiguous(), "Expected contiguous inplace state."
+
+    if requires_grad:
+        # the differentiable composition (reference: cuda_impl.py:252-271)
+        addr_idx, addr_val = torch.ops.ramnet_ops.topk_addr_forward(
+            w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re, r_re)
+        return torch.ops.ramnet_ops.topk_segment_forward(
+            addr_idx, addr_val, xs, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps)
 
     if T == 1:
         with torch.no_grad():

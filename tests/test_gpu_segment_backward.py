@@ -1,0 +1,209 @@
+"""Segment backward on the GPU against fp64 autograd of the dense oracle.
+
+The reference's contract (csrc/ram_attn_segment_parallel.cu:418-606,
+ram_attn_ops.cpp:267-310, _cuda_autograd.py:205-287): gradients of the
+decoder weights (with respect to the positive weights for reads; zero for
+events that do not act), of x and gamma (float32), and of the initial slot
+and mass state; the output gradient is taken in x's dtype. The oracle is
+torch autograd in float64 through ``oracle.dense_ram_attn`` (the dense
+restatement of the reference's torch path), given the same decoded events.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+F32, BF16, F16 = torch.float32, torch.bfloat16, torch.float16
+
+CASES = [
+    # B, H, U, P, T, C, Kw, Kr, dtype, masked, mass_aware
+    (2, 2, 2, 8, 40, 16, 4, 4, F32, False, False),
+    (1, 3, 2, 16, 33, 37, 8, 8, F32, True, False),    # odd C: partial channel slices; masked tokens
+    (2, 2, 3, 4, 29, 24, 8, 8, F32, True, True),      # mass_aware
+    (1, 2, 2, 8, 21, 16, 40, 24, F32, False, True),   # top_k > 32: one 64-event pass
+    (1, 1, 2, 16, 13, 8, 100, 70, F32, True, False),  # top_k > 64: two passes
+    (1, 2, 2, 16, 1, 16, 8, 8, F32, False, True),     # T = 1
+    (2, 2, 2, 16, 40, 64, 8, 8, BF16, True, False),
+    (1, 2, 2, 16, 40, 64, 8, 8, F16, False, True),
+    (1, 2, 2, 32, 24, 300, 16, 16, F32, False, False),  # C > 16 slices of 4: wider lanes
+]
+
+
+def _ops():
+    import ramnet_ops  # noqa: F401  (registers torch.ops.ramnet_ops.*)
+    return torch.ops.ramnet_ops
+
+
+def _tol(dtype):
+    return 1e-5 if dtype == F32 else 2e-2
+
+
+def _inputs(B, H, U, P, T, C, Kw, Kr, dtype, masked, seed):
+    g = torch.Generator().manual_seed(seed)
+    A = P ** U
+    w = (1.5 * torch.randn(B, H, U, P, T, generator=g)).to(dtype)
+    r = (1.5 * torch.randn(B, H, U, P, T, generator=g)).to(dtype)
+    pos = torch.randint(0, 4 * A, (B, T), generator=g)
+    x = torch.randn(B, H, T, C, generator=g).to(dtype)
+    gamma = (2.0 * torch.randn(B, H, T, generator=g)).to(dtype)
+    slot = 0.5 * torch.randn(B, H, A, C, generator=g)
+    mass = torch.rand(B, H, A, generator=g) + 0.05
+    mask = (torch.rand(B, T, generator=g) > 0.3) if masked else None
+    Dy = torch.randn(B, H, T, C, generator=g).to(dtype)
+    Ds = torch.randn(B, H, A, C, generator=g)
+    Dm = torch.randn(B, H, A, generator=g)
+    return dict(w=w, r=r, pos=pos, x=x, gamma=gamma, slot=slot, mass=mass, mask=mask, Dy=Dy, Ds=Ds, Dm=Dm, A=A)
+
+
+def _oracle(idx, val, x, gamma, slot, mass, mask, Dy, Ds, Dm, Kw, Kr, mass_aware, eps, U, P):
+    """fp64 autograd of sum(y Dy) + sum(slot' Ds) + sum(mass' Dm) given the decoded events."""
+    B, H, T, C = x.shape
+    wv = val[:, :, :Kw].double().clone().requires_grad_(True)
+    rv = (-val[:, :, Kw:]).double().clone().requires_grad_(True)  # positive read weights
+    x64 = x.double().requires_grad_(True)
+    g64 = gamma.double().requires_grad_(True)
+    s64 = slot.double().requires_grad_(True)
+    m64 = mass.double().requires_grad_(True)
+    dummy = torch.zeros(B, H, U, P, T, dtype=torch.float64)
+    y, s, m = oracle.dense_ram_attn(dummy, dummy, x64, g64, s64, m64, mask, 0, None, (Kw, Kr), (0.0, 0.0),
+                                    mass_aware, eps, decoded=(idx[:, :, :Kw], wv, idx[:, :, Kw:], -rv))
+    keep = torch.ones(B, T, dtype=torch.float64) if mask is None else mask.double()
+    loss = (y * Dy.double() * keep[:, None, :, None]).sum() + (s * Ds.double()).sum() + (m * Dm.double()).sum()
+    loss.backward()
+    dval = torch.cat([wv.grad, rv.grad], dim=2)
+    dval = dval.masked_fill(val == 0, 0)  # events that do not act carry no gradient (the reference skips them)
+    return dval, x64.grad, g64.grad, s64.grad, m64.grad
+
+
+def _check(name, got, ref, tol):
+    err = oracle.rel_err(got.cpu().double(), ref)
+    print(f"  {name}: rel {err:.2e}", flush=True)
+    assert err <= tol, f"{name}: rel err {err:.3e} > {tol}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_segment_backward_matches_oracle(case):
+    B, H, U, P, T, C, Kw, Kr, dtype, masked, mass_aware = case
+    ops = _ops()
+    print(f"segment backward case {case}", flush=True)
+    d = _inputs(B, H, U, P, T, C, Kw, Kr, dtype, masked, seed=B * 1000 + T * 10 + C + Kw)
+    A = d["A"]
+    idx, val = ops.topk_addr_forward(d["w"].to(DEV), d["r"].to(DEV), 1, A, d["pos"].to(DEV).int(), Kw, Kr, 0.0, 0.0)
+    mask = None if d["mask"] is None else d["mask"].to(DEV)
+    got = ops.topk_segment_backward(idx, val, d["x"].to(DEV), d["gamma"].to(DEV), d["slot"].to(DEV),
+                                    d["mass"].to(DEV), mask, d["Dy"].to(DEV), d["Ds"].to(DEV), d["Dm"].to(DEV),
+                                    Kw, Kr, mass_aware, 1e-12)
+    torch.cuda.synchronize()
+    ref = _oracle(idx.cpu(), val.cpu(), d["x"], d["gamma"], d["slot"], d["mass"], d["mask"], d["Dy"], d["Ds"],
+                  d["Dm"], Kw, Kr, mass_aware, 1e-12, U, P)
+    tol = _tol(dtype)
+    for name, g, r in zip(("D_addr_val", "D_x", "D_gamma", "D_slot", "D_mass"), got, ref):
+        _check(name, g, r, tol)
+    # the output gradient of masked tokens is ignored: zeroing it changes nothing
+    if mask is not None:
+        Dy0 = d["Dy"].masked_fill(~d["mask"][:, None, :, None], 0).to(DEV)
+        again = ops.topk_segment_backward(idx, val, d["x"].to(DEV), d["gamma"].to(DEV), d["slot"].to(DEV),
+                                          d["mass"].to(DEV), mask, Dy0, d["Ds"].to(DEV), d["Dm"].to(DEV), Kw, Kr,
+                                          mass_aware, 1e-12)
+        for a, b in zip(got, again):
+            assert torch.equal(a, b)
+
+
+def test_segment_backward_deterministic_and_optional_grads():
+    """Two calls give identical bits; absent final-state gradients act as zeros."""
+    ops = _ops()
+    B, H, U, P, T, C, K = 2, 4, 2, 16, 200, 64, 8
+    d = _inputs(B, H, U, P, T, C, K, K, BF16, True, seed=7)
+    A = d["A"]
+    idx, val = ops.topk_addr_forward(d["w"].to(DEV), d["r"].to(DEV), 2, A, d["pos"].to(DEV).int(), K, K, 0.0, 0.0)
+    args = (idx, val, d["x"].to(DEV), d["gamma"].to(DEV), d["slot"].to(DEV), d["mass"].to(DEV), d["mask"].to(DEV),
+            d["Dy"].to(DEV))
+    a = ops.topk_segment_backward(*args, None, None, K, K, True, 1e-12)
+    b = ops.topk_segment_backward(*args, None, None, K, K, True, 1e-12)
+    z = ops.topk_segment_backward(*args, torch.zeros_like(d["Ds"]).to(DEV), torch.zeros_like(d["Dm"]).to(DEV),
+                                  K, K, True, 1e-12)
+    for u, v, w in zip(a, b, z):
+        assert torch.equal(u, v)
+        assert torch.equal(u, w)
+
+
+def _vals_from_logits(a64, idx, E, pos, K, re_norm):
+    """The decoder's weights in fp64 as a differentiable function of the
+    logits, for a given (GPU) selection."""
+    B, H, U, P, T = a64.shape
+    A = P ** U
+    scores = oracle.content_scores(oracle.log_softmax_digits(a64, torch.float64))  # (B, H, T, A)
+    heads = torch.arange(H).view(1, H, 1, 1)
+    shift = (heads < E).long() * pos.long().view(B, 1, 1, T)
+    content = torch.remainder(idx.long() % A + shift, A)  # (B, H, K, T)
+    s = scores.gather(-1, content.permute(0, 1, 3, 2))  # (B, H, T, K)
+    if re_norm != 0:
+        s = s - re_norm * s.logsumexp(dim=-1, keepdim=True)
+    return s.exp().permute(0, 1, 3, 2)
+
+
+@pytest.mark.parametrize("T,mass_aware,masked,dtype", [(48, False, True, F32), (37, True, False, F32),
+                                                      (1, False, False, F32), (40, True, True, BF16)])
+def test_api_gradients_match_oracle(T, mass_aware, masked, dtype):
+    """random_access_memory_attention with inputs that require grad: the
+    composed decoder + segment backward against fp64 autograd of the dense
+    reference, down to the address logits."""
+    from ramnet_ops import random_access_memory_attention
+    print(f"api gradients T={T} mass_aware={mass_aware} masked={masked} {dtype}", flush=True)
+    B, H, U, P, C, K, E = 2, 3, 2, 8, 24, 6, 2
+    re = (0.5, 0.25)
+    d = _inputs(B, H, U, P, T, C, K, K, dtype, masked, seed=T + 100 * int(mass_aware))
+    A = d["A"]
+    leaves = {k: d[k].to(DEV).requires_grad_(True) for k in ("w", "r", "x", "gamma", "slot", "mass")}
+    mask = None if d["mask"] is None else d["mask"].to(DEV)
+    y, (slot, mass) = random_access_memory_attention(
+        leaves["w"].permute(0, 4, 1, 2, 3), leaves["r"].permute(0, 4, 1, 2, 3), leaves["x"].permute(0, 2, 1, 3),
+        leaves["gamma"].permute(0, 2, 1), init_ram=(leaves["slot"], leaves["mass"]), mask=mask, embed_num=E,
+        position_ids=d["pos"].to(DEV), top_k=K, top_k_re_norm=re, mass_aware=mass_aware)
+    loss = (y.float() * d["Dy"].permute(0, 2, 1, 3).float().to(DEV)).sum() + (slot * d["Ds"].to(DEV)).sum() \
+        + (mass * d["Dm"].to(DEV)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+
+    # the GPU's selection, then the fp64 reference as a function of the logits
+    ops = _ops()
+    idx, _ = ops.topk_addr_forward(d["w"].to(DEV), d["r"].to(DEV), E, A, d["pos"].to(DEV).int(), K, K, *re)
+    idx = idx.cpu()
+    w64 = d["w"].double().requires_grad_(True)
+    r64 = d["r"].double().requires_grad_(True)
+    x64 = d["x"].double().requires_grad_(True)
+    g64 = d["gamma"].double().requires_grad_(True)
+    s64 = d["slot"].double().requires_grad_(True)
+    m64 = d["mass"].double().requires_grad_(True)
+    wv = _vals_from_logits(w64, idx[:, :, :K], E, d["pos"], K, re[0])
+    rv = _vals_from_logits(r64, idx[:, :, K:], E, d["pos"], K, re[1])
+    dummy = torch.zeros(B, H, U, P, T, dtype=torch.float64)
+    ry, rs, rm = oracle.dense_ram_attn(dummy, dummy, x64, g64, s64, m64, d["mask"], 0, None, (K, K), (0.0, 0.0),
+                                       mass_aware, 1e-12, decoded=(idx[:, :, :K], wv, idx[:, :, K:], -rv))
+    keep = torch.ones(B, T, dtype=torch.float64) if d["mask"] is None else d["mask"].double()
+    # the op casts y to the activation dtype: its gradient arrives in that dtype too
+    Dy = d["Dy"].float().to(dtype).double()
+    ref_loss = (ry * Dy * keep[:, None, :, None]).sum() + (rs * d["Ds"].double()).sum() + (rm * d["Dm"].double()).sum()
+    ref_loss.backward()
+    tol = _tol(dtype)
+    for name, leaf, ref in (("w_addr", leaves["w"], w64), ("r_addr", leaves["r"], r64), ("values", leaves["x"], x64),
+                            ("gamma", leaves["gamma"], g64), ("slot", leaves["slot"], s64),
+                            ("mass", leaves["mass"], m64)):
+        _check(name, leaf.grad, ref.grad, tol)
+
+
+def test_inplace_with_grad_raises():
+    from ramnet_ops import random_access_memory_attention
+    B, H, U, P, T, C = 1, 2, 2, 8, 8, 16
+    A = P ** U
+    w = torch.randn(B, T, H, U, P, device=DEV, requires_grad=True)
+    slot = torch.zeros(B, H, A, C, device=DEV)
+    mass = torch.full((B, H, A), 1.0 / A, device=DEV)
+    with pytest.raises(AssertionError, match="inplace"):
+        random_access_memory_attention(w, w, torch.randn(B, T, H, C, device=DEV), init_ram=(slot, mass),
+                                       top_k=4, inplace=True)
