@@ -17,13 +17,14 @@ the same inputs (rank 0, N=1 only).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S]
        [--no-cpu-baseline] [--no-stress] [--no-lm] [--lm-tokens N]
-       [--only prefill|decode|stress|lm] [--copy-probe MIB]
+       [--only prefill|decode|stress|lm|train] [--no-train] [--copy-probe MIB]
 
 Config 4 (B=4, H=8, T=8192, U=3, P=16 -> A=4096, K=16) and its tie-heavy
 variant (decoder logits quantised to multiples of 0.25) are timed the same
 way and reported under ``stress``. Config 5 (the caller harness: a 24-block
 RAM-Net LM, prompt 16 x 2048, greedy in-place decode) is reported under
-``lm``.
+``lm``. A config-2 training step of the operator (differentiable forward,
+then the segment and decoder backward) is reported under ``train``.
 
 ``--copy-probe MIB`` first runs one plain device-to-device copy of MIB MiB
 (torch ``copy_``, fp32): under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE``
@@ -157,6 +158,62 @@ def bench_prefill(steps, warmup, dev, c=C2):
         "op_bytes": op_bytes,
         "op_roofline_frac": (op_bytes / (ms_per_step / 1e3)) / (HBM_PEAK_GBS * 1e9),
         "bytes_per_token_head": per,
+    }
+
+
+def bench_train(steps, warmup, dev, c=C2):
+    """One training step of the operator at a prefill config: the
+    differentiable forward (decoder ops ``topk_addr_forward`` +
+    ``topk_segment_forward``) and its backward (``topk_segment_backward`` +
+    ``topk_addr_backward``), the op sequence autograd runs for
+    ``random_access_memory_attention``. Gradients of y come in as N(0,1)
+    bf16; the final-state gradients are zero (None)."""
+    import ramnet_ops  # noqa: F401
+    ops = torch.ops.ramnet_ops
+    B, H, T, C, U, P, K = c["B"], c["H"], c["T"], c["C"], c["U"], c["P"], c["K"]
+    A = P ** U
+    E = c["embed"]
+    _, d = make_prefill_inputs(dev, c)
+    slot0 = torch.zeros(B, H, A, C, device=dev)
+    mass0 = torch.full((B, H, A), 1.0 / A, device=dev)
+    g = torch.Generator().manual_seed(c["seed"] + 200)
+    dy = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16).to(dev)
+    shape = [B, H, U, P, A, T]
+
+    def step(ev):
+        ev[0].record()
+        idx, val = ops.topk_addr_forward(d["w"], d["r"], E, A, d["pos"], K, K, 0.0, 0.0)
+        ev[1].record()
+        ops.topk_segment_forward(idx, val, d["x"], d["gamma"], slot0, mass0, None, K, K, False, 1e-12)
+        ev[2].record()
+        dval = ops.topk_segment_backward(idx, val, d["x"], d["gamma"], slot0, mass0, None, dy, None, None, K, K,
+                                         False, 1e-12)[0]
+        ev[3].record()
+        ops.topk_addr_backward(idx, val, d["w"], d["r"], dval, E, d["pos"], K, K, 0.0, 0.0, shape, d["w"].dtype)
+        ev[4].record()
+
+    def events(n):
+        return [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(n)]
+
+    for ev in events(warmup):
+        step(ev)
+    evs = events(steps)
+    torch.cuda.synchronize()
+    for ev in evs:
+        step(ev)
+    torch.cuda.synchronize()
+    ms = evs[0][0].elapsed_time(evs[-1][4]) / steps
+    stage = [sum(ev[i].elapsed_time(ev[i + 1]) for ev in evs) / steps for i in range(4)]
+    return {
+        "workload": f"config {c.get('name', 2)} training step of the operator: decoder + segment forward, segment "
+                    f"backward + decoder backward; B={B}, H={H}, T={T}, d_v={C}, A={A}, K={K}, bf16 activations, "
+                    "gradient of y ~ N(0,1), none on the final state",
+        "ms_per_step": ms,
+        "tokens_per_s": B * T / (ms / 1e3),
+        "decoder_forward_ms": stage[0],
+        "segment_forward_ms": stage[1],
+        "segment_backward_ms": stage[2],
+        "decoder_backward_ms": stage[3],
     }
 
 
@@ -368,7 +425,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--only", choices=("prefill", "decode", "stress", "lm"), default=None)
+    ap.add_argument("--only", choices=("prefill", "decode", "stress", "lm", "train"), default=None)
+    ap.add_argument("--no-train", action="store_true", help="skip the config-2 training-step line")
     ap.add_argument("--no-lm", action="store_true", help="skip the config-5 model harness line")
     ap.add_argument("--lm-tokens", type=int, default=C5["new"])
     ap.add_argument("--no-stress", action="store_true", help="skip the config-4 stress prefill lines")
@@ -423,6 +481,13 @@ def main(argv=None) -> int:
             }
             log(f"stress: {name} {st['ms_per_step']:.3f} ms/step = {st['tokens_per_s'] / 1e6:.1f} M tokens/s, "
                 f"segment {st['segment_ms']:.3f} ms, decoder {st['decoder_ms']:.3f} ms")
+    train = None
+    if args.only == "train" or (args.only is None and not args.no_train):
+        log("train: config 2 operator forward + backward")
+        train = bench_train(max(3, args.steps // 4), 1, dev)
+        log(f"train: {train['ms_per_step']:.3f} ms/step = {train['tokens_per_s'] / 1e6:.2f} M tokens/s "
+            f"(decoder fwd {train['decoder_forward_ms']:.3f}, segment fwd {train['segment_forward_ms']:.3f}, "
+            f"segment bwd {train['segment_backward_ms']:.3f}, decoder bwd {train['decoder_backward_ms']:.3f} ms)")
     if args.only in (None, "decode"):
         log("decode: config 3, graph-captured steps")
         dec = bench_decode(args.decode_steps, dev, graph=not args.no_graph)
@@ -496,6 +561,13 @@ def main(argv=None) -> int:
                         "warmup": 1, "ms_per_step": lm["prefill_ms"], "higher_is_better": True, "scaling": "weak",
                         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
                         "config": {"workload": lm["workload"]}})
+    if train is not None:
+        out["train"] = train
+        if args.only == "train":
+            out.update({"value": train["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+                        "steps": max(3, args.steps // 4), "warmup": 1, "ms_per_step": train["ms_per_step"],
+                        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+                        "data": "synthetic", "config": {"workload": train["workload"]}})
     if stress:
         out["stress"] = stress
         if pre is None and dec is None:

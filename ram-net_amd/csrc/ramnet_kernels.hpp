@@ -113,10 +113,10 @@ struct SegmentJob {
 // Per-event forward quantities of the segment backward, written by the mass
 // pre-pass in its record-keeping mode. Token-major: (B*H, T, K).
 struct MassAux {
-    int2 *wev;   // (B*H, T, Kw) {slot, or -2 for a no-op; gain g = w / (m + eps) as bits}
-    float *wm;   // (B*H, T, Kw) slot mass before the write
-    int2 *rev;   // (B*H, T, Kr) {slot, or -1 for a no-op; effective read weight as bits}
-    float *rm;   // (B*H, T, Kr) post-write mass of the read slot
+    int4 *wev;   // (B*H, T, Kw) {slot, or -2 for a no-op; gain g = w / (m + eps); effective weight of
+                 //  the read of the same slot in this token, or 0; slot mass before the write} (floats as bits)
+    int4 *rev;   // (B*H, T, Kr) {slot, or -1 for a no-op; effective read weight; post-write mass of
+                 //  the slot; 0} (floats as bits)
 };
 
 // Segment backward (gradients of ramnet_topk_segment_forward).
@@ -133,9 +133,11 @@ struct SegmentBwdJob {
     float *grad_gamma;        // (B, H, T)
     float *grad_init_slot;    // (B, H, A, C)
     float *grad_init_mass;    // (B, H, A)
-    float *delta;             // (B*H*n_sub, T, Kw, CSW) x - s before each write
-    float *dr_part;           // (n_sub, B*H, T, Kr) per-slice read dot products
-    float *dg_part;           // (n_sub, B*H, T, Kw) per-slice gain gradients
+    float *delta;             // (B*H*n_sub, T, KP, CSW) x - s before each write (KP: padded event count)
+    float *dr_part;           // (n_sub, B*H, T_pad, KP) per-slice read dot products
+    float *dg_part;           // (n_sub, B*H, T_pad, KP) per-slice gain gradients
+    float *dr_sum;            // (B*H, T, Kr) read dot products d_j
+    float *dg_sum;            // (B*H, T, Kw) gain gradients Dg
     float *mass_scratch;      // (B*H*A)
     void *maps;               // chunk maps of the mass replay
     size_t maps_bytes;
@@ -189,6 +191,8 @@ int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes);
 // `aux` receives the per-event quantities. `maps` holds the chunk maps
 // (mass_replay_scratch_bytes of it); the final masses go to job.mass_out.
 int64_t mass_replay_scratch_bytes(int B, int H, int T, int A);
+// Time chunks (and their length) the pre-pass uses with maps_bytes of maps.
+int mass_replay_chunks(const SegmentJob &job, size_t maps_bytes, int *chunk_len);
 hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *maps, size_t maps_bytes,
                               hipStream_t stream);
 

@@ -41,6 +41,7 @@
 //      dL/dw, dL/drho, dL/dgamma and dL/d init_mass.
 #include "ramnet_device.hpp"
 #include "ramnet_kernels.hpp"
+#include "ramnet_search.hpp"
 #include "segment_scan.hpp"
 
 #include <algorithm>
@@ -61,8 +62,16 @@ int pow2_at_least(int x) {
 
 struct BwdPlan {
     int epp, np, vec, csw, n_sub;
-    int64_t lds;
+    int64_t lds;  // dynamic LDS (the slot rows); the chunk stage is static
 };
+
+// Tokens per staged chunk of the slice kernel, and the stage's LDS bytes:
+// write records (16 B) and read records (8 B) per event slot, x and Dy per
+// channel, per token.
+__host__ __device__ constexpr int bwd_chunk(int epp, int np) { return epp * np >= 64 ? 8 : 16; }
+constexpr int64_t bwd_stage_bytes(int epp, int np, int vec) {
+    return static_cast<int64_t>(bwd_chunk(epp, np)) * (epp * np * (16 + 8) + 2 * (kWave / epp) * vec * 4);
+}
 
 // Lane layout of the slice kernel: EPP events per pass (NP passes), LPE =
 // 64 / EPP lanes per event, VEC channels per lane, CSW = LPE * VEC channels
@@ -78,80 +87,160 @@ bool bwd_plan(int A, int C, int Kw, int Kr, BwdPlan *p) {
     int vec = 1;
     while (vec < 4 && static_cast<int64_t>(lpe) * vec * kBwdMaxSlices < C)
         vec *= 2;
-    while (vec > 1 && static_cast<int64_t>(A + 2) * lpe * vec * 4 > kBwdLdsLimit)
+    auto total = [&](int v) { return static_cast<int64_t>(A + 2) * lpe * v * 4 + bwd_stage_bytes(epp, np, v); };
+    while (vec > 1 && total(vec) > kBwdLdsLimit)
         vec /= 2;
-    const int64_t lds = static_cast<int64_t>(A + 2) * lpe * vec * 4;
-    if (lds > kBwdLdsLimit)
+    if (total(vec) > kBwdLdsLimit)
         return false;
+    const int64_t lds = static_cast<int64_t>(A + 2) * lpe * vec * 4;
     *p = {epp, np, vec, lpe * vec, (C + lpe * vec - 1) / (lpe * vec), lds};
     return true;
 }
 
-// Sum over the lanes of one event (the LPE lanes with equal lane % EPP).
-template<int EPP>
-__device__ __forceinline__ float chan_sum(float v) {
-#pragma unroll
-    for (int o = EPP; o < kWave; o <<= 1)
-        v += __shfl_xor(v, o);
-    return v;
+// Sum over the lanes whose indices differ only in bits LO .. HI/2 (powers of
+// two): a butterfly of DPP and permlane exchanges, with no LDS traffic.
+template<int LO, int HI>
+__device__ __forceinline__ float xor_sum(float v) {
+    if constexpr (LO < HI)
+        return xor_sum<LO * 2, HI>(v + lane_xor_f<LO>(v));
+    else
+        return v;
 }
 
-// One token's loads for a lane of the slice kernel.
-template<int NP, int VEC, bool FWD>
-struct BwdTok {
-    int2 w[NP];             // write event {slot, gain bits}
-    int2 r[NP];             // read event {slot, effective weight bits}
-    float dy[VEC];          // Dy_t on the lane's channels
-    float xd[FWD ? VEC : NP * VEC];  // forward: x_t; backward: saved x - s per write pass
-};
+// Raw bits of one activation element (converted at use, so that a prefetch
+// needs no wait when it is issued).
+template<typename Scalar>
+__device__ __forceinline__ uint32_t raw_load(const Scalar *p) {
+    if constexpr (sizeof(Scalar) == 4)
+        return *reinterpret_cast<const uint32_t *>(p);
+    else
+        return *reinterpret_cast<const uint16_t *>(p);
+}
+
+template<int VEC>
+__device__ __forceinline__ void raw_load_vec(const float *p, uint32_t *out) {
+    if constexpr (VEC == 4) {
+        const uint4 t = *reinterpret_cast<const uint4 *>(p);
+        out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
+    } else if constexpr (VEC == 2) {
+        const uint2 t = *reinterpret_cast<const uint2 *>(p);
+        out[0] = t.x; out[1] = t.y;
+    } else {
+        out[0] = *reinterpret_cast<const uint32_t *>(p);
+    }
+}
+
+// Sum over the lanes whose indices differ from a lane's own only in bits
+// J .. 32 (J a power of two): exact xor exchanges by DPP within a row
+// (quad_perm, row_shl/shr:4, row_ror:8), then v_permlane16/32_swap, whose two
+// outputs hold the two halves being combined.
+template<int J>
+__device__ __forceinline__ float strided_sum(float v) {
+    if constexpr (J >= kWave) {
+        return v;
+    } else if constexpr (J < 8) {
+        return strided_sum<J * 2>(v + lane_xor_f<J>(v));
+    } else if constexpr (J == 8) {
+        return strided_sum<16>(v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, true)));
+    } else if constexpr (J == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return strided_sum<32>(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+    } else {
+        static_assert(J == 32, "strided_sum: J in {8, 16, 32}");
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
 
 template<typename Scalar, int EPP, int NP, int VEC>
 __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBwdJob job, int n_sub) {
-    constexpr int LPE = kWave / EPP;
+    constexpr int LPE = kWave / EPP;               // lanes per event (consecutive: channel groups)
     constexpr int CSW = LPE * VEC;
-    constexpr int CH = NP * VEC >= 4 ? 4 : 8;  // tokens per prefetch chunk
+    constexpr int KP = NP * EPP;                   // event slots per token (padded)
+    constexpr int CH = bwd_chunk(EPP, NP);         // tokens per staged chunk
+    constexpr int NREC = CH * KP;                  // records of each kind per chunk
+    constexpr int RPL = (NREC + kWave - 1) / kWave;
+    constexpr int NXE = CH * CSW;                  // x (and Dy) elements per chunk
+    constexpr int XPL = (NXE + kWave - 1) / kWave;
+    constexpr int GX = EPP < CH ? EPP : CH;        // tokens per batched grad_x store
+    // The chunk's event records and activations, loaded once per chunk
+    // (one element per lane) and read back per token as LDS broadcasts.
+    __shared__ int4 stw[NREC];   // write records {slot, g, matched read weight, mass}
+    __shared__ int2 str[NREC];   // read records {slot, effective weight}
+    __shared__ float stx[NXE];   // x_t (forward) on the slice's channels
+    __shared__ float sdy[NXE];   // Dy_t on the slice's channels
     extern __shared__ __align__(16) float st[];  // (A + 2) rows of CSW: rows -2 and -1 are the no-op rows
     const SegmentJob &fj = job.fwd;
     const int A = fj.A, C = fj.C, T = fj.T, Kw = fj.Kw, Kr = fj.Kr;
     const int BH = fj.B * fj.H;
+    const int t_pad = (T + CH - 1) / CH * CH;
     const int unit = static_cast<int>(blockIdx.x);
     const int bh = unit / n_sub, sub = unit - bh * n_sub;
     const int lane = static_cast<int>(threadIdx.x);
-    const int e = lane % EPP, q = lane / EPP;
+    const int e = lane / LPE, q = lane % LPE;
     const int c0 = sub * CSW + q * VEC;  // first channel of this lane
     float *rows = st + 2 * CSW;
     const Scalar *xs = static_cast<const Scalar *>(fj.x);
     const Scalar *dys = static_cast<const Scalar *>(job.grad_y);
+    const int2 *rev2 = reinterpret_cast<const int2 *>(job.aux.rev);  // {slot, weight} of each 16-byte record
+    // per-slice partial sums of this unit: [t][KP]
+    float *drp = job.dr_part + (static_cast<int64_t>(sub) * BH + bh) * t_pad * KP;
+    float *dgp = job.dg_part + (static_cast<int64_t>(sub) * BH + bh) * t_pad * KP;
+    float *dlt = job.delta + static_cast<int64_t>(unit) * T * KP * CSW + e * CSW + q * VEC;  // + (t * KP + p * EPP) * CSW
 
-    auto load_tok = [&](int t, auto &k, auto fwd_tag) {
-        constexpr bool F = decltype(fwd_tag)::value;
-        const int64_t tb = static_cast<int64_t>(bh) * T + t;
+    struct Pre {
+        int4 w[RPL];
+        int2 r[RPL];
+        uint32_t x[XPL];
+        uint32_t dy[XPL];
+    };
+    // token j of chunk ci, clamped into [0, T)
+    auto token = [&](int ci, int j, auto fwd_tag) {
+        const int t = decltype(fwd_tag)::value ? ci * CH + j : T - 1 - ci * CH - j;
+        return min(max(t, 0), T - 1);
+    };
+    auto prefetch = [&](int ci, Pre &pf, auto fwd_tag) {
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const int kw = p * EPP + e, kr = p * EPP + e;
-            k.w[p] = kw < Kw ? job.aux.wev[tb * Kw + kw] : make_int2(-2, 0);
-            k.r[p] = kr < Kr ? job.aux.rev[tb * Kr + kr] : make_int2(-1, 0);
+        for (int i = 0; i < RPL; ++i) {
+            const int idx = min(lane + kWave * i, NREC - 1);
+            const int k = idx % KP;
+            const int64_t tb = static_cast<int64_t>(bh) * T + token(ci, idx / KP, fwd_tag);
+            pf.w[i] = job.aux.wev[tb * Kw + min(k, Kw - 1)];
+            pf.r[i] = rev2[2 * (tb * Kr + min(k, Kr - 1))];
         }
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-            const int c = c0 + v;
-            k.dy[v] = c < C ? load_f32(dys + tb * C + c) : 0.f;
-            if constexpr (F)
-                k.xd[v] = c < C ? load_f32(xs + tb * C + c) : 0.f;
+        for (int i = 0; i < XPL; ++i) {
+            const int idx = min(lane + kWave * i, NXE - 1);
+            const int c = min(sub * CSW + idx % CSW, C - 1);
+            const int64_t tb = static_cast<int64_t>(bh) * T + token(ci, idx / CSW, fwd_tag);
+            pf.dy[i] = raw_load(dys + tb * C + c);
+            if constexpr (decltype(fwd_tag)::value)
+                pf.x[i] = raw_load(xs + tb * C + c);
         }
-        if constexpr (!F) {
+    };
+    auto stage = [&](const Pre &pf, auto fwd_tag) {
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                const int kw = p * EPP + e;
-                const float *src = job.delta + ((static_cast<int64_t>(unit) * T + t) * Kw + (kw < Kw ? kw : 0)) * CSW +
-                                   q * VEC;
-                const FVec<VEC> d = lds_load<VEC>(src);  // plain vector load (global here)
+        for (int i = 0; i < RPL; ++i) {
+            const int idx = lane + kWave * i;
+            if (NREC % kWave == 0 || idx < NREC) {
+                const int k = idx % KP;
+                stw[idx] = k < Kw ? pf.w[i] : make_int4(-2, 0, 0, 0);
+                str[idx] = k < Kr ? pf.r[i] : make_int2(-1, 0);
+            }
+        }
 #pragma unroll
-                for (int v = 0; v < VEC; ++v)
-                    k.xd[p * VEC + v] = d.v[v];
+        for (int i = 0; i < XPL; ++i) {
+            const int idx = lane + kWave * i;
+            if (NXE % kWave == 0 || idx < NXE) {
+                const bool real = sub * CSW + idx % CSW < C;
+                sdy[idx] = real ? half_bits_to_f<Scalar>(pf.dy[i]) : 0.f;
+                if constexpr (decltype(fwd_tag)::value)
+                    stx[idx] = real ? half_bits_to_f<Scalar>(pf.x[i]) : 0.f;
             }
         }
     };
+    auto lds_vec = [&](const float *p) { return lds_load<VEC>(p); };
+    const int nck = (T + CH - 1) / CH;
 
     // ---- forward over t: s in LDS; save x - s before each write, d_j per read
     for (int i = lane; i < (A + 2) * CSW; i += kWave) {
@@ -160,55 +249,69 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     }
     __syncthreads();
     {
-        using Tok = BwdTok<NP, VEC, true>;
         using Tag = std::true_type;
-        Tok cur[CH], nxt[CH];
-#pragma unroll
-        for (int j = 0; j < CH; ++j)
-            load_tok(min(j, T - 1), cur[j], Tag{});
-        const int nck = (T + CH - 1) / CH;
+        Pre cur, nxt;
+        prefetch(0, cur, Tag{});
         for (int ci = 0; ci < nck; ++ci) {
+            stage(cur, Tag{});
+            prefetch(min(ci + 1, nck - 1), nxt, Tag{});
+            // write rows of the current token, loaded one token ahead:
+            // after the previous token's writes, with its reads
+            FVec<VEC> sw[NP];
 #pragma unroll
-            for (int j = 0; j < CH; ++j)
-                load_tok(min((ci + 1) * CH + j, T - 1), nxt[j], Tag{});
+            for (int p = 0; p < NP; ++p)
+                sw[p] = lds_vec(rows + stw[p * EPP + e].x * CSW + q * VEC);
+            float keep[NP];  // d_j of token (group start + q), stored once per LPE tokens
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int t = ci * CH + j;
                 if (t >= T)
                     break;
-                const Tok &k = cur[j];
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    const int kw = p * EPP + e;
-                    const float g = __int_as_float(k.w[p].y);
-                    float *row = rows + k.w[p].x * CSW + q * VEC;
-                    FVec<VEC> s = lds_load<VEC>(row);
-                    FVec<VEC> d;
+                    const int4 wr = stw[j * KP + p * EPP + e];
+                    const float g = __int_as_float(wr.y);
+                    FVec<VEC> s = sw[p], d;
 #pragma unroll
                     for (int v = 0; v < VEC; ++v) {
-                        d.v[v] = k.xd[v] - s.v[v];
+                        d.v[v] = stx[j * CSW + q * VEC + v] - s.v[v];
                         s.v[v] = fmaf(g, d.v[v], s.v[v]);
                     }
-                    lds_store<VEC>(row, s);
-                    if (kw < Kw)
-                        lds_store<VEC>(job.delta + ((static_cast<int64_t>(unit) * T + t) * Kw + kw) * CSW + q * VEC, d);
+                    lds_store<VEC>(rows + wr.x * CSW + q * VEC, s);
+                    lds_store<VEC>(dlt + (static_cast<int64_t>(t) * KP + p * EPP) * CSW, d);
+                }
+                FVec<VEC> sr[NP];
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+                    sr[p] = lds_vec(rows + str[j * KP + p * EPP + e].x * CSW + q * VEC);
+                if (j + 1 < CH) {
+#pragma unroll
+                    for (int p = 0; p < NP; ++p)
+                        sw[p] = lds_vec(rows + stw[(j + 1) * KP + p * EPP + e].x * CSW + q * VEC);
                 }
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    const int kr = p * EPP + e;
-                    const FVec<VEC> s = lds_load<VEC>(rows + k.r[p].x * CSW + q * VEC);
                     float part = 0.f;
 #pragma unroll
                     for (int v = 0; v < VEC; ++v)
-                        part = fmaf(s.v[v], k.dy[v], part);
-                    part = chan_sum<EPP>(part);
-                    if (kr < Kr && q == 0)
-                        job.dr_part[((static_cast<int64_t>(sub) * BH + bh) * T + t) * Kr + kr] = part;
+                        part = fmaf(sr[p].v[v], sdy[j * CSW + q * VEC + v], part);
+                    part = event_sum<LPE>(part);
+                    keep[p] = q == j % LPE ? part : keep[p];
+                }
+                if (j % LPE == LPE - 1) {
+                    const int tg = t - (LPE - 1) + q;  // this lane's token of the group
+#pragma unroll
+                    for (int p = 0; p < NP; ++p)
+                        drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
                 }
             }
+            if (T - ci * CH < CH && (T - ci * CH) % LPE != 0) {  // ragged last group
+                const int n = T - ci * CH, tg = ci * CH + n / LPE * LPE + q;
 #pragma unroll
-            for (int j = 0; j < CH; ++j)
-                cur[j] = nxt[j];
+                for (int p = 0; p < NP; ++p)
+                    drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
+            }
+            cur = nxt;
         }
     }
     __syncthreads();
@@ -220,32 +323,64 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     }
     __syncthreads();
     {
-        using Tok = BwdTok<NP, VEC, false>;
         using Tag = std::false_type;
-        Tok cur[CH], nxt[CH];
+        // the saved rows x - s of this lane's write events, per token of a chunk
+        struct Saved {
+            uint32_t v[CH][NP * VEC];
+        };
+        auto load_saved = [&](int ci, Saved &sv) {
 #pragma unroll
-        for (int j = 0; j < CH; ++j)
-            load_tok(max(T - 1 - j, 0), cur[j], Tag{});
-        const int nck = (T + CH - 1) / CH;
+            for (int j = 0; j < CH; ++j) {
+                const int t = token(ci, j, Tag{});
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+                    raw_load_vec<VEC>(dlt + (static_cast<int64_t>(t) * KP + p * EPP) * CSW, sv.v[j] + p * VEC);
+            }
+        };
+        Pre cur, nxt;
+        Saved scur, snxt;
+        prefetch(0, cur, Tag{});
+        load_saved(0, scur);
+        float *gx = job.grad_x + static_cast<int64_t>(bh) * T * C;
         for (int ci = 0; ci < nck; ++ci) {
-#pragma unroll
-            for (int j = 0; j < CH; ++j)
-                load_tok(max(T - 1 - (ci + 1) * CH - j, 0), nxt[j], Tag{});
+            stage(cur, Tag{});
+            prefetch(min(ci + 1, nck - 1), nxt, Tag{});
+            load_saved(min(ci + 1, nck - 1), snxt);
+            float keep[NP];       // Dg of token (group start - q), stored once per LPE tokens
+            float keep_x[VEC];    // Dx of token (group start - e), stored once per GX tokens
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int t = T - 1 - ci * CH - j;
                 if (t < 0)
                     break;
-                const Tok &k = cur[j];
+                // all rows of token t in one round trip: a write takes the
+                // read of its own slot (same token) from its matched weight,
+                // and its store lands after that read's
+                int4 wr[NP];
+                int2 rr[NP];
+                FVec<VEC> dr[NP], dw[NP];
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    const float r = __int_as_float(k.r[p].y);
-                    float *row = rows + k.r[p].x * CSW + q * VEC;
-                    FVec<VEC> D = lds_load<VEC>(row);
+                    wr[p] = stw[j * KP + p * EPP + e];
+                    rr[p] = str[j * KP + p * EPP + e];
+                }
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+                    dr[p] = lds_vec(rows + rr[p].x * CSW + q * VEC);
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+                    dw[p] = lds_vec(rows + wr[p].x * CSW + q * VEC);
+                float dy[VEC];
+#pragma unroll
+                for (int v = 0; v < VEC; ++v)
+                    dy[v] = sdy[j * CSW + q * VEC + v];
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const float r = __int_as_float(rr[p].y);
 #pragma unroll
                     for (int v = 0; v < VEC; ++v)
-                        D.v[v] = fmaf(r, k.dy[v], D.v[v]);
-                    lds_store<VEC>(row, D);
+                        dr[p].v[v] = fmaf(r, dy[v], dr[p].v[v]);
+                    lds_store<VEC>(rows + rr[p].x * CSW + q * VEC, dr[p]);
                 }
                 float dx[VEC];
 #pragma unroll
@@ -253,33 +388,46 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     dx[v] = 0.f;
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    const int kw = p * EPP + e;
-                    const float g = __int_as_float(k.w[p].y);
-                    float *row = rows + k.w[p].x * CSW + q * VEC;
-                    FVec<VEC> D = lds_load<VEC>(row);
+                    const float g = __int_as_float(wr[p].y);
+                    const float rm = __int_as_float(wr[p].z);
+                    FVec<VEC> D = dw[p];
                     float part = 0.f;
 #pragma unroll
                     for (int v = 0; v < VEC; ++v) {
-                        part = fmaf(D.v[v], k.xd[p * VEC + v], part);
+                        D.v[v] = fmaf(rm, dy[v], D.v[v]);
+                        part = fmaf(D.v[v], __uint_as_float(scur.v[j][p * VEC + v]), part);
                         dx[v] = fmaf(g, D.v[v], dx[v]);
                         D.v[v] = fmaf(-g, D.v[v], D.v[v]);
                     }
-                    lds_store<VEC>(row, D);
-                    part = chan_sum<EPP>(part);
-                    if (kw < Kw && q == 0)
-                        job.dg_part[((static_cast<int64_t>(sub) * BH + bh) * T + t) * Kw + kw] = part;
+                    lds_store<VEC>(rows + wr[p].x * CSW + q * VEC, D);
+                    part = event_sum<LPE>(part);
+                    keep[p] = q == j % LPE ? part : keep[p];
                 }
-                const int64_t tb = static_cast<int64_t>(bh) * T + t;
+                if (j % LPE == LPE - 1 || t == 0) {
+                    const int tg = t + (j % LPE) - q;  // this lane's token of the group
+                    if (tg >= t) {
+#pragma unroll
+                        for (int p = 0; p < NP; ++p)
+                            dgp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
+                    }
+                }
 #pragma unroll
                 for (int v = 0; v < VEC; ++v) {
-                    const float s = event_sum<EPP>(dx[v]);
-                    if (e == 0 && c0 + v < C)
-                        job.grad_x[tb * C + c0 + v] = s;
+                    const float sx = strided_sum<LPE>(dx[v]);
+                    keep_x[v] = e == j % GX ? sx : keep_x[v];
+                }
+                if (j % GX == GX - 1 || t == 0) {
+                    const int tg = t + (j % GX) - e;  // this lane's token of the group
+                    if (tg >= t && e < GX) {
+#pragma unroll
+                        for (int v = 0; v < VEC; ++v)
+                            if (c0 + v < C)
+                                gx[static_cast<int64_t>(tg) * C + c0 + v] = keep_x[v];
+                    }
                 }
             }
-#pragma unroll
-            for (int j = 0; j < CH; ++j)
-                cur[j] = nxt[j];
+            cur = nxt;
+            scur = snxt;
         }
     }
     __syncthreads();
@@ -290,84 +438,117 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     }
 }
 
-// Per-slice partial sums -> totals in slice 0, summed in slice order.
-__global__ __launch_bounds__(256) void segment_bwd_sum_kernel(float *part, int n_sub, int64_t n) {
+// Per-slice partial sums [sub][bh][t_pad][KP] -> totals [bh][t][K], summed in
+// slice order.
+__global__ __launch_bounds__(256) void segment_bwd_sum_kernel(const float *part, float *out, int n_sub, int BH, int T,
+                                                              int t_pad, int KP, int K) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t n = static_cast<int64_t>(BH) * T * K;
     if (i >= n)
         return;
-    float s = part[i];
-    for (int k = 1; k < n_sub; ++k)
-        s += part[static_cast<int64_t>(k) * n + i];
-    part[i] = s;
+    const int k = static_cast<int>(i % K);
+    const int64_t bt = i / K;
+    const int t = static_cast<int>(bt % T);
+    const int64_t bh = bt / T;
+    const int64_t stride = static_cast<int64_t>(BH) * t_pad * KP;
+    const float *src = part + (bh * t_pad + t) * KP + k;
+    float s = src[0];
+    for (int u = 1; u < n_sub; ++u)
+        s += src[u * stride];
+    out[i] = s;
 }
 
-// One token's loads for a lane of the mass kernel: lanes 0..31 take write
-// events p * 32 + lane, lanes 32..63 read events p * 32 + lane - 32.
+// ---- the mass chain, chunked over time
+//
+// Walking back in time, each slot's Dm evolves affinely with coefficients
+// that do not depend on Dm: a write maps Dm to alpha (Dm - Dg g / den), a
+// mass-aware read adds c rho (d - Q). So, as in the forward mass pre-pass:
+//   1. MAP: per (b, h, chunk), every slot's composed map
+//      Dm(chunk start) = a Dm(chunk end) + b;
+//   2. segment_bwd_mass_scan_kernel: per (b, h, slot), Dm at every chunk's
+//      end from the final-state gradient and the maps (last chunk first), and
+//      dL/d init_mass;
+//   3. REPLAY: per (b, h, chunk), the chunk walked back from its end values,
+//      writing dL/dw, dL/drho and dL/dgamma.
+// Lanes 0..31 take write events p * 32 + lane, lanes 32..63 read events.
+
+// One token's loads for a lane of the mass kernels.
 template<int MP>
 struct MassTok {
-    int2 ev[MP];   // {slot, gain or effective weight}
-    float m[MP];   // write: mass before; read: post-write mass
-    float v[MP];   // write: w; read: raw weight rho (positive)
+    int4 ev[MP];   // the event's record (write: {slot, g, matched read weight, mass before};
+                   // read: {slot, effective weight, post-write mass, 0})
+    float v[MP];   // write: w; read: the stored (negated) weight
     float dd[MP];  // write: Dg; read: d_j
-    float gam;
+    uint32_t gam;  // gamma_t bits
 };
 
-template<typename Scalar, bool MA, int MP>
-__global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBwdJob job) {
-    constexpr int CH = MP == 1 ? 8 : MP == 2 ? 4 : 2;
+template<typename Scalar, bool MA, int MP, bool REPLAY>
+__global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBwdJob job, float2 *maps,
+                                                                int chunk_len) {
+    constexpr int CH = MP == 1 ? 16 : MP == 2 ? 8 : 4;
     extern __shared__ __align__(16) float lds[];
     const SegmentJob &fj = job.fwd;
     const int A = fj.A, T = fj.T, Kw = fj.Kw, Kr = fj.Kr, Kt = Kw + Kr;
     const float eps = fj.eps;
-    const int bh = static_cast<int>(blockIdx.x);
+    const int bh = static_cast<int>(blockIdx.x), ck = static_cast<int>(blockIdx.y), nck = static_cast<int>(gridDim.y);
     const int lane = static_cast<int>(threadIdx.x);
     const int hl = lane & 31;
     const bool wlane = lane < 32;
-    float *dm = lds + 2;  // dm[-2], dm[-1]: the no-op slots
-    for (int a = lane; a < A; a += kWave)
-        dm[a] = job.grad_mass ? job.grad_mass[static_cast<int64_t>(bh) * A + a] : 0.f;
-    if (lane < 2)
-        lds[lane] = 0.f;
+    float *dm = lds + 2;                              // REPLAY: Dm per slot; dm[-2], dm[-1] the no-op slots
+    float2 *mp = reinterpret_cast<float2 *>(lds) + 2;  // MAP: (a, b) per slot
+    const float2 *ends = maps + (static_cast<int64_t>(bh) * nck + ck) * A;
+    if constexpr (REPLAY) {
+        for (int a = lane; a < A; a += kWave)
+            dm[a] = nck > 1 ? ends[a].x : (job.grad_mass ? job.grad_mass[static_cast<int64_t>(bh) * A + a] : 0.f);
+        if (lane < 2)
+            lds[lane] = 0.f;
+    } else {
+        for (int a = lane - 2; a < A; a += kWave)
+            mp[a] = make_float2(1.f, 0.f);
+    }
     __syncthreads();
     const Scalar *gs = static_cast<const Scalar *>(job.gamma) + static_cast<int64_t>(bh) * T;
     const float *val = job.addr_val + static_cast<int64_t>(bh) * Kt * T;
     float *gval = job.grad_val + static_cast<int64_t>(bh) * Kt * T;
+    bool on[MP];
+    int ec[MP];
+#pragma unroll
+    for (int p = 0; p < MP; ++p) {
+        const int ev = p * 32 + hl;
+        on[p] = wlane ? ev < Kw : ev < Kr;
+        ec[p] = min(ev, (wlane ? Kw : Kr) - 1);
+    }
+    const int4 *evp = wlane ? job.aux.wev : job.aux.rev;
+    const float *ddp = wlane ? job.dg_sum : job.dr_sum;
+    const int kl = wlane ? Kw : Kr, koff = wlane ? 0 : Kw;
 
     auto load_tok = [&](int t, MassTok<MP> &k) {
         const int64_t tb = static_cast<int64_t>(bh) * T + t;
 #pragma unroll
         for (int p = 0; p < MP; ++p) {
-            const int ev = p * 32 + hl;
-            const bool on = wlane ? ev < Kw : ev < Kr;
-            const int ec = on ? ev : 0;
-            if (wlane) {
-                k.ev[p] = on ? job.aux.wev[tb * Kw + ec] : make_int2(-2, 0);
-                k.m[p] = job.aux.wm[tb * Kw + ec];
-                k.v[p] = val[static_cast<int64_t>(ec) * T + t];
-                k.dd[p] = job.dg_part[tb * Kw + ec];
-            } else {
-                k.ev[p] = on ? job.aux.rev[tb * Kr + ec] : make_int2(-1, 0);
-                k.m[p] = MA ? job.aux.rm[tb * Kr + ec] : 0.f;
-                k.v[p] = -val[static_cast<int64_t>(Kw + ec) * T + t];
-                k.dd[p] = job.dr_part[tb * Kr + ec];
-            }
+            const int64_t o = tb * kl + ec[p];
+            k.ev[p] = evp[o];
+            k.v[p] = val[static_cast<int64_t>(koff + ec[p]) * T + t];
+            k.dd[p] = ddp[o];
         }
-        k.gam = load_f32(gs + t);
+        k.gam = raw_load(gs + t);
     };
 
+    const int t_begin = ck * chunk_len, t_end = min(T, t_begin + chunk_len);
+    const int n = t_end - t_begin;
     MassTok<MP> cur[CH], nxt[CH];
 #pragma unroll
     for (int j = 0; j < CH; ++j)
-        load_tok(max(T - 1 - j, 0), cur[j]);
-    const int nck = (T + CH - 1) / CH;
-    for (int ci = 0; ci < nck; ++ci) {
+        load_tok(max(t_end - 1 - j, t_begin), cur[j]);
+    const int nc = (n + CH - 1) / CH;
+    for (int ci = 0; ci < nc; ++ci) {
 #pragma unroll
         for (int j = 0; j < CH; ++j)
-            load_tok(max(T - 1 - (ci + 1) * CH - j, 0), nxt[j]);
+            load_tok(max(t_end - 1 - (ci + 1) * CH - j, t_begin), nxt[j]);
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
-            const int t = T - 1 - ci * CH - j;
-            if (t < 0)
+            const int t = t_end - 1 - ci * CH - j;
+            if (t < t_begin)
                 break;
             const MassTok<MP> &k = cur[j];
             // reads of token t (they follow its writes in the forward)
@@ -376,73 +557,113 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
                 float sr = 0.f, srm = 0.f, sdm = 0.f;
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
-                    const bool act = !wlane && k.ev[p].x >= 0;
-                    const float rho = act ? k.v[p] : 0.f;
+                    const bool a_on = !wlane && on[p] && k.ev[p].x >= 0;
+                    const float rho = a_on ? -k.v[p] : 0.f;
                     sr += rho;
-                    srm = fmaf(rho, k.m[p], srm);
-                    sdm = fmaf(rho * k.m[p], act ? k.dd[p] : 0.f, sdm);
+                    srm = fmaf(rho, __int_as_float(k.ev[p].z), srm);
+                    sdm = fmaf(rho * __int_as_float(k.ev[p].z), a_on ? k.dd[p] : 0.f, sdm);
                 }
-                sr = event_sum<32>(sr);
-                srm = event_sum<32>(srm);
-                sdm = event_sum<32>(sdm);
+                sr = xor_sum<1, 32>(sr);
+                srm = xor_sum<1, 32>(srm);
+                sdm = xor_sum<1, 32>(sdm);
                 const float inv = 1.f / (srm + eps);
                 const float c = sr * inv, Q = sdm * inv;
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
-                    const bool act = !wlane && k.ev[p].x >= 0;
+                    const bool a_on = !wlane && on[p] && k.ev[p].x >= 0;
                     const float diff = k.dd[p] - Q;
-                    dr[p] = act ? fmaf(c * k.m[p], diff, Q) : 0.f;
-                    if (act)
-                        dm[k.ev[p].x] += c * k.v[p] * diff;
+                    dr[p] = a_on ? fmaf(c * __int_as_float(k.ev[p].z), diff, Q) : 0.f;
+                    if (a_on) {
+                        const float kap = -c * k.v[p] * diff;
+                        if constexpr (REPLAY)
+                            dm[k.ev[p].x] += kap;
+                        else
+                            mp[k.ev[p].x].y += kap;
+                    }
                 }
+                __syncthreads();
             } else {
 #pragma unroll
                 for (int p = 0; p < MP; ++p)
-                    dr[p] = (!wlane && k.ev[p].x >= 0) ? k.dd[p] : 0.f;
+                    dr[p] = (!wlane && on[p] && k.ev[p].x >= 0) ? k.dd[p] : 0.f;
             }
-            __syncthreads();
             // writes of token t
             float dgam = 0.f;
             float dw[MP];
+            const float gm = half_bits_to_f<Scalar>(k.gam);
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
                 dw[p] = 0.f;
-                const bool act = wlane && k.ev[p].x >= 0;
-                if (act) {
-                    const float w = k.v[p], m = k.m[p], gm = k.gam, Dg = k.dd[p];
+                if (wlane && on[p] && k.ev[p].x >= 0) {
+                    const float w = k.v[p], m = __int_as_float(k.ev[p].w), Dg = k.dd[p];
                     const float g = __int_as_float(k.ev[p].y);
                     const float al = gsu_alpha(w, gm);
                     const float den = fmaf(al, m, w) + eps;
+                    const float q0 = Dg * g / den;
                     const int a = k.ev[p].x;
-                    const float dtot = dm[a] - Dg * g / den;
-                    const float qd = expf(-fabsf(gm));
-                    const float cw = 1.f - w;
-                    const float dn = gm >= 0.f ? fmaf(qd, cw, w) : fmaf(qd, w, cw);
-                    const float t2 = qd / (dn * dn);
-                    dw[p] = Dg / den + dtot * fmaf(-m, t2, 1.f);
-                    dgam = fmaf(-dtot * m, cw * w * t2, dgam);
-                    dm[a] = dtot * al;
+                    if constexpr (REPLAY) {
+                        const float dtot = dm[a] - q0;
+                        const float qd = expf(-fabsf(gm));
+                        const float cw = 1.f - w;
+                        const float dn = gm >= 0.f ? fmaf(qd, cw, w) : fmaf(qd, w, cw);
+                        const float t2 = qd / (dn * dn);
+                        dw[p] = Dg / den + dtot * fmaf(-m, t2, 1.f);
+                        dgam = fmaf(-dtot * m, cw * w * t2, dgam);
+                        dm[a] = dtot * al;
+                    } else {
+                        const float2 ab = mp[a];
+                        mp[a] = make_float2(al * ab.x, al * (ab.y - q0));
+                    }
                 }
             }
-            dgam = event_sum<32>(dgam);
-            if (lane == 0)
-                job.grad_gamma[static_cast<int64_t>(bh) * T + t] = dgam;
+            if constexpr (REPLAY) {
+                dgam = xor_sum<1, 32>(dgam);
+                if (lane == 0)
+                    job.grad_gamma[static_cast<int64_t>(bh) * T + t] = dgam;
 #pragma unroll
-            for (int p = 0; p < MP; ++p) {
-                const int ev = p * 32 + hl;
-                if (wlane && ev < Kw)
-                    gval[static_cast<int64_t>(ev) * T + t] = dw[p];
-                if (!wlane && ev < Kr)
-                    gval[static_cast<int64_t>(Kw + ev) * T + t] = dr[p];
+                for (int p = 0; p < MP; ++p) {
+                    const int ev = p * 32 + hl;
+                    if (on[p])
+                        gval[static_cast<int64_t>(koff + ev) * T + t] = wlane ? dw[p] : dr[p];
+                }
             }
-            __syncthreads();
+            if constexpr (MA)
+                __syncthreads();
         }
 #pragma unroll
         for (int j = 0; j < CH; ++j)
             cur[j] = nxt[j];
     }
-    for (int a = lane; a < A; a += kWave)
-        job.grad_init_mass[static_cast<int64_t>(bh) * A + a] = dm[a];
+    __syncthreads();
+    if constexpr (REPLAY) {
+        if (nck == 1) {
+            for (int a = lane; a < A; a += kWave)
+                job.grad_init_mass[static_cast<int64_t>(bh) * A + a] = dm[a];
+        }
+    } else {
+        float2 *dst = maps + (static_cast<int64_t>(bh) * nck + ck) * A;
+        for (int a = lane; a < A; a += kWave)
+            dst[a] = mp[a];
+    }
+}
+
+// Per (b, h, slot): Dm at the end of every chunk (last chunk first) in
+// place of its map, and the gradient of the initial mass.
+__global__ __launch_bounds__(256) void segment_bwd_mass_scan_kernel(const SegmentBwdJob job, float2 *maps, int nck) {
+    const int A = job.fwd.A;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(job.fwd.B) * job.fwd.H * A)
+        return;
+    const int64_t bh = i / A;
+    const int a = static_cast<int>(i - bh * A);
+    float D = job.grad_mass ? job.grad_mass[i] : 0.f;
+    float2 *mp = maps + bh * nck * A + a;
+    for (int c = nck - 1; c >= 0; --c) {
+        const float2 ab = mp[static_cast<int64_t>(c) * A];
+        mp[static_cast<int64_t>(c) * A] = make_float2(D, 0.f);
+        D = fmaf(ab.x, D, ab.y);
+    }
+    job.grad_init_mass[i] = D;
 }
 
 template<typename Scalar, int EPP, int NP>
@@ -469,18 +690,33 @@ hipError_t launch_bwd_scan(const SegmentBwdJob &job, const BwdPlan &p, hipStream
     }
 }
 
+template<typename Scalar, bool MA, int MP>
+hipError_t launch_bwd_mass_mp(const SegmentBwdJob &job, hipStream_t stream) {
+    const SegmentJob &fj = job.fwd;
+    int len = 0;
+    const int nck = mass_replay_chunks(fj, job.maps_bytes, &len);
+    const dim3 grid(static_cast<unsigned>(fj.B * fj.H), static_cast<unsigned>(nck));
+    auto *maps = static_cast<float2 *>(job.maps);
+    if (nck > 1) {
+        hipLaunchKernelGGL((segment_bwd_mass_kernel<Scalar, MA, MP, false>), grid, dim3(kWave),
+                           static_cast<size_t>(fj.A + 2) * 8, stream, job, maps, len);
+        const int64_t n = static_cast<int64_t>(fj.B) * fj.H * fj.A;
+        hipLaunchKernelGGL(segment_bwd_mass_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                           stream, job, maps, nck);
+    }
+    hipLaunchKernelGGL((segment_bwd_mass_kernel<Scalar, MA, MP, true>), grid, dim3(kWave),
+                       static_cast<size_t>(fj.A + 2) * 4, stream, job, maps, len);
+    return hipGetLastError();
+}
+
 template<typename Scalar, bool MA>
 hipError_t launch_bwd_mass(const SegmentBwdJob &job, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(job.fwd.B * job.fwd.H));
-    const size_t lds = static_cast<size_t>(job.fwd.A + 2) * 4;
     const int kmax = std::max(job.fwd.Kw, job.fwd.Kr);
     if (kmax <= 32)
-        hipLaunchKernelGGL((segment_bwd_mass_kernel<Scalar, MA, 1>), grid, dim3(kWave), lds, stream, job);
-    else if (kmax <= 64)
-        hipLaunchKernelGGL((segment_bwd_mass_kernel<Scalar, MA, 2>), grid, dim3(kWave), lds, stream, job);
-    else
-        hipLaunchKernelGGL((segment_bwd_mass_kernel<Scalar, MA, 4>), grid, dim3(kWave), lds, stream, job);
-    return hipGetLastError();
+        return launch_bwd_mass_mp<Scalar, MA, 1>(job, stream);
+    if (kmax <= 64)
+        return launch_bwd_mass_mp<Scalar, MA, 2>(job, stream);
+    return launch_bwd_mass_mp<Scalar, MA, 4>(job, stream);
 }
 
 template<typename Scalar>
@@ -489,16 +725,16 @@ hipError_t launch_typed(const SegmentBwdJob &job, const BwdPlan &p, hipStream_t 
     if (err != hipSuccess)
         return err;
     const SegmentJob &fj = job.fwd;
-    const int64_t nw = static_cast<int64_t>(fj.B) * fj.H * fj.T * fj.Kw;
-    const int64_t nr = static_cast<int64_t>(fj.B) * fj.H * fj.T * fj.Kr;
-    if (p.n_sub > 1) {
-        hipLaunchKernelGGL(segment_bwd_sum_kernel, dim3(static_cast<unsigned>((nw + 255) / 256)), dim3(256), 0, stream,
-                           job.dg_part, p.n_sub, nw);
-        hipLaunchKernelGGL(segment_bwd_sum_kernel, dim3(static_cast<unsigned>((nr + 255) / 256)), dim3(256), 0, stream,
-                           job.dr_part, p.n_sub, nr);
-        if ((err = hipGetLastError()) != hipSuccess)
-            return err;
-    }
+    const int BH = fj.B * fj.H, KP = p.epp * p.np;
+    const int t_pad = (fj.T + bwd_chunk(p.epp, p.np) - 1) / bwd_chunk(p.epp, p.np) * bwd_chunk(p.epp, p.np);
+    const int64_t nw = static_cast<int64_t>(BH) * fj.T * fj.Kw;
+    const int64_t nr = static_cast<int64_t>(BH) * fj.T * fj.Kr;
+    hipLaunchKernelGGL(segment_bwd_sum_kernel, dim3(static_cast<unsigned>((nw + 255) / 256)), dim3(256), 0, stream,
+                       job.dg_part, job.dg_sum, p.n_sub, BH, fj.T, t_pad, KP, fj.Kw);
+    hipLaunchKernelGGL(segment_bwd_sum_kernel, dim3(static_cast<unsigned>((nr + 255) / 256)), dim3(256), 0, stream,
+                       job.dr_part, job.dr_sum, p.n_sub, BH, fj.T, t_pad, KP, fj.Kr);
+    if ((err = hipGetLastError()) != hipSuccess)
+        return err;
     return fj.mass_aware ? launch_bwd_mass<Scalar, true>(job, stream) : launch_bwd_mass<Scalar, false>(job, stream);
 }
 
@@ -526,21 +762,24 @@ int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int K
         off += align256(bytes);
         return ptr;
     };
-    char *wev = take(nw * 8), *wm = take(nw * 4), *rev = take(nr * 8), *rm = take(nr * 4);
+    char *wev = take(nw * 16), *rev = take(nr * 16);
     char *mass = take(bh * A * 4);
     const int64_t maps_bytes = mass_replay_scratch_bytes(B, H, T, A);
     char *maps = take(maps_bytes);
-    char *delta = take(bh * p.n_sub * T * Kw * p.csw * 4);
-    char *dr = take(p.n_sub * nr * 4), *dg = take(p.n_sub * nw * 4);
+    const int64_t kp = p.epp * p.np, ch = bwd_chunk(p.epp, p.np), t_pad = (T + ch - 1) / ch * ch;
+    char *delta = take(bh * p.n_sub * T * kp * p.csw * 4);
+    char *dr = take(p.n_sub * bh * t_pad * kp * 4), *dg = take(p.n_sub * bh * t_pad * kp * 4);
+    char *drs = take(nr * 4), *dgs = take(nw * 4);
     if (job) {
-        job->aux = MassAux{reinterpret_cast<int2 *>(wev), reinterpret_cast<float *>(wm), reinterpret_cast<int2 *>(rev),
-                           reinterpret_cast<float *>(rm)};
+        job->aux = MassAux{reinterpret_cast<int4 *>(wev), reinterpret_cast<int4 *>(rev)};
         job->mass_scratch = reinterpret_cast<float *>(mass);
         job->maps = maps;
         job->maps_bytes = static_cast<size_t>(maps_bytes);
         job->delta = reinterpret_cast<float *>(delta);
         job->dr_part = reinterpret_cast<float *>(dr);
         job->dg_part = reinterpret_cast<float *>(dg);
+        job->dr_sum = reinterpret_cast<float *>(drs);
+        job->dg_sum = reinterpret_cast<float *>(dgs);
     }
     return off;
 }

@@ -334,19 +334,15 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
         auto finish = [&](int j, const int (&a)[MP], const float (&w)[MP], const float (&al)[MP], float (&m)[MP]) {
             const int t = t0 + j;
             const bool live = t < t_end;
+            float gn[MP];
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
                 const float m2 = fmaf(al[p], m[p], w[p]);
                 ms[a[p]] = m2;
-                if (wlane && ln.on[p] && live) {
-                    const float gn = scan_gain(w[p], m2 + eps);
-                    if constexpr (AUX) {
-                        const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kw + ln.ev[p];
-                        aux.wev[o] = make_int2(a[p], __float_as_int(gn));
-                        aux.wm[o] = m[p];
-                    } else {
-                        gw[static_cast<int64_t>(ln.ev[p]) * t_pad + t].alpha = gn;
-                    }
+                gn[p] = scan_gain(w[p], m2 + eps);
+                if constexpr (!AUX) {
+                    if (wlane && ln.on[p] && live)
+                        gw[static_cast<int64_t>(ln.ev[p]) * t_pad + t].alpha = gn[p];
                 }
             }
             if constexpr (MA || AUX) {
@@ -368,16 +364,42 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                     srm = event_sum<32>(srm);
                     scale = sr / (srm + eps);
                 }
+                float re[MP];
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
+                    re[p] = MA ? rr[p] * mm[p] * scale : rr[p];
                     if (!wlane && ln.on[p] && live) {
-                        const float re = MA ? rr[p] * mm[p] * scale : rr[p];
                         if constexpr (AUX) {
                             const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kr + ln.ev[p];
-                            aux.rev[o] = make_int2(rb[p], __float_as_int(re));
-                            aux.rm[o] = mm[p];
+                            aux.rev[o] = make_int4(rb[p], __float_as_int(re[p]), __float_as_int(mm[p]), 0);
                         } else {
-                            gr[static_cast<int64_t>(ln.ev[p]) * t_pad + t].r = re;
+                            gr[static_cast<int64_t>(ln.ev[p]) * t_pad + t].r = re[p];
+                        }
+                    }
+                }
+                if constexpr (AUX) {
+                    // each write's record carries the effective weight of the read of
+                    // the same slot in this token (0 if none)
+                    float rmatch[MP];
+#pragma unroll
+                    for (int p = 0; p < MP; ++p)
+                        rmatch[p] = 0.f;
+#pragma unroll
+                    for (int p2 = 0; p2 < MP; ++p2) {
+                        for (int jj = 0; jj < 32 && p2 * 32 + jj < Kr; ++jj) {
+                            const int sl = __builtin_amdgcn_readlane(rb[p2], 32 + jj);
+                            const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(re[p2]), 32 + jj));
+#pragma unroll
+                            for (int p = 0; p < MP; ++p)
+                                rmatch[p] = (a[p] >= 0 && a[p] == sl) ? rv : rmatch[p];
+                        }
+                    }
+#pragma unroll
+                    for (int p = 0; p < MP; ++p) {
+                        if (wlane && ln.on[p] && live) {
+                            const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kw + ln.ev[p];
+                            aux.wev[o] = make_int4(a[p], __float_as_int(gn[p]), __float_as_int(rmatch[p]),
+                                                   __float_as_int(m[p]));
                         }
                     }
                 }
@@ -485,6 +507,10 @@ int64_t mass_replay_scratch_bytes(int B, int H, int T, int A) {
     int len = 0;
     const int nck = mass_chunks(job, static_cast<size_t>(1) << 62, cu_count(), &len);
     return nck <= 1 ? 0 : static_cast<int64_t>(B) * H * nck * A * static_cast<int64_t>(sizeof(float2));
+}
+
+int mass_replay_chunks(const SegmentJob &job, size_t maps_bytes, int *chunk_len) {
+    return mass_chunks(job, maps_bytes, cu_count(), chunk_len);
 }
 
 hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *maps, size_t maps_bytes,
