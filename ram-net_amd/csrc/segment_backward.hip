@@ -68,9 +68,9 @@ struct BwdPlan {
 // Tokens per staged chunk of the slice kernel, and the stage's LDS bytes:
 // write records (16 B) and read records (8 B) per event slot, x and Dy per
 // channel, per token.
-__host__ __device__ constexpr int bwd_chunk(int epp, int np) { return epp * np >= 64 ? 8 : 16; }
+__host__ __device__ constexpr int bwd_chunk(int epp, int np, int vec) { return epp * np >= 64 || np * vec >= 2 ? 8 : 16; }
 constexpr int64_t bwd_stage_bytes(int epp, int np, int vec) {
-    return static_cast<int64_t>(bwd_chunk(epp, np)) * (epp * np * (16 + 8) + 2 * (kWave / epp) * vec * 4);
+    return static_cast<int64_t>(bwd_chunk(epp, np, vec)) * (epp * np * (16 + 8) + 2 * (kWave / epp) * vec * 4);
 }
 
 // Lane layout of the slice kernel: EPP events per pass (NP passes), LPE =
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     constexpr int LPE = kWave / EPP;               // lanes per event (consecutive: channel groups)
     constexpr int CSW = LPE * VEC;
     constexpr int KP = NP * EPP;                   // event slots per token (padded)
-    constexpr int CH = bwd_chunk(EPP, NP);         // tokens per staged chunk
+    constexpr int CH = bwd_chunk(EPP, NP, VEC);         // tokens per staged chunk
     constexpr int NREC = CH * KP;                  // records of each kind per chunk
     constexpr int RPL = (NREC + kWave - 1) / kWave;
     constexpr int NXE = CH * CSW;                  // x (and Dy) elements per chunk
@@ -174,7 +174,14 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     const int A = fj.A, C = fj.C, T = fj.T, Kw = fj.Kw, Kr = fj.Kr;
     const int BH = fj.B * fj.H;
     const int t_pad = (T + CH - 1) / CH * CH;
-    const int unit = static_cast<int>(blockIdx.x);
+    // Workgroups are dealt round-robin to the 8 XCDs; give each XCD a
+    // contiguous run of units so the slices of one (b, h), which read the
+    // same records and activations, share an L2.
+    const int n_units = BH * n_sub;
+    const int per_xcd = (n_units + 7) / 8;
+    const int unit = static_cast<int>(blockIdx.x % 8) * per_xcd + static_cast<int>(blockIdx.x / 8);
+    if (unit >= n_units)
+        return;
     const int bh = unit / n_sub, sub = unit - bh * n_sub;
     const int lane = static_cast<int>(threadIdx.x);
     const int e = lane / LPE, q = lane % LPE;
@@ -255,13 +262,52 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
         for (int ci = 0; ci < nck; ++ci) {
             stage(cur, Tag{});
             prefetch(min(ci + 1, nck - 1), nxt, Tag{});
+            // the chunk's records and activations for this lane, read back in
+            // one batch, so that each token costs one LDS round trip
+            int wsl[CH][NP], rsl[CH][NP];
+            float wg[CH][NP], xv[CH][VEC], dyv[CH][VEC];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const int2 w2 = *reinterpret_cast<const int2 *>(&stw[j * KP + p * EPP + e]);
+                    wsl[j][p] = w2.x;
+                    wg[j][p] = __int_as_float(w2.y);
+                    rsl[j][p] = str[j * KP + p * EPP + e].x;
+                }
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) {
+                    xv[j][v] = stx[j * CSW + q * VEC + v];
+                    dyv[j][v] = sdy[j * CSW + q * VEC + v];
+                }
+            }
             // write rows of the current token, loaded one token ahead:
             // after the previous token's writes, with its reads
             FVec<VEC> sw[NP];
 #pragma unroll
             for (int p = 0; p < NP; ++p)
-                sw[p] = lds_vec(rows + stw[p * EPP + e].x * CSW + q * VEC);
+                sw[p] = lds_vec(rows + wsl[0][p] * CSW + q * VEC);
             float keep[NP];  // d_j of token (group start + q), stored once per LPE tokens
+            // d_j of token j: the dot of its read rows with Dy_t, reduced over
+            // the event's lanes and kept by lane q = j % LPE
+            auto read_dot = [&](int j, const FVec<VEC> (&sr)[NP]) {
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    float part = 0.f;
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v)
+                        part = fmaf(sr[p].v[v], dyv[j][v], part);
+                    part = event_sum<LPE>(part);
+                    keep[p] = q == j % LPE ? part : keep[p];
+                }
+                if (j % LPE == LPE - 1) {
+                    const int tg = ci * CH + j - (LPE - 1) + q;  // this lane's token of the group
+#pragma unroll
+                    for (int p = 0; p < NP; ++p)
+                        drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
+                }
+            };
+            FVec<VEC> sr[NP];  // read rows of the previous token, reduced one token late
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int t = ci * CH + j;
@@ -269,41 +315,31 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     break;
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    const int4 wr = stw[j * KP + p * EPP + e];
-                    const float g = __int_as_float(wr.y);
                     FVec<VEC> s = sw[p], d;
 #pragma unroll
                     for (int v = 0; v < VEC; ++v) {
-                        d.v[v] = stx[j * CSW + q * VEC + v] - s.v[v];
-                        s.v[v] = fmaf(g, d.v[v], s.v[v]);
+                        d.v[v] = xv[j][v] - s.v[v];
+                        s.v[v] = fmaf(wg[j][p], d.v[v], s.v[v]);
                     }
-                    lds_store<VEC>(rows + wr.x * CSW + q * VEC, s);
+                    lds_store<VEC>(rows + wsl[j][p] * CSW + q * VEC, s);
                     lds_store<VEC>(dlt + (static_cast<int64_t>(t) * KP + p * EPP) * CSW, d);
                 }
-                FVec<VEC> sr[NP];
+                FVec<VEC> srn[NP];
 #pragma unroll
                 for (int p = 0; p < NP; ++p)
-                    sr[p] = lds_vec(rows + str[j * KP + p * EPP + e].x * CSW + q * VEC);
+                    srn[p] = lds_vec(rows + rsl[j][p] * CSW + q * VEC);
                 if (j + 1 < CH) {
 #pragma unroll
                     for (int p = 0; p < NP; ++p)
-                        sw[p] = lds_vec(rows + stw[(j + 1) * KP + p * EPP + e].x * CSW + q * VEC);
+                        sw[p] = lds_vec(rows + wsl[j + 1][p] * CSW + q * VEC);
                 }
+                if (j > 0)
+                    read_dot(j - 1, sr);
 #pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    float part = 0.f;
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v)
-                        part = fmaf(sr[p].v[v], sdy[j * CSW + q * VEC + v], part);
-                    part = event_sum<LPE>(part);
-                    keep[p] = q == j % LPE ? part : keep[p];
-                }
-                if (j % LPE == LPE - 1) {
-                    const int tg = t - (LPE - 1) + q;  // this lane's token of the group
-#pragma unroll
-                    for (int p = 0; p < NP; ++p)
-                        drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
-                }
+                for (int p = 0; p < NP; ++p)
+                    sr[p] = srn[p];
+                if (j == CH - 1 || t == T - 1)
+                    read_dot(j, sr);
             }
             if (T - ci * CH < CH && (T - ci * CH) % LPE != 0) {  // ragged last group
                 const int n = T - ci * CH, tg = ci * CH + n / LPE * LPE + q;
@@ -346,62 +382,79 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
             stage(cur, Tag{});
             prefetch(min(ci + 1, nck - 1), nxt, Tag{});
             load_saved(min(ci + 1, nck - 1), snxt);
+            int wsl[CH][NP], rsl[CH][NP];
+            float wg[CH][NP], wrm[CH][NP], rw[CH][NP], dyv[CH][VEC];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const int4 w4 = stw[j * KP + p * EPP + e];
+                    const int2 r2 = str[j * KP + p * EPP + e];
+                    wsl[j][p] = w4.x;
+                    wg[j][p] = __int_as_float(w4.y);
+                    wrm[j][p] = __int_as_float(w4.z);
+                    rsl[j][p] = r2.x;
+                    rw[j][p] = __int_as_float(r2.y);
+                }
+#pragma unroll
+                for (int v = 0; v < VEC; ++v)
+                    dyv[j][v] = sdy[j * CSW + q * VEC + v];
+            }
             float keep[NP];       // Dg of token (group start - q), stored once per LPE tokens
             float keep_x[VEC];    // Dx of token (group start - e), stored once per GX tokens
+            // rows of the current token, loaded before the previous token's
+            // reductions (after its stores)
+            FVec<VEC> dr[NP], dw[NP];
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                dr[p] = lds_vec(rows + rsl[0][p] * CSW + q * VEC);
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                dw[p] = lds_vec(rows + wsl[0][p] * CSW + q * VEC);
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int t = T - 1 - ci * CH - j;
                 if (t < 0)
                     break;
-                // all rows of token t in one round trip: a write takes the
-                // read of its own slot (same token) from its matched weight,
-                // and its store lands after that read's
-                int4 wr[NP];
-                int2 rr[NP];
-                FVec<VEC> dr[NP], dw[NP];
+                // a write takes the read of its own slot (same token) from its
+                // matched weight, and its store lands after that read's
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    wr[p] = stw[j * KP + p * EPP + e];
-                    rr[p] = str[j * KP + p * EPP + e];
-                }
-#pragma unroll
-                for (int p = 0; p < NP; ++p)
-                    dr[p] = lds_vec(rows + rr[p].x * CSW + q * VEC);
-#pragma unroll
-                for (int p = 0; p < NP; ++p)
-                    dw[p] = lds_vec(rows + wr[p].x * CSW + q * VEC);
-                float dy[VEC];
-#pragma unroll
-                for (int v = 0; v < VEC; ++v)
-                    dy[v] = sdy[j * CSW + q * VEC + v];
-#pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    const float r = __int_as_float(rr[p].y);
 #pragma unroll
                     for (int v = 0; v < VEC; ++v)
-                        dr[p].v[v] = fmaf(r, dy[v], dr[p].v[v]);
-                    lds_store<VEC>(rows + rr[p].x * CSW + q * VEC, dr[p]);
+                        dr[p].v[v] = fmaf(rw[j][p], dyv[j][v], dr[p].v[v]);
+                    lds_store<VEC>(rows + rsl[j][p] * CSW + q * VEC, dr[p]);
                 }
-                float dx[VEC];
+                float dx[VEC], part[NP];
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
                     dx[v] = 0.f;
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    const float g = __int_as_float(wr[p].y);
-                    const float rm = __int_as_float(wr[p].z);
+                    const float g = wg[j][p];
                     FVec<VEC> D = dw[p];
-                    float part = 0.f;
+                    part[p] = 0.f;
 #pragma unroll
                     for (int v = 0; v < VEC; ++v) {
-                        D.v[v] = fmaf(rm, dy[v], D.v[v]);
-                        part = fmaf(D.v[v], __uint_as_float(scur.v[j][p * VEC + v]), part);
+                        D.v[v] = fmaf(wrm[j][p], dyv[j][v], D.v[v]);
+                        part[p] = fmaf(D.v[v], __uint_as_float(scur.v[j][p * VEC + v]), part[p]);
                         dx[v] = fmaf(g, D.v[v], dx[v]);
                         D.v[v] = fmaf(-g, D.v[v], D.v[v]);
                     }
-                    lds_store<VEC>(rows + wr[p].x * CSW + q * VEC, D);
-                    part = event_sum<LPE>(part);
-                    keep[p] = q == j % LPE ? part : keep[p];
+                    lds_store<VEC>(rows + wsl[j][p] * CSW + q * VEC, D);
+                }
+                if (j + 1 < CH) {
+#pragma unroll
+                    for (int p = 0; p < NP; ++p)
+                        dr[p] = lds_vec(rows + rsl[j + 1][p] * CSW + q * VEC);
+#pragma unroll
+                    for (int p = 0; p < NP; ++p)
+                        dw[p] = lds_vec(rows + wsl[j + 1][p] * CSW + q * VEC);
+                }
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const float sp = event_sum<LPE>(part[p]);
+                    keep[p] = q == j % LPE ? sp : keep[p];
                 }
                 if (j % LPE == LPE - 1 || t == 0) {
                     const int tg = t + (j % LPE) - q;  // this lane's token of the group
@@ -668,7 +721,7 @@ __global__ __launch_bounds__(256) void segment_bwd_mass_scan_kernel(const Segmen
 
 template<typename Scalar, int EPP, int NP>
 hipError_t launch_bwd_scan_vec(const SegmentBwdJob &job, const BwdPlan &p, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(job.fwd.B * job.fwd.H * p.n_sub));
+    const dim3 grid(static_cast<unsigned>((job.fwd.B * job.fwd.H * p.n_sub + 7) / 8 * 8));
     const size_t lds = static_cast<size_t>(p.lds);
     switch (p.vec) {
         case 1: hipLaunchKernelGGL((segment_bwd_scan_kernel<Scalar, EPP, NP, 1>), grid, dim3(kWave), lds, stream, job, p.n_sub); break;
@@ -726,7 +779,7 @@ hipError_t launch_typed(const SegmentBwdJob &job, const BwdPlan &p, hipStream_t 
         return err;
     const SegmentJob &fj = job.fwd;
     const int BH = fj.B * fj.H, KP = p.epp * p.np;
-    const int t_pad = (fj.T + bwd_chunk(p.epp, p.np) - 1) / bwd_chunk(p.epp, p.np) * bwd_chunk(p.epp, p.np);
+    const int t_pad = (fj.T + bwd_chunk(p.epp, p.np, p.vec) - 1) / bwd_chunk(p.epp, p.np, p.vec) * bwd_chunk(p.epp, p.np, p.vec);
     const int64_t nw = static_cast<int64_t>(BH) * fj.T * fj.Kw;
     const int64_t nr = static_cast<int64_t>(BH) * fj.T * fj.Kr;
     hipLaunchKernelGGL(segment_bwd_sum_kernel, dim3(static_cast<unsigned>((nw + 255) / 256)), dim3(256), 0, stream,
@@ -766,7 +819,7 @@ int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int K
     char *mass = take(bh * A * 4);
     const int64_t maps_bytes = mass_replay_scratch_bytes(B, H, T, A);
     char *maps = take(maps_bytes);
-    const int64_t kp = p.epp * p.np, ch = bwd_chunk(p.epp, p.np), t_pad = (T + ch - 1) / ch * ch;
+    const int64_t kp = p.epp * p.np, ch = bwd_chunk(p.epp, p.np, p.vec), t_pad = (T + ch - 1) / ch * ch;
     char *delta = take(bh * p.n_sub * T * kp * p.csw * 4);
     char *dr = take(p.n_sub * bh * t_pad * kp * 4), *dg = take(p.n_sub * bh * t_pad * kp * 4);
     char *drs = take(nr * 4), *dgs = take(nw * 4);
