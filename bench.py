@@ -294,7 +294,7 @@ def bench_decode(n_steps, dev, graph=True):
     ms = s_ev.elapsed_time(e_ev) / reps
     per_step_ms = ms / n_steps
     bytes_step = event_model_bytes(U, P, C, K, H)["op"] * B * H
-    return {
+    out = {
         "mode": mode,
         "steps": n_steps,
         "ms_per_step": per_step_ms,
@@ -304,6 +304,35 @@ def bench_decode(n_steps, dev, graph=True):
         "roofline_frac": (bytes_step / (per_step_ms / 1e3)) / (HBM_PEAK_GBS * 1e9),
         "kernel_roofline_frac": (bytes_step / (kernel_ms / 1e3)) / (HBM_PEAK_GBS * 1e9),
     }
+    if mode == "hip-graph":
+        out["graph_node_floor_us"] = graph_node_floor_us(dev, n_steps)
+    return out
+
+
+def graph_node_floor_us(dev, n_nodes):
+    """Per-node time of a captured graph of n_nodes trivial kernels (an
+    in-place add on 64 floats): the launch floor under one decode step."""
+    x = torch.zeros(64, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        x.add_(1.0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for _ in range(n_nodes):
+            x.add_(1.0)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / n_nodes)
+    return best
 
 
 def bench_lm(dev, new_tokens):
@@ -491,7 +520,8 @@ def main(argv=None) -> int:
     if args.only in (None, "decode"):
         log("decode: config 3, graph-captured steps")
         dec = bench_decode(args.decode_steps, dev, graph=not args.no_graph)
-        log(f"decode: {dec['ms_per_step'] * 1e3:.2f} us/step ({dec['mode']}), kernel {dec['kernel_ms'] * 1e3:.2f} us")
+        log(f"decode: {dec['ms_per_step'] * 1e3:.2f} us/step ({dec['mode']}), graph node floor "
+            f"{dec.get('graph_node_floor_us', float('nan')):.2f} us")
 
     if pre is not None:
         seg_gbs = pre["segment_bytes"] / (pre["segment_ms"] / 1e3) / 1e9
