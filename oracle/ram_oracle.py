@@ -22,6 +22,10 @@ Never imported by the product package. Functions and what pins them
 * ``sparse_gsu_f64``: fp64 event loop over the selected slots only
   (GPU conventions: masked tokens neither write nor read and get y = 0).
   Pinned by the same closed forms and by agreement with ``dense_ram_attn``.
+* ``sparse_gsu_backward_f64``: fp64 gradients of the event loop by state
+  reconstruction (the reference's segment backward). Pinned by fp64 torch
+  autograd through ``dense_ram_attn`` on the same events (masks, zero
+  weights, mass_aware, large |gamma|).
 * ``topk_f64`` / ``check_topk_indices``: fp64 brute-force top-K with the
   tie rule, and the index comparator that exempts candidates whose fp64
   score lies within ``tol`` of the K-th score.
@@ -37,6 +41,7 @@ __all__ = [
     "dense_topk_addr",
     "dense_ram_attn",
     "sparse_gsu_f64",
+    "sparse_gsu_backward_f64",
     "split_events",
     "topk_f64",
     "check_topk_indices",
@@ -238,6 +243,121 @@ def sparse_gsu_f64(w_idx, w_val, r_idx, r_val, x, gamma, init_slot, init_mass, m
         y[:, t] = np.einsum('bk,bkc->bc', r, S[rows[:, None], a])
         y[~v, t] = 0.0
     return y.reshape(B, H, T, C), S.reshape(B, H, A, C), M.reshape(B, H, A)
+
+
+def sparse_gsu_backward_f64(w_idx, w_val, r_idx, r_val, x, gamma, init_slot, init_mass, grad_y, grad_slot=None,
+                            grad_mass=None, mask=None, mass_aware=False, eps=1e-12, encoded=True):
+    """fp64 gradients of ``sparse_gsu_f64`` by state reconstruction.
+
+    The reference's backward (csrc/ram_attn_segment_parallel.cu:418-606 and
+    packages/ramnet-ops/IMPLEMENTATION.md "Backward by state reconstruction"):
+    a forward pass saves each write's x - s_before; a reverse pass rolls the
+    slot state back (s_before = s_after - g (x - s_before)) while propagating
+    dL/ds and dL/dm through reads and writes. Events that do not act (masked
+    tokens, zero weights) get zero weight gradients, as the reference skips
+    them. Arguments as ``sparse_gsu_f64`` plus grad_y (B, H, T, C) and the
+    final-state gradients grad_slot (B, H, A, C) / grad_mass (B, H, A) (None:
+    zero). Returns (d_w_val (B, H, Kw, T), d_r_val (B, H, Kr, T) with respect
+    to the positive read weights, d_x (B, H, T, C), d_gamma (B, H, T),
+    d_init_slot, d_init_mass), float64 numpy arrays.
+    """
+    f = np.float64
+    x = np.asarray(x, dtype=f)
+    B, H, T, C = x.shape
+    S = np.array(init_slot, dtype=f).reshape(B * H, -1, C)
+    A = S.shape[1]
+    M = np.array(init_mass, dtype=f).reshape(B * H, A)
+    g = np.asarray(gamma, dtype=f).reshape(B * H, T)
+    xs = x.reshape(B * H, T, C)
+    dys = np.asarray(grad_y, dtype=f).reshape(B * H, T, C)
+    wi = np.asarray(w_idx, dtype=np.int64).reshape(B * H, -1, T)
+    wv = np.asarray(w_val, dtype=f).reshape(B * H, -1, T)
+    ri = np.asarray(r_idx, dtype=np.int64).reshape(B * H, -1, T)
+    rv = np.asarray(r_val, dtype=f).reshape(B * H, -1, T)
+    if encoded:
+        base = (np.arange(B * H) * A)[:, None, None]
+        wi = wi - base
+        ri = ri - base
+    Kw, Kr = wi.shape[1], ri.shape[1]
+    valid = np.ones((B, T), dtype=bool) if mask is None else np.asarray(mask, dtype=bool)
+    valid = np.repeat(valid, H, axis=0)
+    rows = np.arange(B * H)
+    # forward: save x - s_before and the mass before of every write, the
+    # post-write mass of every read
+    delta = np.zeros((T, Kw, B * H, C), dtype=f)
+    m_before = np.zeros((T, Kw, B * H), dtype=f)
+    m_read = np.zeros((T, Kr, B * H), dtype=f)
+    for t in range(T):
+        v = valid[:, t]
+        eg = np.exp(g[:, t])
+        for k in range(Kw):
+            a = wi[:, k, t]
+            w = np.where(v, wv[:, k, t], 0.0)
+            comp = 1.0 - w
+            with np.errstate(invalid="ignore", divide="ignore"):
+                alpha = np.where(w == 0.0, 1.0, comp / (comp + eg * w))
+            m_before[t, k] = M[rows, a]
+            m = alpha * M[rows, a] + w
+            M[rows, a] = m
+            gain = w / (m + eps)
+            s = S[rows, a]
+            delta[t, k] = xs[:, t] - s
+            S[rows, a] = s + gain[:, None] * delta[t, k]
+        m_read[t] = M[rows[:, None], ri[:, :, t]].T
+    # reverse: S holds the final state and is rolled back token by token
+    Ds = np.zeros_like(S) if grad_slot is None else np.array(grad_slot, dtype=f).reshape(B * H, A, C)
+    Dm = np.zeros_like(M) if grad_mass is None else np.array(grad_mass, dtype=f).reshape(B * H, A)
+    d_w = np.zeros((B * H, Kw, T), dtype=f)
+    d_r = np.zeros((B * H, Kr, T), dtype=f)
+    d_x = np.zeros((B * H, T, C), dtype=f)
+    d_g = np.zeros((B * H, T), dtype=f)
+    for t in range(T - 1, -1, -1):
+        v = valid[:, t]
+        dy = np.where(v[:, None], dys[:, t], 0.0)
+        # reads (after the token's writes in the forward)
+        a_r = ri[:, :, t]
+        rho = np.where(v[:, None], rv[:, :, t], 0.0)
+        d = np.einsum('bkc,bc->bk', S[rows[:, None], a_r], dy)
+        if mass_aware:
+            m = m_read[t].T
+            R = rho.sum(axis=1, keepdims=True)
+            Z = (m * rho).sum(axis=1, keepdims=True) + eps
+            c = R / Z
+            Q = (d * m * rho).sum(axis=1, keepdims=True) / Z
+            dr = Q + c * m * (d - Q)
+            r_eff = c * m * rho
+            np.add.at(Dm, (rows[:, None], a_r), c * rho * (d - Q))
+        else:
+            dr = d
+            r_eff = rho
+        d_r[:, :, t] = np.where(rho != 0.0, dr, 0.0)
+        for k in range(Kr):
+            Ds[rows, a_r[:, k]] += r_eff[:, k, None] * dy
+        # writes (distinct slots: their order does not matter)
+        eg = np.exp(g[:, t])
+        for k in range(Kw - 1, -1, -1):
+            a = wi[:, k, t]
+            w = np.where(v, wv[:, k, t], 0.0)
+            act = w != 0.0
+            den0 = 1.0 - w + eg * w
+            with np.errstate(invalid="ignore", divide="ignore"):
+                alpha = np.where(act, (1.0 - w) / den0, 1.0)
+                da_dw = np.where(act, -eg / den0 ** 2, 0.0)
+                da_dg = np.where(act, -(1.0 - w) * eg * w / den0 ** 2, 0.0)
+            mb = m_before[t, k]
+            den = alpha * mb + w + eps
+            gain = w / den
+            ds = Ds[rows, a]
+            dgain = np.einsum('bc,bc->b', ds, delta[t, k])
+            d_x[:, t] += gain[:, None] * ds
+            Ds[rows, a] = (1.0 - gain[:, None]) * ds
+            dtot = Dm[rows, a] - dgain * w / den ** 2
+            d_w[:, k, t] = np.where(act, dgain / den + dtot * (1.0 + mb * da_dw), 0.0)
+            d_g[:, t] += np.where(act, dtot * mb * da_dg, 0.0)
+            Dm[rows, a] = np.where(act, alpha * dtot, Dm[rows, a])
+            S[rows, a] = S[rows, a] - gain[:, None] * delta[t, k]
+    return (d_w.reshape(B, H, Kw, T), d_r.reshape(B, H, Kr, T), d_x.reshape(B, H, T, C), d_g.reshape(B, H, T),
+            Ds.reshape(B, H, A, C), Dm.reshape(B, H, A))
 
 
 # ---------------------------------------------------------------------------

@@ -207,3 +207,45 @@ def test_inplace_with_grad_raises():
     with pytest.raises(AssertionError, match="inplace"):
         random_access_memory_attention(w, w, torch.randn(B, T, H, C, device=DEV), init_ram=(slot, mass),
                                        top_k=4, inplace=True)
+
+
+@pytest.mark.parametrize("mass_aware", [False, True])
+def test_config2_full_size_backward_heads(mass_aware):
+    """Config 2 at full size (B=8, H=16, T=4096, d_v=128, A=1024, K=8, bf16):
+    the whole backward on the GPU, then two heads (first and last) against the
+    fp64 state-reconstruction oracle on the GPU's events. Heads are
+    independent, so each head's gradients are complete on its own."""
+    from ram_cases import projected_logits
+    ops = _ops()
+    B, H, U, P, T, C, K = 8, 16, 2, 32, 4096, 128, 8
+    A = P ** U
+    print(f"config 2 full-size backward, mass_aware={mass_aware}", flush=True)
+    w, r = projected_logits(B, H, U, P, T, 128, seed=2)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16)
+    gamma = torch.sigmoid(torch.randn(B, H, T, generator=g) - 1).to(torch.bfloat16)
+    pos = torch.arange(T).view(1, T).expand(B, T)
+    Dy = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16)
+    Ds = torch.randn(B, H, A, C, generator=g)
+    Dm = torch.randn(B, H, A, generator=g)
+    slot0 = torch.zeros(B, H, A, C)
+    mass0 = torch.full((B, H, A), 1.0 / A)
+    idx, val = ops.topk_addr_forward(w.to(DEV), r.to(DEV), H // 2, A, pos.to(DEV), K, K, 0.0, 0.0)
+    got = ops.topk_segment_backward(idx, val, x.to(DEV), gamma.to(DEV), slot0.to(DEV), mass0.to(DEV), None,
+                                    Dy.to(DEV), Ds.to(DEV), Dm.to(DEV), K, K, mass_aware, 1e-12)
+    torch.cuda.synchronize()
+    got = [t.cpu() for t in got]
+    idx_c, val_c = idx.cpu(), val.cpu()
+    heads = ((0, 0), (7, 15))
+    sel = lambda t: torch.stack([t[b, h] for b, h in heads]).unsqueeze(1)  # (2, 1, ...)
+    local = torch.stack([idx_c[b, h] - (b * H + h) * A for b, h in heads]).unsqueeze(1)
+    vsel = sel(val_c)
+    wi, wv, ri, rv = local[:, :, :K], vsel[:, :, :K], local[:, :, K:], -vsel[:, :, K:]
+    ref = oracle.sparse_gsu_backward_f64(wi, wv, ri, rv, sel(x).double(), sel(gamma).double(), sel(slot0),
+                                         sel(mass0), sel(Dy).double(), sel(Ds), sel(Dm), None, mass_aware, 1e-12,
+                                         encoded=False)
+    gval = sel(got[0])
+    names = ("D_w", "D_r", "D_x", "D_gamma", "D_init_slot", "D_init_mass")
+    mine = (gval[:, :, :K], gval[:, :, K:], sel(got[1]), sel(got[2]), sel(got[3]), sel(got[4]))
+    for name, a, b in zip(names, mine, ref):
+        _check(name, a, torch.as_tensor(b), 1e-5)

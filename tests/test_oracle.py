@@ -237,6 +237,40 @@ def test_dense_and_sparse_algorithms_agree(masked, mass_aware, top_k, re_norm):
     assert oracle.rel_err(s, ss) <= 1e-5 and oracle.rel_err(m, ms) <= 1e-5
 
 
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("mass_aware", [False, True])
+@pytest.mark.parametrize("gamma_scale", [0.5, 6.0])
+def test_sparse_backward_matches_dense_autograd(masked, mass_aware, gamma_scale):
+    """The state-reconstruction backward against fp64 torch autograd through
+    the dense restatement on the same events. Some weights are zeroed: such
+    events do not act and their gradient is 0 by contract (autograd's value
+    there is masked out before comparing)."""
+    case = make_case(2, 3, 2, 4, 31, 5, seed=23, masked=masked, gamma_scale=gamma_scale)
+    Kw, Kr = 3, 4
+    wi, wv = oracle.dense_topk_addr(case.w_addr, 1, case.position_ids, Kw, 0.5, dtype=torch.float64)
+    ri, rv = oracle.dense_topk_addr(case.r_addr, 1, case.position_ids, Kr, 0.0, dtype=torch.float64)
+    wv, rv = wv.clone(), rv.clone()
+    wv[..., ::7] = 0.0
+    rv[:, :, 1, ::5] = 0.0
+    gen = torch.Generator().manual_seed(5)
+    Dy = torch.randn(case.values.shape, generator=gen, dtype=torch.float64)
+    Ds = torch.randn(case.init_slot.shape, generator=gen, dtype=torch.float64)
+    Dm = torch.randn(case.init_mass.shape, generator=gen, dtype=torch.float64)
+    got = oracle.sparse_gsu_backward_f64(wi, wv, ri, rv, case.values, case.gamma, case.init_slot, case.init_mass, Dy,
+                                         Ds, Dm, case.mask, mass_aware, 1e-12)
+    wl = wv.double().requires_grad_(True)
+    rl = rv.double().requires_grad_(True)
+    leaves = [t.double().requires_grad_(True) for t in (case.values, case.gamma, case.init_slot, case.init_mass)]
+    y, s, m = oracle.dense_ram_attn(case.w_addr.double(), case.r_addr.double(), *leaves, case.mask, 0, None,
+                                    (Kw, Kr), (0.0, 0.0), mass_aware, 1e-12, decoded=(wi, wl, ri, -rl))
+    keep = torch.ones(2, 31, dtype=torch.float64) if case.mask is None else case.mask.double()
+    ((y * Dy * keep[:, None, :, None]).sum() + (s * Ds).sum() + (m * Dm).sum()).backward()
+    ref = [wl.grad.masked_fill(wv == 0, 0), rl.grad.masked_fill(rv == 0, 0)] + [t.grad for t in leaves]
+    for name, a, b in zip(("w", "r", "x", "gamma", "slot", "mass"), got, ref):
+        assert b.abs().max() > 0, f"{name}: the reference gradient is zero, so the comparison would be vacuous"
+        assert oracle.rel_err(torch.as_tensor(a), b) <= 1e-9, name
+
+
 def test_dense_oracle_is_chunk_invariant():
     case = make_case(1, 2, 2, 4, 40, 4, seed=3, masked=True)
     args = (case.w_addr, case.r_addr, case.values, case.gamma, case.init_slot, case.init_mass, case.mask, 1,
