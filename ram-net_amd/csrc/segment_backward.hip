@@ -76,25 +76,27 @@ constexpr int64_t bwd_stage_bytes(int epp, int np, int vec) {
 // Lane layout of the slice kernel: EPP events per pass (NP passes), LPE =
 // 64 / EPP lanes per event, VEC channels per lane, CSW = LPE * VEC channels
 // per wave. VEC grows until at most 16 slices cover C (bounding the partial
-// sums), and shrinks again if the slice does not fit in LDS.
+// sums), and shrinks again if the slice does not fit in LDS; wide slot spaces
+// then take more event lanes per pass (fewer channels per wave).
 bool bwd_plan(int A, int C, int Kw, int Kr, BwdPlan *p) {
     const int kmax = std::max(Kw, Kr);
-    if (kmax > 2 * kWave || A <= 0 || C <= 0)
-        return false;
-    const int epp = std::min(kWave, std::max(8, pow2_at_least(kmax)));
-    const int np = (kmax + epp - 1) / epp;
-    const int lpe = kWave / epp;
-    int vec = 1;
-    while (vec < 4 && static_cast<int64_t>(lpe) * vec * kBwdMaxSlices < C)
-        vec *= 2;
-    auto total = [&](int v) { return static_cast<int64_t>(A + 2) * lpe * v * 4 + bwd_stage_bytes(epp, np, v); };
-    while (vec > 1 && total(vec) > kBwdLdsLimit)
-        vec /= 2;
-    if (total(vec) > kBwdLdsLimit)
-        return false;
-    const int64_t lds = static_cast<int64_t>(A + 2) * lpe * vec * 4;
-    *p = {epp, np, vec, lpe * vec, (C + lpe * vec - 1) / (lpe * vec), lds};
-    return true;
+    if (kmax > 2 * kWave || A <= 0 || C <= 0 || static_cast<int64_t>(A + 2) * 8 > kBwdLdsLimit)
+        return false;  // (the mass chain keeps an (a, b) map per slot in LDS)
+    for (int epp = std::min(kWave, std::max(8, pow2_at_least(kmax))); epp <= kWave; epp *= 2) {
+        const int np = (kmax + epp - 1) / epp;
+        const int lpe = kWave / epp;
+        auto total = [&](int v) { return static_cast<int64_t>(A + 2) * lpe * v * 4 + bwd_stage_bytes(epp, np, v); };
+        int vec = 1;
+        while (vec < 4 && static_cast<int64_t>(lpe) * vec * kBwdMaxSlices < C)
+            vec *= 2;
+        while (vec > 1 && total(vec) > kBwdLdsLimit)
+            vec /= 2;
+        if (total(vec) > kBwdLdsLimit)
+            continue;
+        *p = {epp, np, vec, lpe * vec, (C + lpe * vec - 1) / (lpe * vec), static_cast<int64_t>(A + 2) * lpe * vec * 4};
+        return true;
+    }
+    return false;
 }
 
 // Sum over the lanes whose indices differ only in bits LO .. HI/2 (powers of
@@ -843,8 +845,7 @@ hipError_t launch_segment_backward(const SegmentBwdJob &job, hipStream_t stream,
         return hipSuccess;
     BwdPlan p{};
     if (!bwd_plan(fj.A, fj.C, fj.Kw, fj.Kr, &p)) {
-        *why = "segment backward: shape outside the LDS-resident scan (top_k <= 128 and (A + 2) * 4 * slice "
-               "channels <= 160 KiB)";
+        *why = "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A <= 20478)";
         return hipErrorInvalidValue;
     }
     if (fj.T == 0) {

@@ -31,6 +31,7 @@ CASES = [
     (2, 2, 2, 16, 40, 64, 8, 8, BF16, True, False),
     (1, 2, 2, 16, 40, 64, 8, 8, F16, False, True),
     (1, 2, 2, 32, 24, 300, 16, 16, F32, False, False),  # C > 16 slices of 4: wider lanes
+    (1, 2, 2, 90, 20, 12, 8, 8, F32, True, True),     # A = 8100: 8-channel slices do not fit, 16 event lanes
 ]
 
 
