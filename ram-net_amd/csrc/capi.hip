@@ -472,7 +472,7 @@ int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val,
     if (B == 0)
         return RAMNET_OK;
     const int64_t need = backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k);
-    RAMNET_REQUIRE(need >= 0, "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A <= 20478)");
+    RAMNET_REQUIRE(need >= 0, "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A <= 13652)");
     RAMNET_REQUIRE(workspace_bytes >= need && workspace,
                    "workspace too small: see ramnet_segment_backward_workspace_bytes");
     RAMNET_REQUIRE(T == 0 || (addr_idx && addr_val && grad_y && grad_addr_val && grad_gamma), "null tensor pointer");

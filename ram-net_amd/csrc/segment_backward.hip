@@ -80,8 +80,9 @@ constexpr int64_t bwd_stage_bytes(int epp, int np, int vec) {
 // then take more event lanes per pass (fewer channels per wave).
 bool bwd_plan(int A, int C, int Kw, int Kr, BwdPlan *p) {
     const int kmax = std::max(Kw, Kr);
-    if (kmax > 2 * kWave || A <= 0 || C <= 0 || static_cast<int64_t>(A + 2) * 8 > kBwdLdsLimit)
-        return false;  // (the mass chain keeps an (a, b) map per slot in LDS)
+    // the mass replay keeps a mass and a read tag and weight per slot in LDS
+    if (kmax > 2 * kWave || A <= 0 || C <= 0 || static_cast<int64_t>(A) * 12 + 8 > kBwdLdsLimit)
+        return false;
     for (int epp = std::min(kWave, std::max(8, pow2_at_least(kmax))); epp <= kWave; epp *= 2) {
         const int np = (kmax + epp - 1) / epp;
         const int lpe = kWave / epp;
@@ -845,7 +846,7 @@ hipError_t launch_segment_backward(const SegmentBwdJob &job, hipStream_t stream,
         return hipSuccess;
     BwdPlan p{};
     if (!bwd_plan(fj.A, fj.C, fj.Kw, fj.Kr, &p)) {
-        *why = "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A <= 20478)";
+        *why = "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A <= 13652)";
         return hipErrorInvalidValue;
     }
     if (fj.T == 0) {

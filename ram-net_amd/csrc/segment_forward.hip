@@ -318,6 +318,13 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     }
     if (lane < 2)
         lds[lane] = 1.f;
+    // AUX: per slot, the token whose read last posted there and its weight
+    int *rtag = reinterpret_cast<int *>(lds + A + 2);
+    float *rval = lds + 2 * A + 2;
+    if constexpr (AUX) {
+        for (int a = lane; a < A; a += kWave)
+            rtag[a] = -1;
+    }
     __syncthreads();
 
     const L ln(lane, Kw, Kr);
@@ -379,20 +386,21 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 }
                 if constexpr (AUX) {
                     // each write's record carries the effective weight of the read of
-                    // the same slot in this token (0 if none)
+                    // the same slot in this token (0 if none): the reads post
+                    // (token, weight) under their slots, then the writes look up theirs
+#pragma unroll
+                    for (int p = 0; p < MP; ++p) {
+                        if (!wlane && rb[p] >= 0) {
+                            rtag[rb[p]] = t;
+                            rval[rb[p]] = re[p];
+                        }
+                    }
                     float rmatch[MP];
 #pragma unroll
-                    for (int p = 0; p < MP; ++p)
-                        rmatch[p] = 0.f;
-#pragma unroll
-                    for (int p2 = 0; p2 < MP; ++p2) {
-                        for (int jj = 0; jj < 32 && p2 * 32 + jj < Kr; ++jj) {
-                            const int sl = __builtin_amdgcn_readlane(rb[p2], 32 + jj);
-                            const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(re[p2]), 32 + jj));
-#pragma unroll
-                            for (int p = 0; p < MP; ++p)
-                                rmatch[p] = (a[p] >= 0 && a[p] == sl) ? rv : rmatch[p];
-                        }
+                    for (int p = 0; p < MP; ++p) {
+                        const int sl = a[p] < 0 ? 0 : a[p];
+                        const bool hit = wlane && a[p] >= 0 && rtag[sl] == t;
+                        rmatch[p] = hit ? rval[sl] : 0.f;
                     }
 #pragma unroll
                     for (int p = 0; p < MP; ++p) {
@@ -459,6 +467,9 @@ int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chun
     return (job.T + *chunk_len - 1) / *chunk_len;
 }
 
+// LDS of the replay kernel: the masses (and with AUX the read tag table).
+size_t mass_lds_bytes(int A, bool aux) { return static_cast<size_t>(A + 2) * 4 + (aux ? static_cast<size_t>(A) * 8 : 0); }
+
 // `maps` is scratch for the chunk maps (maps_bytes of it); the final masses
 // go to job.mass_out.
 template<bool MA, int MP, bool AUX>
@@ -470,8 +481,8 @@ hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void 
     const int nck = mass_chunks(job, maps_bytes, n_cu, &len);
     const unsigned bh = static_cast<unsigned>(job.B * job.H);
     if (nck <= 1) {
-        hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, 1), dim3(kWave),
-                           static_cast<size_t>(job.A + 2) * 4, stream, job, w, r, t_pad, job.T, nullptr, aux);
+        hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, 1), dim3(kWave), mass_lds_bytes(job.A, AUX),
+                           stream, job, w, r, t_pad, job.T, nullptr, aux);
         return hipGetLastError();
     }
     auto *maps = static_cast<float2 *>(maps_buf);
@@ -480,8 +491,8 @@ hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void 
     const int64_t n = static_cast<int64_t>(bh) * job.A;
     hipLaunchKernelGGL(mass_chunk_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, job,
                        maps, nck);
-    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, nck), dim3(kWave),
-                       static_cast<size_t>(job.A + 2) * 4, stream, job, w, r, t_pad, len, maps, aux);
+    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, nck), dim3(kWave), mass_lds_bytes(job.A, AUX),
+                       stream, job, w, r, t_pad, len, maps, aux);
     return hipGetLastError();
 }
 
