@@ -597,6 +597,24 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
     for (int j = 0; j < CH; ++j)
         load_tok(max(t_end - 1 - j, t_begin), cur[j]);
     const int nc = (n + CH - 1) / CH;
+    // REPLAY: the chunk's gradients per lane (event) and of gamma, stored as
+    // runs of consecutive tokens once the chunk is done
+    float outv[CH][MP], outg[CH];
+    auto store_run = [&](float *row, int t_hi, const float *vals, int stride) {
+        const int t_lo = t_hi - (CH - 1);
+        if (t_lo >= t_begin && (t_lo & 3) == 0 && (T & 3) == 0) {
+#pragma unroll
+            for (int i = 0; i < CH; i += 4)
+                *reinterpret_cast<float4 *>(row + t_lo + i) =
+                    make_float4(vals[(CH - 1 - i) * stride], vals[(CH - 2 - i) * stride],
+                                vals[(CH - 3 - i) * stride], vals[(CH - 4 - i) * stride]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < CH; ++j)
+                if (t_hi - j >= t_begin)
+                    row[t_hi - j] = vals[j * stride];
+        }
+    };
     for (int ci = 0; ci < nc; ++ci) {
 #pragma unroll
         for (int j = 0; j < CH; ++j)
@@ -673,18 +691,22 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
                 }
             }
             if constexpr (REPLAY) {
-                dgam = xor_sum<1, 32>(dgam);
-                if (lane == 0)
-                    job.grad_gamma[static_cast<int64_t>(bh) * T + t] = dgam;
+                outg[j] = xor_sum<1, 32>(dgam);
 #pragma unroll
-                for (int p = 0; p < MP; ++p) {
-                    const int ev = p * 32 + hl;
-                    if (on[p])
-                        gval[static_cast<int64_t>(koff + ev) * T + t] = wlane ? dw[p] : dr[p];
-                }
+                for (int p = 0; p < MP; ++p)
+                    outv[j][p] = wlane ? dw[p] : dr[p];
             }
             if constexpr (MA)
                 __syncthreads();
+        }
+        if constexpr (REPLAY) {
+            const int t_hi = t_end - 1 - ci * CH;
+            if (lane == 0)
+                store_run(job.grad_gamma + static_cast<int64_t>(bh) * T, t_hi, outg, 1);
+#pragma unroll
+            for (int p = 0; p < MP; ++p)
+                if (on[p])
+                    store_run(gval + static_cast<int64_t>(koff + p * 32 + hl) * T, t_hi, &outv[0][p], MP);
         }
 #pragma unroll
         for (int j = 0; j < CH; ++j)
