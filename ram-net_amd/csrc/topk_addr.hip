@@ -283,10 +283,11 @@ hipError_t launch_typed(const AddrJob &job, hipStream_t stream, const char **why
 //     dL/dx_u[q] = sum_{k: d_u(k) = q} D_k - softmax(x_u)[q] (1 - r) sum_k D_k,
 // since the p_k sum to one. The selection itself carries no gradient, and an
 // inactive address (all weights 0) gets none. One lane per (b, h, t); the
-// logits of a digit are read in three passes (max, sum, gradient), coalesced
-// across the lanes' consecutive t. KM > 0 keeps the K terms in registers;
-// KM = 0 streams them for any K.
-template<typename Scalar, int KM>
+// logits of a digit are read coalesced across the lanes' consecutive t,
+// once into registers when P <= PR, else in three passes (max, sum,
+// gradient). KM > 0 keeps the K terms in registers; KM = 0 streams them for
+// any K.
+template<typename Scalar, int KM, int PR>
 __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJob job) {
     const int T = job.T, H = job.H, A = job.A, P = job.P, U = job.U, K = job.K;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -342,13 +343,30 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
     for (int u = 0; u < U; ++u, stride *= P) {
         const Scalar *xu = xp + static_cast<int64_t>(u) * P * T;
         Scalar *gu = gp + static_cast<int64_t>(u) * P * T;
+        float xr[PR > 0 ? PR : 1];  // the digit's logits, then their exponentials
         float mx = -__builtin_huge_valf();
-        for (int q = 0; q < P; ++q)
-            mx = fmaxf(mx, load_f32(xu + static_cast<int64_t>(q) * T));
+        if constexpr (PR > 0) {
+#pragma unroll
+            for (int q = 0; q < PR; ++q) {
+                xr[q] = load_f32(xu + static_cast<int64_t>(q < P ? q : P - 1) * T);
+                mx = q < P ? fmaxf(mx, xr[q]) : mx;
+            }
+        } else {
+            for (int q = 0; q < P; ++q)
+                mx = fmaxf(mx, load_f32(xu + static_cast<int64_t>(q) * T));
+        }
         const bool live = mx > -__builtin_huge_valf();
         float se = 0.f;
-        for (int q = 0; q < P; ++q)
-            se += live ? expf(load_f32(xu + static_cast<int64_t>(q) * T) - mx) : 0.f;
+        if constexpr (PR > 0) {
+#pragma unroll
+            for (int q = 0; q < PR; ++q) {
+                xr[q] = live && q < P ? expf(xr[q] - mx) : 0.f;
+                se += xr[q];
+            }
+        } else {
+            for (int q = 0; q < P; ++q)
+                se += live ? expf(load_f32(xu + static_cast<int64_t>(q) * T) - mx) : 0.f;
+        }
         const float scale = live ? dsoft / se : 0.f;
         int du[KM > 0 ? KM : 1];
         if constexpr (KM > 0) {
@@ -356,7 +374,7 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
             for (int k = 0; k < KM; ++k)
                 du[k] = c[k] < 0 ? -1 : (c[k] / stride) % P;
         }
-        for (int q = 0; q < P; ++q) {
+        auto grad_of = [&](int q) {
             float g = 0.f;
             if constexpr (KM > 0) {
 #pragma unroll
@@ -366,8 +384,18 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
                 for (int k = 0; k < K; ++k)
                     g += (content(k) / stride) % P == q ? dk(k) : 0.f;
             }
-            const float sm = live ? expf(load_f32(xu + static_cast<int64_t>(q) * T) - mx) : 0.f;
-            store_f32(gu + static_cast<int64_t>(q) * T, g - sm * scale);
+            return g;
+        };
+        if constexpr (PR > 0) {
+#pragma unroll
+            for (int q = 0; q < PR; ++q)
+                if (q < P)
+                    store_f32(gu + static_cast<int64_t>(q) * T, grad_of(q) - xr[q] * scale);
+        } else {
+            for (int q = 0; q < P; ++q) {
+                const float sm = live ? expf(load_f32(xu + static_cast<int64_t>(q) * T) - mx) : 0.f;
+                store_f32(gu + static_cast<int64_t>(q) * T, grad_of(q) - sm * scale);
+            }
         }
     }
 }
@@ -376,14 +404,23 @@ template<typename T>
 hipError_t launch_backward_typed(const AddrBwdJob &job, hipStream_t stream) {
     const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
     const dim3 grid(static_cast<unsigned>((n + 255) / 256)), blk(256);
+    const bool reg = job.P <= 32;  // a digit's logits fit in registers
+#define RAMNET_ADDR_BWD(KM)                                                                          \
+    do {                                                                                             \
+        if (reg)                                                                                     \
+            hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 32>), grid, blk, 0, stream, job);   \
+        else                                                                                         \
+            hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 0>), grid, blk, 0, stream, job);    \
+    } while (0)
     if (job.K <= 8)
-        hipLaunchKernelGGL((topk_addr_backward_kernel<T, 8>), grid, blk, 0, stream, job);
+        RAMNET_ADDR_BWD(8);
     else if (job.K <= 16)
-        hipLaunchKernelGGL((topk_addr_backward_kernel<T, 16>), grid, blk, 0, stream, job);
+        RAMNET_ADDR_BWD(16);
     else if (job.K <= 32)
-        hipLaunchKernelGGL((topk_addr_backward_kernel<T, 32>), grid, blk, 0, stream, job);
+        RAMNET_ADDR_BWD(32);
     else
-        hipLaunchKernelGGL((topk_addr_backward_kernel<T, 0>), grid, blk, 0, stream, job);
+        RAMNET_ADDR_BWD(0);
+#undef RAMNET_ADDR_BWD
     return hipGetLastError();
 }
 
