@@ -509,6 +509,11 @@ hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, int n_cu, void *ma
 
 }  // namespace
 
+// The backward's mass passes (the replay here and the chain in the segment
+// backward) cut time four times finer than the forward's pre-pass: their
+// per-token chains are longer, so more waves per SIMD pay for the extra maps.
+constexpr int kReplayChunkFactor = 4;
+
 int64_t mass_replay_scratch_bytes(int B, int H, int T, int A) {
     SegmentJob job{};
     job.B = B;
@@ -516,12 +521,12 @@ int64_t mass_replay_scratch_bytes(int B, int H, int T, int A) {
     job.T = T;
     job.A = A;
     int len = 0;
-    const int nck = mass_chunks(job, static_cast<size_t>(1) << 62, cu_count(), &len);
+    const int nck = mass_chunks(job, static_cast<size_t>(1) << 62, kReplayChunkFactor * cu_count(), &len);
     return nck <= 1 ? 0 : static_cast<int64_t>(B) * H * nck * A * static_cast<int64_t>(sizeof(float2));
 }
 
 int mass_replay_chunks(const SegmentJob &job, size_t maps_bytes, int *chunk_len) {
-    return mass_chunks(job, maps_bytes, cu_count(), chunk_len);
+    return mass_chunks(job, maps_bytes, kReplayChunkFactor * cu_count(), chunk_len);
 }
 
 hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *maps, size_t maps_bytes,
@@ -529,8 +534,9 @@ hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *m
     if (static_cast<int64_t>(job.B) * job.H * job.T == 0)
         return hipSuccess;
     const int t_pad = scan_t_pad(job.T);
-    return job.mass_aware ? launch_mass_pass<true, true>(job, t_pad, cu_count(), maps, maps_bytes, aux, stream)
-                          : launch_mass_pass<false, true>(job, t_pad, cu_count(), maps, maps_bytes, aux, stream);
+    const int n = kReplayChunkFactor * cu_count();
+    return job.mass_aware ? launch_mass_pass<true, true>(job, t_pad, n, maps, maps_bytes, aux, stream)
+                          : launch_mass_pass<false, true>(job, t_pad, n, maps, maps_bytes, aux, stream);
 }
 
 hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const char **why) {
