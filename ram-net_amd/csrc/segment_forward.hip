@@ -454,6 +454,10 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     }
 }
 
+// Time chunks of the mass passes: about four waves per SIMD (the per-token
+// chain is latency-bound, so more waves per SIMD pay for the extra maps).
+constexpr int kReplayChunkFactor = 4;
+
 // Chunks of the mass pre-pass: enough (b, h, chunk) waves to fill the GPU,
 // chunks a multiple of 16 tokens, and maps that fit the scratch buffer.
 int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chunk_len) {
@@ -508,11 +512,6 @@ hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, int n_cu, void *ma
 }
 
 }  // namespace
-
-// The backward's mass passes (the replay here and the chain in the segment
-// backward) cut time four times finer than the forward's pre-pass: their
-// per-token chains are longer, so more waves per SIMD pay for the extra maps.
-constexpr int kReplayChunkFactor = 4;
 
 int64_t mass_replay_scratch_bytes(int B, int H, int T, int A) {
     SegmentJob job{};
@@ -613,9 +612,10 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
         // the chunk maps use y as scratch: the scan overwrites it afterwards
         const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);
         const MassAux none{};
+        const int n = kReplayChunkFactor * cu_count();
         const hipError_t err =
-            job.mass_aware ? launch_mass_pass<true, false>(job, geo.t_pad, cu_count(), job.y, y_bytes, none, stream)
-                           : launch_mass_pass<false, false>(job, geo.t_pad, cu_count(), job.y, y_bytes, none, stream);
+            job.mass_aware ? launch_mass_pass<true, false>(job, geo.t_pad, n, job.y, y_bytes, none, stream)
+                           : launch_mass_pass<false, false>(job, geo.t_pad, n, job.y, y_bytes, none, stream);
         if (err != hipSuccess)
             return err;
     }
