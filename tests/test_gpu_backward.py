@@ -128,3 +128,49 @@ def test_topk_addr_autograd(dtype):
     oracle.check_topk_indices(idx.cpu(), addr, E, pos, K)
     _, rgrad = _reference(addr, E, pos, K, 0.25, True, D, idx=idx.cpu())
     assert oracle.rel_err(a.grad.float().cpu(), rgrad) <= _tol(dtype)
+
+
+@pytest.mark.parametrize("re_norm", [0.0, 0.5, 1.0])
+@pytest.mark.parametrize("neg", [False, True])
+def test_inactive_addresses_have_zero_weights_and_gradients(re_norm, neg):
+    """The reference's inactive-address test (test_address_numerics.py:58-71)
+    through the HIP decoder and its backward: token 0 has every logit -inf,
+    token 1 a whole digit of -inf; their weights and gradients are exactly 0
+    and everything is finite."""
+    from ramnet_ops import topk_addr
+    g = torch.Generator().manual_seed(58)
+    source = torch.randn(2, 2, 2, 3, 3, generator=g)
+    source[..., 0] = float("-inf")
+    source[:, :, 0, :, 1] = float("-inf")
+    positions = torch.arange(3).expand(2, -1)
+    addr = source.to(DEV).requires_grad_(True)
+    _, val = topk_addr(addr, 1, positions.to(DEV), 4, re_norm, neg)
+    up = torch.randn(val.shape, generator=g).to(DEV)
+    grad, = torch.autograd.grad(val, addr, up)
+    torch.cuda.synchronize()
+    assert bool((val[..., :2] == 0).all()) and bool((grad[..., :2] == 0).all())
+    assert bool(torch.isfinite(val).all()) and bool(torch.isfinite(grad).all())
+
+
+@pytest.mark.parametrize("top_k", [1, 4, 9])
+@pytest.mark.parametrize("re_norm", [0.0, 0.5, 1.0])
+def test_extreme_logit_gradients(golden, top_k, re_norm):
+    """The reference's extreme-logit test (test_address_numerics.py:83-102):
+    logits of magnitude ~1000 in float32; weights against the fixture and
+    gradients against fp64 autograd of the closed form, on the GPU's selection."""
+    from ramnet_ops import topk_addr
+    fx = golden("extreme_logits.json")
+    src = torch.tensor(fx["addr"], dtype=torch.float64).view(fx["shape"])  # (1, 1, 2, 3, 2)
+    positions = torch.arange(2).view(1, 2)
+    a = src.float().to(DEV).requires_grad_(True)
+    idx, val = topk_addr(a, 0, positions.to(DEV), top_k, re_norm)
+    up = torch.randn(val.shape, generator=torch.Generator().manual_seed(top_k)).double()
+    grad, = torch.autograd.grad(val, a, up.float().to(DEV))
+    torch.cuda.synchronize()
+    case = next(c for c in fx["cases"] if c["top_k"] == top_k and c["re_norm"] == re_norm)
+    dense = torch.zeros(2, fx["A"], dtype=torch.float64)  # (T, A)
+    dense.scatter_(1, idx.cpu()[0, 0].long().t(), val.detach().cpu()[0, 0].double().t())
+    assert oracle.rel_err(dense, torch.tensor(case["dense"])) <= 1e-5
+    _, rgrad = _reference(src, 0, positions, top_k, re_norm, True, up, idx=idx.cpu())
+    assert bool(torch.isfinite(grad).all())
+    assert oracle.rel_err(grad.cpu().double(), rgrad) <= 1e-5
