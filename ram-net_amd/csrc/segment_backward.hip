@@ -35,10 +35,12 @@
 //      then backward over t with Ds in LDS: Dx, the per-slice Dg and
 //      dL/d init_slot. The saved rows replace the reference's state roll-back
 //      by subtraction, so no slot value is ever reconstructed;
-//   3. segment_bwd_sum_kernel: per-slice dot products -> totals (in slice 0),
-//      in a fixed order, so the gradients are deterministic;
-//   4. segment_bwd_mass_kernel, per (b, h): backward over t with Dm in LDS:
-//      dL/dw, dL/drho, dL/dgamma and dL/d init_mass.
+//   3. segment_bwd_sum_kernel: per-slice dot products -> totals, summed in
+//      slice order, so the gradients are deterministic;
+//   4. segment_bwd_mass_kernel, per (b, h, time chunk): the Dm chain is
+//      affine in Dm, so it runs as chunk maps, a scan over chunks
+//      (segment_bwd_mass_scan_kernel) and chunk replays that write dL/dw,
+//      dL/drho and dL/dgamma; the scan gives dL/d init_mass.
 #include "ramnet_device.hpp"
 #include "ramnet_kernels.hpp"
 #include "ramnet_search.hpp"
