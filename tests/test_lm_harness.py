@@ -127,3 +127,49 @@ def test_harness_greedy_generate_bf16():
     assert ids.shape == (4, 8)
     assert bool(((ids >= 0) & (ids < cfg.vocab)).all())
     assert all(bool(torch.isfinite(s).all()) and bool(torch.isfinite(m).all()) for s, m in states)
+
+
+@pytest.mark.gpu
+def test_harness_training_step():
+    """A training step through the caller: the operator's differentiable path
+    inside the layers. Every parameter gradient is finite; the RAM layer's
+    address projections, scales, gamma and value projections get nonzero
+    gradients; and along the gradient of the last layer's value and gamma
+    projections (which move no top-K selection) a central difference of the
+    loss matches the directional derivative."""
+    import torch.nn.functional as F
+    cfg, model = _tiny()
+    model = model.to(DEV)
+    B, T = 2, 48
+    g = torch.Generator().manual_seed(3)
+    tokens = torch.randint(0, cfg.vocab, (B, T), generator=g).to(DEV)
+    pos = torch.arange(T - 1, device=DEV).view(1, T - 1).expand(B, T - 1)
+
+    def loss_fn():
+        logits, _ = model(tokens[:, :-1], model.fresh_state(B, DEV), pos, inplace=False)
+        return F.cross_entropy(logits.double().reshape(-1, cfg.vocab), tokens[:, 1:].reshape(-1))
+
+    loss = loss_fn()
+    loss.backward()
+    torch.cuda.synchronize()
+    for name, p in model.named_parameters():
+        assert p.grad is not None and bool(torch.isfinite(p.grad).all()), name
+    for blk in model.blocks:
+        ram = blk.ram
+        for p in (ram.w_addr.weight, ram.r_addr.weight, ram.w_scale, ram.r_scale, ram.gamma.weight,
+                  ram.value.weight):
+            assert p.grad.abs().max() > 0
+    last = model.blocks[-1].ram
+    for p in (last.value.weight, last.gamma.weight):
+        d = p.grad / p.grad.norm()
+        slope = float((p.grad * d).sum())
+        eps = 0.05
+        with torch.no_grad():
+            p += eps * d
+            lp = float(loss_fn())
+            p -= 2 * eps * d
+            lm = float(loss_fn())
+            p += eps * d
+        fd = (lp - lm) / (2 * eps)
+        print(f"  directional derivative {slope:.6e}, central difference {fd:.6e}", flush=True)
+        assert abs(fd - slope) <= 2e-2 * abs(slope)
