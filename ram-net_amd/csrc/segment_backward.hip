@@ -135,28 +135,6 @@ __device__ __forceinline__ void raw_load_vec(const float *p, uint32_t *out) {
     }
 }
 
-// Sum over the lanes whose indices differ from a lane's own only in bits
-// J .. 32 (J a power of two): exact xor exchanges by DPP within a row
-// (quad_perm, row_shl/shr:4, row_ror:8), then v_permlane16/32_swap, whose two
-// outputs hold the two halves being combined.
-template<int J>
-__device__ __forceinline__ float strided_sum(float v) {
-    if constexpr (J >= kWave) {
-        return v;
-    } else if constexpr (J < 8) {
-        return strided_sum<J * 2>(v + lane_xor_f<J>(v));
-    } else if constexpr (J == 8) {
-        return strided_sum<16>(v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, true)));
-    } else if constexpr (J == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        return strided_sum<32>(__uint_as_float(r[0]) + __uint_as_float(r[1]));
-    } else {
-        static_assert(J == 32, "strided_sum: J in {8, 16, 32}");
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-}
-
 template<typename Scalar, int EPP, int NP, int VEC>
 __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBwdJob job, int n_sub) {
     constexpr int LPE = kWave / EPP;               // lanes per event (consecutive: channel groups)

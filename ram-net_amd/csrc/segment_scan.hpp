@@ -4,7 +4,7 @@
 // whole sequence with the unit's A x CS slot slice resident in LDS; each
 // wave owns CSW channels of the slice and keeps its own copy of the slot
 // masses. The lane layout is fixed at compile time:
-//   EPP events per pass (lane % EPP), LPE = 64 / EPP lanes per event,
+//   EPP events per pass, LPE = 64 / EPP lanes per event,
 //   VEC channels per lane, CSW = LPE * VEC channels per wave,
 //   NP passes cover up to NP * EPP write and NP * EPP read events per token.
 // Per-event records ({slot, w, alpha} for writes, {slot, r} for reads; see
@@ -17,6 +17,7 @@
 
 #include "ramnet_device.hpp"
 #include "ramnet_kernels.hpp"
+#include "ramnet_search.hpp"
 
 #include <type_traits>
 
@@ -54,6 +55,28 @@ __device__ __forceinline__ float event_sum(float v) {
     if constexpr (EPP >= 32) v += __shfl_xor(v, 16);
     if constexpr (EPP >= 64) v += __shfl_xor(v, 32);
     return v;
+}
+
+// Sum over the lanes whose indices differ from a lane's own only in bits
+// J .. 32 (J a power of two): exact xor exchanges by DPP within a row
+// (quad_perm, row_shl/shr:4, row_ror:8), then v_permlane16/32_swap, whose two
+// outputs hold the two halves being combined.
+template<int J>
+__device__ __forceinline__ float strided_sum(float v) {
+    if constexpr (J >= kWave) {
+        return v;
+    } else if constexpr (J < 8) {
+        return strided_sum<J * 2>(v + lane_xor_f<J>(v));
+    } else if constexpr (J == 8) {
+        return strided_sum<16>(v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, true)));
+    } else if constexpr (J == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return strided_sum<32>(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+    } else {
+        static_assert(J == 32, "strided_sum: J in {8, 16, 32}");
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
 }
 
 // VEC consecutive floats with the widest LDS access their alignment allows.
@@ -464,8 +487,15 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     };
 
     // ---- state waves
-    const int ev = lane % EPP;                // event slot within a pass
-    const int cg = lane / EPP;                // channel group within the wave
+    // Lane order. With LPE >= 8 lanes per event, channel-fastest: an event's
+    // lanes read consecutive channels of its row, so an LDS pass meets fewer
+    // distinct (random) rows and fewer bank conflicts, and the event sum is
+    // a strided butterfly of three exchanges. With fewer lanes per event the
+    // strided butterfly costs more than the conflicts it saves, and events
+    // run fastest (event sum by DPP within a row).
+    constexpr bool CFL = LPE >= 8;
+    const int ev = CFL ? lane / LPE : lane % EPP;  // event slot within a pass
+    const int cg = CFL ? lane % LPE : lane / EPP;  // channel group within the wave
     const int cl = wave * CSW + cg * VEC;     // first channel of this lane within the slice
     const Scalar *gx = static_cast<const Scalar *>(job.x) + static_cast<int64_t>(bh) * T * C;
     Scalar *gy = static_cast<Scalar *>(job.y) + static_cast<int64_t>(bh) * T * C;
@@ -543,13 +573,24 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             const int v = (j % 4) == 0 ? q.x : (j % 4) == 1 ? q.y : (j % 4) == 2 ? q.z : q.w;
             return __builtin_amdgcn_readfirstlane(v);
         };
+        // Byte offsets (from st) of every event's row, computed once per chunk
+        // in 32 bits, off the token chain.
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                rec[p][j].x = (rec[p][j].x * RS + cl) * 4;
+                rec[p][j].z = (rec[p][j].z * RS + cl) * 4;
+            }
+        const char *stb = reinterpret_cast<const char *>(st);
+        auto row = [&](int off) { return reinterpret_cast<float *>(const_cast<char *>(stb) + off); };
         auto load_rows = [&](int j, FVec<VEC> (&s)[NP]) {
 #pragma unroll
             for (int p = 0; p < NP; ++p)
-                s[p] = lds_load<VEC>(st + rec[p][j].x * RS + cl);
+                s[p] = lds_load<VEC>(row(rec[p][j].x));
         };
-        // writes s <- s + g (x - s) of token j, then its reads
-        auto token = [&](int j, const FVec<VEC> (&s)[NP]) {
+        // writes s <- s + g (x - s) of token j, then the loads of its read rows
+        auto write_read = [&](int j, const FVec<VEC> (&s)[NP], FVec<VEC> (&rv)[NP]) {
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 const float g = __int_as_float(rec[p][j].y);
@@ -557,8 +598,14 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
                     o.v[v] = fmaf(g, x_at(v, j) - s[p].v[v], s[p].v[v]);
-                lds_store<VEC>(st + rec[p][j].x * RS + cl, o);
+                lds_store<VEC>(row(rec[p][j].x), o);
             }
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                rv[p] = lds_load<VEC>(row(rec[p][j].z));
+        };
+        // weighted read sum of token j, kept in the lanes that store its y
+        auto reduce = [&](int j, const FVec<VEC> (&rv)[NP]) {
             FVec<VEC> acc;
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
@@ -566,33 +613,45 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 const float wgt = __int_as_float(rec[p][j].w);
-                const FVec<VEC> rv = lds_load<VEC>(st + rec[p][j].z * RS + cl);
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
-                    acc.v[v] = fmaf(wgt, rv.v[v], acc.v[v]);
+                    acc.v[v] = fmaf(wgt, rv[p].v[v], acc.v[v]);
             }
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
-                acc.v[v] = event_sum<EPP>(acc.v[v]);
-            // keep the sum in the lanes that store token j
+                acc.v[v] = CFL ? strided_sum<LPE>(acc.v[v]) : event_sum<EPP>(acc.v[v]);
             const bool mine = EPP <= CH ? ev == j % EPP : ev % CH == j;
             const int q = EPP <= CH ? j / EPP : 0;
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
                 ykeep[q].v[v] = mine ? acc.v[v] : ykeep[q].v[v];
         };
-        // Token pairs: the second token's rows are read before the first
-        // token's writes, and read again if the write sets may overlap.
+        // Token pairs: the second token's rows are loaded before the first
+        // token's writes, and loaded again if the write sets may overlap.
+        // The read sums of a pair are reduced after the next pair's row
+        // loads are issued, so the only LDS round trip on the token chain is
+        // the row load. The reload path drains LDS itself (a rare branch);
+        // otherwise the wait merged at its join would also cover the first
+        // token's read rows.
+        FVec<VEC> rp0[NP], rp1[NP];
 #pragma unroll
         for (int j0 = 0; j0 < CH; j0 += 2) {
             FVec<VEC> s0[NP], s1[NP];
             load_rows(j0, s0);
             load_rows(j0 + 1, s1);
-            token(j0, s0);
-            if (flag(j0 + 1))
+            if (j0 > 0) {
+                reduce(j0 - 2, rp0);
+                reduce(j0 - 1, rp1);
+            }
+            write_read(j0, s0, rp0);
+            if (flag(j0 + 1)) {
                 load_rows(j0 + 1, s1);
-            token(j0 + 1, s1);
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            }
+            write_read(j0 + 1, s1, rp1);
         }
+        reduce(CH - 2, rp0);
+        reduce(CH - 1, rp1);
         // y of this chunk: lane stores tokens q * EPP + ev (or ev % 16)
 #pragma unroll
         for (int q = 0; q < NSL; ++q) {
