@@ -288,3 +288,60 @@ def test_config4_full_size_backward_heads():
     mine = (gval[:, :, :K], gval[:, :, K:], sel(got[1]), sel(got[2]), sel(got[3]), sel(got[4]))
     for name, a, b in zip(names, mine, ref):
         _check(name, a, torch.as_tensor(b), 1e-5)
+
+
+@pytest.mark.parametrize("masked", [False, True], ids=["unmasked", "masked"])
+@pytest.mark.parametrize("re_norm", [(0.0, 0.0), (1.0, 1.0), (0.25, 0.75), (0.75, 0.25)])
+@pytest.mark.parametrize("mass_aware", [False, True], ids=["plain", "mass_aware"])
+def test_chunked_state_and_gradients_match_full(masked, re_norm, mass_aware):
+    """The reference's chunk contract with gradients
+    (test_ram_attention_behavior.py:55-75, ram_attention_helpers.py:114-190):
+    the sequence run in chunks of 22, 32 and 33 tokens, each chunk starting
+    from the previous chunk's post state, gives the full run's outputs and
+    the same gradients of all six inputs; with a mask, a whole chunk of
+    tokens carries the state without updates."""
+    from ramnet_ops.impl.cuda_impl import _cuda_ram_attn
+    g = torch.Generator().manual_seed(55)
+    B, H, U, P, C, T = 2, 4, 3, 4, 8, 65
+    A = P ** U
+
+    def rn(*s):
+        return torch.randn(*s, generator=g).to(DEV)
+
+    w, r, x, gamma = rn(B, H, U, P, T), rn(B, H, U, P, T), rn(B, H, T, C), 0.2 * rn(B, H, T)
+    slot0, mass0 = rn(B, H, A, C), (torch.rand(B, H, A, generator=g) + 0.1).to(DEV)
+    d_y, d_slot, d_mass = rn(B, H, T, C), rn(B, H, A, C), rn(B, H, A)
+    if masked:
+        mask = torch.ones(B, T, dtype=torch.bool, device=DEV)
+        mask[:, 22:44] = False
+        mask[0, ::5] = False
+        mask[1, 1::7] = False
+        pos = (mask.long().cumsum(-1) - 1).masked_fill(~mask, 0)
+        d_y = d_y * mask[:, None, :, None]
+    else:
+        mask = None
+        pos = torch.arange(T, device=DEV).view(1, T).expand(B, T)
+
+    def run(chunk):
+        inputs = [t.detach().clone().requires_grad_() for t in (w, r, x, gamma, slot0, mass0)]
+        wa, ra, xa, ga, slot, mass = inputs
+        ys = []
+        for s in range(0, T, chunk):
+            st = slice(s, s + chunk)
+            y, slot, mass = _cuda_ram_attn(wa[..., st], ra[..., st], xa[..., st, :], ga[..., st], slot, mass,
+                                           None if mask is None else mask[:, st], 1, pos[:, st], (4, 8), re_norm,
+                                           mass_aware, 1e-12, False)
+            ys.append(y)
+        outs = (torch.cat(ys, dim=-2), slot, mass)
+        grads = torch.autograd.grad(outs, inputs, (d_y, d_slot, d_mass))
+        return outs, grads
+
+    (y_full, s_full, m_full), g_full = run(T)
+    for chunk in (22, 32, 33):
+        (y, s, m), gr = run(chunk)
+        keep = torch.ones(B, T, dtype=torch.bool, device=DEV) if mask is None else mask
+        torch.testing.assert_close(y * keep[:, None, :, None], y_full * keep[:, None, :, None], atol=1e-4, rtol=1e-4)
+        torch.testing.assert_close(s, s_full, atol=1e-4, rtol=1e-4)
+        torch.testing.assert_close(m, m_full, atol=1e-4, rtol=1e-4)
+        for a, b in zip(gr, g_full):
+            torch.testing.assert_close(a, b, atol=1e-4, rtol=1e-4)
