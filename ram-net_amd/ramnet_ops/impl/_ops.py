@@ -33,6 +33,14 @@ def _require_gpu(name: str, *tensors: Tensor) -> None:
             raise RuntimeError(f"{name}: tensors must be on a GPU (HIP) device, got {t.device}")
 
 
+def _require_given(name: str, **tensors: Tensor) -> None:
+    """Required tensor arguments (the dispatcher passes None through to a
+    Python operator); the reference's native checks raise RuntimeError."""
+    for arg, t in tensors.items():
+        if not isinstance(t, Tensor):
+            raise RuntimeError(f"{name}: {arg} must be a tensor, got {type(t).__name__}")
+
+
 # --------------------------------------------------------------------------
 # address decoder
 
@@ -95,6 +103,7 @@ def _(w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re_norm, r
 def topk_addr_single_backward(idx: Tensor, val: Tensor, addr: Tensor, D_val: Tensor, embed_num: int,
                               position_ids: Tensor, top_k: int, top_k_re_norm: float, addr_val_neg: bool,
                               shape: list[int], dtype: torch.dtype) -> Tensor:
+    _require_given("topk_addr_single_backward", idx=idx, val=val, addr=addr, D_val=D_val, position_ids=position_ids)
     _require_gpu("topk_addr_single_backward", idx, val, addr, D_val, position_ids)
     B, H, U, P, A, T = shape
     addr = addr.to(dtype).contiguous()
@@ -119,6 +128,8 @@ def _(idx, val, addr, D_val, embed_num, position_ids, top_k, top_k_re_norm, addr
 def topk_addr_backward(idx: Tensor, val: Tensor, w_addr: Tensor, r_addr: Tensor, D_val: Tensor, embed_num: int,
                        position_ids: Tensor, w_top_k: int, r_top_k: int, w_re_norm: float, r_re_norm: float,
                        shape: list[int], dtype: torch.dtype) -> tuple[Tensor, Tensor]:
+    _require_given("topk_addr_backward", idx=idx, val=val, w_addr=w_addr, r_addr=r_addr, D_val=D_val,
+                   position_ids=position_ids)
     _require_gpu("topk_addr_backward", idx, val, w_addr, r_addr, D_val, position_ids)
     B, H, U, P, A, T = shape
     w_addr, r_addr = w_addr.to(dtype).contiguous(), r_addr.to(dtype).contiguous()
@@ -246,6 +257,8 @@ def topk_segment_backward(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: 
     gradients with respect to the positive read weights, the contract
     ``topk_addr_backward`` expects; events that do not act get 0.
     """
+    _require_given("topk_segment_backward", addr_idx=addr_idx, addr_val=addr_val, x=x, gamma=gamma,
+                   init_slot=init_slot, init_mass=init_mass, D_y=D_y)
     _require_gpu("topk_segment_backward", addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, D_y,
                  D_post_slot, D_post_mass)
     B, H, T, C = x.shape
