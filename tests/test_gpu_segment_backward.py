@@ -290,58 +290,81 @@ def test_config4_full_size_backward_heads():
         _check(name, a, torch.as_tensor(b), 1e-5)
 
 
-@pytest.mark.parametrize("masked", [False, True], ids=["unmasked", "masked"])
-@pytest.mark.parametrize("re_norm", [(0.0, 0.0), (1.0, 1.0), (0.25, 0.75), (0.75, 0.25)])
-@pytest.mark.parametrize("mass_aware", [False, True], ids=["plain", "mass_aware"])
-def test_chunked_state_and_gradients_match_full(masked, re_norm, mass_aware):
-    """The reference's chunk contract with gradients
-    (test_ram_attention_behavior.py:55-75, ram_attention_helpers.py:114-190):
-    the sequence run in chunks of 22, 32 and 33 tokens, each chunk starting
-    from the previous chunk's post state, gives the full run's outputs and
-    the same gradients of all six inputs; with a mask, a whole chunk of
-    tokens carries the state without updates."""
-    from ramnet_ops.impl.cuda_impl import _cuda_ram_attn
-    g = torch.Generator().manual_seed(55)
-    B, H, U, P, C, T = 2, 4, 3, 4, 8, 65
+RE_NORMS = [(0.0, 0.0), (1.0, 1.0), (0.25, 0.75), (0.75, 0.25)]
+
+
+def _chunk_case(B, H, U, P, C, T, seed, masked):
+    g = torch.Generator().manual_seed(seed)
     A = P ** U
 
     def rn(*s):
         return torch.randn(*s, generator=g).to(DEV)
 
-    w, r, x, gamma = rn(B, H, U, P, T), rn(B, H, U, P, T), rn(B, H, T, C), 0.2 * rn(B, H, T)
-    slot0, mass0 = rn(B, H, A, C), (torch.rand(B, H, A, generator=g) + 0.1).to(DEV)
-    d_y, d_slot, d_mass = rn(B, H, T, C), rn(B, H, A, C), rn(B, H, A)
+    d = dict(w=rn(B, H, U, P, T), r=rn(B, H, U, P, T), x=rn(B, H, T, C), gamma=0.2 * rn(B, H, T),
+             slot=rn(B, H, A, C), mass=(torch.rand(B, H, A, generator=g) + 0.1).to(DEV),
+             d_y=rn(B, H, T, C), d_slot=rn(B, H, A, C), d_mass=rn(B, H, A), mask=None,
+             pos=torch.arange(T, device=DEV).view(1, T).expand(B, T))
     if masked:
         mask = torch.ones(B, T, dtype=torch.bool, device=DEV)
-        mask[:, 22:44] = False
+        mask[:, 22:44] = False  # a whole chunk carries the state without updates
         mask[0, ::5] = False
         mask[1, 1::7] = False
-        pos = (mask.long().cumsum(-1) - 1).masked_fill(~mask, 0)
-        d_y = d_y * mask[:, None, :, None]
-    else:
-        mask = None
-        pos = torch.arange(T, device=DEV).view(1, T).expand(B, T)
+        d.update(mask=mask, pos=(mask.long().cumsum(-1) - 1).masked_fill(~mask, 0),
+                 d_y=d["d_y"] * mask[:, None, :, None])
+    return d
 
-    def run(chunk):
-        inputs = [t.detach().clone().requires_grad_() for t in (w, r, x, gamma, slot0, mass0)]
-        wa, ra, xa, ga, slot, mass = inputs
-        ys = []
-        for s in range(0, T, chunk):
-            st = slice(s, s + chunk)
-            y, slot, mass = _cuda_ram_attn(wa[..., st], ra[..., st], xa[..., st, :], ga[..., st], slot, mass,
-                                           None if mask is None else mask[:, st], 1, pos[:, st], (4, 8), re_norm,
-                                           mass_aware, 1e-12, False)
-            ys.append(y)
-        outs = (torch.cat(ys, dim=-2), slot, mass)
-        grads = torch.autograd.grad(outs, inputs, (d_y, d_slot, d_mass))
-        return outs, grads
 
-    (y_full, s_full, m_full), g_full = run(T)
-    for chunk in (22, 32, 33):
-        (y, s, m), gr = run(chunk)
-        keep = torch.ones(B, T, dtype=torch.bool, device=DEV) if mask is None else mask
-        torch.testing.assert_close(y * keep[:, None, :, None], y_full * keep[:, None, :, None], atol=1e-4, rtol=1e-4)
-        torch.testing.assert_close(s, s_full, atol=1e-4, rtol=1e-4)
-        torch.testing.assert_close(m, m_full, atol=1e-4, rtol=1e-4)
-        for a, b in zip(gr, g_full):
-            torch.testing.assert_close(a, b, atol=1e-4, rtol=1e-4)
+def _chunked_run(d, chunk, top_k, re_norm, mass_aware):
+    """Outputs and the gradients of all six inputs with the sequence run in
+    chunks, each from the previous chunk's post state
+    (ram_attention_helpers.py:114-190)."""
+    from ramnet_ops.impl.cuda_impl import _cuda_ram_attn
+    T = d["x"].shape[2]
+    inputs = [d[k].detach().clone().requires_grad_() for k in ("w", "r", "x", "gamma", "slot", "mass")]
+    wa, ra, xa, ga, slot, mass = inputs
+    ys = []
+    for s in range(0, T, chunk):
+        st = slice(s, s + chunk)
+        y, slot, mass = _cuda_ram_attn(wa[..., st], ra[..., st], xa[..., st, :], ga[..., st], slot, mass,
+                                       None if d["mask"] is None else d["mask"][:, st], 1, d["pos"][:, st], top_k,
+                                       re_norm, mass_aware, 1e-12, False)
+        ys.append(y)
+    outs = (torch.cat(ys, dim=-2), slot, mass)
+    grads = torch.autograd.grad(outs, inputs, (d["d_y"], d["d_slot"], d["d_mass"]))
+    if d["mask"] is not None:
+        outs = (outs[0] * d["mask"][:, None, :, None], *outs[1:])
+    return outs, grads
+
+
+def _assert_chunked_matches_full(d, chunks, top_k, re_norm, mass_aware, tol=1e-4):
+    full, g_full = _chunked_run(d, d["x"].shape[2], top_k, re_norm, mass_aware)
+    for chunk in chunks:
+        outs, grads = _chunked_run(d, chunk, top_k, re_norm, mass_aware)
+        for a, b in zip((*outs, *grads), (*full, *g_full)):
+            torch.testing.assert_close(a, b, atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("masked", [False, True], ids=["unmasked", "masked"])
+@pytest.mark.parametrize("re_norm", RE_NORMS)
+@pytest.mark.parametrize("mass_aware", [False, True], ids=["plain", "mass_aware"])
+def test_chunked_state_and_gradients_match_full(masked, re_norm, mass_aware):
+    """The reference's chunk contract with gradients
+    (test_ram_attention_behavior.py:55-75): the sequence run in chunks of 22,
+    32 and 33 tokens gives the full run's outputs (y on valid tokens) and the
+    same gradients of all six inputs; with a mask, a whole chunk of tokens
+    carries the state without updates."""
+    d = _chunk_case(2, 4, 3, 4, 8, 65, seed=55, masked=masked)
+    _assert_chunked_matches_full(d, (22, 32, 33), (4, 8), re_norm, mass_aware)
+
+
+@pytest.mark.parametrize("top_k", [(4, 4), (8, 8), (4, 12), (16, 16), (32, 32), (64, 64), (128, 128)],
+                         ids=lambda k: "k{}x{}".format(*k))
+@pytest.mark.parametrize("re_norm", RE_NORMS)
+def test_top_k_range_and_long_sequence(top_k, re_norm):
+    """The reference's top-K range on a long sequence
+    (test_ram_attention_behavior.py:77-88, ram_attention_helpers.py:14-15):
+    A = 4^5 = 1024 slots, 16 channels, T = 1024 in chunks of 128 against the
+    full run, outputs and gradients, for every top-K and re-norm setting."""
+    print(f"long sequence top_k={top_k} re_norm={re_norm}", flush=True)
+    d = _chunk_case(2, 4, 5, 4, 16, 1024, seed=77, masked=False)
+    _assert_chunked_matches_full(d, (128,), top_k, re_norm, False)
