@@ -244,7 +244,9 @@ inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem, 
     const int cs = nw * (kWave / epp) * vec;
     const int ch = scan_chunk_len(epp * np);
     const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs), pre);
-    const size_t rec = (pre ? 0 : sizeof(StageRec)) + sizeof(WriteRec) + sizeof(ReadRec);
+    // PRE stages one compact StageRec per event; the mass-wave form stages
+    // the raw records for the mass wave and the StageRec it produces.
+    const size_t rec = pre ? sizeof(StageRec) : sizeof(StageRec) + sizeof(WriteRec) + sizeof(ReadRec);
     const size_t stage = static_cast<size_t>(ch) * epp * np * rec + static_cast<size_t>(cs) * (ch * elem + 16) +
                          ch * sizeof(int);
     return state + 2 * stage;
@@ -283,8 +285,9 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     constexpr int XI = (CS * CH + NST - 1) / NST;  // staged x elements per state thread
     constexpr int NSL = EPP <= CH ? CH / EPP : 1;  // tokens whose y a lane stores
     constexpr int kStageRecBytes = PRE ? 0 : static_cast<int>(sizeof(StageRec));
-    constexpr int kStageBytes =
-        CH * E * (kStageRecBytes + static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec))) + CS * XRB + CH * 4;
+    constexpr int kRawBytes = PRE ? static_cast<int>(sizeof(StageRec))
+                                  : static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec));
+    constexpr int kStageBytes = CH * E * (kStageRecBytes + kRawBytes) + CS * XRB + CH * 4;
     constexpr int RI = (E * CH + NST - 1) / NST;  // raw records per state thread
     using Bits = std::conditional_t<ES == 4, uint32_t, uint16_t>;
 
@@ -313,6 +316,8 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     auto stage_f = [&](int buf) { return reinterpret_cast<int *>(stage_x(buf) + CS * XRB); };
     auto raw_w = [&](int buf) { return reinterpret_cast<WriteRec *>(stage_f(buf) + CH); };
     auto raw_r = [&](int buf) { return reinterpret_cast<ReadRec *>(raw_w(buf) + CH * E); };
+    // PRE: the compact records {write slot, gain, read slot, read weight}
+    auto pre_rec = [&](int buf) { return reinterpret_cast<int4 *>(stage_f(buf) + CH); };
 
     // ---- state slice and masses -> LDS
     {
@@ -356,8 +361,10 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             rg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
         }
     };
-    // PRE: events past top-K become no-ops here (the state waves read the
-    // records directly), and event 0 carries the token's overlap flag.
+    // PRE: the thread holding an event's write and read records stages
+    // them as one compact record (one 16-byte LDS read per event and token
+    // for the state waves); events past top-K become no-ops here, and event
+    // 0 carries the token's overlap flag.
     auto raw_deposit = [&](int buf, const RawRegs &rg) {
         WriteRec *rw = raw_w(buf);
         ReadRec *rr = raw_r(buf);
@@ -365,16 +372,17 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
         for (int k = 0; k < RI; ++k) {
             const int it = min(tid + k * NST, E * CH - 1);
             const int e = it / CH, j = it % CH;
-            int4 w = rg.w[k];
-            int2 r = rg.r[k];
+            const int4 w = rg.w[k];
+            const int2 r = rg.r[k];
             if constexpr (PRE) {
-                w = e < Kw ? w : make_int4(-2, 0, 0, w.w);
-                r = e < Kr ? r : make_int2(-1, 0);
                 if (e == 0)
                     stage_f(buf)[j] = w.w;
+                pre_rec(buf)[j * E + e] = make_int4(e < Kw ? w.x : -2, e < Kw ? w.z : 0, e < Kr ? r.x : -1,
+                                                    e < Kr ? r.y : 0);
+            } else {
+                *reinterpret_cast<int4 *>(rw + j * E + e) = w;
+                *reinterpret_cast<int2 *>(rr + j * E + e) = r;
             }
-            *reinterpret_cast<int4 *>(rw + j * E + e) = w;
-            *reinterpret_cast<int2 *>(rr + j * E + e) = r;
         }
     };
     struct Raw {
@@ -533,9 +541,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 if constexpr (PRE) {
-                    const int4 w4 = *reinterpret_cast<const int4 *>(raw_w(buf) + j * E + p * EPP + ev);
-                    const int2 r2 = *reinterpret_cast<const int2 *>(raw_r(buf) + j * E + p * EPP + ev);
-                    rec[p][j] = make_int4(w4.x, w4.z, r2.x, r2.y);
+                    rec[p][j] = pre_rec(buf)[j * E + p * EPP + ev];
                 } else {
                     rec[p][j] = *reinterpret_cast<const int4 *>(se + j * E + p * EPP + ev);
                 }
