@@ -38,9 +38,6 @@ __device__ __forceinline__ float gsu_gain(float w, float d) {
     return w * r;
 }
 
-// Buffer resource word 3 for untyped 32-bit accesses on gfx9 parts.
-constexpr int kBufWord3 = 0x00020000;
-
 // 32-bit buffer accesses of fp32 data (the builtins move raw bits).
 __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));

@@ -193,23 +193,52 @@ __device__ __forceinline__ uint64_t prefix_key(float s, int c) {
 
 // One digit: sorted top-KM log-probabilities (lv) and digit values (dv),
 // valid flags; returns false when every logit of the digit is -inf.
-template<typename Scalar, int NP, int KM>
-__device__ __forceinline__ bool digit_top(const Scalar *row, int64_t stride, int P, float (&lv)[KM], int (&dv)[KM],
-                                          bool (&ok)[KM]) {
+// Logit loaders: load(u, p) gives the raw bits of logit p of digit u.
+// GlobalLogits walks a per-lane pointer (any tensor size); BufferLogits
+// reads through one buffer resource based at the wave's first lane with
+// 32-bit per-lane offsets, which keeps the per-load addresses out of scalar
+// registers (the host picks it when every offset fits in 31 bits).
+template<typename Scalar>
+struct GlobalLogits {
+    const Scalar *base;  // logit 0 of digit 0 for this lane
+    int stride;          // elements between consecutive logits (T); U * P * T fits an int
+    int P;
+    __device__ __forceinline__ uint32_t operator()(int u, int p) const {
+        return raw_bits<Scalar>(base + (u * P + p) * stride);
+    }
+};
+template<typename Scalar>
+struct BufferLogits {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int lane_off;  // bytes from the resource base to this lane's logit 0 of digit 0
+    int step;      // bytes between consecutive logits (T * sizeof(Scalar))
+    int P;
+    __device__ __forceinline__ uint32_t operator()(int u, int p) const {
+        const int off = lane_off + (u * P + p) * step;
+        if constexpr (sizeof(Scalar) == 2)
+            return __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+        else
+            return __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0);
+    }
+};
+
+// Validity flags are kept as 0 / all-ones 32-bit masks in vector registers
+// (bool arrays would live as 64-bit lane masks in scalar registers and spill).
+// FULL: P == NP, so no logit is padding (the padding selects compile away).
+template<typename Scalar, int NP, int KM, bool FULL, typename Load>
+__device__ __forceinline__ bool digit_top(const Load &load, int u, int P_, float (&lv)[KM], int (&dv)[KM],
+                                          uint32_t (&ok)[KM]) {
     using K = DigitKey<Scalar>;
+    const int P = FULL ? NP : P_;
     K keys[NP];
     float x[NP];
-    // All loads first, unconditional: the pointer walks the P logits of the
-    // digit and stays on the last one for the padding. A guarded load or a
-    // branch on P would wait for each load's data before issuing the next.
-    const char *ptr = reinterpret_cast<const char *>(row);
-    const int64_t step = stride * static_cast<int64_t>(sizeof(Scalar));
+    // All loads first, unconditional: the padding repeats the digit's last
+    // logit. A guarded load or a branch on P would wait for each load's data
+    // before issuing the next.
     uint32_t bits[NP];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        bits[p] = raw_bits<Scalar>(reinterpret_cast<const Scalar *>(ptr));
-        ptr += p + 1 < P ? step : 0;
-    }
+    for (int p = 0; p < NP; ++p)
+        bits[p] = load(u, p < P ? p : P - 1);
     // padding keys are masked to 0 arithmetically (no branch)
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -241,7 +270,7 @@ __device__ __forceinline__ bool digit_top(const Scalar *row, int64_t stride, int
         float xv;
         int p;
         digit_unkey<Scalar>(top[k], xv, p);
-        ok[k] = top[k] != K(0);
+        ok[k] = top[k] != K(0) ? ~0u : 0u;
         lv[k] = (xv - mx) - ls;
         dv[k] = p;
     }
@@ -251,8 +280,9 @@ __device__ __forceinline__ bool digit_top(const Scalar *row, int64_t stride, int
 // Prefix (score sv, content cv) x digit (lv, dv) over the staircase ->
 // sorted top-KM new prefix. `stride` is P^u of the digit.
 template<int KM>
-__device__ __forceinline__ void combine_prefix(float (&sv)[KM], int (&cv)[KM], bool (&ok)[KM], const float (&lv)[KM],
-                                               const int (&dv)[KM], const bool (&dok)[KM], int stride) {
+__device__ __forceinline__ void combine_prefix(float (&sv)[KM], int (&cv)[KM], uint32_t (&ok)[KM],
+                                               const float (&lv)[KM], const int (&dv)[KM], const uint32_t (&dok)[KM],
+                                               int stride) {
     constexpr int NC = stair_count<KM>();
     constexpr int NG = (NC + KM - 1) / KM * KM;
     uint64_t cand[NG];
@@ -260,7 +290,8 @@ __device__ __forceinline__ void combine_prefix(float (&sv)[KM], int (&cv)[KM], b
     for (int n = 0; n < NG; ++n) {
         if (n < NC) {
             const int i = stair_i<KM>(n), j = stair_j<KM>(n);
-            cand[n] = (ok[i] && dok[j]) ? prefix_key(sv[i] + lv[j], cv[i] + stride * dv[j]) : uint64_t(0);
+            const uint64_t m = ok[i] & dok[j];
+            cand[n] = prefix_key(sv[i] + lv[j], cv[i] + stride * dv[j]) & ((m << 32) | m);
         } else {
             cand[n] = 0;
         }
@@ -269,7 +300,7 @@ __device__ __forceinline__ void combine_prefix(float (&sv)[KM], int (&cv)[KM], b
     top_keys<KM>(cand, top);
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
-        ok[k] = top[k] != 0;
+        ok[k] = top[k] != 0 ? ~0u : 0u;
         sv[k] = __uint_as_float(unord32(static_cast<uint32_t>(top[k] >> 32)));
         cv[k] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(top[k]));
     }
@@ -277,16 +308,17 @@ __device__ __forceinline__ void combine_prefix(float (&sv)[KM], int (&cv)[KM], b
 
 // Full search of one address: sorted top-KM (score, content index, valid)
 // over all U digits. Returns false if any digit is all -inf (inactive).
-template<typename Scalar, int NP, int KM>
-__device__ __forceinline__ bool lane_search(const Scalar *base, int64_t T, int U, int P, float (&sv)[KM],
-                                            int (&cv)[KM], bool (&ok)[KM]) {
-    bool live = digit_top<Scalar, NP, KM>(base, T, P, sv, cv, ok);
+template<typename Scalar, int NP, int KM, bool FULL, typename Load>
+__device__ __forceinline__ bool lane_search(const Load &load, int U, int P_, float (&sv)[KM], int (&cv)[KM],
+                                            uint32_t (&ok)[KM]) {
+    const int P = FULL ? NP : P_;
+    bool live = digit_top<Scalar, NP, KM, FULL>(load, 0, P, sv, cv, ok);
     int stride = P;
     for (int u = 1; u < U; ++u) {
         float lv[KM];
         int dv[KM];
-        bool dok[KM];
-        live = digit_top<Scalar, NP, KM>(base + static_cast<int64_t>(u) * P * T, T, P, lv, dv, dok) && live;
+        uint32_t dok[KM];
+        live = digit_top<Scalar, NP, KM, FULL>(load, u, P, lv, dv, dok) && live;
         combine_prefix<KM>(sv, cv, ok, lv, dv, dok, stride);
         stride *= P;
     }

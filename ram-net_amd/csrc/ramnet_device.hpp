@@ -9,6 +9,9 @@
 
 namespace ramnet {
 
+// Buffer resource word 3 for untyped 32-bit accesses on gfx9 parts.
+constexpr int kBufWord3 = 0x00020000;
+
 constexpr int kWave = 64;
 // Index value marking an invalid (padding) top-K entry. Real content
 // indices are < A < 2^30, so a padding entry never collides with one.

@@ -75,7 +75,10 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
     }
 }
 
-template<typename Scalar, int NP, int KM>
+// FAST: P == NP and the logits are read through a buffer resource with
+// 32-bit lane offsets (the host checks that every offset fits); otherwise
+// any P <= NP, through 64-bit pointers.
+template<typename Scalar, int NP, int KM, bool FAST>
 // At least three waves per SIMD: the per-lane search holds its digit in
 // registers (about 210 VGPRs unconstrained, two waves); capping it at 168
 // costs a few spills and lets a third wave hide the sort chains' latency
@@ -101,8 +104,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
 
     float mv[KM];  // sorted top-KM scores
     int mi[KM];    // their content indices
-    bool ok[KM];
-    const bool inactive = !lane_search<Scalar, NP, KM>(base, static_cast<int64_t>(T), U, P, mv, mi, ok);
+    uint32_t ok[KM];
+    bool found;
+    if constexpr (FAST) {
+        // resource based at the first active lane's logits: later lanes sit at
+        // equal or higher addresses (same or later (b, h, t)), within
+        // 2 * U * P * T elements of it
+        // (readfirstlane returns a signed int: widen each half through
+        // uint32_t, or a low half with bit 31 set would sign-extend over the
+        // high half)
+        const uint64_t mine = reinterpret_cast<uint64_t>(base);
+        const uint32_t first_hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(mine >> 32)));
+        const uint32_t first_lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(mine)));
+        const uint64_t first = (static_cast<uint64_t>(first_hi) << 32) | first_lo;
+        const uint64_t end = reinterpret_cast<uint64_t>(static_cast<const Scalar *>(src.addr) +
+                                                        static_cast<int64_t>(job.B) * H * U * P * T);
+        const uint64_t span = end - first;
+        const int records = span < 0x7fffffffull ? static_cast<int>(span) : 0x7fffffff;
+        const BufferLogits<Scalar> load{
+            __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(first), 0, records, kBufWord3),
+            static_cast<int>(mine - first), T * static_cast<int>(sizeof(Scalar)), P};
+        found = lane_search<Scalar, NP, KM, true>(load, U, P, mv, mi, ok);
+    } else {
+        const GlobalLogits<Scalar> load{base, T, P};
+        found = lane_search<Scalar, NP, KM, false>(load, U, P, mv, mi, ok);
+    }
+    const bool inactive = !found;
 
     const int K = src.top_k;
     float lse = 0.f;
@@ -227,7 +254,13 @@ template<typename T, int NP, int KM>
 hipError_t launch_lane(const AddrJob &job, hipStream_t stream) {
     const int64_t n = static_cast<int64_t>(job.B) * job.H * grid_t(job);
     const dim3 grid(static_cast<unsigned>((n + 255) / 256), job.n_src);
-    hipLaunchKernelGGL((topk_addr_lane_kernel<T, NP, KM>), grid, dim3(256), 0, stream, job);
+    // a wave spans at most two (b, h) rows: lane offsets stay below
+    // 2 * U * P * T elements from the wave's first lane
+    const int64_t span = 2 * static_cast<int64_t>(job.U) * job.P * job.T * static_cast<int64_t>(sizeof(T)) + 256;
+    if (span <= 0x7fffffff && job.P == NP)
+        hipLaunchKernelGGL((topk_addr_lane_kernel<T, NP, KM, true>), grid, dim3(256), 0, stream, job);
+    else
+        hipLaunchKernelGGL((topk_addr_lane_kernel<T, NP, KM, false>), grid, dim3(256), 0, stream, job);
     return hipGetLastError();
 }
 

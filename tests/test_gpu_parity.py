@@ -88,6 +88,32 @@ def test_decoder_matches_oracle(case, dtype):
     _check_decoder(addr, idx, val, E, pos, K, re_norm)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decoder_logit_address_high_bit(dtype):
+    """The lane decoder bases a buffer resource at each wave's first logit
+    address: logits whose address has bit 31 of its low word set, and clear,
+    give the same bits as a plain allocation (a signed widening of the low
+    word once turned such an address into a wild one)."""
+    ops = _ops()
+    B, H, U, P, T, K, E = 2, 4, 2, 16, 200, 8, 2
+    g = torch.Generator().manual_seed(31)
+    addr = torch.randn(B, H, U, P, T, generator=g).to(dtype).to(DEV)
+    pos = torch.randint(0, 1000, (B, T), generator=g).to(DEV)
+    ref = ops.topk_addr_single_forward(addr, E, P ** U, pos, K, 0.5, False, True)
+    nbytes = addr.numel() * addr.element_size()
+    pool = torch.empty((1 << 31) + (1 << 22), dtype=torch.uint8, device=DEV)
+    base = pool.data_ptr()
+    for bit in (True, False):
+        off = next(o for o in range(0, pool.numel() - nbytes, 1 << 20) if bool((base + o) & (1 << 31)) == bit)
+        print(f"logits at {base + off:#x} (bit 31 of the low word {'set' if bit else 'clear'})", flush=True)
+        view = pool[off:off + nbytes].view(dtype).view(B, H, U, P, T)
+        view.copy_(addr)
+        got = ops.topk_addr_single_forward(view, E, P ** U, pos, K, 0.5, False, True)
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])
+    del pool
+
+
 @pytest.mark.parametrize("neg,encode", [(False, False), (True, True), (True, False)])
 def test_decoder_sign_and_encoding(neg, encode):
     from ramnet_ops import topk_addr
