@@ -87,10 +87,11 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
     __shared__ float s_wv[KE];
     __shared__ float s_row[KE][kWave * kCpl];
 
-    const int bh = blockIdx.x;
+    // grid (B, H): the (b, h) pair without a division
+    const int b = blockIdx.x, h = blockIdx.y;
     const int lane = threadIdx.x;
     const int H = job.H, A = job.A, C = job.C, U = job.U, P = job.P, Kw = job.Kw, Kr = job.Kr;
-    const int b = bh / H, h = bh - (bh / H) * H;
+    const int bh = b * H + h;
     T *yrow = static_cast<T *>(job.y) + static_cast<int64_t>(bh) * C;
 
     // ---- every input of the step in one batch of loads
@@ -309,10 +310,11 @@ template<typename T>
 __global__ __launch_bounds__(64) void autoregressive_general_kernel(const DecodeJob job, int NA, int NPD) {
     extern __shared__ float smem[];
     __shared__ int s_flag;
-    const int bh = blockIdx.x;
+    // grid (B, H): the (b, h) pair without a division
+    const int b = blockIdx.x, h = blockIdx.y;
     const int lane = threadIdx.x;
     const int H = job.H, A = job.A, C = job.C, U = job.U, P = job.P, Kw = job.Kw, Kr = job.Kr;
-    const int b = bh / H, h = bh - (bh / H) * H;
+    const int bh = b * H + h;
     T *yrow = static_cast<T *>(job.y) + static_cast<int64_t>(bh) * C;
     if (job.mask && !job.mask[b]) {
         for (int c = lane; c < C; c += kWave)
@@ -401,12 +403,16 @@ hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **w
     const int stair = staircase_count(kmax);
     const bool fast_ok = job.P <= 64 && kmax <= kEv && job.C <= kWave * kMaxCpl && stair <= 64 &&
                          static_cast<int64_t>(job.A) * job.C * 4 <= INT32_MAX;
-    const unsigned grid = static_cast<unsigned>(job.B * job.H);
+    if (job.H > 65535) {
+        *why = "decode step: at most 65535 heads (grid y dimension)";
+        return hipErrorInvalidValue;
+    }
+    const dim3 grid(static_cast<unsigned>(job.B), static_cast<unsigned>(job.H));
     if (fast_ok) {
         const bool half = job.P <= 32 && stair <= 32;
         const bool narrow = job.C <= 2 * kWave;
         const bool few = kmax <= 8;
-        const dim3 g(grid), blk(kWave);
+        const dim3 g(grid), blk(kWave);  // one wave per (b, h)
 #define RAMNET_AR_LAUNCH(GW, KE, CPL)                                                                          \
     do {                                                                                                        \
         if (job.C == (CPL) * kWave)                                                                             \
@@ -431,7 +437,7 @@ hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **w
         *why = "decode step: shape needs P <= 64, top_k <= 16, C <= 256 and A*C*4 < 2^31, or P**U small enough for the exact LDS search (A <= 8192)";
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(autoregressive_general_kernel<T>, dim3(grid), dim3(kWave), lds, stream, job, NA, NPD);
+    hipLaunchKernelGGL(autoregressive_general_kernel<T>, grid, dim3(kWave), lds, stream, job, NA, NPD);
     return hipGetLastError();
 }
 
