@@ -152,9 +152,34 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
     const bool live = t < T && *mp != 0 && static_cast<unsigned>(a) < static_cast<unsigned>(A);
     if (k < job.Kw) {
         const bool act = live && v != 0.f;
-        // overlap with token t - 1 is not computed here: assumed (the scan
-        // then orders the two tokens' row accesses strictly)
-        const float overlap = __int_as_float(1);
+        // Event 0 carries the token's overlap flag, which the scan reads:
+        // whether a slot this token writes is also written by token t - 1.
+        // Computed exactly for top-K up to 16; assumed for wider top-K.
+        int ov = 1;
+        if (k == 0 && job.Kw <= 16) {
+            ov = 0;
+            if (t > 0 && t < T) {
+                // slot written by write event kk of token tt (tt < T), or -1
+                auto written = [&](int tt, int kk) {
+                    const int64_t s = (static_cast<int64_t>(bh) * Kt + kk) * T + tt;
+                    const int aa = job.addr_idx[s] - bh * A;
+                    const uint8_t *m = job.mask ? job.mask + static_cast<int64_t>(b) * T + tt : &kScanAllValid;
+                    return *m != 0 && static_cast<unsigned>(aa) < static_cast<unsigned>(A) && job.addr_val[s] != 0.f
+                               ? aa : -1;
+                };
+                int prev[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    prev[i] = i < job.Kw ? written(t - 1, i) : -1;
+                for (int i = 0; i < job.Kw; ++i) {
+                    const int x = written(t, i);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        ov |= x >= 0 && x == prev[j] ? 1 : 0;
+                }
+            }
+        }
+        const float overlap = __int_as_float(ov);
         WriteRec rec{-2, 0.f, 1.f, overlap};
         if (act)
             rec = WriteRec{a, v, gsu_alpha(v, g), overlap};
