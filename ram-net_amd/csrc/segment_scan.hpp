@@ -1,9 +1,11 @@
 // Time-ordered segment scan kernel (gated sparse update + top-K read).
 //
-// A workgroup of NW waves owns one (b, h, channel slice) unit and walks the
-// whole sequence with the unit's A x CS slot slice resident in LDS; each
-// wave owns CSW channels of the slice and keeps its own copy of the slot
-// masses. The lane layout is fixed at compile time:
+// A workgroup of NW state waves owns one (b, h, channel slice) unit and walks
+// the whole sequence with the unit's A x CS slot slice resident in LDS; each
+// state wave owns CSW channels of the slice. The slot masses are kept by one
+// extra mass wave, or, in the precomputed-gain form, replaced by the gains a
+// mass pre-pass wrote into the records. The lane layout is fixed at compile
+// time:
 //   EPP events per pass, LPE = 64 / EPP lanes per event,
 //   VEC channels per lane, CSW = LPE * VEC channels per wave,
 //   NP passes cover up to NP * EPP write and NP * EPP read events per token.
