@@ -79,11 +79,12 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
 // 32-bit lane offsets (the host checks that every offset fits); otherwise
 // any P <= NP, through 64-bit pointers.
 template<typename Scalar, int NP, int KM, bool FAST>
-// At least three waves per SIMD: the per-lane search holds its digit in
-// registers (about 210 VGPRs unconstrained, two waves); capping it at 168
-// costs a few spills and lets a third wave hide the sort chains' latency
-// (config 2 decoder: 0.19 -> 0.17 ms).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void topk_addr_lane_kernel(
+// Occupancy: the per-lane search holds its digit in registers (about 210
+// VGPRs unconstrained, two waves per SIMD). Capping it at 168 (three waves)
+// costs a few spills and hides more of the sort chains' latency; the FAST
+// form with K <= 8 fits 128 (four waves) with a few spills (config 2
+// decoder: 0.092 -> 0.088 ms).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FAST && KM <= 8 ? 4 : 3))) void topk_addr_lane_kernel(
     const AddrJob job) {
     const AddrSource &src = job.src[blockIdx.y];
     const int T = job.T, H = job.H, U = job.U, P = job.P, A = job.A;
