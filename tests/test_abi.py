@@ -184,3 +184,20 @@ def test_cuda_path_capacity_asserts():
         run(1, 1, 31, 2, 2, 4)
     with pytest.raises(AssertionError, match="CUDA index overflow"):
         run(64, 64, 2, 64, 4, 256)
+
+
+def test_scan_plan_envelope():
+    """The scan planner (``ramnet_segment_plan``, no device work) accepts every
+    shape up to A = 8190 slots and top-K 128 with an LDS footprint within the
+    160 KiB of a CU, and refuses wider slot spaces and top-K beyond 128."""
+    from ramnet_ops import _native as nat
+    for A in (4, 16, 256, 1024, 2401, 4096, 6561, 8100, 8190):
+        for C in (1, 7, 16, 100, 128, 512):
+            for K in (1, 8, 16, 64, 100, 128):
+                plan = nat.segment_plan(A, C, K, K)
+                assert plan is not None, (A, C, K)
+                cs, lds = plan
+                assert 1 <= cs and 0 < lds <= 160 * 1024, (A, C, K, cs, lds)
+    assert nat.segment_plan(1024, 128, 8, 129) is None
+    assert nat.segment_plan(8192, 128, 8, 8) is None
+    assert nat.segment_plan(1024, 128, 4, 12) is not None  # Kw != Kr
