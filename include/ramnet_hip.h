@@ -235,8 +235,8 @@ int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const vo
 
 /*
  * Planning query (no device work): channel-slice width and LDS bytes per
- * wave the segment scan uses for slot count A, C channels and top-k.
- * Returns 1 if the shape is supported, else 0.
+ * workgroup the segment scan uses for slot count A, C channels and top-k.
+ * Returns 1 if the shape is supported (A <= 8190, top-k <= 128), else 0.
  */
 int ramnet_segment_plan(int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int *slice_channels,
                         int *lds_bytes);
