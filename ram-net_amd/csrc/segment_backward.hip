@@ -295,15 +295,15 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
             // the token body is one basic block.
             auto tokens = [&](auto tail_tag) {
                 constexpr bool TL = decltype(tail_tag)::value;
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < CH; ++j) {
                     const int t = ci * CH + j;
                     if (TL && t >= T)
                         break;
-    #pragma unroll
+#pragma unroll
                     for (int p = 0; p < NP; ++p) {
                         FVec<VEC> s = sw[p], d;
-    #pragma unroll
+#pragma unroll
                         for (int v = 0; v < VEC; ++v) {
                             d.v[v] = xv[j][v] - s.v[v];
                             s.v[v] = fmaf(wg[j][p], d.v[v], s.v[v]);
@@ -312,17 +312,17 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                         lds_store<VEC>(dlt + (static_cast<int64_t>(t) * KP + p * EPP) * CSW, d);
                     }
                     FVec<VEC> srn[NP];
-    #pragma unroll
+#pragma unroll
                     for (int p = 0; p < NP; ++p)
                         srn[p] = lds_vec(rows + rsl[j][p] * CSW + q * VEC);
                     if (j + 1 < CH) {
-    #pragma unroll
+#pragma unroll
                         for (int p = 0; p < NP; ++p)
                             sw[p] = lds_vec(rows + wsl[j + 1][p] * CSW + q * VEC);
                     }
                     if (j > 0)
                         read_dot(j - 1, sr);
-    #pragma unroll
+#pragma unroll
                     for (int p = 0; p < NP; ++p)
                         sr[p] = srn[p];
                     if (j == CH - 1 || (TL && t == T - 1))
@@ -406,30 +406,30 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
             // chunks wholly inside T run without the per-token guards
             auto tokens = [&](auto tail_tag) {
                 constexpr bool TL = decltype(tail_tag)::value;
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < CH; ++j) {
                     const int t = T - 1 - ci * CH - j;
                     if (TL && t < 0)
                         break;
                     // a write takes the read of its own slot (same token) from its
                     // matched weight, and its store lands after that read's
-    #pragma unroll
+#pragma unroll
                     for (int p = 0; p < NP; ++p) {
-    #pragma unroll
+#pragma unroll
                         for (int v = 0; v < VEC; ++v)
                             dr[p].v[v] = fmaf(rw[j][p], dyv[j][v], dr[p].v[v]);
                         lds_store<VEC>(rows + rsl[j][p] * CSW + q * VEC, dr[p]);
                     }
                     float dx[VEC], part[NP];
-    #pragma unroll
+#pragma unroll
                     for (int v = 0; v < VEC; ++v)
                         dx[v] = 0.f;
-    #pragma unroll
+#pragma unroll
                     for (int p = 0; p < NP; ++p) {
                         const float g = wg[j][p];
                         FVec<VEC> D = dw[p];
                         part[p] = 0.f;
-    #pragma unroll
+#pragma unroll
                         for (int v = 0; v < VEC; ++v) {
                             D.v[v] = fmaf(wrm[j][p], dyv[j][v], D.v[v]);
                             part[p] = fmaf(D.v[v], __uint_as_float(scur.v[j][p * VEC + v]), part[p]);
@@ -439,14 +439,14 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                         lds_store<VEC>(rows + wsl[j][p] * CSW + q * VEC, D);
                     }
                     if (j + 1 < CH) {
-    #pragma unroll
+#pragma unroll
                         for (int p = 0; p < NP; ++p)
                             dr[p] = lds_vec(rows + rsl[j + 1][p] * CSW + q * VEC);
-    #pragma unroll
+#pragma unroll
                         for (int p = 0; p < NP; ++p)
                             dw[p] = lds_vec(rows + wsl[j + 1][p] * CSW + q * VEC);
                     }
-    #pragma unroll
+#pragma unroll
                     for (int p = 0; p < NP; ++p) {
                         const float sp = event_sum<LPE>(part[p]);
                         keep[p] = q == j % LPE ? sp : keep[p];
@@ -454,12 +454,12 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     if (j % LPE == LPE - 1 || (TL && t == 0)) {
                         const int tg = t + (j % LPE) - q;  // this lane's token of the group
                         if (tg >= t) {
-    #pragma unroll
+#pragma unroll
                             for (int p = 0; p < NP; ++p)
                                 dgp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
                         }
                     }
-    #pragma unroll
+#pragma unroll
                     for (int v = 0; v < VEC; ++v) {
                         const float sx = strided_sum<LPE>(dx[v]);
                         keep_x[v] = e == j % GX ? sx : keep_x[v];
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     if (j % GX == GX - 1 || (TL && t == 0)) {
                         const int tg = t + (j % GX) - e;  // this lane's token of the group
                         if (tg >= t && e < GX) {
-    #pragma unroll
+#pragma unroll
                             for (int v = 0; v < VEC; ++v)
                                 if (c0 + v < C)
                                     gx[static_cast<int64_t>(tg) * C + c0 + v] = keep_x[v];
