@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RAMNET_ABI_VERSION 1
+#define RAMNET_ABI_VERSION 2
 
 enum {
     RAMNET_OK = 0,
@@ -66,7 +66,7 @@ int ramnet_topk_addr_single_forward(const void *addr, int dtype, int64_t B, int6
 /*
  * Write and read address decoders in one launch.
  * Replaces ramnet_ops::topk_addr_forward
- * (ram_attn_bind.cpp:36-45, ram_attn_ops.cpp:137-172).
+ * (ram_attn_bind.cpp:46-54, ram_attn_ops.cpp:137-172).
  *   w_addr, r_addr  (B, H, U, P, T) logits, `dtype`
  *   idx_out         (B, H, w_top_k + r_top_k, T) int32; write rows first
  *   val_out         (B, H, w_top_k + r_top_k, T) fp32; write weights
@@ -108,8 +108,10 @@ int ramnet_topk_addr_backward(const int32_t *idx, const float *val, const void *
 
 /*
  * Bytes of device workspace the segment scan needs for B x H heads, T tokens
- * and the given top-k (per-event records, T padded to 32). The 32-bit form
- * returns -1 when the size does not fit an int.
+ * and the given top-k: the decoder's per-event records (T padded to 32),
+ * then the gain records the precomputed-gain form writes. A scan only reads
+ * the decoder records, so the same records can be scanned again. The 32-bit
+ * form returns -1 when the size does not fit an int.
  */
 int ramnet_scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k);
 int64_t ramnet_scan_workspace_bytes64(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k);
@@ -234,12 +236,15 @@ int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const vo
                                 int mass_aware, float eps, void *y, void *stream);
 
 /*
- * Planning query (no device work): channel-slice width and LDS bytes per
- * workgroup the segment scan uses for slot count A, C channels and top-k.
+ * Planning query (no device work beyond reading the device's CU count): the
+ * layout a segment-scan launch of this shape uses on the current device --
+ * channel-slice width, LDS bytes per workgroup, and whether it is the
+ * precomputed-gain form (a mass pre-pass writes the gain records of the
+ * workspace first). Honours RAMNET_SCAN_LAYOUT like the launch does.
  * Returns 1 if the shape is supported (A <= 8190, top-k <= 128), else 0.
  */
-int ramnet_segment_plan(int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int *slice_channels,
-                        int *lds_bytes);
+int ramnet_segment_plan(int64_t B, int64_t H, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int dtype,
+                        int *slice_channels, int *lds_bytes, int *precomputed_gains);
 
 #ifdef __cplusplus
 }

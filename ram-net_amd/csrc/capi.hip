@@ -219,18 +219,17 @@ int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, 
     return finish(err, why, "topk_addr_forward launch");
 }
 
+// Decoder records, then the gain records of the precomputed-gain scan.
 static int64_t scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t Kw, int64_t Kr) {
-    const int64_t t_pad = ramnet::scan_t_pad64(T);
-    return B * H * t_pad * (Kw * static_cast<int64_t>(sizeof(ramnet::WriteRec)) +
-                            Kr * static_cast<int64_t>(sizeof(ramnet::ReadRec))) +
-           ramnet::kScanChunk * static_cast<int64_t>(sizeof(ramnet::WriteRec) + sizeof(ramnet::ReadRec));
+    return ramnet::scan_record_bytes(B, H, T, Kw, Kr) + ramnet::scan_gain_bytes(B, H, T, Kw, Kr);
 }
 
 // Checks shared by the segment entry points; fills the scan job.
+// `need` is the workspace the caller's entry point requires (-1: the scan's).
 static int segment_checks(const void *x, const void *gamma, int dtype, const float *init_slot, const float *init_mass,
                           float *slot_out, float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A,
                           int64_t C, int64_t w_top_k, int64_t r_top_k, float eps, void *workspace,
-                          int64_t workspace_bytes) {
+                          int64_t workspace_bytes, int64_t need = -1) {
     RAMNET_REQUIRE(B >= 0 && H > 0 && T >= 0 && C > 0, "segment shape must have B, T >= 0 and H, C > 0");
     RAMNET_REQUIRE(A > 0 && A < kAddressLimit, "Address space overflow: A must be in (0, 2**30)");
     RAMNET_REQUIRE(valid_dtype(dtype), "x dtype must be float32, float16 or bfloat16");
@@ -244,7 +243,9 @@ static int segment_checks(const void *x, const void *gamma, int dtype, const flo
     RAMNET_REQUIRE(static_cast<const void *>(init_mass) != static_cast<const void *>(mass_out),
                    "mass_out must not alias init_mass");
     RAMNET_REQUIRE(T == 0 || (x && gamma && y), "null tensor pointer");
-    RAMNET_REQUIRE(workspace_bytes >= scan_workspace_bytes(B, H, T, w_top_k, r_top_k) && (T == 0 || workspace),
+    if (need < 0)
+        need = scan_workspace_bytes(B, H, T, w_top_k, r_top_k);
+    RAMNET_REQUIRE(workspace_bytes >= need && (T == 0 || workspace),
                    "workspace too small: see ramnet_scan_workspace_bytes");
     return RAMNET_OK;
 }
@@ -260,9 +261,7 @@ static ramnet::SegmentJob make_segment_job(const void *x, int dtype, const float
     const int64_t w_bytes = B * H * t_pad * w_top_k * static_cast<int64_t>(sizeof(ramnet::WriteRec));
     const int64_t r_bytes = B * H * t_pad * r_top_k * static_cast<int64_t>(sizeof(ramnet::ReadRec));
     job.rrec = reinterpret_cast<const ramnet::ReadRec *>(ws + w_bytes);
-    job.noop_w = reinterpret_cast<const ramnet::WriteRec *>(ws + w_bytes + r_bytes);
-    job.noop_r = reinterpret_cast<const ramnet::ReadRec *>(ws + w_bytes + r_bytes +
-                                                            ramnet::kScanChunk * sizeof(ramnet::WriteRec));
+    job.gain = reinterpret_cast<ramnet::GainRec *>(const_cast<char *>(ws) + w_bytes + r_bytes);
     job.x = x;
     job.init_slot = init_slot;
     job.init_mass = init_mass;
@@ -292,8 +291,6 @@ static hipError_t pack_decoded(const ramnet::SegmentJob &job, const int32_t *add
     pack.mask = mask;
     pack.wrec = const_cast<ramnet::WriteRec *>(job.wrec);
     pack.rrec = const_cast<ramnet::ReadRec *>(job.rrec);
-    pack.noop_w = const_cast<ramnet::WriteRec *>(job.noop_w);
-    pack.noop_r = const_cast<ramnet::ReadRec *>(job.noop_r);
     pack.dtype = job.dtype;
     pack.B = job.B;
     pack.H = job.H;
@@ -398,8 +395,6 @@ int ramnet_topk_addr_records(const void *w_addr, const void *r_addr, const void 
     dec.position_ids = position_ids;
     dec.wrec = const_cast<ramnet::WriteRec *>(lay.wrec);
     dec.rrec = const_cast<ramnet::ReadRec *>(lay.rrec);
-    dec.noop_w = const_cast<ramnet::WriteRec *>(lay.noop_w);
-    dec.noop_r = const_cast<ramnet::ReadRec *>(lay.noop_r);
     dec.gamma = gamma;
     dec.mask = mask;
     const char *why = nullptr;
@@ -447,7 +442,7 @@ static int64_t backward_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t
     if (B < 0 || H <= 0 || T < 0 || A <= 0 || C <= 0 || Kw <= 0 || Kr <= 0 || A >= kAddressLimit ||
         !fits_int({B * H * A * C, B * H * (A + 2), B * H * T * C, B * H * (T + ramnet::kScanPad) * (Kw + Kr)}))
         return -1;
-    const int64_t rec = (scan_workspace_bytes(B, H, T, Kw, Kr) + 255) / 256 * 256;
+    const int64_t rec = (ramnet::scan_record_bytes(B, H, T, Kw, Kr) + 255) / 256 * 256;
     const int64_t extra = ramnet::segment_backward_layout(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T),
                                                           static_cast<int>(A), static_cast<int>(C), static_cast<int>(Kw),
                                                           static_cast<int>(Kr), nullptr, nullptr);
@@ -466,18 +461,19 @@ int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val,
                                  float *grad_init_mass, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
                                  int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *workspace,
                                  int64_t workspace_bytes, void *stream) {
+    const int64_t need = backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k);
     if (int rc = segment_checks(x, gamma, dtype, init_slot, init_mass, grad_init_slot, grad_init_mass, grad_x, B, H,
-                                T, A, C, w_top_k, r_top_k, eps, workspace, workspace_bytes))
+                                T, A, C, w_top_k, r_top_k, eps, workspace, workspace_bytes, need < 0 ? 0 : need))
         return rc;
     if (B == 0)
         return RAMNET_OK;
-    const int64_t need = backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k);
     RAMNET_REQUIRE(need >= 0, "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A <= 13652)");
     RAMNET_REQUIRE(workspace_bytes >= need && workspace,
                    "workspace too small: see ramnet_segment_backward_workspace_bytes");
     RAMNET_REQUIRE(T == 0 || (addr_idx && addr_val && grad_y && grad_addr_val && grad_gamma), "null tensor pointer");
     ramnet::SegmentJob fj = make_segment_job(x, dtype, init_slot, init_mass, nullptr, nullptr, nullptr, B, H, T, A, C,
                                              w_top_k, r_top_k, mass_aware, eps, workspace);
+    fj.gain = nullptr;  // the backward's own buffers follow the records
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const char *why = nullptr;
     if (T > 0) {
@@ -497,7 +493,7 @@ int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val,
     job.grad_gamma = grad_gamma;
     job.grad_init_slot = grad_init_slot;
     job.grad_init_mass = grad_init_mass;
-    const int64_t rec = (scan_workspace_bytes(B, H, T, w_top_k, r_top_k) + 255) / 256 * 256;
+    const int64_t rec = (ramnet::scan_record_bytes(B, H, T, w_top_k, r_top_k) + 255) / 256 * 256;
     ramnet::segment_backward_layout(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T), static_cast<int>(A),
                                     static_cast<int>(C), static_cast<int>(w_top_k), static_cast<int>(r_top_k),
                                     static_cast<char *>(workspace) + rec, &job);
@@ -551,11 +547,14 @@ int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const vo
     return finish(err, why, "topk_autoregressive_ launch");
 }
 
-int ramnet_segment_plan(int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int *slice_channels, int *lds_bytes) {
-    if (A <= 0 || A >= kAddressLimit || C <= 0 || w_top_k <= 0 || r_top_k <= 0)
+int ramnet_segment_plan(int64_t B, int64_t H, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int dtype,
+                        int *slice_channels, int *lds_bytes, int *precomputed_gains) {
+    if (B <= 0 || H <= 0 || A <= 0 || A >= kAddressLimit || C <= 0 || w_top_k <= 0 || r_top_k <= 0 ||
+        !valid_dtype(dtype) || !fits_int({B * H * A * C, B * H * (A + 2)}))
         return 0;
-    return ramnet::segment_plan(static_cast<int>(A), static_cast<int>(C), static_cast<int>(w_top_k),
-                                static_cast<int>(r_top_k), slice_channels, lds_bytes);
+    return ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(A), static_cast<int>(C),
+                                static_cast<int>(w_top_k), static_cast<int>(r_top_k), dtype, slice_channels,
+                                lds_bytes, precomputed_gains);
 }
 
 }  // extern "C"

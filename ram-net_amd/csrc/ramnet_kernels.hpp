@@ -27,8 +27,10 @@ struct AddrSource {
 // padding tokens, inactive addresses, zero weights) point at dummy LDS rows
 // in front of the state: writes at slot -2 (weight 0, alpha 1), reads at
 // slot -1 (weight 0). The workspace holds, in order: write records
-// (B*H, Kw, T_pad), read records (B*H, Kr, T_pad), then one chunk of no-op
-// write records and one of no-op read records (read by lanes beyond top-K).
+// (B*H, Kw, T_pad), read records (B*H, Kr, T_pad), then the gain records of
+// the precomputed-gain scan (B*H, max(Kw, Kr), T_pad) of GainRec. The
+// decoder records are never modified after they are written, so one set of
+// records can be scanned any number of times.
 constexpr int kScanChunk = 16;
 constexpr int kScanPad = 2 * kScanChunk;
 struct WriteRec {
@@ -42,15 +44,26 @@ struct ReadRec {
     float r;
 };
 
+// One event of the precomputed-gain scan, written by the mass pre-pass:
+// write event e and read event e of one token. The sign bit of event 0's
+// gain carries the token's overlap flag (gains are never negative).
+struct GainRec {
+    int wslot;
+    float gain;
+    int rslot;
+    float r;  // effective read weight (mass-aware), else the read weight
+};
+
 __host__ __device__ inline int scan_t_pad(int T) { return (T + kScanPad - 1) / kScanPad * kScanPad; }
 inline int64_t scan_t_pad64(int64_t T) { return (T + kScanPad - 1) / kScanPad * kScanPad; }
 
-// Written by every record producer (the first kScanChunk threads of the grid).
-__device__ __forceinline__ void write_noop_chunk(WriteRec *w, ReadRec *r, int64_t tid) {
-    if (tid < kScanChunk) {
-        w[tid] = WriteRec{-2, 0.f, 1.f, 0.f};
-        r[tid] = ReadRec{-1, 0.f};
-    }
+// Workspace bytes: the decoder records alone, and with the gain records.
+inline int64_t scan_record_bytes(int64_t B, int64_t H, int64_t T, int64_t Kw, int64_t Kr) {
+    return B * H * scan_t_pad64(T) *
+           (Kw * static_cast<int64_t>(sizeof(WriteRec)) + Kr * static_cast<int64_t>(sizeof(ReadRec)));
+}
+inline int64_t scan_gain_bytes(int64_t B, int64_t H, int64_t T, int64_t Kw, int64_t Kr) {
+    return B * H * scan_t_pad64(T) * (Kw > Kr ? Kw : Kr) * static_cast<int64_t>(sizeof(GainRec));
 }
 
 // Decode one or two address tensors (write and read) sharing a shape.
@@ -69,8 +82,6 @@ struct AddrJob {
     // t < T_pad, source 0 as writes, source 1 as reads.
     WriteRec *wrec;               // (B*H, Kw, T_pad)
     ReadRec *rrec;                // (B*H, Kr, T_pad)
-    WriteRec *noop_w;             // kScanChunk no-op records (written too)
-    ReadRec *noop_r;
     const void *gamma;            // (B, H, T) in dtype, for alpha
     const uint8_t *mask;          // (B, T) or null
 };
@@ -96,8 +107,7 @@ struct AddrBwdJob {
 struct SegmentJob {
     const WriteRec *wrec;     // (B*H, Kw, T_pad) scan records
     const ReadRec *rrec;      // (B*H, Kr, T_pad)
-    const WriteRec *noop_w;   // kScanChunk no-op write records
-    const ReadRec *noop_r;    // kScanChunk no-op read records
+    GainRec *gain;            // (B*H, max(Kw, Kr), T_pad): written by the mass pre-pass, or null
     const void *x;            // (B, H, T, C) in dtype
     const float *init_slot;   // (B, H, A, C)
     const float *init_mass;   // (B, H, A)
@@ -176,16 +186,15 @@ struct PackJob {
     const uint8_t *mask;      // (B, T) or null
     WriteRec *wrec;
     ReadRec *rrec;
-    WriteRec *noop_w;
-    ReadRec *noop_r;
     int dtype;
     int B, H, T, A, Kw, Kr;
 };
 hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const char **why);
 hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const char **why);
 
-// Channel-slice width and dynamic LDS bytes the segment kernel would use.
-int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes);
+// Channel-slice width, dynamic LDS bytes and form (1: precomputed gains)
+// that a segment-scan launch of this shape uses on the current device.
+int segment_plan(int B, int H, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre);
 
 // Mass pre-pass in record-keeping mode: the records stay as they are and
 // `aux` receives the per-event quantities. `maps` holds the chunk maps

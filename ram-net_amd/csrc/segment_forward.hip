@@ -134,7 +134,6 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
     const int Kt = job.Kw + job.Kr;
     const int64_t n = static_cast<int64_t>(job.B) * job.H * Kt * t_pad;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    write_noop_chunk(job.noop_w, job.noop_r, gid);
     if (gid >= n)
         return;
     const int t = static_cast<int>(gid % t_pad);
@@ -193,9 +192,11 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
 
 // Mass pre-pass: the slot-mass recurrence (m <- alpha m + w per write
 // event, in token order), once per (b, h) instead of once per channel
-// slice. Each write record's alpha field is replaced by its gain
-// g = w / (m + eps); mass-aware, each read record's weight by its effective
-// weight (sum r) (m r) / (sum m r + eps) on the post-write masses.
+// slice. It writes the gain records of the precomputed-gain scan: per token
+// and event, the write slot with its gain g = w / (m + eps) and the read
+// slot with its weight (mass-aware: the effective weight
+// (sum r) (m r) / (sum m r + eps) on the post-write masses). The decoder
+// records are only read, so they can be scanned again.
 //
 // The sequence is cut into NC time chunks run in parallel. The recurrence is
 // affine in m with coefficients independent of m, so:
@@ -319,9 +320,8 @@ __global__ __launch_bounds__(256) void mass_chunk_scan_kernel(const SegmentJob j
 // as they are and the per-event quantities go to `aux` instead (the forward
 // replay of the segment backward).
 template<bool MA, int MP, bool AUX = false>
-__global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, WriteRec *wrec, ReadRec *rrec,
-                                                            int t_pad, int chunk_len, const float2 *starts,
-                                                            const MassAux aux) {
+__global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, int t_pad, int chunk_len,
+                                                            const float2 *starts, const MassAux aux) {
     using L = MassLanes<MP>;
     constexpr int CH = L::CH;
     extern __shared__ __align__(16) float lds[];
@@ -353,8 +353,10 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     __syncthreads();
 
     const L ln(lane, Kw, Kr);
-    WriteRec *gw = wrec + static_cast<int64_t>(bh) * Kw * t_pad;
-    ReadRec *gr = rrec + static_cast<int64_t>(bh) * Kr * t_pad;
+    const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * t_pad;
+    const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad;
+    // gain records of this head (not written in the record-keeping mode)
+    GainRec *gg = AUX ? nullptr : job.gain + static_cast<int64_t>(bh) * max(Kw, Kr) * t_pad;
     const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
     auto run = [&](int t0, const MassRecs<MP, CH> &c) {
         auto wev = [&](int p, int j, int &a, float &w, float &al) {
@@ -373,11 +375,15 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 ms[a[p]] = m2;
                 gn[p] = scan_gain(w[p], m2 + eps);
                 if constexpr (!AUX) {
-                    if (wlane && ln.on[p] && live)
-                        gw[static_cast<int64_t>(ln.ev[p]) * t_pad + t].alpha = gn[p];
+                    if (wlane && ln.on[p] && live) {
+                        // event 0 carries the token's overlap flag in the gain's sign bit
+                        const int fl = p == 0 && hl == 0 && c.w[0][j].w != 0 ? static_cast<int>(0x80000000u) : 0;
+                        *reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(ln.ev[p]) * t_pad + t].wslot) =
+                            make_int2(a[p], __float_as_int(gn[p]) | fl);
+                    }
                 }
             }
-            if constexpr (MA || AUX) {
+            {
                 int rb[MP];
                 float rr[MP], mm[MP];
                 float sr = 0.f, srm = 0.f;
@@ -386,9 +392,12 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                     const bool act = !wlane && ln.on[p] && live;
                     rb[p] = act ? c.r[p][j].x : -1;
                     rr[p] = act ? __int_as_float(c.r[p][j].y) : 0.f;
-                    mm[p] = ms[rb[p]];  // post-write mass
-                    sr += rr[p];
-                    srm += rr[p] * mm[p];
+                    mm[p] = 0.f;
+                    if constexpr (MA || AUX) {
+                        mm[p] = ms[rb[p]];  // post-write mass
+                        sr += rr[p];
+                        srm += rr[p] * mm[p];
+                    }
                 }
                 float scale = 1.f;
                 if constexpr (MA) {
@@ -405,7 +414,8 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                             const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kr + ln.ev[p];
                             aux.rev[o] = make_int4(rb[p], __float_as_int(re[p]), __float_as_int(mm[p]), 0);
                         } else {
-                            gr[static_cast<int64_t>(ln.ev[p]) * t_pad + t].r = re[p];
+                            *reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(ln.ev[p]) * t_pad + t].rslot) =
+                                make_int2(rb[p], __float_as_int(re[p]));
                         }
                     }
                 }
@@ -504,14 +514,12 @@ size_t mass_lds_bytes(int A, bool aux) { return static_cast<size_t>(A + 2) * 4 +
 template<bool MA, int MP, bool AUX>
 hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void *maps_buf, size_t maps_bytes,
                                const MassAux &aux, hipStream_t stream) {
-    auto *w = const_cast<WriteRec *>(job.wrec);  // the records are the caller's workspace
-    auto *r = const_cast<ReadRec *>(job.rrec);
     int len = 0;
     const int nck = mass_chunks(job, maps_bytes, n_cu, &len);
     const unsigned bh = static_cast<unsigned>(job.B * job.H);
     if (nck <= 1) {
         hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, 1), dim3(kWave), mass_lds_bytes(job.A, AUX),
-                           stream, job, w, r, t_pad, job.T, nullptr, aux);
+                           stream, job, t_pad, job.T, nullptr, aux);
         return hipGetLastError();
     }
     auto *maps = static_cast<float2 *>(maps_buf);
@@ -521,7 +529,7 @@ hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void 
     hipLaunchKernelGGL(mass_chunk_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, job,
                        maps, nck);
     hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, nck), dim3(kWave), mass_lds_bytes(job.A, AUX),
-                       stream, job, w, r, t_pad, len, maps, aux);
+                       stream, job, t_pad, len, maps, aux);
     return hipGetLastError();
 }
 
@@ -578,17 +586,6 @@ hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const cha
     return hipGetLastError();
 }
 
-int segment_plan(int A, int C, int Kw, int Kr, int *cs, int *lds_bytes) {
-    Plan p{};
-    if (!make_plan(8, 16, A, C, Kw, Kr, 2, 256, &p))
-        return 0;
-    if (cs)
-        *cs = p.cs;
-    if (lds_bytes)
-        *lds_bytes = static_cast<int>(p.lds);
-    return 1;
-}
-
 // RAMNET_SCAN_LAYOUT="vec,epp,np,nw[,pre]" replaces the planner's choice (tests
 // sweep every compiled layout with it; also a tuning knob). The layout must
 // be compiled, cover max(Kw, Kr) events and fit in LDS.
@@ -612,16 +609,50 @@ static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
     return 1;
 }
 
+// The layout a launch of this job uses: the override, else the planner's
+// choice for the job's B, H, dtype and this device's CU count.
+static bool pick_plan(const SegmentJob &job, Plan *p, const char **why) {
+    const int forced = layout_override(job, p, why);
+    if (forced < 0)
+        return false;
+    if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, dtype_bytes(job.dtype), cu_count(), p)) {
+        *why = "segment forward: shape outside the LDS-resident scan (needs (A*CS + A)*4 bytes <= 160 KiB for some "
+               "slice width and top_k <= 128)";
+        return false;
+    }
+    return true;
+}
+
+int segment_plan(int B, int H, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre) {
+    SegmentJob job{};
+    job.B = B;
+    job.H = H;
+    job.A = A;
+    job.C = C;
+    job.Kw = Kw;
+    job.Kr = Kr;
+    job.dtype = dtype;
+    Plan p{};
+    const char *why = nullptr;
+    if (!pick_plan(job, &p, &why))
+        return 0;
+    if (cs)
+        *cs = p.cs;
+    if (lds_bytes)
+        *lds_bytes = static_cast<int>(p.lds);
+    if (pre)
+        *pre = p.pre ? 1 : 0;
+    return 1;
+}
+
 hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, const char **why) {
     if (static_cast<int64_t>(job.B) * job.H == 0)
         return hipSuccess;
     Plan p{};
-    const int forced = layout_override(job, &p, why);
-    if (forced < 0)
+    if (!pick_plan(job, &p, why))
         return hipErrorInvalidValue;
-    if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, dtype_bytes(job.dtype), cu_count(), &p)) {
-        *why = "segment forward: shape outside the LDS-resident scan (needs (A*CS + A)*4 bytes <= 160 KiB for some "
-               "slice width and top_k <= 128)";
+    if (p.pre && !job.gain) {
+        *why = "segment forward: the precomputed-gain layout needs the gain records of the scan workspace";
         return hipErrorInvalidValue;
     }
     ScanGeom geo{};

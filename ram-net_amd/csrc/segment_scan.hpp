@@ -266,10 +266,10 @@ inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem, 
 //    per-token dependency chain is one LDS row read-modify-write;
 //  * one barrier per chunk hands the double-buffered stage over.
 // FAST: C is a multiple of CS, so every lane owns VEC real channels.
-// PRE: the mass pre-pass (segment_mass_kernel) has already replaced each
-// write record's alpha by its gain and, mass-aware, each read weight by its
-// effective weight; there is no mass wave and no mass column, and the state
-// waves stage the records of the next chunk themselves.
+// PRE: the mass pre-pass (segment_mass_kernel) has already written the gain
+// records (each write event's gain and, mass-aware, each read's effective
+// weight); there is no mass wave and no mass column, and the state waves
+// stage the gain records of the next chunk themselves.
 template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
 __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_kernel(const SegmentJob job,
                                                                                      const ScanGeom geo) {
@@ -347,27 +347,35 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     // p * 32 + lane and lanes 32..63 read events p * 32 + lane - 32.
     const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * Tp;
     const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * Tp;
+    // PRE: the gain records of the mass pre-pass, max(Kw, Kr) events per token
+    const int EK = Kw > Kr ? Kw : Kr;
+    const GainRec *gp = PRE ? job.gain + static_cast<int64_t>(bh) * EK * Tp : nullptr;
     const int hl = lane & 31;
     const bool wlane = lane < 32;
     struct RawRegs {
-        int4 w[RI];
-        int2 r[RI];
+        int4 w[RI];  // write record (PRE: gain record)
+        int2 r[RI];  // read record (unused in PRE)
     };
     auto raw_fetch = [&](int t0, RawRegs &rg) {
 #pragma unroll
         for (int k = 0; k < RI; ++k) {
             const int it = min(tid + k * NST, E * CH - 1);
             const int e = it / CH, j = it % CH;
-            const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
-            rg.w[k] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ew) * Tp + t0 + j);
-            rg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
+            if constexpr (PRE) {
+                const int ee = e < EK ? e : EK - 1;
+                rg.w[k] = *reinterpret_cast<const int4 *>(gp + static_cast<int64_t>(ee) * Tp + t0 + j);
+            } else {
+                const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
+                rg.w[k] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ew) * Tp + t0 + j);
+                rg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
+            }
         }
     };
-    // PRE: the thread holding an event's write and read records stages
-    // them as one compact record (one 16-byte LDS read per event and token
-    // for the state waves); events past top-K become no-ops here, and event
-    // 0 carries the token's overlap flag.
-    auto raw_deposit = [&](int buf, const RawRegs &rg) {
+    // PRE: the gain record goes to the stage as it is (one 16-byte LDS read
+    // per event and token for the state waves); events past top-K and tokens
+    // past T (which the pre-pass does not write) become no-ops here, and the
+    // sign bit of event 0's gain is the token's overlap flag.
+    auto raw_deposit = [&](int buf, int t0, const RawRegs &rg) {
         WriteRec *rw = raw_w(buf);
         ReadRec *rr = raw_r(buf);
 #pragma unroll
@@ -377,10 +385,12 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             const int4 w = rg.w[k];
             const int2 r = rg.r[k];
             if constexpr (PRE) {
+                const bool live = t0 + j < T;
                 if (e == 0)
-                    stage_f(buf)[j] = w.w;
-                pre_rec(buf)[j * E + e] = make_int4(e < Kw ? w.x : -2, e < Kw ? w.z : 0, e < Kr ? r.x : -1,
-                                                    e < Kr ? r.y : 0);
+                    stage_f(buf)[j] = live ? static_cast<int>(static_cast<uint32_t>(w.y) >> 31) : 0;
+                const bool wok = live && e < Kw, rok = live && e < Kr;
+                pre_rec(buf)[j * E + e] =
+                    make_int4(wok ? w.x : -2, wok ? (w.y & 0x7fffffff) : 0, rok ? w.z : -1, rok ? w.w : 0);
             } else {
                 *reinterpret_cast<int4 *>(rw + j * E + e) = w;
                 *reinterpret_cast<int2 *>(rr + j * E + e) = r;
@@ -696,7 +706,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
         if (nc > 0) {
             raw_fetch(0, rg);
             x_fetch(0, xb);
-            raw_deposit(0, rg);
+            raw_deposit(0, 0, rg);
             x_deposit(0, xb);
         }
         __syncthreads();
@@ -710,7 +720,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
                 state_chunk(ci & 1, ci * CH, Tail{});
             __builtin_amdgcn_sched_barrier(0);
             x_deposit((ci + 1) & 1, xb);
-            raw_deposit((ci + 1) & 1, rg);
+            raw_deposit((ci + 1) & 1, clampc(ci + 1), rg);
             __syncthreads();
         }
     } else {
@@ -718,9 +728,9 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
         if (nc > 0) {
             if (!mass_wave) {
                 raw_fetch(0, rg);
-                raw_deposit(0, rg);
+                raw_deposit(0, 0, rg);
                 raw_fetch(clampc(1), rg);
-                raw_deposit(1, rg);
+                raw_deposit(1, clampc(1), rg);
                 x_fetch(0, xb);
                 x_deposit(0, xb);
             }
@@ -748,7 +758,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
                     state_chunk(ci & 1, ci * CH, Tail{});
                 __builtin_amdgcn_sched_barrier(0);
                 x_deposit((ci + 1) & 1, xb);
-                raw_deposit(ci & 1, rg);
+                raw_deposit(ci & 1, clampc(ci + 2), rg);
             }
             __syncthreads();
         }

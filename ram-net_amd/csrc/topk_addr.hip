@@ -92,8 +92,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FAST && KM 
     const int Tg = rec_mode ? scan_t_pad(T) : T;  // record mode also writes the padding tokens
     const int64_t n = static_cast<int64_t>(job.B) * job.H * Tg;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (rec_mode && blockIdx.y == 0)
-        write_noop_chunk(job.noop_w, job.noop_r, gid);
     if (gid >= n)
         return;
     const int t = static_cast<int>(gid % Tg);
@@ -199,8 +197,6 @@ __global__ __launch_bounds__(256) void topk_addr_bruteforce_kernel(const AddrJob
     const int T = job.T, H = job.H, U = job.U, P = job.P, A = job.A;
     const bool rec_mode = job.wrec != nullptr;
     const int Tg = rec_mode ? scan_t_pad(T) : T;
-    if (rec_mode && blockIdx.x == 0 && blockIdx.y == 0)
-        write_noop_chunk(job.noop_w, job.noop_r, threadIdx.x);
     const int64_t gid = blockIdx.x;  // (b, h, t)
     const int t = static_cast<int>(gid % Tg);
     const int tl = t < T ? t : T - 1;

@@ -77,7 +77,8 @@ SIGNATURES: dict[str, tuple[type, list]] = {
         _c_int, _c_float, _c_ptr, _c_i64, _c_ptr]),
     "ramnet_segment_backward_workspace_bytes": (_c_i64, [_c_i64] * 7),
     "ramnet_segment_plan": (_c_int, [
-        _c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int),
+        ctypes.POINTER(_c_int)]),
 }
 
 _lock = threading.Lock()
@@ -118,11 +119,14 @@ def int_bits() -> int:
     return int(lib().ramnet_int_bits())
 
 
-def segment_plan(A: int, C: int, w_top_k: int, r_top_k: int) -> tuple[int, int] | None:
-    """(channel-slice width, LDS bytes) of the segment scan, or None if unsupported."""
-    cs, lds = _c_int(0), _c_int(0)
-    ok = lib().ramnet_segment_plan(A, C, w_top_k, r_top_k, ctypes.byref(cs), ctypes.byref(lds))
-    return (cs.value, lds.value) if ok else None
+def segment_plan(B: int, H: int, A: int, C: int, w_top_k: int, r_top_k: int,
+                 dtype: torch.dtype = torch.bfloat16) -> tuple[int, int, bool] | None:
+    """(channel-slice width, LDS bytes, precomputed-gain form) of a segment-scan
+    launch of this shape on the current device, or None if unsupported."""
+    cs, lds, pre = _c_int(0), _c_int(0), _c_int(0)
+    ok = lib().ramnet_segment_plan(B, H, A, C, w_top_k, r_top_k, DTYPE_CODES[dtype], ctypes.byref(cs),
+                                   ctypes.byref(lds), ctypes.byref(pre))
+    return (cs.value, lds.value, bool(pre.value)) if ok else None
 
 
 def scan_workspace_bytes(B: int, H: int, T: int, w_top_k: int, r_top_k: int) -> int:

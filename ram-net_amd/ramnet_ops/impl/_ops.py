@@ -33,6 +33,36 @@ def _require_gpu(name: str, *tensors: Tensor) -> None:
             raise RuntimeError(f"{name}: tensors must be on a GPU (HIP) device, got {t.device}")
 
 
+def _dims(op: str, name: str, t: Tensor, n: int) -> tuple[int, ...]:
+    """The sizes of a tensor argument that must have ``n`` dimensions."""
+    if not isinstance(t, Tensor):
+        raise RuntimeError(f"{op}: {name} must be a tensor, got {type(t).__name__}")
+    if t.dim() != n:
+        raise RuntimeError(f"{op}: Tensor {name} must have {n} dimensions, but got shape {tuple(t.shape)}")
+    return tuple(t.shape)
+
+
+def _check_shapes(op: str, **named: tuple[Tensor | None, tuple[int, ...]]) -> None:
+    """Exact sizes of every tensor argument, checked before any launch, as the
+    reference's native checks do (check_tensor, csrc/cuda_utils.cuh:375-391;
+    e.g. ram_attn_topk_autoregressive.cu:216-224). The kernels index every
+    tensor with sizes taken from the leading ones, so a mis-shaped tensor
+    raises RuntimeError here instead of reaching device memory. ``None``
+    entries are optional tensors that were not given."""
+    for name, (t, shape) in named.items():
+        if t is None:
+            continue
+        if not isinstance(t, Tensor):
+            raise RuntimeError(f"{op}: {name} must be a tensor, got {type(t).__name__}")
+        if tuple(t.shape) != tuple(shape):
+            raise RuntimeError(f"{op}: Tensor {name} shape mismatch: expect {tuple(shape)}, but got {tuple(t.shape)}")
+
+
+def _check_slots(op: str, U: int, P: int, A: int) -> None:
+    if P ** U != A:
+        raise RuntimeError(f"{op}: the slot count A={A} must equal P**U = {P}**{U}")
+
+
 def _require_given(name: str, **tensors: Tensor) -> None:
     """Required tensor arguments (the dispatcher passes None through to a
     Python operator); the reference's native checks raise RuntimeError."""
@@ -48,8 +78,11 @@ def _require_given(name: str, **tensors: Tensor) -> None:
 def topk_addr_single_forward(addr: Tensor, embed_num: int, A: int, position_ids: Tensor, top_k: int,
                              top_k_re_norm: float, addr_val_neg: bool = False,
                              encode_batch_idx: bool = True) -> tuple[Tensor, Tensor]:
-    _require_gpu("topk_addr_single_forward", addr, position_ids)
-    B, H, U, P, T = addr.shape
+    op = "topk_addr_single_forward"
+    _require_gpu(op, addr, position_ids)
+    B, H, U, P, T = _dims(op, "addr", addr, 5)
+    _check_slots(op, U, P, A)
+    _check_shapes(op, position_ids=(position_ids, (B, T)))
     addr = addr.contiguous()
     pos = position_ids.to(device=addr.device, dtype=torch.int32).contiguous()
     idx = torch.empty((B, H, top_k, T), dtype=torch.int32, device=addr.device)
@@ -72,9 +105,12 @@ def _(addr, embed_num, A, position_ids, top_k, top_k_re_norm, addr_val_neg=False
 def topk_addr_forward(w_addr: Tensor, r_addr: Tensor, embed_num: int, A: int, position_ids: Tensor, w_top_k: int,
                       r_top_k: int, w_re_norm: float, r_re_norm: float,
                       encode_batch_idx: bool = True) -> tuple[Tensor, Tensor]:
-    _require_gpu("topk_addr_forward", w_addr, r_addr, position_ids)
-    B, H, U, P, T = w_addr.shape
-    if r_addr.shape != w_addr.shape or r_addr.dtype != w_addr.dtype:
+    op = "topk_addr_forward"
+    _require_gpu(op, w_addr, r_addr, position_ids)
+    B, H, U, P, T = _dims(op, "w_addr", w_addr, 5)
+    _check_slots(op, U, P, A)
+    _check_shapes(op, r_addr=(r_addr, (B, H, U, P, T)), position_ids=(position_ids, (B, T)))
+    if r_addr.dtype != w_addr.dtype:
         raise RuntimeError("topk_addr_forward: w_addr and r_addr must share shape and dtype")
     w_addr, r_addr = w_addr.contiguous(), r_addr.contiguous()
     pos = position_ids.to(device=w_addr.device, dtype=torch.int32).contiguous()
@@ -104,8 +140,13 @@ def topk_addr_single_backward(idx: Tensor, val: Tensor, addr: Tensor, D_val: Ten
                               position_ids: Tensor, top_k: int, top_k_re_norm: float, addr_val_neg: bool,
                               shape: list[int], dtype: torch.dtype) -> Tensor:
     _require_given("topk_addr_single_backward", idx=idx, val=val, addr=addr, D_val=D_val, position_ids=position_ids)
-    _require_gpu("topk_addr_single_backward", idx, val, addr, D_val, position_ids)
+    op = "topk_addr_single_backward"
+    _require_gpu(op, idx, val, addr, D_val, position_ids)
     B, H, U, P, A, T = shape
+    _check_slots(op, U, P, A)
+    ev = (B, H, top_k, T)
+    _check_shapes(op, idx=(idx, ev), val=(val, ev), D_val=(D_val, ev), addr=(addr, (B, H, U, P, T)),
+                  position_ids=(position_ids, (B, T)))
     addr = addr.to(dtype).contiguous()
     pos = position_ids.to(device=addr.device, dtype=torch.int32).contiguous()
     grad = torch.empty((B, H, U, P, T), dtype=dtype, device=addr.device)
@@ -130,8 +171,13 @@ def topk_addr_backward(idx: Tensor, val: Tensor, w_addr: Tensor, r_addr: Tensor,
                        shape: list[int], dtype: torch.dtype) -> tuple[Tensor, Tensor]:
     _require_given("topk_addr_backward", idx=idx, val=val, w_addr=w_addr, r_addr=r_addr, D_val=D_val,
                    position_ids=position_ids)
-    _require_gpu("topk_addr_backward", idx, val, w_addr, r_addr, D_val, position_ids)
+    op = "topk_addr_backward"
+    _require_gpu(op, idx, val, w_addr, r_addr, D_val, position_ids)
     B, H, U, P, A, T = shape
+    _check_slots(op, U, P, A)
+    ev = (B, H, w_top_k + r_top_k, T)
+    _check_shapes(op, idx=(idx, ev), val=(val, ev), D_val=(D_val, ev), w_addr=(w_addr, (B, H, U, P, T)),
+                  r_addr=(r_addr, (B, H, U, P, T)), position_ids=(position_ids, (B, T)))
     w_addr, r_addr = w_addr.to(dtype).contiguous(), r_addr.to(dtype).contiguous()
     pos = position_ids.to(device=w_addr.device, dtype=torch.int32).contiguous()
     gw = torch.empty((B, H, U, P, T), dtype=dtype, device=w_addr.device)
@@ -201,6 +247,17 @@ topk_addr_forward.register_autograd(_pair_backward, setup_context=_pair_setup)
 # --------------------------------------------------------------------------
 # segment scan (prefill)
 
+def _check_segment(op, addr_idx, addr_val, x, gamma, slot, mass, mask, w_top_k, r_top_k, slot_name="init_slot",
+                   mass_name="init_mass") -> tuple[int, int, int, int, int]:
+    """Shapes of the segment ops' arguments: (B, H, T, C, A)."""
+    B, H, T, C = _dims(op, "x", x, 4)
+    A = _dims(op, slot_name, slot, 4)[2]
+    ev = (B, H, w_top_k + r_top_k, T)
+    _check_shapes(op, addr_idx=(addr_idx, ev), addr_val=(addr_val, ev), gamma=(gamma, (B, H, T)),
+                  mask=(mask, (B, T)), **{slot_name: (slot, (B, H, A, C)), mass_name: (mass, (B, H, A))})
+    return B, H, T, C, A
+
+
 def _segment_args(x, gamma, mask):
     x = x.contiguous()
     gamma = gamma.to(dtype=x.dtype).contiguous()
@@ -219,12 +276,12 @@ def _workspace(x: Tensor, B: int, H: int, T: int, w_top_k: int, r_top_k: int) ->
 def topk_segment_forward(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, init_slot: Tensor,
                          init_mass: Tensor, mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool,
                          eps: float) -> tuple[Tensor, Tensor, Tensor]:
-    _require_gpu("topk_segment_forward", addr_idx, addr_val, x, gamma, init_slot, init_mass, mask)
-    B, H, T, C = x.shape
+    op = "topk_segment_forward"
+    _require_gpu(op, addr_idx, addr_val, x, gamma, init_slot, init_mass, mask)
+    B, H, T, C, A = _check_segment(op, addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k)
     x, gamma, mask = _segment_args(x, gamma, mask)
     addr_idx = addr_idx.to(torch.int32).contiguous()
     addr_val = addr_val.to(torch.float32).contiguous()
-    A = init_slot.shape[-2]
     init_slot = init_slot.to(torch.float32).contiguous()
     init_mass = init_mass.to(torch.float32).contiguous()
     slot = torch.empty_like(init_slot)
@@ -259,13 +316,14 @@ def topk_segment_backward(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: 
     """
     _require_given("topk_segment_backward", addr_idx=addr_idx, addr_val=addr_val, x=x, gamma=gamma,
                    init_slot=init_slot, init_mass=init_mass, D_y=D_y)
-    _require_gpu("topk_segment_backward", addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, D_y,
-                 D_post_slot, D_post_mass)
-    B, H, T, C = x.shape
+    op = "topk_segment_backward"
+    _require_gpu(op, addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, D_y, D_post_slot, D_post_mass)
+    B, H, T, C, A = _check_segment(op, addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k)
+    _check_shapes(op, D_y=(D_y, (B, H, T, C)), D_post_slot=(D_post_slot, (B, H, A, C)),
+                  D_post_mass=(D_post_mass, (B, H, A)))
     x, gamma, mask = _segment_args(x, gamma, mask)
     addr_idx = addr_idx.to(torch.int32).contiguous()
     addr_val = addr_val.to(torch.float32).contiguous()
-    A = init_slot.shape[-2]
     init_slot = init_slot.to(torch.float32).contiguous()
     init_mass = init_mass.to(torch.float32).contiguous()
     D_y = D_y.to(dtype=x.dtype).contiguous()  # as the reference, the output gradient is taken in x's dtype
@@ -334,13 +392,14 @@ topk_segment_forward.register_autograd(_segment_backward, setup_context=_segment
 @torch.library.custom_op(f"{_NS}::topk_segment_forward_", mutates_args=("slot", "mass"), device_types="cuda")
 def topk_segment_forward_(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
                           mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool, eps: float) -> Tensor:
-    _require_gpu("topk_segment_forward_", addr_idx, addr_val, x, gamma, slot, mass, mask)
-    _require_state("topk_segment_forward_", slot, mass)
-    B, H, T, C = x.shape
+    op = "topk_segment_forward_"
+    _require_gpu(op, addr_idx, addr_val, x, gamma, slot, mass, mask)
+    B, H, T, C, A = _check_segment(op, addr_idx, addr_val, x, gamma, slot, mass, mask, w_top_k, r_top_k, "slot",
+                                   "mass")
+    _require_state(op, slot, mass)
     x, gamma, mask = _segment_args(x, gamma, mask)
     addr_idx = addr_idx.to(torch.int32).contiguous()
     addr_val = addr_val.to(torch.float32).contiguous()
-    A = slot.shape[-2]
     # channel slices of one head may start after another has stored the new
     # masses, so every slice reads the masses from a snapshot
     mass_in = mass.clone()
@@ -364,12 +423,22 @@ def _require_state(name: str, slot: Tensor, mass: Tensor) -> None:
         raise RuntimeError(f"{name}: slot and mass must be contiguous float32 tensors")
 
 
+def _check_ram_attn(op, w_addr, r_addr, x, gamma, slot, mass, mask, position_ids, slot_name="init_slot",
+                    mass_name="init_mass") -> None:
+    B, H, U, P, T = _dims(op, "w_addr", w_addr, 5)
+    C = _dims(op, "x", x, 4)[-1]
+    A = P ** U
+    _check_shapes(op, r_addr=(r_addr, (B, H, U, P, T)), x=(x, (B, H, T, C)), gamma=(gamma, (B, H, T)),
+                  mask=(mask, (B, T)), position_ids=(position_ids, (B, T)),
+                  **{slot_name: (slot, (B, H, A, C)), mass_name: (mass, (B, H, A))})
+
+
 def _ram_attn_call(w_addr, r_addr, x, gamma, mask, embed_num, position_ids, init_slot, init_mass, slot, mass,
                    w_top_k, r_top_k, w_re_norm, r_re_norm, mass_aware, eps):
     B, H, U, P, T = w_addr.shape
     C = x.shape[-1]
     A = P ** U
-    if r_addr.shape != w_addr.shape or r_addr.dtype != w_addr.dtype or x.dtype != w_addr.dtype:
+    if r_addr.dtype != w_addr.dtype or x.dtype != w_addr.dtype:
         raise RuntimeError("ram_attn_forward: w_addr, r_addr and x must share dtype and address shape")
     w_addr, r_addr = w_addr.contiguous(), r_addr.contiguous()
     x, gamma, mask = _segment_args(x, gamma, mask)
@@ -392,6 +461,7 @@ def ram_attn_forward(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tensor, i
                      eps: float) -> tuple[Tensor, Tensor, Tensor]:
     """Whole parallel forward (decoders + segment scan) returning y, new slot and mass."""
     _require_gpu("ram_attn_forward", w_addr, r_addr, x, gamma, init_slot, init_mass, position_ids, mask)
+    _check_ram_attn("ram_attn_forward", w_addr, r_addr, x, gamma, init_slot, init_mass, mask, position_ids)
     init_slot = init_slot.to(torch.float32).contiguous()
     init_mass = init_mass.to(torch.float32).contiguous()
     slot = torch.empty_like(init_slot)
@@ -414,6 +484,7 @@ def ram_attn_forward_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tensor, 
                       w_re_norm: float, r_re_norm: float, mass_aware: bool, eps: float) -> Tensor:
     """In-place whole parallel forward: updates slot and mass, returns y."""
     _require_gpu("ram_attn_forward_", w_addr, r_addr, x, gamma, slot, mass, position_ids, mask)
+    _check_ram_attn("ram_attn_forward_", w_addr, r_addr, x, gamma, slot, mass, mask, position_ids, "slot", "mass")
     _require_state("ram_attn_forward_", slot, mass)
     mass_in = mass.clone()  # see topk_segment_forward_
     return _ram_attn_call(w_addr, r_addr, x, gamma, mask, embed_num, position_ids, slot, mass_in, slot, mass,
@@ -433,11 +504,16 @@ def _(w_addr, r_addr, x, gamma, slot, mass, mask, embed_num, position_ids, w_top
 def topk_autoregressive_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
                          mask: Tensor, embed_num: int, position_ids: Tensor, w_top_k: int, r_top_k: int,
                          w_re_norm: float, r_re_norm: float, mass_aware: bool, eps: float) -> Tensor:
-    _require_gpu("topk_autoregressive_", w_addr, r_addr, x, gamma, slot, mass, position_ids)
-    _require_state("topk_autoregressive_", slot, mass)
-    B, H, U, P = w_addr.shape
-    C = x.shape[-1]
-    A = slot.shape[-2]
+    op = "topk_autoregressive_"
+    _require_gpu(op, w_addr, r_addr, x, gamma, slot, mass, position_ids)
+    B, H, U, P = _dims(op, "w_addr", w_addr, 4)
+    C = _dims(op, "x", x, 3)[-1]
+    A = _dims(op, "slot", slot, 4)[2]
+    _check_slots(op, U, P, A)
+    _check_shapes(op, r_addr=(r_addr, (B, H, U, P)), x=(x, (B, H, C)), gamma=(gamma, (B, H)),
+                  slot=(slot, (B, H, A, C)), mass=(mass, (B, H, A)), position_ids=(position_ids, (B,)),
+                  mask=(None if mask is None or mask.numel() == 0 else mask, (B,)))
+    _require_state(op, slot, mass)
     w_addr, r_addr, x = w_addr.contiguous(), r_addr.contiguous(), x.contiguous()
     gamma = gamma.to(dtype=x.dtype).contiguous()
     pos = position_ids.to(device=x.device, dtype=torch.int32).contiguous()

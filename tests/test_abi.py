@@ -66,7 +66,9 @@ def test_workspace_size_formula():
     lib = _native().lib()
     for B, H, T, kw, kr in ((8, 16, 4096, 8, 8), (1, 1, 1, 1, 1), (2, 3, 33, 4, 12), (1, 2, 0, 3, 3)):
         t_pad = (T + 31) // 32 * 32
-        want = B * H * t_pad * (kw * 16 + kr * 8) + 16 * (16 + 8)
+        # write records (16 B) and read records (8 B), then one 16-byte gain
+        # record per (event, token) for the precomputed-gain scan
+        want = B * H * t_pad * (kw * 16 + kr * 8) + B * H * t_pad * max(kw, kr) * 16
         assert lib.ramnet_scan_workspace_bytes64(B, H, T, kw, kr) == want
     assert lib.ramnet_scan_workspace_bytes(1 << 20, 64, 1 << 20, 8, 8) == -1  # > int32
 
@@ -194,10 +196,32 @@ def test_scan_plan_envelope():
     for A in (4, 16, 256, 1024, 2401, 4096, 6561, 8100, 8190):
         for C in (1, 7, 16, 100, 128, 512):
             for K in (1, 8, 16, 64, 100, 128):
-                plan = nat.segment_plan(A, C, K, K)
-                assert plan is not None, (A, C, K)
-                cs, lds = plan
-                assert 1 <= cs and 0 < lds <= 160 * 1024, (A, C, K, cs, lds)
-    assert nat.segment_plan(1024, 128, 8, 129) is None
-    assert nat.segment_plan(8192, 128, 8, 8) is None
-    assert nat.segment_plan(1024, 128, 4, 12) is not None  # Kw != Kr
+                for dtype in (torch.float32, torch.bfloat16):
+                    plan = nat.segment_plan(8, 16, A, C, K, K, dtype)
+                    assert plan is not None, (A, C, K, dtype)
+                    cs, lds, _ = plan
+                    assert 1 <= cs and 0 < lds <= 160 * 1024, (A, C, K, cs, lds)
+    assert nat.segment_plan(8, 16, 1024, 128, 8, 129) is None
+    assert nat.segment_plan(8, 16, 8192, 128, 8, 8) is None
+    assert nat.segment_plan(8, 16, 1024, 128, 4, 12) is not None  # Kw != Kr
+    assert nat.segment_plan(0, 16, 1024, 128, 8, 8) is None
+
+
+def test_scan_plan_follows_shape_and_override(monkeypatch):
+    """The query plans for the shape it is given: the activation width enters
+    the LDS footprint (the staged x rows), and a layout forced through
+    RAMNET_SCAN_LAYOUT -- which the launch honours too -- is what the query
+    reports, including its form; a layout that does not fit is refused."""
+    from ramnet_ops import _native as nat
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", "1,8,1,4")
+    f32 = nat.segment_plan(8, 16, 1024, 128, 8, 8, torch.float32)
+    bf16 = nat.segment_plan(8, 16, 1024, 128, 8, 8, torch.bfloat16)
+    assert f32[0] == bf16[0] and f32[1] > bf16[1]  # same slice, wider staged x
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", "1,16,1,2,1")
+    cs, lds, pre = nat.segment_plan(4, 8, 4096, 128, 16, 16, torch.bfloat16)
+    assert (cs, pre) == (2 * (64 // 16) * 1, True)
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", "1,8,1,4")
+    cs, lds, pre = nat.segment_plan(8, 16, 1024, 128, 8, 8, torch.bfloat16)
+    assert (cs, pre) == (4 * (64 // 8), False)
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", "1,8,1,4")
+    assert nat.segment_plan(8, 16, 1024, 128, 16, 16, torch.bfloat16) is None  # 8 event lanes < top-K 16
