@@ -1,0 +1,246 @@
+"""The exact paths ``bench.py`` times, at the benchmark configurations,
+against the CPU oracle.
+
+* Config 2: the record decoder (``ramnet_topk_addr_records``) followed by
+  ``ramnet_segment_scan``, called through the C ABI exactly as the benchmark
+  calls them (bf16, P=32, K=8, CAPE on 8 of 16 heads). Its per-event records
+  must equal, bit for bit, the records ``pack_records_kernel`` builds from
+  ``ramnet_topk_addr_forward``'s (idx, val) -- slot, weight and forget
+  coefficient -- and its per-token overlap flag must be set wherever the
+  packer's exact flag is (it may also be set where the packer's is not: a
+  wave's first lane assumes overlap). y, slot and mass on several heads
+  match the fp64 event loop.
+* Config 3: 16 consecutive decode steps at B=64, H=16 on the 64x16x1024x128
+  fp32 state, captured in one HIP graph as the benchmark captures them and
+  replayed; every step's indices against the fp64 ranking, and y of every
+  step plus the whole state of several (b, h) heads against the stepwise
+  fp64 event loop.
+* A scan only reads its records: two scans from one set of records give the
+  same bits, in the mass-wave form and in the precomputed-gain form.
+
+Bars: indices bit-exact except fp64 ties within 1e-6; fp32 state
+rel <= 1e-5; bf16 outputs rel <= 2e-2 (max|a-b| / max|b|).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from ram_cases import make_case, projected_logits
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+LOW_TOL = 2e-2
+DEV = "cuda"
+
+
+def _nat():
+    import ramnet_ops  # noqa: F401  (registers torch.ops.ramnet_ops.*)
+    from ramnet_ops import _native
+    _native.lib()
+    return _native
+
+
+def _records(ws: torch.Tensor, B: int, H: int, T: int, Kw: int, Kr: int):
+    """Views of a scan workspace: write records (B*H, Kw, T_pad, 4) and read
+    records (B*H, Kr, T_pad, 2), as int32 words."""
+    tp = (T + 31) // 32 * 32
+    wb = B * H * Kw * tp * 16
+    rb = B * H * Kr * tp * 8
+    w = ws[:wb].view(torch.int32).view(B * H, Kw, tp, 4)
+    r = ws[wb:wb + rb].view(torch.int32).view(B * H, Kr, tp, 2)
+    return w, r
+
+
+def test_config2_benched_path_matches_packed_records_and_oracle():
+    nat = _nat()
+    ops = torch.ops.ramnet_ops
+    B, H, U, P, T, C, K, E = 8, 16, 2, 32, 4096, 128, 8, 8
+    A = P ** U
+    print("config 2 benched path (record decoder + segment scan), full size", flush=True)
+    # the benchmark's inputs (bench.py make_prefill_inputs, config 2)
+    w, r = projected_logits(B, H, U, P, T, 128, seed=2, dtype=torch.float32)
+    w, r = w.to(torch.bfloat16), r.to(torch.bfloat16)
+    g = torch.Generator().manual_seed(102)
+    x = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16)
+    gamma = torch.sigmoid(torch.randn(B, H, T, generator=g) - 1.0).to(torch.bfloat16)
+    pos = torch.arange(T, dtype=torch.int32).view(1, T).expand(B, T).contiguous()
+    d = {k: v.to(DEV) for k, v in dict(w=w, r=r, x=x, gamma=gamma, pos=pos).items()}
+    slot0 = torch.zeros(B, H, A, C, device=DEV)
+    mass0 = torch.full((B, H, A), 1.0 / A, device=DEV)
+    n = nat.scan_workspace_bytes(B, H, T, K, K)
+    code = nat.DTYPE_CODES[torch.bfloat16]
+    stream = torch.cuda.current_stream().cuda_stream
+
+    # (a) the benchmark's two calls
+    ws_a = torch.empty(n, dtype=torch.uint8, device=DEV)
+    slot_a, mass_a, y_a = torch.empty_like(slot0), torch.empty_like(mass0), torch.empty_like(d["x"])
+    nat.call("ramnet_topk_addr_records", d["w"].data_ptr(), d["r"].data_ptr(), d["gamma"].data_ptr(), code, None,
+             E, d["pos"].data_ptr(), B, H, U, P, T, A, K, K, 0.0, 0.0, ws_a.data_ptr(), n, stream)
+    nat.call("ramnet_segment_scan", d["x"].data_ptr(), code, slot0.data_ptr(), mass0.data_ptr(), slot_a.data_ptr(),
+             mass_a.data_ptr(), y_a.data_ptr(), B, H, T, A, C, K, K, 0, 1e-12, ws_a.data_ptr(), n, stream)
+    # (b) decoder outputs, packed into records by the segment op
+    idx, val = ops.topk_addr_forward(d["w"], d["r"], E, A, d["pos"], K, K, 0.0, 0.0)
+    ws_b = torch.empty(n, dtype=torch.uint8, device=DEV)
+    slot_b, mass_b, y_b = torch.empty_like(slot0), torch.empty_like(mass0), torch.empty_like(d["x"])
+    nat.call("ramnet_topk_segment_forward", idx.data_ptr(), val.data_ptr(), d["x"].data_ptr(), d["gamma"].data_ptr(),
+             code, None, slot0.data_ptr(), mass0.data_ptr(), slot_b.data_ptr(), mass_b.data_ptr(), y_b.data_ptr(),
+             B, H, T, A, C, K, K, 0, 1e-12, ws_b.data_ptr(), n, stream)
+    torch.cuda.synchronize()
+
+    wa, ra = _records(ws_a, B, H, T, K, K)
+    wb, rb = _records(ws_b, B, H, T, K, K)
+    assert torch.equal(wa[..., :3], wb[..., :3]), "write records (slot, w, alpha) differ from the packed records"
+    assert torch.equal(ra, rb), "read records (slot, r) differ from the packed records"
+    fa, fb = wa[:, 0, :, 3], wb[:, 0, :, 3]  # event 0 carries the token's overlap flag
+    assert bool(((fa == 1) | (fb == 0)).all()), "record-mode overlap flag missing where the write sets overlap"
+    print(f"overlap flags: record mode {int(fa[:, :T].sum())}, exact {int(fb[:, :T].sum())} of {B * H * T} tokens",
+          flush=True)
+    # the flag only selects a reload: both scans give the same bits
+    assert torch.equal(y_a, y_b) and torch.equal(slot_a, slot_b) and torch.equal(mass_a, mass_b)
+
+    # indices on a token subset against the fp64 ranking
+    idx_c, val_c = idx.cpu(), val.cpu()
+    ts = slice(0, T, 61)
+    for lg, rows in ((w, slice(0, K)), (r, slice(K, 2 * K))):
+        oracle.check_topk_indices(idx_c[:, :, rows, ts], lg[..., ts], E, pos[:, ts].long(), K)
+    # outputs and state of CAPE and plain heads against the fp64 event loop
+    y_c, s_c, m_c = y_a.cpu(), slot_a.cpu(), mass_a.cpu()
+    for b, h in ((0, 0), (3, 7), (5, 8), (7, 15)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        wi, wv, ri, rv = oracle.split_events(idx_c[sl] - (b * H + h) * A, val_c[sl], K)
+        ry, rslot, rmass = oracle.sparse_gsu_f64(wi, wv, ri, rv, x[sl].double(), gamma[sl].double(),
+                                                 torch.zeros(1, 1, A, C), torch.full((1, 1, A), 1.0 / A),
+                                                 None, False, 1e-12, encoded=False)
+        assert oracle.rel_err(s_c[sl], rslot) <= FP32_TOL, f"slot (b={b}, h={h})"
+        assert oracle.rel_err(m_c[sl], rmass) <= FP32_TOL, f"mass (b={b}, h={h})"
+        assert oracle.rel_err(y_c[sl], ry) <= LOW_TOL, f"y (b={b}, h={h})"
+
+
+def test_config3_graph_captured_steps_match_oracle():
+    """Config 3 decode as the benchmark runs it (bench.py bench_decode): the
+    steps captured in one HIP graph, replayed on the persistent state."""
+    _nat()
+    ops = torch.ops.ramnet_ops
+    B, H, C, U, P, K, S = 64, 16, 128, 2, 32, 8, 16
+    A = P ** U
+    E = H // 2
+    print(f"config 3: {S} graph-captured decode steps at B={B}, H={H}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    slot = 0.5 * torch.randn(B, H, A, C, device=DEV, generator=g)
+    mass = torch.full((B, H, A), 1.0 / A, device=DEV)
+    d_k = 128
+    W = torch.randn(H, d_k, U * P, device=DEV, generator=g) / d_k ** 0.5
+    q = torch.randn(S, 2, B, H, d_k, device=DEV, generator=g)
+    lg = (torch.einsum('sqbhd,hdn->sqbhn', q, W) / U ** 0.5).to(torch.bfloat16).view(S, 2, B, H, U, P)
+    w_all, r_all = lg[:, 0].contiguous(), lg[:, 1].contiguous()
+    x_all = torch.randn(S, B, H, C, device=DEV, generator=g).to(torch.bfloat16)
+    g_all = torch.sigmoid(torch.randn(S, B, H, device=DEV, generator=g)).to(torch.bfloat16)
+    t0 = torch.randint(0, 8192, (B,), device=DEV, generator=g)
+    pos_all = (t0.view(1, B) + torch.arange(S, device=DEV).view(S, 1)).to(torch.int32).contiguous()
+    no_mask = torch.empty(0, dtype=torch.bool, device=DEV)
+    ys = []
+
+    def run_all():
+        ys.clear()
+        for s in range(S):
+            ys.append(ops.topk_autoregressive_(w_all[s], r_all[s], x_all[s], g_all[s], slot, mass, no_mask, E,
+                                               pos_all[s], K, K, 0.0, 0.0, False, 1e-12))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run_all()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_all()
+    torch.cuda.synchronize()
+
+    heads = ((0, 0), (17, 5), (33, 8), (63, 15), (40, 12))
+    sel = lambda t: torch.stack([t[b, h] for b, h in heads]).unsqueeze(1).cpu()  # (n, 1, ...)
+    slot_before, mass_before = sel(slot), sel(mass)
+    graph.replay()
+    torch.cuda.synchronize()
+    y_steps = torch.stack([y.cpu() for y in ys], dim=2)  # (B, H, S, C)
+    slot_after, mass_after = sel(slot), sel(mass)
+
+    # every step's indices (all B x H addresses) against the fp64 ranking;
+    # the same decoder gives the events of the heads checked below
+    wi, wv, ri, rv = [], [], [], []
+    for s in range(S):
+        for lgs, ii, vv in ((w_all[s], wi, wv), (r_all[s], ri, rv)):
+            idx, val = ops.topk_addr_single_forward(lgs.unsqueeze(-1), E, A, pos_all[s].view(B, 1), K, 0.0, False,
+                                                    False)
+            oracle.check_topk_indices(idx.cpu(), lgs.unsqueeze(-1).cpu(), E, pos_all[s].view(B, 1).cpu().long(), K,
+                                      encode_batch_idx=False)
+            local = idx.cpu() - (torch.arange(H) * A).view(1, H, 1, 1)
+            ii.append(sel(local)[..., 0])
+            vv.append(sel(val)[..., 0])
+    stack = lambda lst: torch.stack(lst, dim=-1)  # (n, 1, K, S)
+    xs = torch.stack([sel(x_all[s]) for s in range(S)], dim=2).double()  # (n, 1, S, C)
+    gs = torch.stack([sel(g_all[s]) for s in range(S)], dim=-1).double()  # (n, 1, S)
+    ry, rslot, rmass = oracle.sparse_gsu_f64(stack(wi), stack(wv), stack(ri), stack(rv), xs, gs, slot_before,
+                                             mass_before, None, False, 1e-12, encoded=False)
+    ry = torch.as_tensor(ry)
+    y_sel = sel(y_steps)  # (n, 1, S, C)
+    for s in range(S):
+        err = oracle.rel_err(y_sel[:, :, s], ry[:, :, s])
+        assert err <= LOW_TOL, f"y of step {s}: rel err {err:.3e}"
+    assert oracle.rel_err(slot_after, rslot) <= FP32_TOL, "slot state after the captured steps"
+    assert oracle.rel_err(mass_after, rmass) <= FP32_TOL, "mass state after the captured steps"
+    touched = (slot_after != slot_before).any(-1)
+    print(f"rows changed per checked head: {touched.sum(-1).flatten().tolist()}", flush=True)
+
+
+@pytest.mark.parametrize("layout,pre", [("1,16,1,1", False), ("1,16,1,2,1", True)],
+                         ids=["mass_wave", "precomputed_gains"])
+def test_scan_reads_records_only(layout, pre, monkeypatch):
+    """``ramnet_segment_scan`` run twice on one set of records from
+    ``ramnet_topk_addr_records`` gives identical outputs, and both match the
+    fp64 event loop: the precomputed-gain form writes its gains to its own
+    part of the workspace, never into the decoder records."""
+    nat = _nat()
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", layout)
+    B, H, U, P, T, C, K, E = 2, 2, 3, 16, 700, 64, 8, 1
+    A = P ** U
+    plan = nat.segment_plan(B, H, A, C, K, K, torch.bfloat16)
+    assert plan is not None and plan[2] == pre, plan
+    print(f"scan twice from one record set, layout {layout} {plan}", flush=True)
+    case = make_case(B, H, U, P, T, C, dtype=torch.bfloat16, seed=71, masked=True)
+    d = case.to(DEV)
+    pos = d.position_ids.to(torch.int32).contiguous()
+    mask = d.mask.to(torch.uint8).contiguous()
+    n = nat.scan_workspace_bytes(B, H, T, K, K)
+    ws = torch.empty(n, dtype=torch.uint8, device=DEV)
+    code = nat.DTYPE_CODES[torch.bfloat16]
+    stream = torch.cuda.current_stream().cuda_stream
+    nat.call("ramnet_topk_addr_records", d.w_addr.data_ptr(), d.r_addr.data_ptr(), d.gamma.data_ptr(), code,
+             mask.data_ptr(), E, pos.data_ptr(), B, H, U, P, T, A, K, K, 0.0, 0.0, ws.data_ptr(), n, stream)
+    w0, r0 = (t.clone() for t in _records(ws, B, H, T, K, K))
+    outs = []
+    for _ in range(2):
+        slot, mass, y = torch.empty_like(d.init_slot), torch.empty_like(d.init_mass), torch.empty_like(d.values)
+        nat.call("ramnet_segment_scan", d.values.data_ptr(), code, d.init_slot.data_ptr(), d.init_mass.data_ptr(),
+                 slot.data_ptr(), mass.data_ptr(), y.data_ptr(), B, H, T, A, C, K, K, 0, 1e-12, ws.data_ptr(), n,
+                 stream)
+        outs.append((y, slot, mass))
+    torch.cuda.synchronize()
+    w1, r1 = _records(ws, B, H, T, K, K)
+    assert torch.equal(w0, w1) and torch.equal(r0, r1), "the scan modified the decoder records"
+    for a, b in zip(*outs):
+        assert torch.equal(a, b), "second scan of the same records differs"
+    # the events those records hold, from the decoder op on the same inputs
+    idx, val = torch.ops.ramnet_ops.topk_addr_forward(d.w_addr, d.r_addr, E, A, d.position_ids, K, K, 0.0, 0.0)
+    wi, wv, ri, rv = oracle.split_events(idx.cpu(), val.cpu(), K)
+    ry, rslot, rmass = oracle.sparse_gsu_f64(wi, wv, ri, rv, case.values.double(), case.gamma.double(),
+                                             case.init_slot, case.init_mass, case.mask)
+    y, slot, mass = (t.cpu() for t in outs[0])
+    keep = case.mask[0]
+    assert bool((y[:, :, ~keep] == 0).all())
+    assert oracle.rel_err(slot, rslot) <= FP32_TOL
+    assert oracle.rel_err(mass, rmass) <= FP32_TOL
+    assert oracle.rel_err(y[:, :, keep], torch.as_tensor(ry)[:, :, keep]) <= LOW_TOL

@@ -173,3 +173,82 @@ def test_harness_training_step():
         fd = (lp - lm) / (2 * eps)
         print(f"  directional derivative {slope:.6e}, central difference {fd:.6e}", flush=True)
         assert abs(fd - slope) <= 2e-2 * abs(slope)
+
+
+def _c5_model():
+    """Config 5: 24 blocks, d_model 1024, 8 heads of d_v 128, U=2, P=32, K=8,
+    CAPE on 4 heads, SwiGLU 2816, vocab 32000, bf16, random init."""
+    from ramnet_harness import HarnessConfig, RamLM
+    cfg = HarnessConfig(vocab=32000, layers=24, d_model=1024, heads=8, value_chs=128, addr_order=2, addr_radix=32,
+                        top_k=8, embed_num=4, mlp_width=2816, dtype=torch.bfloat16)
+    torch.manual_seed(5)
+    model = RamLM(cfg)
+    model.init_weights()
+    return cfg, model.to(device=DEV, dtype=torch.bfloat16).eval()
+
+
+def _layer_check(cap, state_after, cfg, heads, label, t_sub):
+    """One layer's operator call, from the inputs the model produced: the
+    decoder's indices on a token subset of every head against the fp64
+    ranking (near ties exempt), then y and the post state of ``heads``
+    against the fp64 event loop on the decoder's selection."""
+    ops = torch.ops.ramnet_ops
+    to_b = lambda t: t.permute(0, 2, 3, 4, 1).contiguous()  # (B, T, H, U, P) -> (B, H, U, P, T)
+    w, r = to_b(cap["w"]), to_b(cap["r"])
+    B, H, U, P, T = w.shape
+    A, K, E = cfg.slots, cfg.top_k, cfg.embed_num
+    pos = cap["pos"].to(torch.int32).contiguous()
+    idx, val = ops.topk_addr_forward(w, r, E, A, pos, K, K, 0.0, 0.0)
+    idx_c, val_c, pos_c = idx.cpu(), val.cpu(), pos.cpu().long()
+    for lg, rows in ((w, slice(0, K)), (r, slice(K, 2 * K))):
+        oracle.check_topk_indices(idx_c[:, :, rows, t_sub], lg.cpu().float()[..., t_sub], E, pos_c[:, t_sub], K)
+    v = cap["v"].permute(0, 2, 1, 3).cpu()  # (B, H, T, C)
+    g = cap["g"].permute(0, 2, 1).cpu()     # (B, H, T)
+    y = cap["y"].permute(0, 2, 1, 3).cpu()
+    slot0 = None if cap["slot"] is None else cap["slot"]
+    mass0 = cap["mass"]
+    for b, h in heads:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        s_in = torch.zeros(1, 1, A, cfg.value_chs) if slot0 is None else slot0[sl].cpu()
+        m_in = torch.full((1, 1, A), 1.0 / A) if not isinstance(mass0, torch.Tensor) else mass0[sl].cpu()
+        wi, wv, ri, rv = oracle.split_events(idx_c[sl] - (b * H + h) * A, val_c[sl], K)
+        ry, rslot, rmass = oracle.sparse_gsu_f64(wi, wv, ri, rv, v[sl].double(), g[sl].double(), s_in, m_in, None,
+                                                 False, cfg.ram_eps, encoded=False)
+        assert oracle.rel_err(state_after[0][sl].cpu(), rslot) <= FP32_TOL, f"{label}: slot (b={b}, h={h})"
+        assert oracle.rel_err(state_after[1][sl].cpu(), rmass) <= FP32_TOL, f"{label}: mass (b={b}, h={h})"
+        assert oracle.rel_err(y[sl], torch.as_tensor(ry)) <= 2e-2, f"{label}: y (b={b}, h={h})"
+
+
+@pytest.mark.gpu
+def test_config5_scale_layers_match_oracle():
+    """Config 5 at its size (decision D11: parity per layer at the operator
+    boundary): the 24-block bf16 model prefills a 16 x 2048 prompt, then
+    takes two greedy in-place decode steps. For the first and the last layer,
+    the operator inputs the model produced are captured and the layer's
+    output and state are checked against the oracle on several heads (CAPE
+    and plain), with every head's indices checked against the fp64 ranking."""
+    cfg, model = _c5_model()
+    B, T, L = 16, 2048, cfg.layers
+    print(f"config 5 at scale: {L} blocks, prompt {B} x {T}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    prompt = torch.randint(0, cfg.vocab, (B, T), device=DEV, generator=g)
+    pos = torch.arange(T, device=DEV).view(1, T).expand(B, T)
+    heads = ((0, 0), (7, 3), (15, 4), (9, 7))
+    with torch.no_grad():
+        cap = []
+        logits, states = model(prompt, model.fresh_state(B, DEV), pos, inplace=False, capture=cap)
+        torch.cuda.synchronize()
+        assert len(cap) == L
+        for layer in (0, L - 1):
+            _layer_check(cap[layer], states[layer], cfg, heads, f"prefill layer {layer}", slice(0, T, 97))
+        del cap
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        for s in range(2):
+            cap = []
+            p = torch.full((B, 1), T + s, device=DEV, dtype=torch.long)
+            logits, states = model(tok, states, p, inplace=True, capture=cap)
+            torch.cuda.synchronize()
+            for layer in (0, L - 1):
+                _layer_check(cap[layer], states[layer], cfg, heads, f"decode step {s} layer {layer}", slice(None))
+            tok = logits[:, -1].argmax(-1, keepdim=True)
+    assert all(bool(torch.isfinite(sl).all()) for sl, _ in states)
