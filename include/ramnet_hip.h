@@ -235,6 +235,29 @@ int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const vo
                                 int64_t C, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
                                 int mass_aware, float eps, void *y, void *stream);
 
+/* Bytes of the per-GPU scratch of ramnet_ram_attn_forward_noalloc (128 MiB). */
+#define RAMNET_NOALLOC_SCRATCH_BYTES (128LL << 20)
+
+/*
+ * ramnet_ram_attn_forward without a workspace argument. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It allocates nothing: the per-event records live in a
+ * file-scope device array of RAMNET_NOALLOC_SCRATCH_BYTES, one per GPU the
+ * library runs on, held until the process ends. A shape whose records
+ * (B*H*T_pad*(16*w_top_k + 8*r_top_k) bytes, plus B*H*T_pad*16*max(w_top_k,
+ * r_top_k) when the scan uses the precomputed-gain form) exceed it returns
+ * RAMNET_EINVAL. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race, and the caller
+ * must order them. Other arguments and results as ramnet_ram_attn_forward.
+ */
+int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, const void *x, const void *gamma,
+                                    int dtype, const uint8_t *mask, int64_t embed_num, const int32_t *position_ids,
+                                    const float *init_slot, const float *init_mass, float *slot_out, float *mass_out,
+                                    void *y, int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int64_t A,
+                                    int64_t C, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
+                                    int mass_aware, float eps, void *stream);
+
 /*
  * Planning query (no device work beyond reading the device's CU count): the
  * layout a segment-scan launch of this shape uses on the current device --

@@ -6,6 +6,8 @@
 #include "ramnet_kernels.hpp"
 #include "ramnet_search.hpp"
 
+#include <atomic>
+#include <mutex>
 #include <stdio.h>
 #include <string>
 
@@ -358,11 +360,12 @@ int ramnet_topk_segment_forward_(const int32_t *addr_idx, const float *addr_val,
                                 "topk_segment_forward_ launch");
 }
 
-int ramnet_topk_addr_records(const void *w_addr, const void *r_addr, const void *gamma, int dtype,
-                              const uint8_t *mask, int64_t embed_num, const int32_t *position_ids, int64_t B,
-                              int64_t H, int64_t U, int64_t P, int64_t T, int64_t A, int64_t w_top_k, int64_t r_top_k,
-                              float w_re_norm, float r_re_norm, void *workspace, int64_t workspace_bytes,
-                              void *stream) {
+// Bodies of the record decoder, the scan and the fused forward; `need` is
+// the workspace the calling entry point requires (-1: the scan workspace).
+static int addr_records(const void *w_addr, const void *r_addr, const void *gamma, int dtype, const uint8_t *mask,
+                        int64_t embed_num, const int32_t *position_ids, int64_t B, int64_t H, int64_t U, int64_t P,
+                        int64_t T, int64_t A, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
+                        void *workspace, int64_t workspace_bytes, int64_t need, void *stream) {
     if (int rc = check_addr_shape(B, H, U, P, T, embed_num, A))
         return rc;
     RAMNET_REQUIRE(valid_dtype(dtype), "addr dtype must be float32, float16 or bfloat16");
@@ -371,8 +374,9 @@ int ramnet_topk_addr_records(const void *w_addr, const void *r_addr, const void 
                    "top_k_re_norm exponents must be in [0, 1]");
     RAMNET_REQUIRE(fits_int({B * H * U * P * T, B * H * (T + ramnet::kScanPad) * (w_top_k + r_top_k)}),
                    "CUDA index overflow: sizes exceed int32");
-    RAMNET_REQUIRE(workspace_bytes >= scan_workspace_bytes(B, H, T, w_top_k, r_top_k) && workspace,
-                   "workspace too small: see ramnet_scan_workspace_bytes");
+    if (need < 0)
+        need = scan_workspace_bytes(B, H, T, w_top_k, r_top_k);
+    RAMNET_REQUIRE(workspace_bytes >= need && workspace, "workspace too small: see ramnet_scan_workspace_bytes");
     if (B * T == 0)
         return RAMNET_OK;
     RAMNET_REQUIRE(w_addr && r_addr && gamma && position_ids, "null tensor pointer");
@@ -402,12 +406,12 @@ int ramnet_topk_addr_records(const void *w_addr, const void *r_addr, const void 
     return finish(err, why, "topk_addr_records launch");
 }
 
-int ramnet_segment_scan(const void *x, int dtype, const float *init_slot, const float *init_mass, float *slot_out,
+static int segment_scan(const void *x, int dtype, const float *init_slot, const float *init_mass, float *slot_out,
                         float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
                         int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *workspace,
-                        int64_t workspace_bytes, void *stream) {
+                        int64_t workspace_bytes, int64_t need, void *stream) {
     if (int rc = segment_checks(x, x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k,
-                                r_top_k, eps, workspace, workspace_bytes))
+                                r_top_k, eps, workspace, workspace_bytes, need))
         return rc;
     if (B == 0)
         return RAMNET_OK;
@@ -418,23 +422,50 @@ int ramnet_segment_scan(const void *x, int dtype, const float *init_slot, const 
     return finish(err, why, "segment_scan launch");
 }
 
+static int ram_attn_forward(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
+                            const uint8_t *mask, int64_t embed_num, const int32_t *position_ids,
+                            const float *init_slot, const float *init_mass, float *slot_out, float *mass_out, void *y,
+                            int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int64_t A, int64_t C,
+                            int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm, int mass_aware,
+                            float eps, void *workspace, int64_t workspace_bytes, int64_t need, void *stream) {
+    if (int rc = segment_checks(x, gamma, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k,
+                                r_top_k, eps, workspace, workspace_bytes, need))
+        return rc;
+    if (B > 0 && T > 0) {
+        if (int rc = addr_records(w_addr, r_addr, gamma, dtype, mask, embed_num, position_ids, B, H, U, P, T, A,
+                                  w_top_k, r_top_k, w_re_norm, r_re_norm, workspace, workspace_bytes, need, stream))
+            return rc;
+    }
+    return segment_scan(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k, r_top_k,
+                        mass_aware, eps, workspace, workspace_bytes, need, stream);
+}
+
+int ramnet_topk_addr_records(const void *w_addr, const void *r_addr, const void *gamma, int dtype,
+                             const uint8_t *mask, int64_t embed_num, const int32_t *position_ids, int64_t B, int64_t H,
+                             int64_t U, int64_t P, int64_t T, int64_t A, int64_t w_top_k, int64_t r_top_k,
+                             float w_re_norm, float r_re_norm, void *workspace, int64_t workspace_bytes,
+                             void *stream) {
+    return addr_records(w_addr, r_addr, gamma, dtype, mask, embed_num, position_ids, B, H, U, P, T, A, w_top_k,
+                        r_top_k, w_re_norm, r_re_norm, workspace, workspace_bytes, -1, stream);
+}
+
+int ramnet_segment_scan(const void *x, int dtype, const float *init_slot, const float *init_mass, float *slot_out,
+                        float *mass_out, void *y, int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                        int64_t w_top_k, int64_t r_top_k, int mass_aware, float eps, void *workspace,
+                        int64_t workspace_bytes, void *stream) {
+    return segment_scan(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k, r_top_k,
+                        mass_aware, eps, workspace, workspace_bytes, -1, stream);
+}
+
 int ramnet_ram_attn_forward(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
                             const uint8_t *mask, int64_t embed_num, const int32_t *position_ids,
                             const float *init_slot, const float *init_mass, float *slot_out, float *mass_out, void *y,
                             int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int64_t A, int64_t C,
                             int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm, int mass_aware,
                             float eps, void *workspace, int64_t workspace_bytes, void *stream) {
-    if (int rc = segment_checks(x, gamma, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k,
-                                r_top_k, eps, workspace, workspace_bytes))
-        return rc;
-    if (B > 0 && T > 0) {
-        if (int rc = ramnet_topk_addr_records(w_addr, r_addr, gamma, dtype, mask, embed_num, position_ids, B, H, U, P,
-                                              T, A, w_top_k, r_top_k, w_re_norm, r_re_norm, workspace,
-                                              workspace_bytes, stream))
-            return rc;
-    }
-    return ramnet_segment_scan(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k, r_top_k,
-                               mass_aware, eps, workspace, workspace_bytes, stream);
+    return ram_attn_forward(w_addr, r_addr, x, gamma, dtype, mask, embed_num, position_ids, init_slot, init_mass,
+                            slot_out, mass_out, y, B, H, U, P, T, A, C, w_top_k, r_top_k, w_re_norm, r_re_norm,
+                            mass_aware, eps, workspace, workspace_bytes, -1, stream);
 }
 
 static int64_t backward_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t Kw,
@@ -555,6 +586,80 @@ int ramnet_segment_plan(int64_t B, int64_t H, int64_t A, int64_t C, int64_t w_to
     return ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(A), static_cast<int>(C),
                                 static_cast<int>(w_top_k), static_cast<int>(r_top_k), dtype, slice_channels,
                                 lds_bytes, precomputed_gains);
+}
+
+// ---- prefill forward without a workspace argument
+//
+// The per-event records (and the gain records of the precomputed-gain form)
+// live in `scratch`, one copy per GPU, held by the loaded code object until
+// the process ends. Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in): each device's address comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+// Nothing in it needs to start at zero: the record decoder writes every
+// record the scan reads. Calls on one GPU share that GPU's copy.
+static __device__ __align__(256) unsigned char scratch[RAMNET_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::atomic<void *> g_scratch[kScratchDevices];
+std::mutex g_scratch_mu;
+
+int scratch_address(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return fail(RAMNET_ELAUNCH, std::string("ram_attn_forward_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+    RAMNET_REQUIRE(dev >= 0 && dev < kScratchDevices, "ram_attn_forward_noalloc: device ordinal beyond 63");
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p)
+                return fail(RAMNET_ELAUNCH, std::string("ram_attn_forward_noalloc: hipGetSymbolAddress(scratch): ") +
+                                                hipGetErrorString(e));
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return RAMNET_OK;
+}
+}  // namespace
+
+int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, const void *x, const void *gamma,
+                                    int dtype, const uint8_t *mask, int64_t embed_num, const int32_t *position_ids,
+                                    const float *init_slot, const float *init_mass, float *slot_out, float *mass_out,
+                                    void *y, int64_t B, int64_t H, int64_t U, int64_t P, int64_t T, int64_t A,
+                                    int64_t C, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
+                                    int mass_aware, float eps, void *stream) {
+    void *ws = nullptr;
+    int64_t need = 0;
+    // sizes the scan's own checks accept (anything else fails there first)
+    const bool plausible = B > 0 && H > 0 && T > 0 && C > 0 && A > 0 && A < kAddressLimit && w_top_k > 0 &&
+                           r_top_k > 0 && w_top_k <= A && r_top_k <= A && valid_dtype(dtype) &&
+                           fits_int({B * H * A * C, B * H * (A + 2), B * H * T * C,
+                                     B * H * (T + ramnet::kScanPad) * (w_top_k + r_top_k)});
+    if (plausible) {
+        int pre = 0;
+        RAMNET_REQUIRE(ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(A),
+                                            static_cast<int>(C), static_cast<int>(w_top_k), static_cast<int>(r_top_k),
+                                            dtype, nullptr, nullptr, &pre),
+                       "segment forward: shape outside the LDS-resident scan (A <= 8190 and top_k <= 128)");
+        // the decoder records, then the gain records if the launch uses them
+        need = ramnet::scan_record_bytes(B, H, T, w_top_k, r_top_k) +
+               (pre ? ramnet::scan_gain_bytes(B, H, T, w_top_k, r_top_k) : 0);
+        if (need > RAMNET_NOALLOC_SCRATCH_BYTES)
+            return fail(RAMNET_EINVAL, "ram_attn_forward_noalloc: this shape needs " + std::to_string(need) +
+                                           " bytes of records, more than the " +
+                                           std::to_string(static_cast<long long>(RAMNET_NOALLOC_SCRATCH_BYTES)) +
+                                           "-byte scratch; use ramnet_ram_attn_forward with a workspace");
+        if (int rc = scratch_address(&ws))
+            return rc;
+    }
+    return ram_attn_forward(w_addr, r_addr, x, gamma, dtype, mask, embed_num, position_ids, init_slot, init_mass,
+                            slot_out, mass_out, y, B, H, U, P, T, A, C, w_top_k, r_top_k, w_re_norm, r_re_norm,
+                            mass_aware, eps, ws, RAMNET_NOALLOC_SCRATCH_BYTES, need, stream);
 }
 
 }  // extern "C"
