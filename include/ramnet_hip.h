@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define RAMNET_ABI_VERSION 2
+#define RAMNET_ABI_VERSION 3
 
 enum {
     RAMNET_OK = 0,
@@ -234,6 +234,27 @@ int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const vo
                                 const int32_t *position_ids, int64_t B, int64_t H, int64_t U, int64_t P, int64_t A,
                                 int64_t C, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
                                 int mass_aware, float eps, void *y, void *stream);
+
+/*
+ * S consecutive decode steps in one call, the same as S calls of
+ * ramnet_topk_autoregressive_ on the step slices of the inputs. No
+ * counterpart in the reference: a multi-step form of topk_autoregressive_
+ * for callers that hold the inputs of several steps at once (replay,
+ * benchmarking, speculative verification). Shapes that take the half-wave
+ * fast path (P <= 32, top-k <= 11, C <= 256) run as one persistent launch
+ * in which step s + 1's addresses are decoded while step s's rows are in
+ * flight; other shapes run one launch per step.
+ *   w_addr, r_addr  (S, B, H, U, P) `dtype`;  x (S, B, H, C);  gamma (S, B, H)
+ *   position_ids    (S, B) int32;  mask (S, B) uint8/bool or NULL
+ *   slot, mass      (B, H, A, C), (B, H, A) fp32, read-modify-write
+ *   y               (S, B, H, C) `dtype`
+ */
+int ramnet_topk_autoregressive_steps_(const void *w_addr, const void *r_addr, const void *x, const void *gamma,
+                                      int dtype, float *slot, float *mass, const uint8_t *mask, int64_t embed_num,
+                                      const int32_t *position_ids, int64_t S, int64_t B, int64_t H, int64_t U,
+                                      int64_t P, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k,
+                                      float w_re_norm, float r_re_norm, int mass_aware, float eps, void *y,
+                                      void *stream);
 
 /* Bytes of the per-GPU scratch of ramnet_ram_attn_forward_noalloc (128 MiB). */
 #define RAMNET_NOALLOC_SCRATCH_BYTES (128LL << 20)

@@ -73,16 +73,360 @@ __device__ __forceinline__ float lane_f(float v, int L) {
 }
 __device__ __forceinline__ int lane_i(int v, int L) { return __builtin_amdgcn_readlane(v, L); }
 
-// FULLC: C == 64 * kCpl, so every lane owns kCpl real channels.
-// Events live one per lane: write event k on lane k, read event k on lane
-// RB + k (RB = 32 when the two addresses share the wave as half-waves, else
-// 0 with separate registers). The event math (mass, alpha, gain) runs lane
-// parallel; each row's scalars are then broadcast with v_readlane. Rows and
-// masses of one (b, h) are addressed through buffer resources (32-bit
-// offsets; the launcher keeps A * C * 4 below 2^31).
-template<typename T, int GW, int KE, int kCpl, bool FULLC>
-__global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob job) {
+// Channels of one lane. FULLC (C == 64 * kCpl, pointers aligned to the
+// vector width): the kCpl consecutive channels lane * kCpl ..., moved with
+// one vector access per row. Otherwise channels lane + 64 j, clamped into
+// the row, one dword each. coff[j] is channel j's byte offset in a row (for
+// FULLC only coff[0] is used).
+template<int kCpl, bool FULLC>
+__device__ __forceinline__ void lane_channels(int lane, int C, int *coff) {
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j) {
+        const int c = FULLC ? lane * kCpl + j : lane + j * kWave;
+        coff[j] = (FULLC || c < C ? c : C - 1) * 4;
+    }
+}
+template<int kCpl, bool FULLC>
+__device__ __forceinline__ bool owns(int lane, int j, int C) {
+    return FULLC || lane + j * kWave < C;
+}
+
+template<int kCpl, bool FULLC>
+__device__ __forceinline__ void row_load(__amdgpu_buffer_rsrc_t r, const int *coff, int so, float *v) {
+    if constexpr (FULLC && kCpl == 2) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b64(r, coff[0], so, 0);
+        v[0] = __uint_as_float(q[0]);
+        v[1] = __uint_as_float(q[1]);
+    } else if constexpr (FULLC && kCpl == 4) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(r, coff[0], so, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            v[j] = __uint_as_float(q[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j)
+            v[j] = buf_load_f32(r, coff[j], so);
+    }
+}
+template<int kCpl, bool FULLC>
+__device__ __forceinline__ void row_store(const float *v, __amdgpu_buffer_rsrc_t r, const int *coff, int so, int lane,
+                                          int C) {
+    if constexpr (FULLC && kCpl == 2) {
+        using u2 = __attribute__((ext_vector_type(2))) unsigned int;
+        const u2 q = {__float_as_uint(v[0]), __float_as_uint(v[1])};
+        __builtin_amdgcn_raw_buffer_store_b64(q, r, coff[0], so, 0);
+    } else if constexpr (FULLC && kCpl == 4) {
+        using u4 = __attribute__((ext_vector_type(4))) unsigned int;
+        const u4 q = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(q, r, coff[0], so, 0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j)
+            if (owns<kCpl, FULLC>(lane, j, C))
+                buf_store_f32(v[j], r, coff[j], so);
+    }
+}
+
+// Storage bits of one lane's kCpl values of x, converted when read (a
+// prefetch waits for nothing until the values are used).
+template<typename T, int kCpl, bool FULLC>
+struct XRaw {
+    static constexpr int kWords = FULLC ? (kCpl * static_cast<int>(sizeof(T)) + 3) / 4 : kCpl;
+    uint32_t w[kWords];
+
+    __device__ __forceinline__ void load(const T *row, const int *coff, int lane) {
+        if constexpr (FULLC) {
+            const uint32_t *p = reinterpret_cast<const uint32_t *>(row + lane * kCpl);
+            if constexpr (kWords == 1) {
+                w[0] = *p;
+            } else if constexpr (kWords == 2) {
+                const uint2 q = *reinterpret_cast<const uint2 *>(p);
+                w[0] = q.x;
+                w[1] = q.y;
+            } else {
+                const uint4 q = *reinterpret_cast<const uint4 *>(p);
+                w[0] = q.x;
+                w[1] = q.y;
+                w[2] = q.z;
+                w[3] = q.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j)
+                w[j] = load_bits(row + coff[j] / 4);
+        }
+    }
+    __device__ __forceinline__ float get(int j) const {
+        if constexpr (FULLC && sizeof(T) == 2)
+            return bits_f32<T>((j & 1) ? w[j / 2] >> 16 : w[j / 2] & 0xffffu);
+        else
+            return bits_f32<T>(w[j]);
+    }
+};
+
+template<typename T>
+__device__ __forceinline__ uint32_t f32_storage_bits(float v) {
+    if constexpr (sizeof(T) == 4)
+        return __float_as_uint(v);
+    else if constexpr (__is_same(T, bf16_t))
+        return f32_to_bf16_bits(v);
+    else
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// y of one lane's channels, in T.
+template<typename T, int kCpl, bool FULLC>
+__device__ __forceinline__ void store_y(T *row, const float *v, int lane, int C) {
+    if constexpr (FULLC) {
+        uint32_t *p = reinterpret_cast<uint32_t *>(row + lane * kCpl);
+        if constexpr (sizeof(T) == 4) {
+            if constexpr (kCpl == 2)
+                *reinterpret_cast<uint2 *>(p) = make_uint2(__float_as_uint(v[0]), __float_as_uint(v[1]));
+            else
+                *reinterpret_cast<uint4 *>(p) = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                           __float_as_uint(v[2]), __float_as_uint(v[3]));
+        } else {
+            uint32_t q[kCpl / 2];
+#pragma unroll
+            for (int i = 0; i < kCpl / 2; ++i)
+                q[i] = f32_storage_bits<T>(v[2 * i]) | (f32_storage_bits<T>(v[2 * i + 1]) << 16);
+            if constexpr (kCpl == 2)
+                *p = q[0];
+            else
+                *reinterpret_cast<uint2 *>(p) = make_uint2(q[0], q[1]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j)
+            if (owns<kCpl, FULLC>(lane, j, C))
+                store_f32(row + lane + j * kWave, v[j]);
+    }
+}
+
+// The fast path in four stages, shared by the single-step kernel and the
+// multi-step kernel. Events live one per lane: write event k on lane k, read
+// event k on lane RB + k (RB = 32 when the two addresses share the wave as
+// half-waves, else 0 with separate registers). The event math (mass, alpha,
+// gain) runs lane parallel; each row's scalars are then broadcast with
+// v_readlane. Rows and masses of one (b, h) are addressed through buffer
+// resources (32-bit offsets; the launcher keeps A * C * 4 below 2^31).
+template<int KE, int kCpl>
+struct StepState {
+    int ow, orr;             // write / read event slot of this lane
+    float vw, vr;            // their weights
+    float emw, emr;          // their pre-step masses
+    int fwd[KE];             // write event on read k's slot, or -1
+    bool any_fwd;            // some read takes a row this step writes
+    float wrow[KE][kCpl];    // pre-step rows of the write events
+    float rrow[KE][kCpl];    // pre-step rows of the read events
+};
+
+// Stage 1: decode both addresses into per-lane events and the LDS slot
+// tables (s_ws/s_rs/s_wv) that stage 3 reads.
+template<typename T, int GW, int KE, int kCpl>
+__device__ __forceinline__ void decode_events(const DecodeJob &job, const GroupLogits<T> &lw,
+                                              const GroupLogits<T> &lr, int shift, int lane, int *s_ws, int *s_rs,
+                                              float *s_wv, StepState<KE, kCpl> &st) {
+    const int A = job.A, U = job.U, P = job.P, Kw = job.Kw, Kr = job.Kr;
+    float v;
+    int c;
+    if constexpr (GW == 32) {
+        const int half = lane >> 5, li = lane & 31;
+        const int K = half ? Kr : Kw;
+        const bool inactive = group_search<T, 32>(lw, U, P, K, li, v, c);
+        lane_event(v, c, inactive, K, half ? job.r_re_norm : job.w_re_norm, li, half * 32, shift, A, st.ow, st.vw);
+        st.orr = st.ow;
+        st.vr = st.vw;
+        if (li < KE) {
+            (half ? s_rs : s_ws)[li] = st.ow;
+            if (!half)
+                s_wv[li] = st.vw;
+        }
+    } else {
+        bool inactive = group_search<T, 64>(lw, U, P, Kw, lane, v, c);
+        lane_event(v, c, inactive, Kw, job.w_re_norm, lane, 0, shift, A, st.ow, st.vw);
+        inactive = group_search<T, 64>(lr, U, P, Kr, lane, v, c);
+        lane_event(v, c, inactive, Kr, job.r_re_norm, lane, 0, shift, A, st.orr, st.vr);
+        if (lane < KE) {
+            s_ws[lane] = st.ow;
+            s_wv[lane] = st.vw;
+            s_rs[lane] = st.orr;
+        }
+    }
+}
+
+// Stage 2: one batch of requests for the events' masses and rows (row k's
+// offset is a scalar). Loads come from clamped in-bounds slots, unguarded.
+template<int GW, int KE, int kCpl, bool FULLC>
+__device__ __forceinline__ void issue_rows(__amdgpu_buffer_rsrc_t srs, __amdgpu_buffer_rsrc_t mrs, const int *coff,
+                                           int rowb, StepState<KE, kCpl> &st) {
     constexpr int RB = GW == 32 ? 32 : 0;
+    st.emw = buf_load_f32(mrs, st.ow * 4, 0);
+    st.emr = GW == 32 ? st.emw : buf_load_f32(mrs, st.orr * 4, 0);
+#pragma unroll
+    for (int k = 0; k < KE; ++k)
+        row_load<kCpl, FULLC>(srs, coff, lane_i(st.ow, k) * rowb, st.wrow[k]);
+#pragma unroll
+    for (int k = 0; k < KE; ++k)
+        row_load<kCpl, FULLC>(srs, coff, lane_i(st.orr, RB + k) * rowb, st.rrow[k]);
+}
+
+// Stage 3: forwarding, fwd[k] = the write event (nonzero weight) on read k's
+// slot, or -1. One lane per (read, write) pair compares the slots; a ballot
+// per 64 pairs collects the matches (top-K slots are distinct, so at most one
+// write matches a read). The event tables are read unconditionally (both
+// indices are below KE) and the conditions combined bitwise, so the
+// comparison has no divergent branch. (One wave per workgroup: its LDS
+// accesses complete in order, so the tables written in stage 1 are visible.)
+template<int KE, int kCpl>
+__device__ __forceinline__ void forward_map(const DecodeJob &job, int lane, const int *s_ws, const int *s_rs,
+                                            const float *s_wv, StepState<KE, kCpl> &st) {
+    __builtin_amdgcn_wave_barrier();
+    static_assert((KE * KE) % kWave == 0, "forwarding rounds cover whole waves");
+    uint64_t any = 0;
+#pragma unroll
+    for (int base = 0; base < KE * KE; base += kWave) {
+        const int l = base + lane;
+        const int k = (l / KE) % KE, j2 = l % KE;
+        const int ws = s_ws[j2], rs = s_rs[k];
+        const float wvj = s_wv[j2];
+        const bool match = (j2 < job.Kw) & (k < job.Kr) & (wvj != 0.f) & (ws == rs);
+        const uint64_t hits = __ballot(match);
+        any |= hits;
+#pragma unroll
+        for (int k2 = 0; k2 < KE; ++k2) {
+            if (k2 * KE >= base && k2 * KE < base + kWave) {
+                const uint32_t bits =
+                    static_cast<uint32_t>(hits >> (k2 * KE - base)) & ((KE >= 32 ? 0u : (1u << KE)) - 1u);
+                // highest set bit, -1 when none, without a zero test:
+                // clz(2b + 1) = clz(b) - 1 for b != 0 and 31 for b = 0. (hipcc
+                // 7.2 turned `bits ? 31 - clz(bits) : -1` on the top field of
+                // the ballot into a 64-bit VALU compare and left the select
+                // reading a stale SCC, dropping those forwards.)
+                static_assert(KE <= 16, "2 * bits + 1 must fit 32 bits");
+                st.fwd[k2] = 30 - __builtin_clz(2u * bits + 1u);
+            }
+        }
+    }
+    st.any_fwd = any != 0;
+}
+
+// Stage 4: the K writes (masses, then rows), then the reads of the
+// post-write state into y (`yrow`, C values). A step with valid == false (a
+// masked batch row) has all its weights taken as 0: nothing is written and
+// y is 0. A write event of weight 0 stores its row and mass back unchanged
+// (gain 0); top-K slots are distinct, so no such store meets another write.
+template<typename T, int GW, int KE, int kCpl, bool FULLC, bool FULLK>
+__device__ __forceinline__ void apply_step(const DecodeJob &job, const StepState<KE, kCpl> &st,
+                                           const XRaw<T, kCpl, FULLC> &xr, float gamma, bool valid,
+                                           __amdgpu_buffer_rsrc_t srs, __amdgpu_buffer_rsrc_t mrs, const int *coff,
+                                           int rowb, int lane, float (*s_row)[kWave * kCpl], T *yrow) {
+    constexpr int RB = GW == 32 ? 32 : 0;
+    const int C = job.C, Kw = FULLK ? KE : job.Kw;
+    float xv[kCpl];
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j)
+        xv[j] = xr.get(j);
+    // write math, one write event per lane. e^-|gamma| is shared by the
+    // events: alpha = num / den with the stable form of gsu_alpha, divided
+    // with one Newton-refined reciprocal.
+    const float vw = valid ? st.vw : 0.f;
+    const bool gpos = gamma >= 0.f;
+    const float eg = expf(gpos ? -gamma : gamma);
+    const float cw = 1.f - vw;
+    const float den = gpos ? fmaf(eg, cw, vw) : fmaf(eg, vw, cw);
+    const float alpha = gsu_gain(gpos ? cw * eg : cw, den);
+    const float m2 = vw != 0.f ? fmaf(alpha, st.emw, vw) : st.emw;
+    const float gain = gsu_gain(vw, m2 + job.eps);
+    const bool wlane = GW == 32 ? lane < 32 : true;
+    if (valid && wlane && lane < Kw)
+        buf_store_f32(m2, mrs, st.ow * 4, 0);
+    // every row load is in flight before the first update (the fence stops
+    // the scheduler from sinking loads into the update branches, where each
+    // would wait for its own data)
+    __builtin_amdgcn_sched_barrier(0);
+    if (valid) {
+#pragma unroll
+        for (int k = 0; k < KE; ++k) {
+            if (FULLK || k < Kw) {
+                const float g = lane_f(gain, k);
+                float upd[kCpl];
+#pragma unroll
+                for (int j = 0; j < kCpl; ++j)
+                    upd[j] = fmaf(g, xv[j] - st.wrow[k][j], st.wrow[k][j]);
+                row_store<kCpl, FULLC>(upd, srs, coff, lane_i(st.ow, k) * rowb, lane, C);
+            }
+        }
+    }
+
+    // reads of the post-write state, summed in event order
+    const float vr = valid ? st.vr : 0.f;
+    float rv[KE];
+#pragma unroll
+    for (int k = 0; k < KE; ++k)
+        rv[k] = lane_f(vr, RB + k);
+    float acc[kCpl];
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j)
+        acc[j] = 0.f;
+    float sr = 0.f, srm = 0.f;
+    if (!(valid && st.any_fwd)) {
+        // no read meets a row written this step (the common case)
+#pragma unroll
+        for (int k = 0; k < KE; ++k) {
+            const float rw = job.mass_aware ? rv[k] * lane_f(st.emr, RB + k) : rv[k];
+            sr += rv[k];
+            srm += rw;
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j)
+                acc[j] = fmaf(rw, st.rrow[k][j], acc[j]);
+        }
+    } else {
+        // forwarded rows: the written rows (recomputed from the same
+        // operands) go through LDS, each lane re-reading only what it wrote
+#pragma unroll
+        for (int k = 0; k < KE; ++k) {
+            if (FULLK || k < Kw) {
+                const float g = lane_f(gain, k);
+#pragma unroll
+                for (int j = 0; j < kCpl; ++j)
+                    s_row[k][lane * kCpl + j] = fmaf(g, xv[j] - st.wrow[k][j], st.wrow[k][j]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        float wm[KE];
+#pragma unroll
+        for (int k = 0; k < KE; ++k)
+            wm[k] = lane_f(m2, k);
+#pragma unroll
+        for (int k = 0; k < KE; ++k) {
+            const int f = st.fwd[k];
+            const int fc = f < 0 ? 0 : f;
+            float m = lane_f(st.emr, RB + k);
+#pragma unroll
+            for (int j2 = 0; j2 < KE; ++j2)
+                m = f == j2 ? wm[j2] : m;
+            const float rw = job.mass_aware ? rv[k] * m : rv[k];
+            sr += rv[k];
+            srm += rw;
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) {
+                const float lv = s_row[fc][lane * kCpl + j];
+                acc[j] = fmaf(rw, f >= 0 ? lv : st.rrow[k][j], acc[j]);
+            }
+        }
+    }
+    const float scale = job.mass_aware ? sr / (srm + job.eps) : 1.f;
+    float yv[kCpl];
+#pragma unroll
+    for (int j = 0; j < kCpl; ++j)
+        yv[j] = acc[j] * scale;
+    store_y<T, kCpl, FULLC>(yrow, yv, lane, C);
+}
+
+// One decode step, one wave per (b, h).
+template<typename T, int GW, int KE, int kCpl, bool FULLC, bool FULLK>
+__global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob job) {
     __shared__ int s_ws[KE], s_rs[KE];
     __shared__ float s_wv[KE];
     __shared__ float s_row[KE][kWave * kCpl];
@@ -90,11 +434,11 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
     // grid (B, H): the (b, h) pair without a division
     const int b = blockIdx.x, h = blockIdx.y;
     const int lane = threadIdx.x;
-    const int H = job.H, A = job.A, C = job.C, U = job.U, P = job.P, Kw = job.Kw, Kr = job.Kr;
+    const int H = job.H, A = job.A, C = job.C, U = job.U, P = job.P;
     const int bh = b * H + h;
     T *yrow = static_cast<T *>(job.y) + static_cast<int64_t>(bh) * C;
 
-    // ---- every input of the step in one batch of loads
+    // every input of the step in one batch of loads
     const T *wp = static_cast<const T *>(job.w_addr) + static_cast<int64_t>(bh) * U * P;
     const T *rp = static_cast<const T *>(job.r_addr) + static_cast<int64_t>(bh) * U * P;
     GroupLogits<T> lw, lr;
@@ -104,17 +448,10 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
         lw.load(wp, U, P, lane);
         lr.load(rp, U, P, lane);
     }
-    int coff[kCpl];  // byte offset of each owned channel (clamped into the row)
-#pragma unroll
-    for (int j = 0; j < kCpl; ++j) {
-        const int c = lane + j * kWave;
-        coff[j] = (FULLC || c < C ? c : C - 1) * 4;
-    }
-    const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
-    float xv[kCpl];
-#pragma unroll
-    for (int j = 0; j < kCpl; ++j)
-        xv[j] = load_f32(xp + coff[j] / 4);
+    int coff[kCpl];
+    lane_channels<kCpl, FULLC>(lane, C, coff);
+    XRaw<T, kCpl, FULLC> xr;
+    xr.load(static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C, coff, lane);
     const float gamma = load_f32(static_cast<const T *>(job.gamma) + bh);
     const int pos = job.position_ids[b];
     const uint8_t valid = job.mask ? job.mask[b] : 1;
@@ -127,181 +464,113 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
     const auto srs = __builtin_amdgcn_make_buffer_rsrc(job.slot + static_cast<int64_t>(bh) * A * C, 0, A * C * 4,
                                                        kBufWord3);
     const auto mrs = __builtin_amdgcn_make_buffer_rsrc(job.mass + static_cast<int64_t>(bh) * A, 0, A * 4, kBufWord3);
-
-    // ---- address decode: per-lane events, their masses, the slot tables
-    int ow, orr;      // write / read event slot of this lane
-    float vw, vr;     // their weights
-    float emw, emr;   // their pre-step masses
-    if constexpr (GW == 32) {
-        const int half = lane >> 5, li = lane & 31;
-        const int K = half ? Kr : Kw;
-        float v;
-        int c;
-        const bool inactive = group_search<T, 32>(lw, U, P, K, li, v, c);
-        lane_event(v, c, inactive, K, half ? job.r_re_norm : job.w_re_norm, li, half * 32, shift, A, ow, vw);
-        orr = ow;
-        vr = vw;
-        emw = buf_load_f32(mrs, ow * 4, 0);
-        emr = emw;
-        if (li < KE) {
-            (half ? s_rs : s_ws)[li] = ow;
-            if (!half)
-                s_wv[li] = vw;
-        }
-    } else {
-        float v;
-        int c;
-        bool inactive = group_search<T, 64>(lw, U, P, Kw, lane, v, c);
-        lane_event(v, c, inactive, Kw, job.w_re_norm, lane, 0, shift, A, ow, vw);
-        emw = buf_load_f32(mrs, ow * 4, 0);
-        inactive = group_search<T, 64>(lr, U, P, Kr, lane, v, c);
-        lane_event(v, c, inactive, Kr, job.r_re_norm, lane, 0, shift, A, orr, vr);
-        emr = buf_load_f32(mrs, orr * 4, 0);
-        if (lane < KE) {
-            s_ws[lane] = ow;
-            s_wv[lane] = vw;
-            s_rs[lane] = orr;
-        }
-    }
-
-    // ---- one batch of row requests (row k's offset is a scalar)
     const int rowb = C * 4;
-    float wrow[KE][kCpl], rrow[KE][kCpl];
-#pragma unroll
-    for (int k = 0; k < KE; ++k) {
-        const int so = lane_i(ow, k) * rowb;
-#pragma unroll
-        for (int j = 0; j < kCpl; ++j)
-            wrow[k][j] = buf_load_f32(srs, coff[j], so);
-    }
-#pragma unroll
-    for (int k = 0; k < KE; ++k) {
-        const int so = lane_i(orr, RB + k) * rowb;
-#pragma unroll
-        for (int j = 0; j < kCpl; ++j)
-            rrow[k][j] = buf_load_f32(srs, coff[j], so);
-    }
-    // (one wave per workgroup: its LDS accesses complete in order, so the
-    // slot tables written above are visible to the reads below)
-    __builtin_amdgcn_wave_barrier();
-    // Forwarding: fwd[k] = the write event (nonzero weight) on read k's slot,
-    // or -1. One lane per (read, write) pair compares the slots; a ballot per
-    // 64 pairs collects the matches (top-K slots are distinct, so at most one
-    // write matches a read). The event tables are read unconditionally (both
-    // indices are below KE) and the conditions combined bitwise, so the
-    // comparison has no divergent branch.
-    static_assert((KE * KE) % kWave == 0, "forwarding rounds cover whole waves");
-    int fwd[KE];
-#pragma unroll
-    for (int base = 0; base < KE * KE; base += kWave) {
-        const int l = base + lane;
-        const int k = (l / KE) % KE, j2 = l % KE;
-        const int ws = s_ws[j2], rs = s_rs[k];
-        const float wvj = s_wv[j2];
-        const bool match = (j2 < Kw) & (k < Kr) & (wvj != 0.f) & (ws == rs);
-        const uint64_t hits = __ballot(match);
-#pragma unroll
-        for (int k2 = 0; k2 < KE; ++k2) {
-            if (k2 * KE >= base && k2 * KE < base + kWave) {
-                const uint32_t bits =
-                    static_cast<uint32_t>(hits >> (k2 * KE - base)) & ((KE >= 32 ? 0u : (1u << KE)) - 1u);
-                // highest set bit, -1 when none, without a zero test:
-                // clz(2b + 1) = clz(b) - 1 for b != 0 and 31 for b = 0. (hipcc
-                // 7.2 turned `bits ? 31 - clz(bits) : -1` on the top field of
-                // the ballot into a 64-bit VALU compare and left the select
-                // reading a stale SCC, dropping those forwards.)
-                static_assert(KE <= 16, "2 * bits + 1 must fit 32 bits");
-                fwd[k2] = 30 - __builtin_clz(2u * bits + 1u);
-            }
-        }
-    }
-    // ---- write math, one write event per lane. e^-|gamma| is shared by the
-    // events: alpha = num / den with the stable form of gsu_alpha, divided
-    // with one Newton-refined reciprocal.
-    const bool gpos = gamma >= 0.f;
-    const float eg = expf(gpos ? -gamma : gamma);
-    const float cw = 1.f - vw;
-    const float den = gpos ? fmaf(eg, cw, vw) : fmaf(eg, vw, cw);
-    const float alpha = gsu_gain(gpos ? cw * eg : cw, den);
-    const float m2 = fmaf(alpha, emw, vw);
-    const float gain = gsu_gain(vw, m2 + job.eps);
-    const bool wlane = GW == 32 ? lane < 32 : true;
-    if (wlane && lane < Kw && vw != 0.f)
-        buf_store_f32(m2, mrs, ow * 4, 0);
-    // every row load is in flight before the first update (the fence stops
-    // the scheduler from sinking loads into the update branches, where each
-    // would wait for its own data)
-    __builtin_amdgcn_sched_barrier(0);
-    // ---- row updates
-#pragma unroll
-    for (int k = 0; k < KE; ++k) {
-        if (lane_f(vw, k) != 0.f) {
-            const float g = lane_f(gain, k);
-            const int so = lane_i(ow, k) * rowb;
-#pragma unroll
-            for (int j = 0; j < kCpl; ++j) {
-                const int c = lane + j * kWave;
-                const float sv = fmaf(g, xv[j] - wrow[k][j], wrow[k][j]);
-                s_row[k][c] = sv;  // each lane re-reads only what it wrote
-                if (FULLC || c < C)
-                    buf_store_f32(sv, srs, coff[j], so);
-            }
-        }
-    }
 
-    // ---- reads of the post-write state. The forwarded rows of every read
-    // are fetched from LDS in one batch (index clamped, value selected), so
-    // the reads cost one LDS round trip; events past top-K have r = 0.
-    float sval[KE][kCpl];
-#pragma unroll
-    for (int k = 0; k < KE; ++k) {
-        const int f = fwd[k];
-        const int fc = f < 0 ? 0 : f;
-#pragma unroll
-        for (int j = 0; j < kCpl; ++j) {
-            const float lv = s_row[fc][lane + j * kWave];
-            sval[k][j] = f >= 0 ? lv : rrow[k][j];
-        }
+    StepState<KE, kCpl> st;
+    decode_events<T, GW, KE, kCpl>(job, lw, lr, shift, lane, s_ws, s_rs, s_wv, st);
+    issue_rows<GW, KE, kCpl, FULLC>(srs, mrs, coff, rowb, st);
+    forward_map<KE, kCpl>(job, lane, s_ws, s_rs, s_wv, st);
+    apply_step<T, GW, KE, kCpl, FULLC, FULLK>(job, st, xr, gamma, true, srs, mrs, coff, rowb, lane, s_row, yrow);
+}
+
+// S consecutive decode steps in one launch (the multi-step form of
+// ramnet_topk_autoregressive_steps_), one wave per (b, h) walking its steps
+// in order. Inputs and y carry a leading step dimension; position_ids and
+// mask are (S, B). The steps are software-pipelined. Iteration s decodes
+// step s + 1's addresses while step s's rows are in flight, applies step s,
+// prefetches the small inputs of the next steps (kept as raw bits, so the
+// prefetch waits for nothing), then requests step s + 1's rows: the next
+// iteration's search waits only for the prefetch, which was issued first.
+// Step s + 1's rows are requested after step s's stores. Every access to a
+// row channel is made by the lane that owns the channel, so it reads step
+// s's stores in program order; masses are read back by other lanes of the
+// same wave, whose memory instructions are processed in issue order.
+template<typename T, int KE, int kCpl, bool FULLC, bool FULLK>
+__global__ __launch_bounds__(64) void autoregressive_steps_kernel(const DecodeJob job, const int S,
+                                                                  const int32_t *__restrict__ position_ids) {
+    constexpr int GW = 32;
+    __shared__ int s_ws[KE], s_rs[KE];
+    __shared__ float s_wv[KE];
+    __shared__ float s_row[KE][kWave * kCpl];
+
+    const int b = blockIdx.x, h = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int B = job.B, H = job.H, A = job.A, C = job.C, U = job.U, P = job.P;
+    const int bh = b * H + h;
+    const int64_t BH = static_cast<int64_t>(B) * H;
+    const int64_t step_addr = BH * U * P, step_x = BH * C;
+    const T *ap = static_cast<const T *>((lane >> 5) ? job.r_addr : job.w_addr) + static_cast<int64_t>(bh) * U * P;
+    const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
+    const T *gp = static_cast<const T *>(job.gamma) + bh;
+    T *yp = static_cast<T *>(job.y) + static_cast<int64_t>(bh) * C;
+    // position_ids arrives as its own restrict argument: nothing the kernel
+    // stores aliases it, so its wave-uniform reads become scalar loads, whose
+    // values are not moved into scalar registers right after a vector load.
+    const int32_t *pp = position_ids + b;
+    const uint8_t *mp = job.mask ? job.mask + b : nullptr;
+    const bool cape = h < job.embed_num;
+    int coff[kCpl];
+    lane_channels<kCpl, FULLC>(lane, C, coff);
+    const auto srs = __builtin_amdgcn_make_buffer_rsrc(job.slot + static_cast<int64_t>(bh) * A * C, 0, A * C * 4,
+                                                       kBufWord3);
+    const auto mrs = __builtin_amdgcn_make_buffer_rsrc(job.mass + static_cast<int64_t>(bh) * A, 0, A * 4, kBufWord3);
+    const int rowb = C * 4;
+
+    // step 0: its inputs and events; step 1's search inputs; step 0's rows
+    GroupLogits<T> lg;
+    lg.load(ap, U, P, lane & 31);
+    int pos = pp[0];
+    XRaw<T, kCpl, FULLC> xr;
+    xr.load(xp, coff, lane);
+    uint32_t gr = load_bits(gp);
+    int valid = mp ? mp[0] : 1;
+    StepState<KE, kCpl> st;
+    decode_events<T, GW, KE, kCpl>(job, lg, lg, cape ? pos_mod(pos, A) : 0, lane, s_ws, s_rs, s_wv, st);
+    forward_map<KE, kCpl>(job, lane, s_ws, s_rs, s_wv, st);
+    {
+        const int64_t s1 = S > 1 ? 1 : 0;
+        lg.load(ap + s1 * step_addr, U, P, lane & 31);
+        pos = pp[s1 * B];
     }
-    float rv[KE], rw[KE];  // read weights (mass-aware: r * post-write mass)
-#pragma unroll
-    for (int k = 0; k < KE; ++k) {
-        rv[k] = lane_f(vr, RB + k);
-        rw[k] = rv[k];
-    }
-    if (job.mass_aware) {
-        float wm[KE];
+    __builtin_amdgcn_sched_barrier(0);
+    issue_rows<GW, KE, kCpl, FULLC>(srs, mrs, coff, rowb, st);
+
+    // The loop body is straight-line apart from uniform branches that every
+    // path leaves with the same loads pending: on the last iteration the
+    // search and the row requests repeat step S - 1 (clamped inputs,
+    // in-bounds slots) and their results go unused, and a masked step is
+    // applied with zero weights. The memory counter then sees the same issue
+    // order on every path into the loop header and waits only for the
+    // prefetch.
+    for (int s = 0; s < S; ++s) {
+        // decode step s + 1 (its logits and position were prefetched)
+        StepState<KE, kCpl> nx;
+        decode_events<T, GW, KE, kCpl>(job, lg, lg, cape ? pos_mod(pos, A) : 0, lane, s_ws, s_rs, s_wv, nx);
+        forward_map<KE, kCpl>(job, lane, s_ws, s_rs, s_wv, nx);
+        // apply step s
+        apply_step<T, GW, KE, kCpl, FULLC, FULLK>(job, st, xr, bits_f32<T>(gr), valid != 0, srs, mrs, coff, rowb,
+                                                  lane, s_row, yp + s * step_x);
+        // prefetch (step indices clamped to the last step): the search
+        // inputs of step s + 2, the apply inputs of step s + 1
+        const int64_t s1 = s + 1 < S ? s + 1 : S - 1;
+        const int64_t s2 = s + 2 < S ? s + 2 : S - 1;
+        lg.load(ap + s2 * step_addr, U, P, lane & 31);
+        pos = pp[s2 * B];
+        xr.load(xp + s1 * step_x, coff, lane);
+        gr = load_bits(gp + s1 * BH);
+        valid = mp ? mp[s1 * B] : 1;
+        // request step s + 1's rows, after the prefetch (the fence keeps the
+        // scheduler from interleaving the two batches)
+        __builtin_amdgcn_sched_barrier(0);
+        st.ow = nx.ow;
+        st.orr = nx.orr;
+        st.vw = nx.vw;
+        st.vr = nx.vr;
+        st.any_fwd = nx.any_fwd;
 #pragma unroll
         for (int k = 0; k < KE; ++k)
-            wm[k] = lane_f(m2, k);
-#pragma unroll
-        for (int k = 0; k < KE; ++k) {
-            float m = lane_f(emr, RB + k);
-#pragma unroll
-            for (int j2 = 0; j2 < KE; ++j2)
-                m = fwd[k] == j2 ? wm[j2] : m;
-            rw[k] = rv[k] * m;
-        }
-    }
-    float acc[kCpl];
-#pragma unroll
-    for (int j = 0; j < kCpl; ++j)
-        acc[j] = 0.f;
-    float sr = 0.f, srm = 0.f;
-#pragma unroll
-    for (int k = 0; k < KE; ++k) {
-        sr += rv[k];
-        srm += rw[k];
-#pragma unroll
-        for (int j = 0; j < kCpl; ++j)
-            acc[j] = fmaf(rw[k], sval[k][j], acc[j]);
-    }
-    const float scale = job.mass_aware ? sr / (srm + job.eps) : 1.f;
-#pragma unroll
-    for (int j = 0; j < kCpl; ++j) {
-        const int c = lane + j * kWave;
-        if (FULLC || c < C)
-            store_f32(yrow + c, acc[j] * scale);
+            st.fwd[k] = nx.fwd[k];
+        issue_rows<GW, KE, kCpl, FULLC>(srs, mrs, coff, rowb, st);
     }
 }
 
@@ -390,6 +659,17 @@ __global__ __launch_bounds__(64) void autoregressive_general_kernel(const Decode
     }
 }
 
+// Whether x, y and the slot state allow the kernels' vector accesses of cpl
+// channels (the FULLC forms; each row then starts on a multiple of the
+// vector width, since C == 64 * cpl).
+template<typename T>
+bool vector_aligned(const DecodeJob &job, int cpl) {
+    const uintptr_t xa = reinterpret_cast<uintptr_t>(job.x), ya = reinterpret_cast<uintptr_t>(job.y);
+    const uintptr_t sa = reinterpret_cast<uintptr_t>(job.slot);
+    const uintptr_t xw = static_cast<uintptr_t>(cpl) * sizeof(T), sw = static_cast<uintptr_t>(cpl) * 4;
+    return xa % xw == 0 && ya % xw == 0 && sa % sw == 0;
+}
+
 int pow2_ceil(int x) {
     int p = 1;
     while (p < x)
@@ -413,12 +693,19 @@ hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **w
         const bool narrow = job.C <= 2 * kWave;
         const bool few = kmax <= 8;
         const dim3 g(grid), blk(kWave);  // one wave per (b, h)
+#define RAMNET_AR_LAUNCH_K(GW, KE, CPL, FK)                                                                    \
+    do {                                                                                                        \
+        if (job.C == (CPL) * kWave && vector_aligned<T>(job, CPL))                                              \
+            hipLaunchKernelGGL((autoregressive_fast_kernel<T, GW, KE, CPL, true, FK>), g, blk, 0, stream, job); \
+        else                                                                                                    \
+            hipLaunchKernelGGL((autoregressive_fast_kernel<T, GW, KE, CPL, false, FK>), g, blk, 0, stream, job);\
+    } while (0)
 #define RAMNET_AR_LAUNCH(GW, KE, CPL)                                                                          \
     do {                                                                                                        \
-        if (job.C == (CPL) * kWave)                                                                             \
-            hipLaunchKernelGGL((autoregressive_fast_kernel<T, GW, KE, CPL, true>), g, blk, 0, stream, job);    \
+        if (job.Kw == (KE) && job.Kr == (KE))                                                                   \
+            RAMNET_AR_LAUNCH_K(GW, KE, CPL, true);                                                              \
         else                                                                                                    \
-            hipLaunchKernelGGL((autoregressive_fast_kernel<T, GW, KE, CPL, false>), g, blk, 0, stream, job);   \
+            RAMNET_AR_LAUNCH_K(GW, KE, CPL, false);                                                             \
     } while (0)
         if (half) {
             if (few) { if (narrow) RAMNET_AR_LAUNCH(32, 8, 2); else RAMNET_AR_LAUNCH(32, 8, 4); }
@@ -427,6 +714,7 @@ hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **w
             if (few) { if (narrow) RAMNET_AR_LAUNCH(64, 8, 2); else RAMNET_AR_LAUNCH(64, 8, 4); }
             else { if (narrow) RAMNET_AR_LAUNCH(64, 16, 2); else RAMNET_AR_LAUNCH(64, 16, 4); }
         }
+#undef RAMNET_AR_LAUNCH_K
 #undef RAMNET_AR_LAUNCH
         return hipGetLastError();
     }
@@ -441,7 +729,70 @@ hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **w
     return hipGetLastError();
 }
 
+// S steps: one launch of the multi-step kernel when the shape takes the
+// half-wave fast path, else S launches of the single-step kernels on the
+// step's slices of the inputs.
+template<typename T>
+hipError_t launch_typed_steps(const DecodeJob &job, int S, hipStream_t stream, const char **why) {
+    const int kmax = std::max(job.Kw, job.Kr);
+    const int stair = staircase_count(kmax);
+    const bool persistent = job.P <= 32 && kmax <= kEv && stair <= 32 && job.C <= kWave * kMaxCpl &&
+                            static_cast<int64_t>(job.A) * job.C * 4 <= INT32_MAX && job.H <= 65535;
+    if (persistent) {
+        const dim3 g(static_cast<unsigned>(job.B), static_cast<unsigned>(job.H)), blk(kWave);
+        const bool narrow = job.C <= 2 * kWave;
+        const bool few = kmax <= 8;
+#define RAMNET_AR_STEPS_K(KE, CPL, FK)                                                                          \
+    do {                                                                                                        \
+        if (job.C == (CPL) * kWave && vector_aligned<T>(job, CPL))                                              \
+            hipLaunchKernelGGL((autoregressive_steps_kernel<T, KE, CPL, true, FK>), g, blk, 0, stream, job, S,   \
+                               job.position_ids);                                                               \
+        else                                                                                                    \
+            hipLaunchKernelGGL((autoregressive_steps_kernel<T, KE, CPL, false, FK>), g, blk, 0, stream, job, S,  \
+                               job.position_ids);                                                               \
+    } while (0)
+#define RAMNET_AR_STEPS(KE, CPL)                                                                                \
+    do {                                                                                                        \
+        if (job.Kw == (KE) && job.Kr == (KE))                                                                   \
+            RAMNET_AR_STEPS_K(KE, CPL, true);                                                                   \
+        else                                                                                                    \
+            RAMNET_AR_STEPS_K(KE, CPL, false);                                                                  \
+    } while (0)
+        if (few) { if (narrow) RAMNET_AR_STEPS(8, 2); else RAMNET_AR_STEPS(8, 4); }
+        else { if (narrow) RAMNET_AR_STEPS(16, 2); else RAMNET_AR_STEPS(16, 4); }
+#undef RAMNET_AR_STEPS_K
+#undef RAMNET_AR_STEPS
+        return hipGetLastError();
+    }
+    const int64_t BH = static_cast<int64_t>(job.B) * job.H;
+    for (int s = 0; s < S; ++s) {
+        DecodeJob one = job;
+        one.w_addr = static_cast<const T *>(job.w_addr) + s * BH * job.U * job.P;
+        one.r_addr = static_cast<const T *>(job.r_addr) + s * BH * job.U * job.P;
+        one.x = static_cast<const T *>(job.x) + s * BH * job.C;
+        one.gamma = static_cast<const T *>(job.gamma) + s * BH;
+        one.y = static_cast<T *>(job.y) + s * BH * job.C;
+        one.position_ids = job.position_ids + static_cast<int64_t>(s) * job.B;
+        one.mask = job.mask ? job.mask + static_cast<int64_t>(s) * job.B : nullptr;
+        const hipError_t err = launch_typed<T>(one, stream, why);
+        if (err != hipSuccess)
+            return err;
+    }
+    return hipSuccess;
+}
+
 }  // namespace
+
+hipError_t launch_autoregressive_steps(const DecodeJob &job, int S, hipStream_t stream, const char **why) {
+    if (job.B * job.H == 0 || S == 0)
+        return hipSuccess;
+    switch (job.dtype) {
+        case kF32: return launch_typed_steps<float>(job, S, stream, why);
+        case kF16: return launch_typed_steps<_Float16>(job, S, stream, why);
+        case kBF16: return launch_typed_steps<bf16_t>(job, S, stream, why);
+        default: *why = "decode steps: unsupported dtype"; return hipErrorInvalidValue;
+    }
+}
 
 hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const char **why) {
     if (job.B * job.H == 0)

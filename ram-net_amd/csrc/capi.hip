@@ -532,24 +532,24 @@ int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val,
     return finish(err, why, "topk_segment_backward launch");
 }
 
-int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
-                                float *slot, float *mass, const uint8_t *mask, int64_t embed_num,
-                                const int32_t *position_ids, int64_t B, int64_t H, int64_t U, int64_t P, int64_t A,
-                                int64_t C, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
-                                int mass_aware, float eps, void *y, void *stream) {
+// Checks and job of one decode step (S = 1) or S steps of one shape.
+static int decode_job(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
+                      float *slot, float *mass, const uint8_t *mask, int64_t embed_num, const int32_t *position_ids,
+                      int64_t S, int64_t B, int64_t H, int64_t U, int64_t P, int64_t A, int64_t C, int64_t w_top_k,
+                      int64_t r_top_k, float w_re_norm, float r_re_norm, int mass_aware, float eps, void *y,
+                      ramnet::DecodeJob &job) {
     if (int rc = check_addr_shape(B, H, U, P, 1, embed_num, A))
         return rc;
+    RAMNET_REQUIRE(S >= 0, "the step count must be >= 0");
     RAMNET_REQUIRE(C > 0, "C must be > 0");
     RAMNET_REQUIRE(valid_dtype(dtype), "x dtype must be float32, float16 or bfloat16");
     RAMNET_REQUIRE(w_top_k > 0 && w_top_k <= A && r_top_k > 0 && r_top_k <= A, "top_k values must be in [1, A]");
     RAMNET_REQUIRE(w_re_norm >= 0.f && w_re_norm <= 1.f && r_re_norm >= 0.f && r_re_norm <= 1.f,
                    "top_k_re_norm exponents must be in [0, 1]");
     RAMNET_REQUIRE(eps > 0.f, "eps must be > 0");
-    RAMNET_REQUIRE(fits_int({B * H * U * P, B * H * A * C, B * H * A, B * H * C}), "CUDA index overflow: sizes exceed int32");
-    if (B == 0)
-        return RAMNET_OK;
-    RAMNET_REQUIRE(w_addr && r_addr && x && gamma && slot && mass && position_ids && y, "null tensor pointer");
-    ramnet::DecodeJob job{};
+    RAMNET_REQUIRE(fits_int({B * H * U * P, B * H * A * C, B * H * A, B * H * C, S}),
+                   "CUDA index overflow: sizes exceed int32");
+    job = ramnet::DecodeJob{};
     job.w_addr = w_addr;
     job.r_addr = r_addr;
     job.x = x;
@@ -573,9 +573,43 @@ int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const vo
     job.r_re_norm = r_re_norm;
     job.mass_aware = mass_aware ? 1 : 0;
     job.eps = eps;
+    return RAMNET_OK;
+}
+
+int ramnet_topk_autoregressive_(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
+                                float *slot, float *mass, const uint8_t *mask, int64_t embed_num,
+                                const int32_t *position_ids, int64_t B, int64_t H, int64_t U, int64_t P, int64_t A,
+                                int64_t C, int64_t w_top_k, int64_t r_top_k, float w_re_norm, float r_re_norm,
+                                int mass_aware, float eps, void *y, void *stream) {
+    ramnet::DecodeJob job;
+    if (int rc = decode_job(w_addr, r_addr, x, gamma, dtype, slot, mass, mask, embed_num, position_ids, 1, B, H, U, P,
+                            A, C, w_top_k, r_top_k, w_re_norm, r_re_norm, mass_aware, eps, y, job))
+        return rc;
+    if (B == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(w_addr && r_addr && x && gamma && slot && mass && position_ids && y, "null tensor pointer");
     const char *why = nullptr;
     const hipError_t err = ramnet::launch_autoregressive(job, static_cast<hipStream_t>(stream), &why);
     return finish(err, why, "topk_autoregressive_ launch");
+}
+
+int ramnet_topk_autoregressive_steps_(const void *w_addr, const void *r_addr, const void *x, const void *gamma,
+                                      int dtype, float *slot, float *mass, const uint8_t *mask, int64_t embed_num,
+                                      const int32_t *position_ids, int64_t S, int64_t B, int64_t H, int64_t U,
+                                      int64_t P, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k,
+                                      float w_re_norm, float r_re_norm, int mass_aware, float eps, void *y,
+                                      void *stream) {
+    ramnet::DecodeJob job;
+    if (int rc = decode_job(w_addr, r_addr, x, gamma, dtype, slot, mass, mask, embed_num, position_ids, S, B, H, U, P,
+                            A, C, w_top_k, r_top_k, w_re_norm, r_re_norm, mass_aware, eps, y, job))
+        return rc;
+    if (B == 0 || S == 0)
+        return RAMNET_OK;
+    RAMNET_REQUIRE(w_addr && r_addr && x && gamma && slot && mass && position_ids && y, "null tensor pointer");
+    const char *why = nullptr;
+    const hipError_t err =
+        ramnet::launch_autoregressive_steps(job, static_cast<int>(S), static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, "topk_autoregressive_steps_ launch");
 }
 
 int ramnet_segment_plan(int64_t B, int64_t H, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int dtype,

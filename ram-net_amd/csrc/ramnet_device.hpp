@@ -29,6 +29,23 @@ __device__ __forceinline__ float load_f32(const bf16_t *p) {
     return __uint_as_float(static_cast<uint32_t>(p->bits) << 16);
 }
 
+// The raw storage bits of one element (zero-extended) and their value as
+// float. Converting at the use rather than at the load keeps a prefetched
+// load from waiting for its data before the value is needed.
+__device__ __forceinline__ uint32_t load_bits(const float *p) { return __float_as_uint(*p); }
+__device__ __forceinline__ uint32_t load_bits(const _Float16 *p) { return *reinterpret_cast<const uint16_t *>(p); }
+__device__ __forceinline__ uint32_t load_bits(const bf16_t *p) { return p->bits; }
+template<typename T>
+__device__ __forceinline__ float bits_f32(uint32_t b) {
+    if constexpr (sizeof(T) == 4) {
+        return __uint_as_float(b);
+    } else if constexpr (__is_same(T, bf16_t)) {
+        return __uint_as_float(b << 16);
+    } else {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+    }
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     uint32_t u = __float_as_uint(f);
     if ((u & 0x7fffffffu) > 0x7f800000u)  // NaN: keep it a quiet NaN

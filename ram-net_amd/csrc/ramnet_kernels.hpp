@@ -191,6 +191,9 @@ struct PackJob {
 };
 hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const char **why);
 hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const char **why);
+// S consecutive decode steps; the inputs, y, position_ids and mask of a
+// DecodeJob carry a leading step dimension (S, ...).
+hipError_t launch_autoregressive_steps(const DecodeJob &job, int S, hipStream_t stream, const char **why);
 
 // Channel-slice width, dynamic LDS bytes and form (1: precomputed gains)
 // that a segment-scan launch of this shape uses on the current device.

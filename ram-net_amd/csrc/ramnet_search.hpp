@@ -157,6 +157,51 @@ __device__ __forceinline__ uint64_t lane_xor(uint64_t v) {
            lane_xor<J>(static_cast<uint32_t>(v));
 }
 
+// The sort networks below select with per-lane bit masks held in vector
+// registers (v_bfi_b32) instead of 64-bit lane masks in scalar registers: a
+// network has one mask per stage, and as scalar pairs they crowd out the
+// kernels' other scalars. The masks depend only on the lane index, so a
+// caller's loop computes them once. `opaque` hides from the optimiser that a
+// mask is all ones or zero, which would otherwise turn the bitwise select
+// back into a scalar-mask select.
+__device__ __forceinline__ uint32_t opaque(uint32_t m) {
+    asm("" : "+v"(m));
+    return m;
+}
+// All ones where bit J (a power of two) of `idx` is set, else zero.
+template<int J>
+__device__ __forceinline__ uint32_t bit_mask(int idx) {
+    return opaque(0u - ((static_cast<uint32_t>(idx) / J) & 1u));
+}
+// Bitwise select: bits of a where m is set, of b elsewhere (v_bfi_b32).
+__device__ __forceinline__ uint32_t bitsel(uint32_t m, uint32_t a, uint32_t b) { return (a & m) | (b & ~m); }
+
+// lane_xor with the vector-mask selects.
+template<int J>
+__device__ __forceinline__ uint32_t lane_xor_v(uint32_t v) {
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    if constexpr (J == 4) {
+        const uint32_t up = dpp_u<0x104>(v);  // row_shl:4 -> lane + 4
+        const uint32_t dn = dpp_u<0x114>(v);  // row_shr:4 -> lane - 4
+        return bitsel(bit_mask<4>(lane), dn, up);
+    } else if constexpr (J == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return bitsel(bit_mask<16>(lane), r[0], r[1]);
+    } else if constexpr (J == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return bitsel(bit_mask<32>(lane), r[0], r[1]);
+    } else {
+        return lane_xor<J>(v);
+    }
+}
+template<int J>
+__device__ __forceinline__ float lane_xor_vf(float v) { return __uint_as_float(lane_xor_v<J>(__float_as_uint(v))); }
+template<int J>
+__device__ __forceinline__ uint64_t lane_xor_v(uint64_t v) {
+    return (static_cast<uint64_t>(lane_xor_v<J>(static_cast<uint32_t>(v >> 32))) << 32) |
+           lane_xor_v<J>(static_cast<uint32_t>(v));
+}
+
 // Value of the group's first lane (lane 0, or 32 for the upper half-wave).
 template<int GW>
 __device__ __forceinline__ float group_first(float v) {
@@ -165,8 +210,8 @@ __device__ __forceinline__ float group_first(float v) {
         return __int_as_float(__builtin_amdgcn_readlane(b, 0));
     } else {
         static_assert(GW == 32, "group_first: GW is 32 or 64");
-        const int lo = __builtin_amdgcn_readlane(b, 0), hi = __builtin_amdgcn_readlane(b, 32);
-        return __int_as_float((threadIdx.x & 32) ? hi : lo);
+        const uint32_t lo = __builtin_amdgcn_readlane(b, 0), hi = __builtin_amdgcn_readlane(b, 32);
+        return __uint_as_float(bitsel(bit_mask<32>(static_cast<int>(threadIdx.x)), hi, lo));
     }
 }
 // Butterfly sum over GW lanes, widest exchange first; every lane of the group
@@ -175,33 +220,40 @@ __device__ __forceinline__ float group_first(float v) {
 // both paths get the same log-sum-exp bit for bit.
 template<int GW>
 __device__ __forceinline__ float group_sum(float v) {
-    if constexpr (GW >= 64) v += lane_xor_f<32>(v);
-    if constexpr (GW >= 32) v += lane_xor_f<16>(v);
-    if constexpr (GW >= 16) v += lane_xor_f<8>(v);
-    if constexpr (GW >= 8) v += lane_xor_f<4>(v);
-    if constexpr (GW >= 4) v += lane_xor_f<2>(v);
-    if constexpr (GW >= 2) v += lane_xor_f<1>(v);
+    if constexpr (GW >= 64) v += lane_xor_vf<32>(v);
+    if constexpr (GW >= 32) v += lane_xor_vf<16>(v);
+    if constexpr (GW >= 16) v += lane_xor_vf<8>(v);
+    if constexpr (GW >= 8) v += lane_xor_vf<4>(v);
+    if constexpr (GW >= 4) v += lane_xor_vf<2>(v);
+    if constexpr (GW >= 2) v += lane_xor_vf<1>(v);
     return v;
 }
 
 // Descending bitonic sort of one key per lane over GW lanes. A 32-bit
-// compare-exchange is max, min and a lane-pattern select; a 64-bit one is
-// one 64-bit compare whose result is flipped on the lanes that keep the
-// smaller key.
+// compare-exchange is max, min and a bitwise select by the lane's keep-max
+// mask; a 64-bit one is one 64-bit compare whose result is flipped on the
+// lanes that keep the smaller key, then a bitwise select of both halves.
+// The keep-max mask (bits J and K2 of the group lane index agree) is a
+// function of the lane index only.
+template<int J, int K2>
+__device__ __forceinline__ uint32_t keep_max_mask(int li) {
+    return ~(bit_mask<J>(li) ^ bit_mask<K2>(li));
+}
 template<int J, int K2>
 __device__ __forceinline__ void ce_lane(uint32_t &key, int li) {
-    const uint32_t p = lane_xor<J>(key);
-    const bool keep_max = ((li & J) == 0) == ((li & K2) == 0);
+    const uint32_t p = lane_xor_v<J>(key);
     const uint32_t hi = key > p ? key : p;
     const uint32_t lo = key > p ? p : key;
-    key = keep_max ? hi : lo;
+    key = bitsel(keep_max_mask<J, K2>(li), hi, lo);
 }
 template<int J, int K2>
 __device__ __forceinline__ void ce_lane(uint64_t &key, int li) {
-    const uint64_t p = lane_xor<J>(key);
-    const bool keep_max = ((li & J) == 0) == ((li & K2) == 0);
-    const bool take = (p > key) == keep_max;
-    key = take ? p : key;
+    const uint64_t p = lane_xor_v<J>(key);
+    const uint32_t gt = p > key ? 0xffffffffu : 0u;
+    const uint32_t take = ~(gt ^ keep_max_mask<J, K2>(li));
+    key = (static_cast<uint64_t>(bitsel(take, static_cast<uint32_t>(p >> 32), static_cast<uint32_t>(key >> 32)))
+           << 32) |
+          bitsel(take, static_cast<uint32_t>(p), static_cast<uint32_t>(key));
 }
 template<int GW, int K2, int J, typename Key>
 __device__ __forceinline__ void sort_step(Key &key, int li) {
@@ -268,9 +320,11 @@ __constant__ constexpr StairTable kStairTab = make_stair_table();
 // (unconditionally, from a clamped radix), later digits on demand.
 constexpr int kPreDigits = 4;
 
+// The prefetched digits are kept as raw storage bits and converted when
+// read, so a prefetch does not wait for its data before the search.
 template<typename T>
 struct GroupLogits {
-    float pre[kPreDigits];
+    uint32_t pre[kPreDigits];
     const T *ptr;
     int P;
 
@@ -280,16 +334,16 @@ struct GroupLogits {
         const int r = li < P_ ? li : P_ - 1;
 #pragma unroll
         for (int u = 0; u < kPreDigits; ++u)
-            pre[u] = load_f32(p + (u < U ? u : U - 1) * P_ + r);
+            pre[u] = load_bits(p + (u < U ? u : U - 1) * P_ + r);
     }
 
     __device__ __forceinline__ float get(int u, int li) const {
         if (u < kPreDigits) {
-            float v = pre[0];
+            uint32_t v = pre[0];
 #pragma unroll
             for (int k = 1; k < kPreDigits; ++k)
                 v = u == k ? pre[k] : v;
-            return li < P ? v : kNegInfF;
+            return li < P ? bits_f32<T>(v) : kNegInfF;
         }
         return li < P ? load_f32(ptr + u * P + li) : kNegInfF;
     }

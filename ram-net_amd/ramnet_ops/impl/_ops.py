@@ -531,3 +531,42 @@ def topk_autoregressive_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tenso
 def _(w_addr, r_addr, x, gamma, slot, mass, mask, embed_num, position_ids, w_top_k, r_top_k, w_re_norm, r_re_norm,
       mass_aware, eps):
     return x.new_empty(x.shape)
+
+
+@torch.library.custom_op(f"{_NS}::topk_autoregressive_steps_", mutates_args=("slot", "mass"), device_types="cuda")
+def topk_autoregressive_steps_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
+                               mask: Tensor, embed_num: int, position_ids: Tensor, w_top_k: int, r_top_k: int,
+                               w_re_norm: float, r_re_norm: float, mass_aware: bool, eps: float) -> Tensor:
+    """S consecutive ``topk_autoregressive_`` steps in one call: every input
+    carries a leading step dimension (w_addr/r_addr (S, B, H, U, P), x
+    (S, B, H, C), gamma (S, B, H), position_ids and mask (S, B)) and y is
+    (S, B, H, C). This library's multi-step form of the reference decode op
+    (ram_attn_ops.cpp:349-394), which has no such variant: the kernel walks
+    the steps of each (b, h) in one launch."""
+    op = "topk_autoregressive_steps_"
+    _require_gpu(op, w_addr, r_addr, x, gamma, slot, mass, position_ids)
+    S, B, H, U, P = _dims(op, "w_addr", w_addr, 5)
+    C = _dims(op, "x", x, 4)[-1]
+    A = _dims(op, "slot", slot, 4)[2]
+    _check_slots(op, U, P, A)
+    _check_shapes(op, r_addr=(r_addr, (S, B, H, U, P)), x=(x, (S, B, H, C)), gamma=(gamma, (S, B, H)),
+                  slot=(slot, (B, H, A, C)), mass=(mass, (B, H, A)), position_ids=(position_ids, (S, B)),
+                  mask=(None if mask is None or mask.numel() == 0 else mask, (S, B)))
+    _require_state(op, slot, mass)
+    w_addr, r_addr, x = w_addr.contiguous(), r_addr.contiguous(), x.contiguous()
+    gamma = gamma.to(dtype=x.dtype).contiguous()
+    pos = position_ids.to(device=x.device, dtype=torch.int32).contiguous()
+    m = None if mask is None or mask.numel() == 0 else mask.to(device=x.device, dtype=torch.bool).contiguous()
+    y = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        nat.call("ramnet_topk_autoregressive_steps_", w_addr.data_ptr(), r_addr.data_ptr(), x.data_ptr(),
+                 gamma.data_ptr(), _code(x), slot.data_ptr(), mass.data_ptr(), nat.ptr(m), embed_num, pos.data_ptr(),
+                 S, B, H, U, P, A, C, w_top_k, r_top_k, float(w_re_norm), float(r_re_norm), int(mass_aware),
+                 float(eps), y.data_ptr(), nat.stream_of(x))
+    return y
+
+
+@topk_autoregressive_steps_.register_fake
+def _(w_addr, r_addr, x, gamma, slot, mass, mask, embed_num, position_ids, w_top_k, r_top_k, w_re_norm, r_re_norm,
+      mass_aware, eps):
+    return x.new_empty(x.shape)
