@@ -257,15 +257,22 @@ __device__ __forceinline__ void decode_events(const DecodeJob &job, const GroupL
 
 // Stage 2: one batch of requests for the events' masses and rows (row k's
 // offset is a scalar). Loads come from clamped in-bounds slots, unguarded.
-template<int GW, int KE, int kCpl, bool FULLC>
+// Write event k of the row stages: k itself, or, past a top-k below KE, the
+// last real event (so that its row update repeats that event's store).
+template<int KE, bool FULLK>
+__device__ __forceinline__ int write_event(int k, int Kw) {
+    return FULLK || k < Kw ? k : Kw - 1;
+}
+
+template<int GW, int KE, int kCpl, bool FULLC, bool FULLK>
 __device__ __forceinline__ void issue_rows(__amdgpu_buffer_rsrc_t srs, __amdgpu_buffer_rsrc_t mrs, const int *coff,
-                                           int rowb, StepState<KE, kCpl> &st) {
+                                           int rowb, int Kw, StepState<KE, kCpl> &st) {
     constexpr int RB = GW == 32 ? 32 : 0;
     st.emw = buf_load_f32(mrs, st.ow * 4, 0);
     st.emr = GW == 32 ? st.emw : buf_load_f32(mrs, st.orr * 4, 0);
 #pragma unroll
     for (int k = 0; k < KE; ++k)
-        row_load<kCpl, FULLC>(srs, coff, lane_i(st.ow, k) * rowb, st.wrow[k]);
+        row_load<kCpl, FULLC>(srs, coff, lane_i(st.ow, write_event<KE, FULLK>(k, Kw)) * rowb, st.wrow[k]);
 #pragma unroll
     for (int k = 0; k < KE; ++k)
         row_load<kCpl, FULLC>(srs, coff, lane_i(st.orr, RB + k) * rowb, st.rrow[k]);
@@ -313,9 +320,14 @@ __device__ __forceinline__ void forward_map(const DecodeJob &job, int lane, cons
 
 // Stage 4: the K writes (masses, then rows), then the reads of the
 // post-write state into y (`yrow`, C values). A step with valid == false (a
-// masked batch row) has all its weights taken as 0: nothing is written and
-// y is 0. A write event of weight 0 stores its row and mass back unchanged
-// (gain 0); top-K slots are distinct, so no such store meets another write.
+// masked batch row) has all its weights taken as 0, so its state is stored
+// back unchanged and y is 0. A write event of weight 0 stores its row and
+// mass back unchanged (gain 0); top-K slots are distinct, so no such store
+// meets another write. Every memory instruction here executes on every path
+// (lanes and events past top-k repeat a real event's store of the same
+// value): the compiler's memory-counter waits then see the same number of
+// requests on every path, which lets the multi-step kernel's waits skip
+// this stage's stores.
 template<typename T, int GW, int KE, int kCpl, bool FULLC, bool FULLK>
 __device__ __forceinline__ void apply_step(const DecodeJob &job, const StepState<KE, kCpl> &st,
                                            const XRaw<T, kCpl, FULLC> &xr, float gamma, bool valid,
@@ -338,25 +350,23 @@ __device__ __forceinline__ void apply_step(const DecodeJob &job, const StepState
     const float alpha = gsu_gain(gpos ? cw * eg : cw, den);
     const float m2 = vw != 0.f ? fmaf(alpha, st.emw, vw) : st.emw;
     const float gain = gsu_gain(vw, m2 + job.eps);
-    const bool wlane = GW == 32 ? lane < 32 : true;
-    if (valid && wlane && lane < Kw)
-        buf_store_f32(m2, mrs, st.ow * 4, 0);
+    const bool wlane = (GW == 32 ? lane < 32 : true) && lane < Kw;
+    // lanes that are not write events store write event 0's mass again
+    const int mso = wlane ? st.ow * 4 : lane_i(st.ow, 0) * 4;
+    buf_store_f32(wlane ? m2 : lane_f(m2, 0), mrs, mso, 0);
     // every row load is in flight before the first update (the fence stops
     // the scheduler from sinking loads into the update branches, where each
     // would wait for its own data)
     __builtin_amdgcn_sched_barrier(0);
-    if (valid) {
 #pragma unroll
-        for (int k = 0; k < KE; ++k) {
-            if (FULLK || k < Kw) {
-                const float g = lane_f(gain, k);
-                float upd[kCpl];
+    for (int k = 0; k < KE; ++k) {
+        const int e = write_event<KE, FULLK>(k, Kw);
+        const float g = lane_f(gain, e);
+        float upd[kCpl];
 #pragma unroll
-                for (int j = 0; j < kCpl; ++j)
-                    upd[j] = fmaf(g, xv[j] - st.wrow[k][j], st.wrow[k][j]);
-                row_store<kCpl, FULLC>(upd, srs, coff, lane_i(st.ow, k) * rowb, lane, C);
-            }
-        }
+        for (int j = 0; j < kCpl; ++j)
+            upd[j] = fmaf(g, xv[j] - st.wrow[k][j], st.wrow[k][j]);
+        row_store<kCpl, FULLC>(upd, srs, coff, lane_i(st.ow, e) * rowb, lane, C);
     }
 
     // reads of the post-write state, summed in event order
@@ -468,109 +478,158 @@ __global__ __launch_bounds__(64) void autoregressive_fast_kernel(const DecodeJob
 
     StepState<KE, kCpl> st;
     decode_events<T, GW, KE, kCpl>(job, lw, lr, shift, lane, s_ws, s_rs, s_wv, st);
-    issue_rows<GW, KE, kCpl, FULLC>(srs, mrs, coff, rowb, st);
+    issue_rows<GW, KE, kCpl, FULLC, FULLK>(srs, mrs, coff, rowb, job.Kw, st);
     forward_map<KE, kCpl>(job, lane, s_ws, s_rs, s_wv, st);
     apply_step<T, GW, KE, kCpl, FULLC, FULLK>(job, st, xr, gamma, true, srs, mrs, coff, rowb, lane, s_row, yrow);
 }
 
+// The mask byte read by steps without a mask. It lives in global memory
+// (not constant memory) so that the mask pointer stays a global pointer: a
+// pointer that may be either would be read with flat loads, which count on
+// both memory counters and make every wait on them a full wait.
+__device__ uint8_t kValidStep = 1;
+
 // S consecutive decode steps in one launch (the multi-step form of
-// ramnet_topk_autoregressive_steps_), one wave per (b, h) walking its steps
-// in order. Inputs and y carry a leading step dimension; position_ids and
-// mask are (S, B). The steps are software-pipelined. Iteration s decodes
-// step s + 1's addresses while step s's rows are in flight, applies step s,
-// prefetches the small inputs of the next steps (kept as raw bits, so the
-// prefetch waits for nothing), then requests step s + 1's rows: the next
-// iteration's search waits only for the prefetch, which was issued first.
-// Step s + 1's rows are requested after step s's stores. Every access to a
-// row channel is made by the lane that owns the channel, so it reads step
-// s's stores in program order; masses are read back by other lanes of the
-// same wave, whose memory instructions are processed in issue order.
+// ramnet_topk_autoregressive_steps_). Inputs and y carry a leading step
+// dimension; position_ids and mask are (S, B).
+//
+// One workgroup of two waves per (b, h). A single wave would issue every
+// instruction of a step in one dependent chain at one wave per SIMD, so the
+// work is split: wave 0 (the decoder) decodes the addresses of step s + 2
+// while wave 1 (the updater) applies step s and requests step s + 1's rows.
+// They hand the events over through a two-slot LDS ring and meet at one
+// workgroup barrier per step (each role's code passes the same S + 2
+// barriers, in its own loop). The decoder fills ring slot s % 2 with step
+// s + 2's events during iteration s; the updater took that slot's previous
+// contents (step s's events) before the barrier ending iteration s - 1.
+//
+// The updater's memory requests are issued in program order: step s + 1's
+// rows after step s's stores, and every row channel is accessed by the lane
+// that owns it, so step s + 1 reads step s's stores in program order; the
+// masses are read back by other lanes of the same wave, whose memory
+// instructions are processed in issue order. Values are prefetched as raw
+// bits and converted where they are used, and every memory instruction of a
+// loop iteration executes on every path (steps past the last repeat it,
+// clamped), so the compiler's memory-counter waits cover only what each
+// stage needs.
+template<int KE>
+struct StepRing {
+    int2 ev[2][kWave];  // per lane: (event slot, weight bits)
+    int fwd[2][KE];     // forwarding map of the step
+    int any[2];
+};
+
 template<typename T, int KE, int kCpl, bool FULLC, bool FULLK>
-__global__ __launch_bounds__(64) void autoregressive_steps_kernel(const DecodeJob job, const int S,
-                                                                  const int32_t *__restrict__ position_ids) {
+__global__ __launch_bounds__(2 * kWave) void autoregressive_steps_kernel(const DecodeJob job, const int S) {
     constexpr int GW = 32;
     __shared__ int s_ws[KE], s_rs[KE];
     __shared__ float s_wv[KE];
     __shared__ float s_row[KE][kWave * kCpl];
+    __shared__ StepRing<KE> ring;
 
     const int b = blockIdx.x, h = blockIdx.y;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    // the role is uniform per wave; readfirstlane tells the compiler so, and
+    // the role branches become scalar branches
+    const bool decoder = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x)) < kWave;
     const int B = job.B, H = job.H, A = job.A, C = job.C, U = job.U, P = job.P;
     const int bh = b * H + h;
     const int64_t BH = static_cast<int64_t>(B) * H;
     const int64_t step_addr = BH * U * P, step_x = BH * C;
+    const int last = S - 1;
+
+    // decoder state: step logits and position (prefetched a step ahead)
     const T *ap = static_cast<const T *>((lane >> 5) ? job.r_addr : job.w_addr) + static_cast<int64_t>(bh) * U * P;
+    // The position is read per lane (through an index the compiler cannot
+    // see is uniform), so it stays a vector value: a scalar load would share
+    // its completion counter with the LDS accesses, and a uniform vector load
+    // would be moved to a scalar register right after it issues.
+    const int32_t *pp = job.position_ids + b + static_cast<int>(opaque(0u));
+    const bool cape = h < job.embed_num;
+    GroupLogits<T> lg;
+    int pos = 0;
+    // Decode step `t` (clamped) into ring slot `slot`, then prefetch the
+    // logits and position of step `next` (clamped).
+    auto produce = [&](int t, int slot, int next) {
+        StepState<KE, kCpl> ev;
+        decode_events<T, GW, KE, kCpl>(job, lg, lg, cape ? pos_mod(pos, A) : 0, lane, s_ws, s_rs, s_wv, ev);
+        const int64_t n = next < last ? next : last;
+        lg.load(ap + n * step_addr, U, P, lane & 31);
+        pos = pp[n * B];
+        forward_map<KE, kCpl>(job, lane, s_ws, s_rs, s_wv, ev);
+        ring.ev[slot][lane] = make_int2(ev.ow, __float_as_int(ev.vw));
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < KE; ++k)
+                ring.fwd[slot][k] = ev.fwd[k];
+            ring.any[slot] = ev.any_fwd ? 1 : 0;
+        }
+        (void)t;
+    };
+
+    // updater state
     const T *xp = static_cast<const T *>(job.x) + static_cast<int64_t>(bh) * C;
     const T *gp = static_cast<const T *>(job.gamma) + bh;
     T *yp = static_cast<T *>(job.y) + static_cast<int64_t>(bh) * C;
-    // position_ids arrives as its own restrict argument: nothing the kernel
-    // stores aliases it, so its wave-uniform reads become scalar loads, whose
-    // values are not moved into scalar registers right after a vector load.
-    const int32_t *pp = position_ids + b;
-    const uint8_t *mp = job.mask ? job.mask + b : nullptr;
-    const bool cape = h < job.embed_num;
+    // without a mask every step reads a constant 1 (stride 0), so the mask
+    // load is unconditional like every other request of the loop
+    const uint8_t *mp = job.mask ? job.mask + b + static_cast<int>(opaque(0u)) : &kValidStep;
+    const int64_t mstride = job.mask ? B : 0;
     int coff[kCpl];
     lane_channels<kCpl, FULLC>(lane, C, coff);
     const auto srs = __builtin_amdgcn_make_buffer_rsrc(job.slot + static_cast<int64_t>(bh) * A * C, 0, A * C * 4,
                                                        kBufWord3);
     const auto mrs = __builtin_amdgcn_make_buffer_rsrc(job.mass + static_cast<int64_t>(bh) * A, 0, A * 4, kBufWord3);
     const int rowb = C * 4;
-
-    // step 0: its inputs and events; step 1's search inputs; step 0's rows
-    GroupLogits<T> lg;
-    lg.load(ap, U, P, lane & 31);
-    int pos = pp[0];
-    XRaw<T, kCpl, FULLC> xr;
-    xr.load(xp, coff, lane);
-    uint32_t gr = load_bits(gp);
-    int valid = mp ? mp[0] : 1;
     StepState<KE, kCpl> st;
-    decode_events<T, GW, KE, kCpl>(job, lg, lg, cape ? pos_mod(pos, A) : 0, lane, s_ws, s_rs, s_wv, st);
-    forward_map<KE, kCpl>(job, lane, s_ws, s_rs, s_wv, st);
-    {
-        const int64_t s1 = S > 1 ? 1 : 0;
-        lg.load(ap + s1 * step_addr, U, P, lane & 31);
-        pos = pp[s1 * B];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    issue_rows<GW, KE, kCpl, FULLC>(srs, mrs, coff, rowb, st);
-
-    // The loop body is straight-line apart from uniform branches that every
-    // path leaves with the same loads pending: on the last iteration the
-    // search and the row requests repeat step S - 1 (clamped inputs,
-    // in-bounds slots) and their results go unused, and a masked step is
-    // applied with zero weights. The memory counter then sees the same issue
-    // order on every path into the loop header and waits only for the
-    // prefetch.
-    for (int s = 0; s < S; ++s) {
-        // decode step s + 1 (its logits and position were prefetched)
-        StepState<KE, kCpl> nx;
-        decode_events<T, GW, KE, kCpl>(job, lg, lg, cape ? pos_mod(pos, A) : 0, lane, s_ws, s_rs, s_wv, nx);
-        forward_map<KE, kCpl>(job, lane, s_ws, s_rs, s_wv, nx);
-        // apply step s
-        apply_step<T, GW, KE, kCpl, FULLC, FULLK>(job, st, xr, bits_f32<T>(gr), valid != 0, srs, mrs, coff, rowb,
-                                                  lane, s_row, yp + s * step_x);
-        // prefetch (step indices clamped to the last step): the search
-        // inputs of step s + 2, the apply inputs of step s + 1
-        const int64_t s1 = s + 1 < S ? s + 1 : S - 1;
-        const int64_t s2 = s + 2 < S ? s + 2 : S - 1;
-        lg.load(ap + s2 * step_addr, U, P, lane & 31);
-        pos = pp[s2 * B];
-        xr.load(xp + s1 * step_x, coff, lane);
-        gr = load_bits(gp + s1 * BH);
-        valid = mp ? mp[s1 * B] : 1;
-        // request step s + 1's rows, after the prefetch (the fence keeps the
-        // scheduler from interleaving the two batches)
-        __builtin_amdgcn_sched_barrier(0);
-        st.ow = nx.ow;
-        st.orr = nx.orr;
-        st.vw = nx.vw;
-        st.vr = nx.vr;
-        st.any_fwd = nx.any_fwd;
+    XRaw<T, kCpl, FULLC> xr;
+    uint32_t gr = 0;
+    int valid = 1;
+    // Take step `t`'s events from ring slot `slot`, prefetch its apply
+    // inputs, request its rows (t clamped).
+    auto take = [&](int t, int slot) {
+        const int2 e = ring.ev[slot][lane];
+        st.ow = e.x;
+        st.vw = __int_as_float(e.y);
+        st.orr = st.ow;
+        st.vr = st.vw;
 #pragma unroll
         for (int k = 0; k < KE; ++k)
-            st.fwd[k] = nx.fwd[k];
-        issue_rows<GW, KE, kCpl, FULLC>(srs, mrs, coff, rowb, st);
+            st.fwd[k] = ring.fwd[slot][k];
+        st.any_fwd = ring.any[slot] != 0;
+        const int64_t c = t < last ? t : last;
+        xr.load(xp + c * step_x, coff, lane);
+        gr = load_bits(gp + c * BH);
+        valid = mp[c * mstride];
+        // the fence keeps the row requests after the prefetch and after the
+        // previous step's stores
+        __builtin_amdgcn_sched_barrier(0);
+        issue_rows<GW, KE, kCpl, FULLC, FULLK>(srs, mrs, coff, rowb, job.Kw, st);
+    };
+
+    // Each role runs its own loop (so that the compiler's memory-counter
+    // analysis sees one wave's requests per loop); both pass S + 2 barriers.
+    if (decoder) {
+        lg.load(ap, U, P, lane & 31);
+        pos = pp[0];
+        produce(0, 0, 1);
+        __syncthreads();
+        produce(1, 1, 2);
+        __syncthreads();
+        for (int s = 0; s < S; ++s) {
+            produce(s + 2, s & 1, s + 3);
+            __syncthreads();
+        }
+    } else {
+        __syncthreads();
+        take(0, 0);
+        __syncthreads();
+        for (int s = 0; s < S; ++s) {
+            apply_step<T, GW, KE, kCpl, FULLC, FULLK>(job, st, xr, bits_f32<T>(gr), valid != 0, srs, mrs, coff,
+                                                      rowb, lane, s_row, yp + s * step_x);
+            take(s + 1, (s + 1) & 1);
+            __syncthreads();
+        }
     }
 }
 
@@ -739,17 +798,15 @@ hipError_t launch_typed_steps(const DecodeJob &job, int S, hipStream_t stream, c
     const bool persistent = job.P <= 32 && kmax <= kEv && stair <= 32 && job.C <= kWave * kMaxCpl &&
                             static_cast<int64_t>(job.A) * job.C * 4 <= INT32_MAX && job.H <= 65535;
     if (persistent) {
-        const dim3 g(static_cast<unsigned>(job.B), static_cast<unsigned>(job.H)), blk(kWave);
+        const dim3 g(static_cast<unsigned>(job.B), static_cast<unsigned>(job.H)), blk(2 * kWave);
         const bool narrow = job.C <= 2 * kWave;
         const bool few = kmax <= 8;
 #define RAMNET_AR_STEPS_K(KE, CPL, FK)                                                                          \
     do {                                                                                                        \
         if (job.C == (CPL) * kWave && vector_aligned<T>(job, CPL))                                              \
-            hipLaunchKernelGGL((autoregressive_steps_kernel<T, KE, CPL, true, FK>), g, blk, 0, stream, job, S,   \
-                               job.position_ids);                                                               \
+            hipLaunchKernelGGL((autoregressive_steps_kernel<T, KE, CPL, true, FK>), g, blk, 0, stream, job, S);  \
         else                                                                                                    \
-            hipLaunchKernelGGL((autoregressive_steps_kernel<T, KE, CPL, false, FK>), g, blk, 0, stream, job, S,  \
-                               job.position_ids);                                                               \
+            hipLaunchKernelGGL((autoregressive_steps_kernel<T, KE, CPL, false, FK>), g, blk, 0, stream, job, S); \
     } while (0)
 #define RAMNET_AR_STEPS(KE, CPL)                                                                                \
     do {                                                                                                        \

@@ -143,6 +143,8 @@ __device__ __forceinline__ float gsu_alpha(float w, float g) {
 
 // Non-negative remainder of a position modulo the slot count.
 __device__ __forceinline__ int pos_mod(int pos, int A) {
+    if ((A & (A - 1)) == 0)  // a power of two: two's complement gives the non-negative residue
+        return pos & (A - 1);
     int r = pos % A;
     return r < 0 ? r + A : r;
 }

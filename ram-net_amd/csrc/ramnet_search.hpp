@@ -237,7 +237,11 @@ __device__ __forceinline__ float group_sum(float v) {
 // function of the lane index only.
 template<int J, int K2>
 __device__ __forceinline__ uint32_t keep_max_mask(int li) {
-    return ~(bit_mask<J>(li) ^ bit_mask<K2>(li));
+    return opaque(((li & J) == 0) == ((li & K2) == 0) ? 0xffffffffu : 0u);
+}
+template<int J, int K2>
+__device__ __forceinline__ uint32_t keep_min_mask(int li) {
+    return opaque(((li & J) == 0) == ((li & K2) == 0) ? 0u : 0xffffffffu);
 }
 template<int J, int K2>
 __device__ __forceinline__ void ce_lane(uint32_t &key, int li) {
@@ -250,7 +254,7 @@ template<int J, int K2>
 __device__ __forceinline__ void ce_lane(uint64_t &key, int li) {
     const uint64_t p = lane_xor_v<J>(key);
     const uint32_t gt = p > key ? 0xffffffffu : 0u;
-    const uint32_t take = ~(gt ^ keep_max_mask<J, K2>(li));
+    const uint32_t take = gt ^ keep_min_mask<J, K2>(li);  // (p > key) == keep_max
     key = (static_cast<uint64_t>(bitsel(take, static_cast<uint32_t>(p >> 32), static_cast<uint32_t>(key >> 32)))
            << 32) |
           bitsel(take, static_cast<uint32_t>(p), static_cast<uint32_t>(key));
@@ -412,8 +416,13 @@ __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int 
         const bool two = u + 1 < U;
         const float xa = lg.get(u, li);  // -inf for li >= P
         const float xb = two ? lg.get(u + 1, li) : kNegInfF;
-        Key ka = li < P ? group_digit_key<T>(xa, li) : Key(0);
-        Key kb = li < P && two ? group_digit_key<T>(xb, li) : Key(0);
+        // keys of lanes past the digit are 0 (masked, without a branch)
+        const uint32_t pm = opaque(li < P ? 0xffffffffu : 0u);
+        Key pmk = static_cast<Key>(pm);
+        if constexpr (sizeof(Key) == 8)
+            pmk |= static_cast<Key>(pm) << 32;
+        Key ka = group_digit_key<T>(xa, li) & pmk;
+        Key kb = two ? group_digit_key<T>(xb, li) & pmk : Key(0);
         group_sort_desc2<GW>(ka, kb, li);
         // the maxima are the group's first sorted entries
         float xsa, xsb;
