@@ -7,13 +7,19 @@ decoder for write and read logits plus the segment scan (GSU + top-K read)
 over the whole batch, inputs resident in HBM, functional state
 (zeros in, new state out). The decode figure (config 3: B=64, 512 fused
 single-token steps on a persistent 64x16x1024x128 fp32 state, captured in a
-HIP graph) is reported beside it under ``decode``.
+HIP graph, one launch per step) is reported beside it under ``decode``, with
+the labelled multi-step variant (the same 512 steps in one persistent launch
+of ``topk_autoregressive_steps_``) under ``decode.multi_step``. Timings give
+the median, min and max over repetitions. Config 1 (fp32, one fused forward
+call) is reported under ``config1``.
 
 ``roofline`` is for the dominant kernel (the segment scan): algorithmic bytes
 of the event model per launch / the kernel's average duration measured with
 HIP events on the stream it runs on. ``cpu_baseline`` times the CPU
 restatement of the reference's dense PyTorch algorithm on a bounded sample of
-the same inputs (rank 0, N=1 only).
+the same config-2 inputs (rank 0, N=1 only); ``cpu_baselines`` does the same
+for config 1 (in full), config 3 (32 consecutive decode steps) and config 4
+(512 tokens), each with the host CPU's model string.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S]
        [--no-cpu-baseline] [--no-stress] [--no-lm] [--lm-tokens N]
@@ -139,6 +145,7 @@ def bench_prefill(steps, warmup, dev, c=C2):
     ms_per_step = total_ms / steps
     dec_ms = [ev[0].elapsed_time(ev[1]) for ev in evs]
     seg_ms = [ev[1].elapsed_time(ev[2]) for ev in evs]
+    step_ms = [ev[0].elapsed_time(ev[2]) for ev in evs]
     seg_avg = sum(seg_ms) / len(seg_ms)
     dec_avg = sum(dec_ms) / len(dec_ms)
     per = event_model_bytes(U, P, C, K, H)
@@ -154,6 +161,9 @@ def bench_prefill(steps, warmup, dev, c=C2):
         "tokens_per_s": tokens / (ms_per_step / 1e3),
         "segment_ms": seg_avg,
         "decoder_ms": dec_avg,
+        "step_ms_stats": stats(step_ms),
+        "segment_ms_stats": stats(seg_ms),
+        "decoder_ms_stats": stats(dec_ms),
         "segment_bytes": seg_bytes,
         "op_bytes": op_bytes,
         "op_roofline_frac": (op_bytes / (ms_per_step / 1e3)) / (HBM_PEAK_GBS * 1e9),
@@ -217,7 +227,19 @@ def bench_train(steps, warmup, dev, c=C2):
     }
 
 
-def bench_decode(n_steps, dev, graph=True):
+def stats(vals) -> dict:
+    """Median, min, max and mean of a list of timings."""
+    v = sorted(vals)
+    return {"median": v[len(v) // 2], "min": v[0], "max": v[-1], "mean": sum(v) / len(v), "n": len(v)}
+
+
+def bench_decode(n_steps, dev, graph=True, reps=5):
+    """Config 3: n_steps consecutive decode steps on the persistent state, two
+    ways. The primary figure captures one ``topk_autoregressive_`` launch per
+    step in a HIP graph and replays it. The labelled multi-step variant runs
+    the same steps through ``topk_autoregressive_steps_``: one persistent
+    launch in which each (b, h) walks all steps (it needs every step's inputs
+    up front, which a serving loop does not have)."""
     import ramnet_ops  # noqa: F401
     ops = torch.ops.ramnet_ops
     c = C3
@@ -237,6 +259,12 @@ def bench_decode(n_steps, dev, graph=True):
     t0 = torch.randint(0, 8192, (B,), device=dev, generator=g)
     pos_all = (t0.view(1, B) + torch.arange(n_steps, device=dev).view(n_steps, 1)).to(torch.int32).contiguous()
     no_mask = torch.empty(0, dtype=torch.bool, device=dev)
+    # the CPU baseline's sample (first 16 sequences, first 32 steps, in the
+    # oracle's (B, H, ..., T) layout), copied before any step changes the state
+    ns, nb = min(32, n_steps), min(16, B)
+    host = {"w": w_all[:ns, :nb].permute(1, 2, 3, 4, 0).cpu(), "r": r_all[:ns, :nb].permute(1, 2, 3, 4, 0).cpu(),
+            "x": x_all[:ns, :nb].permute(1, 2, 0, 3).cpu(), "gamma": g_all[:ns, :nb].permute(1, 2, 0).cpu(),
+            "pos": pos_all[:ns, :nb].t().long().cpu(), "slot": slot[:nb].cpu(), "mass": mass[:nb].cpu()}
     keep = []
 
     def run_all():
@@ -245,22 +273,8 @@ def bench_decode(n_steps, dev, graph=True):
             keep.append(ops.topk_autoregressive_(w_all[s], r_all[s], x_all[s], g_all[s], slot, mass, no_mask, E,
                                                  pos_all[s], K, K, 0.0, 0.0, False, 1e-12))
 
-    # kernel duration on its stream, eager
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ops.topk_autoregressive_(w_all[0], r_all[0], x_all[0], g_all[0], slot, mass, no_mask, E, pos_all[0], K, K,
-                             0.0, 0.0, False, 1e-12)
-    torch.cuda.synchronize()
-    ks = []
-    for s in range(min(n_steps, 64)):
-        e0.record()
-        ops.topk_autoregressive_(w_all[s], r_all[s], x_all[s], g_all[s], slot, mass, no_mask, E, pos_all[s], K, K,
-                                 0.0, 0.0, False, 1e-12)
-        e1.record()
-        torch.cuda.synchronize()
-        ks.append(e0.elapsed_time(e1))
-    kernel_ms = sorted(ks)[len(ks) // 2]
-
     mode = "eager"
+    runner = run_all
     if graph:
         try:
             side = torch.cuda.Stream()
@@ -279,30 +293,49 @@ def bench_decode(n_steps, dev, graph=True):
             mode = "hip-graph"
         except Exception as exc:  # capture unsupported: fall back to eager launches, reported as such
             log(f"graph capture failed ({exc}); timing eager launches")
-            runner = run_all
-    else:
-        runner = run_all
     runner()
     torch.cuda.synchronize()
-    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 3
-    s_ev.record()
-    for _ in range(reps):
-        runner()
-    e_ev.record()
+
+    def timed(fn):
+        out = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1) * 1e3 / n_steps)  # us per step
+        return out
+
+    per_graph = timed(runner)
+
+    def persistent():
+        ops.topk_autoregressive_steps_(w_all, r_all, x_all, g_all, slot, mass, no_mask, E, pos_all, K, K, 0.0, 0.0,
+                                       False, 1e-12)
+
+    persistent()
     torch.cuda.synchronize()
-    ms = s_ev.elapsed_time(e_ev) / reps
-    per_step_ms = ms / n_steps
+    per_multi = timed(persistent)
     bytes_step = event_model_bytes(U, P, C, K, H)["op"] * B * H
+    us_g, us_m = stats(per_graph), stats(per_multi)
+    frac = lambda us: (bytes_step / (us * 1e-6)) / (HBM_PEAK_GBS * 1e9)
     out = {
+        "host": host,
         "mode": mode,
         "steps": n_steps,
-        "ms_per_step": per_step_ms,
-        "tokens_per_s": B / (per_step_ms / 1e3),
-        "kernel_ms": kernel_ms,
+        "ms_per_step": us_g["median"] / 1e3,
+        "us_per_step": us_g,
+        "tokens_per_s": B / (us_g["median"] * 1e-6),
         "bytes_per_step": bytes_step,
-        "roofline_frac": (bytes_step / (per_step_ms / 1e3)) / (HBM_PEAK_GBS * 1e9),
-        "kernel_roofline_frac": (bytes_step / (kernel_ms / 1e3)) / (HBM_PEAK_GBS * 1e9),
+        "roofline_frac": frac(us_g["median"]),
+        "multi_step": {
+            "variant": "labelled multi-step persistent launch (topk_autoregressive_steps_): all steps' inputs "
+                       "given up front, one launch for the whole sequence",
+            "us_per_step": us_m,
+            "tokens_per_s": B / (us_m["median"] * 1e-6),
+            "achieved_gbs": bytes_step / (us_m["median"] * 1e-6) / 1e9,
+            "roofline_frac": frac(us_m["median"]),
+        },
     }
     if mode == "hip-graph":
         out["graph_node_floor_us"] = graph_node_floor_us(dev, n_steps)
@@ -401,48 +434,142 @@ def bench_lm(dev, new_tokens):
     }
 
 
-def cpu_baseline(host, target_s=12.0, batch_rows=None):
-    """Dense reference algorithm (oracle restatement) on host cores over a bounded sample of the C2 inputs.
+def cpu_model() -> str:
+    """The host CPU's model string (/proc/cpuinfo), or the platform's name."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-    A 16-token calibration run sizes the sample so that the timed run takes
-    about ``target_s`` seconds (capped at the full sequence).
-    """
-    import oracle
+
+def _cpu_threads() -> int:
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
-    c = C2
-    H, C, U, P, K, T = c["H"], c["C"], c["U"], c["P"], c["K"], c["T"]
-    rows = c["B"] if batch_rows is None else batch_rows
+    return n
+
+
+def _dense(w, r, x, gm, slot, mass, E, pos, K, chunk=256):
+    """One timed run of the oracle's dense restatement of the reference
+    algorithm (torch_impl.py:217-288): dense decode of all slots, then the
+    per-step dense GSU."""
+    import oracle
+    t0 = time.perf_counter()
+    oracle.dense_ram_attn(w, r, x, gm, slot, mass, None, E, pos, (K, K), (0.0, 0.0), False, 1e-12, chunk=chunk)
+    return time.perf_counter() - t0
+
+
+def cpu_baseline(host, c=C2, target_s=12.0, min_tokens=512, name="config 2"):
+    """Dense reference algorithm (oracle restatement) on host cores over a
+    bounded sample of a prefill config's inputs: the first ``min_tokens``
+    tokens (or more, up to ``target_s`` seconds) of as many batch rows as fit
+    the time budget (at least one). A 16-token run of one row calibrates."""
+    n = _cpu_threads()
+    H, C, U, P, K, T, B = c["H"], c["C"], c["U"], c["P"], c["K"], c["T"], c["B"]
     A = P ** U
 
-    def run(tokens):
-        w = host["w"][:rows, ..., :tokens]
-        r = host["r"][:rows, ..., :tokens]
-        x = host["x"][:rows, :, :tokens]
-        gm = host["gamma"][:rows, :, :tokens]
-        pos = host["pos"][:rows, :tokens].long()
-        slot = torch.zeros(rows, H, A, C)
-        mass = torch.full((rows, H, A), 1.0 / A)
-        t0 = time.perf_counter()
-        oracle.dense_ram_attn(w, r, x, gm, slot, mass, None, H // 2, pos, (K, K), (0.0, 0.0), False, 1e-12,
-                              chunk=256)
-        return time.perf_counter() - t0
+    def run(rows, tokens):
+        sl = (slice(0, rows), Ellipsis, slice(0, tokens))
+        return _dense(host["w"][sl], host["r"][sl], host["x"][:rows, :, :tokens], host["gamma"][:rows, :, :tokens],
+                      torch.zeros(rows, H, A, C), torch.full((rows, H, A), 1.0 / A), c["embed"],
+                      host["pos"][:rows, :tokens].long(), K)
 
-    cal = run(16)
-    tokens = int(min(T, max(16, 16 * target_s / max(cal, 1e-3))))
+    cal = max(run(1, 16), 1e-3) / 16  # seconds per token-row
+    rows = int(max(1, min(B, target_s / (cal * min_tokens))))
+    tokens = int(min(T, max(min_tokens, target_s / (cal * rows))))
     tokens = max(16, (tokens // 16) * 16)
-    dt = run(tokens)
+    dt = run(rows, tokens)
     return {
         "value": rows * tokens / dt,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"config 2 inputs: {rows} of {c['B']} batch rows x first {tokens} of {T} tokens, all {H} heads; "
-                  f"dense decode of all {A} slots + per-step dense GSU (the reference torch_impl.py algorithm), "
+        "sample": f"{name} inputs: {rows} of {B} batch rows x first {tokens} of {T} tokens, all {H} heads; dense "
+                  f"decode of all {A} slots + per-step dense GSU (the reference torch_impl.py algorithm), "
                   f"{dt:.1f} s",
-        "cpu": platform.processor() or platform.machine(),
+        "cpu": cpu_model(),
         "seconds": dt,
     }
+
+
+def cpu_baseline_c1():
+    """Config 1 in full (B=1, H=4, T=256, d_k=d_v=64, U=2, P=16, K=4, fp32,
+    CAPE on 2 heads, zero state): one warm-up run, then the timed run."""
+    from ram_cases import projected_logits
+    n = _cpu_threads()
+    B, H, T, C, U, P, K = 1, 4, 256, 64, 2, 16, 4
+    A = P ** U
+    w, r = projected_logits(B, H, U, P, T, 64, seed=1, dtype=torch.float32)
+    g = torch.Generator().manual_seed(101)
+    x = torch.randn(B, H, T, C, generator=g)
+    gm = torch.sigmoid(torch.randn(B, H, T, generator=g))
+    pos = torch.arange(T).view(1, T)
+    args = (w, r, x, gm, torch.zeros(B, H, A, C), torch.full((B, H, A), 1.0 / A), 2, pos, K)
+    _dense(*args, chunk=64)
+    dt = _dense(*args, chunk=64)
+    return {"value": B * T / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config 1 in full: B={B}, H={H}, T={T}, d_v={C}, A={A}, K={K}, fp32, {dt:.2f} s",
+            "cpu": cpu_model(), "seconds": dt}
+
+
+def cpu_baseline_c3(host, target_s=10.0, steps=32):
+    """Config 3: ``steps`` consecutive decode steps from the persistent state
+    (the dense restatement walks them in order, one dense GSU per step) for as
+    many batch rows as fit the time budget; one step of one row calibrates."""
+    n = _cpu_threads()
+    c = C3
+    H, C, U, P, K, B = c["H"], c["C"], c["U"], c["P"], c["K"], c["B"]
+    A = P ** U
+    rows_max = host["slot"].shape[0]
+    steps = min(steps, host["w"].shape[-1])
+
+    def run(rows, t):
+        return _dense(host["w"][:rows, ..., :t], host["r"][:rows, ..., :t], host["x"][:rows, :, :t],
+                      host["gamma"][:rows, :, :t], host["slot"][:rows].clone(), host["mass"][:rows].clone(),
+                      H // 2, host["pos"][:rows, :t], K, chunk=t)
+
+    cal = max(run(1, 1), 1e-3)  # seconds per row-step
+    rows = int(max(1, min(rows_max, target_s / (cal * steps))))
+    dt = run(rows, steps)
+    return {"value": rows * steps / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config 3: {rows} of {B} sequences x {steps} consecutive decode steps, all {H} heads on the "
+                      f"{A}x{C} fp32 state per head (dense decode + per-step dense GSU), {dt:.1f} s",
+            "cpu": cpu_model(), "seconds": dt}
+
+
+def bench_c1(dev, reps=20):
+    """Config 1 on the GPU: the fused forward (decoders + scan) of the whole
+    sequence, fp32, through the public API's native op."""
+    import ramnet_ops  # noqa: F401
+    from ram_cases import projected_logits
+    ops = torch.ops.ramnet_ops
+    B, H, T, C, U, P, K = 1, 4, 256, 64, 2, 16, 4
+    A = P ** U
+    w, r = projected_logits(B, H, U, P, T, 64, seed=1, dtype=torch.float32, device=dev)
+    g = torch.Generator().manual_seed(101)
+    x = torch.randn(B, H, T, C, generator=g).to(dev)
+    gm = torch.sigmoid(torch.randn(B, H, T, generator=g)).to(dev)
+    pos = torch.arange(T, dtype=torch.int32, device=dev).view(1, T)
+    slot = torch.zeros(B, H, A, C, device=dev)
+    mass = torch.full((B, H, A), 1.0 / A, device=dev)
+    f = lambda: ops.ram_attn_forward(w, r, x, gm, slot, mass, None, 2, pos, K, K, 0.0, 0.0, False, 1e-12)
+    f()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        f()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    st = stats(ts)
+    return {"workload": f"config 1: B={B}, H={H}, T={T}, d_v={C}, U={U}, P={P} (A={A}), K={K}, fp32, CAPE on 2 "
+                        "heads, one fused forward call (latency-bound)",
+            "ms_per_call": st, "tokens_per_s": B * T / (st["median"] / 1e3)}
 
 
 def main(argv=None) -> int:
@@ -451,7 +578,8 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=C3["steps"])
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU time budget per baseline (config 2; configs 3 and 4 take 3/4 of it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only", choices=("prefill", "decode", "stress", "lm", "train"), default=None)
@@ -491,11 +619,14 @@ def main(argv=None) -> int:
         log(f"prefill: {pre['ms_per_step']:.3f} ms/step, segment {pre['segment_ms']:.3f} ms, "
             f"decoder {pre['decoder_ms']:.3f} ms")
     stress = {}
+    stress_host = None
     if args.only == "stress" or (args.only is None and not args.no_stress):
         for name, c in (("config4", C4), ("config4_tie_heavy", C4_TIES)):
             log(f"stress: {name} prefill")
             st = bench_prefill(max(3, args.steps // 4), 1, dev, c)
-            st.pop("host")
+            host_c4 = st.pop("host")
+            if name == "config4":
+                stress_host = host_c4
             seg_gbs = st["segment_bytes"] / (st["segment_ms"] / 1e3) / 1e9
             stress[name] = {
                 "workload": f"B={c['B']}, H={c['H']}, T={c['T']}, d_v={c['C']}, U={c['U']}, P={c['P']} "
@@ -504,6 +635,7 @@ def main(argv=None) -> int:
                             f"B={c['B']}, H={c['H']}, T={c['T']}, d_v={c['C']}, U={c['U']}, P={c['P']} "
                             f"(A={c['P'] ** c['U']}), K={c['K']}, CAPE on {c['embed']} heads, gamma=sigmoid(N(0,1))",
                 "tokens_per_s": st["tokens_per_s"], "ms_per_step": st["ms_per_step"],
+                "step_ms_stats": st["step_ms_stats"], "segment_ms_stats": st["segment_ms_stats"],
                 "decoder_ms": st["decoder_ms"], "segment_ms": st["segment_ms"],
                 "op_roofline_frac": st["op_roofline_frac"],
                 "segment_roofline_frac": seg_gbs / HBM_PEAK_GBS, "op_bytes_per_step": st["op_bytes"],
@@ -521,7 +653,14 @@ def main(argv=None) -> int:
         log("decode: config 3, graph-captured steps")
         dec = bench_decode(args.decode_steps, dev, graph=not args.no_graph)
         log(f"decode: {dec['ms_per_step'] * 1e3:.2f} us/step ({dec['mode']}), graph node floor "
-            f"{dec.get('graph_node_floor_us', float('nan')):.2f} us")
+            f"{dec.get('graph_node_floor_us', float('nan')):.2f} us; multi-step launch "
+            f"{dec['multi_step']['us_per_step']['median']:.2f} us/step "
+            f"({dec['multi_step']['roofline_frac'] * 100:.0f}% of HBM peak)")
+    c1 = None
+    if args.only is None:
+        log("config 1: fused forward, fp32")
+        c1 = bench_c1(dev)
+        log(f"config 1: {c1['ms_per_call']['median']:.3f} ms per call")
 
     if pre is not None:
         seg_gbs = pre["segment_bytes"] / (pre["segment_ms"] / 1e3) / 1e9
@@ -562,9 +701,11 @@ def main(argv=None) -> int:
                 "traffic_detail": traffic,
                 "algorithmic_bytes": pre["segment_bytes"],
                 "kernel_ms": pre["segment_ms"],
+                "kernel_ms_stats": pre["segment_ms_stats"],
             },
             "prefill": {
                 "tokens_per_s": pre["tokens_per_s"],
+                "step_ms_stats": pre["step_ms_stats"],
                 "op_roofline_frac": pre["op_roofline_frac"],
                 "decoder_ms": pre["decoder_ms"],
                 "segment_ms": pre["segment_ms"],
@@ -572,7 +713,9 @@ def main(argv=None) -> int:
                 "bytes_per_token_head": pre["bytes_per_token_head"],
             },
         })
+    dec_host = None
     if dec is not None:
+        dec_host = dec.pop("host")
         out["decode"] = dec
         if pre is None:
             out.update({"value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": dec["steps"],
@@ -606,9 +749,22 @@ def main(argv=None) -> int:
                         "warmup": 1, "ms_per_step": st["ms_per_step"], "higher_is_better": True, "scaling": "weak",
                         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
                         "config": {"workload": "config 4 stress prefill: " + st["workload"]}})
+    if c1 is not None:
+        out["config1"] = c1
     if pre is not None and not args.no_cpu_baseline:
-        log("cpu baseline: dense reference algorithm on host cores")
+        log("cpu baseline: dense reference algorithm on host cores (config 2)")
         out["cpu_baseline"] = cpu_baseline(pre["host"], target_s=args.cpu_seconds)
+        more = {}
+        if c1 is not None:
+            log("cpu baseline: config 1 in full")
+            more["config1"] = cpu_baseline_c1()
+        if dec_host is not None:
+            log("cpu baseline: config 3, 32 decode steps")
+            more["config3"] = cpu_baseline_c3(dec_host, target_s=args.cpu_seconds * 0.75)
+        if stress_host is not None:
+            log("cpu baseline: config 4, 512 tokens")
+            more["config4"] = cpu_baseline(stress_host, C4, target_s=args.cpu_seconds * 0.75, name="config 4")
+        out["cpu_baselines"] = more
     print(json.dumps(out), flush=True)
     return 0
 
