@@ -59,6 +59,87 @@ __device__ __forceinline__ float event_sum(float v) {
     return v;
 }
 
+// One exchange of a reduce-scatter over lane bit LB, partner = lane ^ (1 <<
+// LB): lanes with the bit clear receive a + a(partner), lanes with it set
+// b + b(partner). Across rows v_permlane16/32_swap trades a's upper half for
+// b's lower half in one instruction, so the two outputs add to the pair sum
+// with no select; within a row, two DPP adds and a bit select (hi = all ones
+// in the lanes with the bit set).
+// a + (lane CTRL of a), for DPP patterns whose source lane always exists or
+// whose missing-source lanes are not used (bound_ctrl: reads 0, no old value)
+template<int CTRL>
+__device__ __forceinline__ float add_dpp(float a) {
+    return a + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), CTRL, 0xf, 0xf, true));
+}
+
+// bits of a where m is set, of b elsewhere, as one v_bfi_b32 (the bitwise
+// form alone is split into two instructions once ~m is hoisted)
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+    return r;
+}
+
+template<int LB>
+__device__ __forceinline__ float scatter_pair(float a, float b, uint32_t hi) {
+    if constexpr (LB == 5) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else if constexpr (LB == 4) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+        float pa, pb;
+        if constexpr (LB == 3) {
+            pa = add_dpp<0x128>(a);  // row_ror:8 (lane ^ 8 within a row)
+            pb = add_dpp<0x128>(b);
+        } else if constexpr (LB == 2) {
+            pa = add_dpp<0x104>(a);  // row_shl:4 -> lane + 4 (used where bit 2 is clear)
+            pb = add_dpp<0x114>(b);  // row_shr:4 -> lane - 4 (used where bit 2 is set)
+        } else if constexpr (LB == 1) {
+            pa = add_dpp<0x4E>(a);  // quad_perm [2,3,0,1]
+            pb = add_dpp<0x4E>(b);
+        } else {
+            static_assert(LB == 0, "scatter_pair: lane bit 0..5");
+            pa = add_dpp<0xB1>(a);  // quad_perm [1,0,3,2]
+            pb = add_dpp<0xB1>(b);
+        }
+        return __uint_as_float(bfi(hi, __float_as_uint(pb), __float_as_uint(pa)));
+    }
+}
+
+// Reduce-scatter of N = 2^(I+1) tokens' partial sums over event lane bits
+// SH .. SH + I (highest first): afterwards part[0] of a lane holds, for the
+// token whose index equals the lane's event bits, the total over the event
+// lanes. N - 1 exchanges serve N tokens, where a per-token all-reduce costs
+// log2(N) exchanges and a select per token.
+template<int I, int SH, int N>
+__device__ __forceinline__ void event_scatter(float (&part)[N], const uint32_t (&hi)[6]) {
+    if constexpr (I >= 0) {
+        constexpr int H = 1 << I;
+#pragma unroll
+        for (int m = 0; m < H; ++m)
+            part[m] = scatter_pair<SH + I>(part[m], part[m + H], hi[SH + I]);
+        event_scatter<I - 1, SH, N>(part, hi);
+    }
+}
+
+// LDS byte address of a pointer into the workgroup's LDS, and back: a row
+// offset computed once per chunk then addresses its LDS access directly.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char *)p));
+}
+__device__ __forceinline__ float *lds_at(uint32_t a) {
+    return (float *)(__attribute__((address_space(3))) float *)(uintptr_t)a;
+}
+// a * b + c for a, b below 2^24, as one v_mad_u32_u24 (left to itself the
+// compiler keeps the product and adds c at every use)
+__device__ __forceinline__ uint32_t mad24(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // Sum over the lanes whose indices differ from a lane's own only in bits
 // J .. 32 (J a power of two): exact xor exchanges by DPP within a row
 // (quad_perm, row_shl/shr:4, row_ror:8), then v_permlane16/32_swap, whose two
@@ -517,6 +598,20 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     const int ev = CFL ? lane / LPE : lane % EPP;  // event slot within a pass
     const int cg = CFL ? lane % LPE : lane / EPP;  // channel group within the wave
     const int cl = wave * CSW + cg * VEC;     // first channel of this lane within the slice
+    // Read sums by reduce-scatter over each run of EPP tokens (EPP <= CH):
+    // event bit i sits on lane bit i + SH. Masks of the lane bits, once.
+    constexpr bool BFLY = EPP <= CH;
+    constexpr int LOGE = __builtin_ctz(EPP);
+    constexpr int SH = CFL ? 6 - LOGE : 0;
+    uint32_t hi[6];
+    hi[0] = bit_mask<1>(lane);
+    hi[1] = bit_mask<2>(lane);
+    hi[2] = bit_mask<4>(lane);
+    hi[3] = bit_mask<8>(lane);
+    hi[4] = bit_mask<16>(lane);
+    hi[5] = bit_mask<32>(lane);
+    // LDS address of this lane's first channel in slot 0
+    const uint32_t lrow = lds_addr(st) + static_cast<uint32_t>(cl) * 4;
     const Scalar *gx = static_cast<const Scalar *>(job.x) + static_cast<int64_t>(bh) * T * C;
     Scalar *gy = static_cast<Scalar *>(job.y) + static_cast<int64_t>(bh) * T * C;
     // Items past the end are clamped to the last item, so the threads that
@@ -591,17 +686,16 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             const int v = (j % 4) == 0 ? q.x : (j % 4) == 1 ? q.y : (j % 4) == 2 ? q.z : q.w;
             return __builtin_amdgcn_readfirstlane(v);
         };
-        // Byte offsets (from st) of every event's row, computed once per chunk
-        // in 32 bits, off the token chain.
+        // LDS addresses of every event's row (one 24-bit multiply-add each),
+        // computed once per chunk, off the token chain.
 #pragma unroll
         for (int j = 0; j < CH; ++j)
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                rec[p][j].x = (rec[p][j].x * RS + cl) * 4;
-                rec[p][j].z = (rec[p][j].z * RS + cl) * 4;
+                rec[p][j].x = static_cast<int>(mad24(static_cast<uint32_t>(rec[p][j].x), RS * 4, lrow));
+                rec[p][j].z = static_cast<int>(mad24(static_cast<uint32_t>(rec[p][j].z), RS * 4, lrow));
             }
-        const char *stb = reinterpret_cast<const char *>(st);
-        auto row = [&](int off) { return reinterpret_cast<float *>(const_cast<char *>(stb) + off); };
+        auto row = [&](int a) { return lds_at(static_cast<uint32_t>(a)); };
         auto load_rows = [&](int j, FVec<VEC> (&s)[NP]) {
 #pragma unroll
             for (int p = 0; p < NP; ++p)
@@ -622,27 +716,45 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             for (int p = 0; p < NP; ++p)
                 rv[p] = lds_load<VEC>(row(rec[p][j].z));
         };
-        // weighted read sum of token j, kept in the lanes that store its y
+        // weighted read sum of token j, kept in the lanes that store its y:
+        // the lane's partial of every token of a run of EPP, then one
+        // reduce-scatter per run (BFLY), else a sum over the event lanes per
+        // token
+        float part[VEC][BFLY ? EPP : 1];
         auto reduce = [&](int j, const FVec<VEC> (&rv)[NP]) {
             FVec<VEC> acc;
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
-                acc.v[v] = 0.f;
+                acc.v[v] = __int_as_float(rec[0][j].w) * rv[0].v[v];
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
+            for (int p = 1; p < NP; ++p) {
                 const float wgt = __int_as_float(rec[p][j].w);
 #pragma unroll
                 for (int v = 0; v < VEC; ++v)
                     acc.v[v] = fmaf(wgt, rv[p].v[v], acc.v[v]);
             }
+            if constexpr (BFLY) {
+                // (opaque: the first exchange's DPP add would otherwise be
+                // contracted with the product into a DPP move and an fma)
 #pragma unroll
-            for (int v = 0; v < VEC; ++v)
-                acc.v[v] = CFL ? strided_sum<LPE>(acc.v[v]) : event_sum<EPP>(acc.v[v]);
-            const bool mine = EPP <= CH ? ev == j % EPP : ev % CH == j;
-            const int q = EPP <= CH ? j / EPP : 0;
+                for (int v = 0; v < VEC; ++v)
+                    part[v][j % EPP] = __uint_as_float(opaque(__float_as_uint(acc.v[v])));
+                if (j % EPP == EPP - 1) {
 #pragma unroll
-            for (int v = 0; v < VEC; ++v)
-                ykeep[q].v[v] = mine ? acc.v[v] : ykeep[q].v[v];
+                    for (int v = 0; v < VEC; ++v) {
+                        event_scatter<LOGE - 1, SH, EPP>(part[v], hi);
+                        ykeep[j / EPP].v[v] = part[v][0];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < VEC; ++v)
+                    acc.v[v] = CFL ? strided_sum<LPE>(acc.v[v]) : event_sum<EPP>(acc.v[v]);
+                const bool mine = ev % CH == j;
+#pragma unroll
+                for (int v = 0; v < VEC; ++v)
+                    ykeep[0].v[v] = mine ? acc.v[v] : ykeep[0].v[v];
+            }
         };
         // Token pairs: the second token's rows are loaded before the first
         // token's writes, and loaded again if the write sets may overlap.
