@@ -28,9 +28,10 @@ struct AddrSource {
 // in front of the state: writes at slot -2 (weight 0, alpha 1), reads at
 // slot -1 (weight 0). The workspace holds, in order: write records
 // (B*H, Kw, T_pad), read records (B*H, Kr, T_pad), then the gain records of
-// the precomputed-gain scan (B*H, max(Kw, Kr), T_pad) of GainRec. The
-// decoder records are never modified after they are written, so one set of
-// records can be scanned any number of times.
+// the precomputed-gain scan (B*H, T_pad, max(Kw, Kr)) of GainRec, token-major
+// so that the events of one token, which the scan's lanes load together,
+// are contiguous. The decoder records are never modified after they are
+// written, so one set of records can be scanned any number of times.
 constexpr int kScanChunk = 16;
 constexpr int kScanPad = 2 * kScanChunk;
 struct WriteRec {
@@ -45,8 +46,9 @@ struct ReadRec {
 };
 
 // One event of the precomputed-gain scan, written by the mass pre-pass:
-// write event e and read event e of one token. The sign bit of event 0's
-// gain carries the token's overlap flag (gains are never negative).
+// write event e and read event e of one token, for every event below
+// max(Kw, Kr) (past Kw a no-op write, past Kr a no-op read) and every token
+// below T (the padding tokens are not written).
 struct GainRec {
     int wslot;
     float gain;

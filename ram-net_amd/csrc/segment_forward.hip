@@ -356,7 +356,8 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * t_pad;
     const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad;
     // gain records of this head (not written in the record-keeping mode)
-    GainRec *gg = AUX ? nullptr : job.gain + static_cast<int64_t>(bh) * max(Kw, Kr) * t_pad;
+    const int ek = max(Kw, Kr);
+    GainRec *gg = AUX ? nullptr : job.gain + static_cast<int64_t>(bh) * ek * t_pad;
     const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
     auto run = [&](int t0, const MassRecs<MP, CH> &c) {
         auto wev = [&](int p, int j, int &a, float &w, float &al) {
@@ -375,12 +376,12 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 ms[a[p]] = m2;
                 gn[p] = scan_gain(w[p], m2 + eps);
                 if constexpr (!AUX) {
-                    if (wlane && ln.on[p] && live) {
-                        // event 0 carries the token's overlap flag in the gain's sign bit
-                        const int fl = p == 0 && hl == 0 && c.w[0][j].w != 0 ? static_cast<int>(0x80000000u) : 0;
-                        *reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(ln.ev[p]) * t_pad + t].wslot) =
-                            make_int2(a[p], __float_as_int(gn[p]) | fl);
-                    }
+                    // every event below max(Kw, Kr) gets a record; past Kw it is
+                    // the no-op write (slot -2, gain 0)
+                    const int e = p * 32 + hl;
+                    if (wlane && e < ek && live)
+                        *reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(t) * ek + e].wslot) =
+                            make_int2(a[p], __float_as_int(gn[p]));
                 }
             }
             {
@@ -409,14 +410,17 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
                     re[p] = MA ? rr[p] * mm[p] * scale : rr[p];
-                    if (!wlane && ln.on[p] && live) {
-                        if constexpr (AUX) {
+                    if constexpr (AUX) {
+                        if (!wlane && ln.on[p] && live) {
                             const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kr + ln.ev[p];
                             aux.rev[o] = make_int4(rb[p], __float_as_int(re[p]), __float_as_int(mm[p]), 0);
-                        } else {
-                            *reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(ln.ev[p]) * t_pad + t].rslot) =
-                                make_int2(rb[p], __float_as_int(re[p]));
                         }
+                    } else {
+                        // past Kr: the no-op read (slot -1, weight 0)
+                        const int e = p * 32 + hl;
+                        if (!wlane && e < ek && live)
+                            *reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(t) * ek + e].rslot) =
+                                make_int2(rb[p], __float_as_int(re[p]));
                     }
                 }
                 if constexpr (AUX) {

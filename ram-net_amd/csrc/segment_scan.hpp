@@ -124,6 +124,18 @@ __device__ __forceinline__ void event_scatter(float (&part)[N], const uint32_t (
     }
 }
 
+// 16-byte load and store through a vector type: int4 is a struct, and its
+// copies between memory and a register array become memcpys that can keep
+// the array in scratch memory.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 ld16(const void *p) {
+    const i32x4 v = *reinterpret_cast<const i32x4 *>(p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st16(void *p, const int4 &v) {
+    *reinterpret_cast<i32x4 *>(p) = i32x4{v.x, v.y, v.z, v.w};
+}
+
 // LDS byte address of a pointer into the workgroup's LDS, and back: a row
 // offset computed once per chunk then addresses its LDS access directly.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -132,11 +144,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 __device__ __forceinline__ float *lds_at(uint32_t a) {
     return (float *)(__attribute__((address_space(3))) float *)(uintptr_t)a;
 }
-// a * b + c for a, b below 2^24, as one v_mad_u32_u24 (left to itself the
-// compiler keeps the product and adds c at every use)
-__device__ __forceinline__ uint32_t mad24(uint32_t a, uint32_t b, uint32_t c) {
-    uint32_t r;
-    asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+// a * b + c for a, b in the signed 24-bit range (slots include the dummy
+// rows -2 and -1), as one v_mad_i32_i24 (left to itself the compiler keeps
+// the product and adds c at every use)
+__device__ __forceinline__ int mad24(int a, int b, int c) {
+    int r;
+    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
     return r;
 }
 
@@ -313,7 +326,8 @@ struct StageRec {
 // the dummy read row, A slots), the masses (2 dummies + A), then two chunk
 // buffers, 16-byte aligned, each holding the staged events (kChunk x E), x
 // (CS rows), the overlap flags and the raw records (kChunk x E) for the mass
-// wave.
+// wave. The precomputed-gain form has no masses and, per state wave, one
+// private stage of its records and x.
 __host__ __device__ constexpr size_t scan_stage_offset(int A, int rs, bool pre = false) {
     return ((static_cast<size_t>(A + 2) * rs + (pre ? 0 : static_cast<size_t>(A + 2))) * 4 + 15) / 16 * 16;
 }
@@ -321,18 +335,19 @@ __host__ __device__ constexpr size_t scan_stage_offset(int A, int rs, bool pre =
 // the double-buffered stage outgrow LDS.
 __host__ __device__ constexpr int scan_chunk_len(int events) { return events > 64 ? 8 : kChunk; }
 
-// PRE: gains precomputed by the mass pre-pass (no mass column, no staged
-// StageRec: the state waves read the records themselves).
+// PRE: gains precomputed by the mass pre-pass (no mass column; the state
+// waves stream their records from global memory and stage only x, one
+// buffer). The mass-wave form double-buffers the raw records for the mass
+// wave, the StageRec it produces, x and the overlap flags.
 inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem, bool pre = false) {
     const int cs = nw * (kWave / epp) * vec;
     const int ch = scan_chunk_len(epp * np);
     const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs), pre);
-    // PRE stages one compact StageRec per event; the mass-wave form stages
-    // the raw records for the mass wave and the StageRec it produces.
-    const size_t rec = pre ? sizeof(StageRec) : sizeof(StageRec) + sizeof(WriteRec) + sizeof(ReadRec);
-    const size_t stage = static_cast<size_t>(ch) * epp * np * rec + static_cast<size_t>(cs) * (ch * elem + 16) +
-                         ch * sizeof(int);
-    return state + 2 * stage;
+    const size_t x = static_cast<size_t>(cs) * (ch * elem + 16);
+    if (pre)  // one private stage per wave: its records and its channels' x
+        return state + static_cast<size_t>(nw) * ch * epp * np * 16 + x;
+    const size_t rec = sizeof(StageRec) + sizeof(WriteRec) + sizeof(ReadRec);
+    return state + 2 * (static_cast<size_t>(ch) * epp * np * rec + x + ch * sizeof(int));
 }
 
 // A workgroup owns one (b, h, CS-channel slice) unit: NW state waves, each
@@ -349,8 +364,10 @@ inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem, 
 // FAST: C is a multiple of CS, so every lane owns VEC real channels.
 // PRE: the mass pre-pass (segment_mass_kernel) has already written the gain
 // records (each write event's gain and, mass-aware, each read's effective
-// weight); there is no mass wave and no mass column, and the state waves
-// stage the gain records of the next chunk themselves.
+// weight); there is no mass wave and no mass column. Each state wave fetches
+// its chunks (records, x of its channels, overlap flags) two chunks ahead
+// into registers and stages them in a private LDS region: the waves run
+// without a barrier from the first chunk to the write-back.
 template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
 __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_kernel(const SegmentJob job,
                                                                                      const ScanGeom geo) {
@@ -368,8 +385,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     constexpr int XI = (CS * CH + NST - 1) / NST;  // staged x elements per state thread
     constexpr int NSL = EPP <= CH ? CH / EPP : 1;  // tokens whose y a lane stores
     constexpr int kStageRecBytes = PRE ? 0 : static_cast<int>(sizeof(StageRec));
-    constexpr int kRawBytes = PRE ? static_cast<int>(sizeof(StageRec))
-                                  : static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec));
+    constexpr int kRawBytes = PRE ? 0 : static_cast<int>(sizeof(WriteRec) + sizeof(ReadRec));
     constexpr int kStageBytes = CH * E * (kStageRecBytes + kRawBytes) + CS * XRB + CH * 4;
     constexpr int RI = (E * CH + NST - 1) / NST;  // raw records per state thread
     using Bits = std::conditional_t<ES == 4, uint32_t, uint16_t>;
@@ -399,8 +415,6 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     auto stage_f = [&](int buf) { return reinterpret_cast<int *>(stage_x(buf) + CS * XRB); };
     auto raw_w = [&](int buf) { return reinterpret_cast<WriteRec *>(stage_f(buf) + CH); };
     auto raw_r = [&](int buf) { return reinterpret_cast<ReadRec *>(raw_w(buf) + CH * E); };
-    // PRE: the compact records {write slot, gain, read slot, read weight}
-    auto pre_rec = [&](int buf) { return reinterpret_cast<int4 *>(stage_f(buf) + CH); };
 
     // ---- state slice and masses -> LDS
     {
@@ -442,40 +456,20 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
         for (int k = 0; k < RI; ++k) {
             const int it = min(tid + k * NST, E * CH - 1);
             const int e = it / CH, j = it % CH;
-            if constexpr (PRE) {
-                const int ee = e < EK ? e : EK - 1;
-                rg.w[k] = *reinterpret_cast<const int4 *>(gp + static_cast<int64_t>(ee) * Tp + t0 + j);
-            } else {
-                const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
-                rg.w[k] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ew) * Tp + t0 + j);
-                rg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
-            }
+            const int ew = e < Kw ? e : Kw - 1, er = e < Kr ? e : Kr - 1;
+            rg.w[k] = ld16(gw + static_cast<int64_t>(ew) * Tp + t0 + j);
+            rg.r[k] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(er) * Tp + t0 + j);
         }
     };
-    // PRE: the gain record goes to the stage as it is (one 16-byte LDS read
-    // per event and token for the state waves); events past top-K and tokens
-    // past T (which the pre-pass does not write) become no-ops here, and the
-    // sign bit of event 0's gain is the token's overlap flag.
-    auto raw_deposit = [&](int buf, int t0, const RawRegs &rg) {
+    auto raw_deposit = [&](int buf, const RawRegs &rg) {
         WriteRec *rw = raw_w(buf);
         ReadRec *rr = raw_r(buf);
 #pragma unroll
         for (int k = 0; k < RI; ++k) {
             const int it = min(tid + k * NST, E * CH - 1);
             const int e = it / CH, j = it % CH;
-            const int4 w = rg.w[k];
-            const int2 r = rg.r[k];
-            if constexpr (PRE) {
-                const bool live = t0 + j < T;
-                if (e == 0)
-                    stage_f(buf)[j] = live ? static_cast<int>(static_cast<uint32_t>(w.y) >> 31) : 0;
-                const bool wok = live && e < Kw, rok = live && e < Kr;
-                pre_rec(buf)[j * E + e] =
-                    make_int4(wok ? w.x : -2, wok ? (w.y & 0x7fffffff) : 0, rok ? w.z : -1, rok ? w.w : 0);
-            } else {
-                *reinterpret_cast<int4 *>(rw + j * E + e) = w;
-                *reinterpret_cast<int2 *>(rr + j * E + e) = r;
-            }
+            st16(rw + j * E + e, rg.w[k]);
+            *reinterpret_cast<int2 *>(rr + j * E + e) = rg.r[k];
         }
     };
     struct Raw {
@@ -635,24 +629,87 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             *reinterpret_cast<Bits *>(sx + c * XRB + j * ES) = xb[k];
         }
     };
-    // One chunk of the state waves. The token body is branch-free; each lane
-    // keeps the read sum of the tokens whose y it stores. TAIL guards tokens
-    // past T.
-    auto state_chunk = [&](int buf, int t0, auto tail_tag) {
-        constexpr bool TAIL = decltype(tail_tag)::value;
-        const StageRec *se = stage_e(buf);
-        const char *sx = stage_x(buf);
-        int4 rec[NP][CH];  // {write slot, gain, read slot, read weight}
+    // Records {write slot, gain, read slot, read weight} of one chunk, per
+    // pass and token, as the state waves use them.
+    struct Recs {
+        int4 r[NP][CH];
+    };
+    // Row address arithmetic per pass: slot * amul + base. In the PRE form
+    // lanes past the head's events (their staged records are copies of the
+    // last event's) write the dummy row -2 and read the zero row -1.
+    int amul[NP], awb[NP], arb[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const bool dead = PRE && p * EPP + ev >= EK;
+        amul[p] = dead ? 0 : RS * 4;
+        awb[p] = dead ? static_cast<int>(lds_addr(lds) + cl * 4) : static_cast<int>(lrow);
+        arb[p] = dead ? static_cast<int>(lds_addr(lds + RS) + cl * 4) : static_cast<int>(lrow);
+    }
+    // PRE: every wave stages its own chunk -- the gain records of all events
+    // (token-major, as the pre-pass writes them) and the x of its CSW
+    // channels -- in a private LDS region, from registers filled two chunks
+    // ahead. A wave's LDS accesses stay in program order, so the waves need
+    // no barrier until the write-back.
+    constexpr int RW = (CH * E + kWave - 1) / kWave;   // records per lane
+    constexpr int XIW = (CSW * CH + kWave - 1) / kWave;  // x elements per lane
+    constexpr int kPrivRec = CH * E * 16;
+    constexpr int kPrivBytes = kPrivRec + CSW * XRB;
+    char *priv = stage0 + wave * kPrivBytes;
+    const char *priv_x = priv + kPrivRec - wave * CSW * XRB;  // row of slice channel c at c * XRB
+    struct Fetch {
+        int4 rec[RW];
+        Bits x[XIW];
+        int flag;  // overlap flag of token (lane), lanes < CH
+    };
+    auto pre_fetch = [&](int t0, Fetch &f) {
+        const char *g = reinterpret_cast<const char *>(gp + static_cast<int64_t>(t0) * EK);
+#pragma unroll
+        for (int k = 0; k < RW; ++k) {
+            const int it = min(lane + k * kWave, CH * E - 1);
+            const int j = it / E, e = it % E;
+            f.rec[k] = ld16(g + static_cast<uint32_t>(j * EK + min(e, EK - 1)) * 16u);
+        }
+#pragma unroll
+        for (int k = 0; k < XIW; ++k) {
+            const int it = min(lane + k * kWave, CSW * CH - 1);
+            const int j = it / CSW, c = wave * CSW + it % CSW;
+            const int t = t0 + j < T ? t0 + j : T - 1;
+            const int ch = c0 + c < C ? c0 + c : C - 1;
+            f.x[k] = *reinterpret_cast<const Bits *>(gx + static_cast<int64_t>(t) * C + ch);
+        }
+        // write event 0's record carries the token's overlap flag
+        f.flag = Kw > 0 ? __float_as_int(gw[t0 + min(lane, CH - 1)].overlap) : 0;
+    };
+    auto pre_deposit = [&](const Fetch &f) {
+#pragma unroll
+        for (int k = 0; k < RW; ++k) {
+            const int it = min(lane + k * kWave, CH * E - 1);
+            st16(priv + it * 16, f.rec[k]);
+        }
+        char *px = const_cast<char *>(priv_x);
+#pragma unroll
+        for (int k = 0; k < XIW; ++k) {
+            const int it = min(lane + k * kWave, CSW * CH - 1);
+            const int j = it / CSW, c = wave * CSW + it % CSW;
+            *reinterpret_cast<Bits *>(px + c * XRB + j * ES) = f.x[k];
+        }
+    };
+    auto flag_mask = [&](int fv) -> uint64_t { return __ballot(lane < CH && fv != 0); };
+    // records of one chunk from a stage laid out [token][event]
+    auto stage_recs = [&](const void *se, Recs &rc) {
 #pragma unroll
         for (int j = 0; j < CH; ++j)
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                if constexpr (PRE) {
-                    rec[p][j] = pre_rec(buf)[j * E + p * EPP + ev];
-                } else {
-                    rec[p][j] = *reinterpret_cast<const int4 *>(se + j * E + p * EPP + ev);
-                }
-            }
+            for (int p = 0; p < NP; ++p)
+                rc.r[p][j] = ld16(static_cast<const int4 *>(se) + j * E + p * EPP + ev);
+    };
+    // One chunk of the state waves. The token body is branch-free; each lane
+    // keeps the read sum of the tokens whose y it stores. TAIL guards tokens
+    // past T.
+    // rc: the chunk's records, consumed (turned into row addresses).
+    auto state_chunk = [&](const char *sx, int t0, auto tail_tag, Recs &rc, uint64_t fm) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        auto &rec = rc.r;
         constexpr int XW = CH * ES / 16;  // 16-byte words per staged channel row
         uint4 xr[VEC][XW];
 #pragma unroll
@@ -676,24 +733,23 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
                 ykeep[q].v[v] = 0.f;
-        const int4 *sf4 = reinterpret_cast<const int4 *>(stage_f(buf));
-        int4 fl[CH / 4];
-#pragma unroll
-        for (int q = 0; q < CH / 4; ++q)
-            fl[q] = sf4[q];
-        auto flag = [&](int j) {
-            const int4 q = fl[j / 4];
-            const int v = (j % 4) == 0 ? q.x : (j % 4) == 1 ? q.y : (j % 4) == 2 ? q.z : q.w;
-            return __builtin_amdgcn_readfirstlane(v);
-        };
+        auto flag = [&](int j) { return ((fm >> j) & 1u) != 0; };
         // LDS addresses of every event's row (one 24-bit multiply-add each),
-        // computed once per chunk, off the token chain.
+        // computed once per chunk, off the token chain. PRE records past T
+        // were never written: those tokens act on the dummy rows.
 #pragma unroll
         for (int j = 0; j < CH; ++j)
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                rec[p][j].x = static_cast<int>(mad24(static_cast<uint32_t>(rec[p][j].x), RS * 4, lrow));
-                rec[p][j].z = static_cast<int>(mad24(static_cast<uint32_t>(rec[p][j].z), RS * 4, lrow));
+                int wa = rec[p][j].x, ra = rec[p][j].z;
+                if constexpr (PRE && TAIL) {
+                    const bool live = t0 + j < T;
+                    wa = live ? wa : -2;
+                    ra = live ? ra : -1;
+                    rec[p][j].w = live ? rec[p][j].w : 0;
+                }
+                rec[p][j].x = mad24(wa, amul[p], awb[p]);
+                rec[p][j].z = mad24(ra, amul[p], arb[p]);
             }
         auto row = [&](int a) { return lds_at(static_cast<uint32_t>(a)); };
         auto load_rows = [&](int j, FVec<VEC> (&s)[NP]) {
@@ -813,36 +869,50 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     RawRegs rg;
     Bits xb[XI];
     if constexpr (PRE) {
-        // Iteration ci: run chunk ci (stage ci & 1) while the records and x
-        // of chunk ci + 1 are in flight; deposit them after the chunk.
+        // Iteration ci: chunk ci runs from the private stage (deposited at
+        // the end of chunk ci - 1) while the registers of chunk ci + 2 fill;
+        // after it, chunk ci + 1 (fetched two chunks earlier) is deposited.
+        Fetch fa, fb;
+        __syncthreads();  // state slice loaded
         if (nc > 0) {
-            raw_fetch(0, rg);
-            x_fetch(0, xb);
-            raw_deposit(0, 0, rg);
-            x_deposit(0, xb);
+            pre_fetch(0, fa);
+            pre_fetch(clampc(1), fb);
+            pre_deposit(fa);
+        }
+        auto run = [&](int ci, int fv) {
+            Recs rc;
+            stage_recs(priv, rc);
+            const uint64_t fm = flag_mask(fv);
+            if (ci < n_full)
+                state_chunk(priv_x, ci * CH, Full{}, rc, fm);
+            else
+                state_chunk(priv_x, ci * CH, Tail{}, rc, fm);
+        };
+        for (int ci = 0; ci < nc; ci += 2) {
+            const int f0 = fa.flag;
+            pre_fetch(clampc(ci + 2), fa);
+            __builtin_amdgcn_sched_barrier(0);
+            run(ci, f0);
+            __builtin_amdgcn_sched_barrier(0);
+            pre_deposit(fb);
+            if (ci + 1 >= nc)
+                break;
+            const int f1 = fb.flag;
+            pre_fetch(clampc(ci + 3), fb);
+            __builtin_amdgcn_sched_barrier(0);
+            run(ci + 1, f1);
+            __builtin_amdgcn_sched_barrier(0);
+            pre_deposit(fa);
         }
         __syncthreads();
-        for (int ci = 0; ci < nc; ++ci) {
-            x_fetch(clampc(ci + 1), xb);
-            raw_fetch(clampc(ci + 1), rg);
-            __builtin_amdgcn_sched_barrier(0);
-            if (ci < n_full)
-                state_chunk(ci & 1, ci * CH, Full{});
-            else
-                state_chunk(ci & 1, ci * CH, Tail{});
-            __builtin_amdgcn_sched_barrier(0);
-            x_deposit((ci + 1) & 1, xb);
-            raw_deposit((ci + 1) & 1, clampc(ci + 1), rg);
-            __syncthreads();
-        }
     } else {
         __syncthreads();  // masses initialised before the mass wave starts
         if (nc > 0) {
             if (!mass_wave) {
                 raw_fetch(0, rg);
-                raw_deposit(0, 0, rg);
+                raw_deposit(0, rg);
                 raw_fetch(clampc(1), rg);
-                raw_deposit(1, clampc(1), rg);
+                raw_deposit(1, rg);
                 x_fetch(0, xb);
                 x_deposit(0, xb);
             }
@@ -864,13 +934,16 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
                 x_fetch(clampc(ci + 1), xb);
                 raw_fetch(clampc(ci + 2), rg);
                 __builtin_amdgcn_sched_barrier(0);
+                Recs rc;
+                stage_recs(stage_e(ci & 1), rc);
+                const uint64_t fm = flag_mask(stage_f(ci & 1)[min(lane, CH - 1)]);
                 if (ci < n_full)
-                    state_chunk(ci & 1, ci * CH, Full{});
+                    state_chunk(stage_x(ci & 1), ci * CH, Full{}, rc, fm);
                 else
-                    state_chunk(ci & 1, ci * CH, Tail{});
+                    state_chunk(stage_x(ci & 1), ci * CH, Tail{}, rc, fm);
                 __builtin_amdgcn_sched_barrier(0);
                 x_deposit((ci + 1) & 1, xb);
-                raw_deposit(ci & 1, clampc(ci + 2), rg);
+                raw_deposit(ci & 1, rg);
             }
             __syncthreads();
         }
