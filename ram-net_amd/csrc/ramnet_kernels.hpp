@@ -38,7 +38,8 @@ struct WriteRec {
     int slot;
     float w;
     float alpha;
-    float overlap;  // int bits: 1 if a slot of this token is also written by token t - 1 (or unknown)
+    float overlap;  // int bits, event 0: bit d - 1 set if a slot of this token is also written by token t - d
+                    // (d = 1, 2, 3), or if that is not known
 };
 struct ReadRec {
     int slot;

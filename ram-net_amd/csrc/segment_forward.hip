@@ -73,11 +73,14 @@ struct Plan {
 // workgroups: a wave's token loop is bound by its dependency chain (LDS
 // read -> update -> LDS write, ~kChainCycles) or by the issue of its VALU
 // work (~10 + 6 * VEC * NP instructions, 4 cycles each, shared by the waves
-// on one SIMD), whichever is longer. Total = rounds * per-token cycles.
+// on one SIMD), whichever is longer. Total = rounds * per-token cycles. In
+// the mass-wave form the mass wave's own chain (mass update, gain, staging:
+// ~kMassWaveCycles per token) paces the state waves; the precomputed-gain
+// form instead pays for its pre-pass, chunked over time across the GPU
+// (~kPrePassCycles per token). Measured per-token figures on MI355X.
 constexpr int64_t kChainCycles = 160;
-// The mass pre-pass: one wave per (b, h) walks the sequence with the masses
-// in LDS; its token chain is one LDS read-modify-write (~kMassChainCycles).
-constexpr int64_t kMassChainCycles = 120;
+constexpr int64_t kMassWaveCycles = 230;
+constexpr int64_t kPrePassCycles = 60;
 constexpr int64_t kMassPassLds = 64 * 1024;  // chunk maps (A + 2) * 8 bytes: A <= 8190
 
 bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, Plan *out) {
@@ -108,11 +111,11 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, P
                     const int64_t resident = std::min<int64_t>(per_cu, (units + n_cu - 1) / n_cu);
                     const int64_t waves_per_simd = (resident * nw + 3) / 4;
                     const int64_t issue = 4 * (10 + 6 * vec * np) * waves_per_simd;
-                    int64_t cost = rounds * std::max(kChainCycles, issue);
+                    int64_t cost = rounds * std::max(pre ? kChainCycles : kMassWaveCycles, issue);
                     if (C % cs != 0)
                         cost = cost * 3 / 2;  // partial slices take the guarded path
-                    if (pre)  // chunked over time: a few chunk replays of tokens
-                        cost += 2 * kMassChainCycles;
+                    if (pre)
+                        cost += kPrePassCycles;
                     const bool better = !found || cost < best ||
                                         (cost == best && (nw > out->nw || (nw == out->nw && cs > out->cs)));
                     if (better) {
@@ -151,13 +154,14 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
     const bool live = t < T && *mp != 0 && static_cast<unsigned>(a) < static_cast<unsigned>(A);
     if (k < job.Kw) {
         const bool act = live && v != 0.f;
-        // Event 0 carries the token's overlap flag, which the scan reads:
-        // whether a slot this token writes is also written by token t - 1.
-        // Computed exactly for top-K up to 16; assumed for wider top-K.
-        int ov = 1;
+        // Event 0 carries the token's overlap flags, which the scan reads:
+        // bit d - 1 set if a slot this token writes is also written by token
+        // t - d (d = 1, 2, 3). Computed exactly for top-K up to 16; assumed
+        // for wider top-K.
+        int ov = 7;
         if (k == 0 && job.Kw <= 16) {
             ov = 0;
-            if (t > 0 && t < T) {
+            if (t < T) {
                 // slot written by write event kk of token tt (tt < T), or -1
                 auto written = [&](int tt, int kk) {
                     const int64_t s = (static_cast<int64_t>(bh) * Kt + kk) * T + tt;
@@ -166,15 +170,20 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
                     return *m != 0 && static_cast<unsigned>(aa) < static_cast<unsigned>(A) && job.addr_val[s] != 0.f
                                ? aa : -1;
                 };
-                int prev[16];
+                int cur[16];
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
-                    prev[i] = i < job.Kw ? written(t - 1, i) : -1;
-                for (int i = 0; i < job.Kw; ++i) {
-                    const int x = written(t, i);
+                    cur[i] = i < job.Kw ? written(t, i) : -1;
+                for (int d = 1; d <= 3 && d <= t; ++d) {
+                    bool hit = false;
+                    for (int i = 0; i < job.Kw; ++i) {
+                        const int x = written(t - d, i);
 #pragma unroll
-                    for (int j = 0; j < 16; ++j)
-                        ov |= x >= 0 && x == prev[j] ? 1 : 0;
+                        for (int j = 0; j < 16; ++j)
+                            hit = hit || (x >= 0 && x == cur[j]);
+                    }
+                    if (hit)
+                        ov |= 1 << (d - 1);
                 }
             }
         }
@@ -455,7 +464,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
 #pragma unroll
         for (int j0 = 0; j0 < CH; j0 += 2) {
             const int j1 = j0 + 1;
-            const int ov = __builtin_amdgcn_readfirstlane(c.w[0][j1].w);
+            const int ov = __builtin_amdgcn_readfirstlane(c.w[0][j1].w) & 1;  // shares a slot with token j0
             int a0[MP], a1[MP];
             float w0[MP], w1[MP], al0[MP], al1[MP], m0[MP], m1[MP];
 #pragma unroll

@@ -124,6 +124,10 @@ __device__ __forceinline__ void event_scatter(float (&part)[N], const uint32_t (
     }
 }
 
+// Overlap flag read when a head has no write events (a global, not a
+// constant: a constant-space pointer would make the flag load a flat one).
+static __device__ int kNoFlag = 0;
+
 // 16-byte load and store through a vector type: int4 is a struct, and its
 // copies between memory and a register array become memcpys that can keep
 // the array in scratch memory.
@@ -546,7 +550,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
 #pragma unroll
         for (int j0 = 0; j0 < CH; j0 += 2) {
             const int j1 = j0 + 1;
-            const int ov = __builtin_amdgcn_readfirstlane(raw.w[0][j1].w);
+            const int ov = __builtin_amdgcn_readfirstlane(raw.w[0][j1].w) & 1;  // shares a slot with token j0
             int a0[MP], a1[MP];
             float w0[MP], w1[MP], al0[MP], al1[MP], m0[MP], m1[MP];
 #pragma unroll
@@ -677,8 +681,10 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             const int ch = c0 + c < C ? c0 + c : C - 1;
             f.x[k] = *reinterpret_cast<const Bits *>(gx + static_cast<int64_t>(t) * C + ch);
         }
-        // write event 0's record carries the token's overlap flag
-        f.flag = Kw > 0 ? __float_as_int(gw[t0 + min(lane, CH - 1)].overlap) : 0;
+        // write event 0's record carries the token's overlap flag (a load
+        // without a branch: a conditional one would be waited for at once)
+        const int *fp = Kw > 0 ? reinterpret_cast<const int *>(&gw[t0 + min(lane, CH - 1)].overlap) : &kNoFlag;
+        f.flag = *fp;
     };
     auto pre_deposit = [&](const Fetch &f) {
 #pragma unroll
@@ -694,7 +700,12 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             *reinterpret_cast<Bits *>(px + c * XRB + j * ES) = f.x[k];
         }
     };
-    auto flag_mask = [&](int fv) -> uint64_t { return __ballot(lane < CH && fv != 0); };
+    // Reload mask of a chunk from its tokens' overlap flags (one token per
+    // lane): token j, at position i = j % 4 of its group, is reloaded when it
+    // may share a written slot with one of the i tokens before it.
+    auto flag_mask = [&](int fv) -> uint64_t {
+        return __ballot(lane < CH && (fv & ((1 << (lane & 3)) - 1)) != 0);
+    };
     // records of one chunk from a stage laid out [token][event]
     auto stage_recs = [&](const void *se, Recs &rc) {
 #pragma unroll
@@ -812,32 +823,41 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
                     ykeep[0].v[v] = mine ? acc.v[v] : ykeep[0].v[v];
             }
         };
-        // Token pairs: the second token's rows are loaded before the first
-        // token's writes, and loaded again if the write sets may overlap.
-        // The read sums of a pair are reduced after the next pair's row
-        // loads are issued, so the only LDS round trip on the token chain is
-        // the row load. The reload path drains LDS itself (a rare branch);
-        // otherwise the wait merged at its join would also cover the first
-        // token's read rows.
-        FVec<VEC> rp0[NP], rp1[NP];
+        // Groups of four tokens: the rows of all four are loaded before the
+        // first token's writes, and a token's rows are loaded again when its
+        // writes may meet an earlier token's of the group (reload mask). The
+        // read sums of a group are reduced after the next group's row loads
+        // are issued, so the only LDS round trip on the token chain is one
+        // row load per group. The reload path drains LDS itself (a rare
+        // branch); otherwise the wait merged at its join would also cover the
+        // earlier tokens' read rows.
+        constexpr int G = 4;
+        static_assert(CH % G == 0, "chunks hold whole token groups");
+        FVec<VEC> rp[G][NP];
 #pragma unroll
-        for (int j0 = 0; j0 < CH; j0 += 2) {
-            FVec<VEC> s0[NP], s1[NP];
-            load_rows(j0, s0);
-            load_rows(j0 + 1, s1);
+        for (int j0 = 0; j0 < CH; j0 += G) {
+            FVec<VEC> sv[G][NP];
+#pragma unroll
+            for (int i = 0; i < G; ++i)
+                load_rows(j0 + i, sv[i]);
             if (j0 > 0) {
-                reduce(j0 - 2, rp0);
-                reduce(j0 - 1, rp1);
+#pragma unroll
+                for (int i = 0; i < G; ++i)
+                    reduce(j0 - G + i, rp[i]);
             }
-            write_read(j0, s0, rp0);
-            if (flag(j0 + 1)) {
-                load_rows(j0 + 1, s1);
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            write_read(j0, sv[0], rp[0]);
+#pragma unroll
+            for (int i = 1; i < G; ++i) {
+                if (flag(j0 + i)) {
+                    load_rows(j0 + i, sv[i]);
+                    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                }
+                write_read(j0 + i, sv[i], rp[i]);
             }
-            write_read(j0 + 1, s1, rp1);
         }
-        reduce(CH - 2, rp0);
-        reduce(CH - 1, rp1);
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+            reduce(CH - G + i, rp[i]);
         // y of this chunk: lane stores tokens q * EPP + ev (or ev % 16)
 #pragma unroll
         for (int q = 0; q < NSL; ++q) {
@@ -872,37 +892,42 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
         // Iteration ci: chunk ci runs from the private stage (deposited at
         // the end of chunk ci - 1) while the registers of chunk ci + 2 fill;
         // after it, chunk ci + 1 (fetched two chunks earlier) is deposited.
+        // The overlap flags become a scalar mask at deposit, so no loaded
+        // vector value is live across the next fetch into its registers (the
+        // copy that would keep it waits for every outstanding memory
+        // operation, the chunk's y stores included).
         Fetch fa, fb;
+        uint64_t fm = 0;  // flags of the chunk in the stage
         __syncthreads();  // state slice loaded
         if (nc > 0) {
             pre_fetch(0, fa);
             pre_fetch(clampc(1), fb);
             pre_deposit(fa);
+            fm = flag_mask(fa.flag);
         }
-        auto run = [&](int ci, int fv) {
+        auto run = [&](int ci, uint64_t m) {
             Recs rc;
             stage_recs(priv, rc);
-            const uint64_t fm = flag_mask(fv);
             if (ci < n_full)
-                state_chunk(priv_x, ci * CH, Full{}, rc, fm);
+                state_chunk(priv_x, ci * CH, Full{}, rc, m);
             else
-                state_chunk(priv_x, ci * CH, Tail{}, rc, fm);
+                state_chunk(priv_x, ci * CH, Tail{}, rc, m);
         };
         for (int ci = 0; ci < nc; ci += 2) {
-            const int f0 = fa.flag;
             pre_fetch(clampc(ci + 2), fa);
             __builtin_amdgcn_sched_barrier(0);
-            run(ci, f0);
+            run(ci, fm);
             __builtin_amdgcn_sched_barrier(0);
             pre_deposit(fb);
+            fm = flag_mask(fb.flag);
             if (ci + 1 >= nc)
                 break;
-            const int f1 = fb.flag;
             pre_fetch(clampc(ci + 3), fb);
             __builtin_amdgcn_sched_barrier(0);
-            run(ci + 1, f1);
+            run(ci + 1, fm);
             __builtin_amdgcn_sched_barrier(0);
             pre_deposit(fa);
+            fm = flag_mask(fa.flag);
         }
         __syncthreads();
     } else {

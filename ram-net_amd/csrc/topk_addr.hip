@@ -142,31 +142,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FAST && KM 
     }
     const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + tl], A) : 0;
     if (rec_mode) {
-        // Overlap flag of the write address: whether any written slot of this
-        // token is also written by token t - 1 (decoded by the previous lane;
-        // in another wave for lane 0, so assumed). The scan uses it to start a
-        // token's reads before the previous token's writes when they are
-        // disjoint.
+        // Overlap flags of the write address, bit d - 1 for d = 1, 2, 3:
+        // whether a written slot of this token is also written by token
+        // t - d (decoded d lanes back; in another wave for the first d
+        // lanes, so assumed). The scan loads the rows of up to four tokens
+        // before their writes and loads a token's rows again only when they
+        // may have been written within its group.
         int overlap = 0;
         if (blockIdx.y == 0) {
             const uint8_t *mp = job.mask ? job.mask + static_cast<int64_t>(b) * T + tl : &kAddrAllValid;
             const bool live = t < T && *mp != 0 && !inactive;
-            int mine[KM], prev[KM];
+            int mine[KM];
 #pragma unroll
             for (int k = 0; k < KM; ++k) {
                 int o = mi[k] - shift;
                 o = o < 0 ? o + A : o;
                 mine[k] = live && k < K ? o : -1;
-                prev[k] = __shfl_up(mine[k], 1);
             }
-            bool hit = false;
+            const int wl = static_cast<int>(threadIdx.x & (kWave - 1));
 #pragma unroll
-            for (int k = 0; k < KM; ++k)
+            for (int d = 1; d <= 3; ++d) {
+                int prev[KM];
 #pragma unroll
-                for (int k2 = 0; k2 < KM; ++k2)
-                    hit = hit || (mine[k] >= 0 && mine[k] == prev[k2]);
-            const bool first_lane = (threadIdx.x & (kWave - 1)) == 0;
-            overlap = t > 0 && (hit || first_lane) ? 1 : 0;
+                for (int k = 0; k < KM; ++k)
+                    prev[k] = __shfl_up(mine[k], d);
+                bool hit = false;
+#pragma unroll
+                for (int k = 0; k < KM; ++k)
+#pragma unroll
+                    for (int k2 = 0; k2 < KM; ++k2)
+                        hit = hit || (mine[k] >= 0 && mine[k] == prev[k2]);
+                if (t >= d && (hit || wl < d))
+                    overlap |= 1 << (d - 1);
+            }
         }
         write_records<Scalar, KM>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
             c = mi[k];
@@ -223,7 +231,7 @@ __global__ __launch_bounds__(256) void topk_addr_bruteforce_kernel(const AddrJob
             write_records<Scalar, 0>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
                 c = si[k];
                 v = expf(sv[k] - src.re_norm * s_lse);
-            }, K, shift, 1);  // overlap with token t - 1 not computed: assumed
+            }, K, shift, 7);  // overlaps with tokens t - 1 .. t - 3 not computed: assumed
         return;
     }
     const int idx_base = (job.encode_batch_idx ? static_cast<int>(bh) : h) * A;

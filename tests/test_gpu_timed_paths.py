@@ -6,10 +6,11 @@ against the CPU oracle.
   calls them (bf16, P=32, K=8, CAPE on 8 of 16 heads). Its per-event records
   must equal, bit for bit, the records ``pack_records_kernel`` builds from
   ``ramnet_topk_addr_forward``'s (idx, val) -- slot, weight and forget
-  coefficient -- and its per-token overlap flag must be set wherever the
-  packer's exact flag is (it may also be set where the packer's is not: a
-  wave's first lane assumes overlap). y, slot and mass on several heads
-  match the fp64 event loop.
+  coefficient -- the packer's per-token overlap flags (bit d - 1: a written
+  slot shared with token t - d, d = 1..3) must equal the exact ones computed
+  here from the slots, and the record decoder's must be set wherever those
+  are (it may also be set where they are not: a wave's first lanes assume
+  overlap). y, slot and mass on several heads match the fp64 event loop.
 * Config 3: 16 consecutive decode steps at B=64, H=16 on the 64x16x1024x128
   fp32 state, captured in one HIP graph as the benchmark captures them and
   replayed; every step's indices against the fp64 ranking, and y of every
@@ -94,10 +95,19 @@ def test_config2_benched_path_matches_packed_records_and_oracle():
     wb, rb = _records(ws_b, B, H, T, K, K)
     assert torch.equal(wa[..., :3], wb[..., :3]), "write records (slot, w, alpha) differ from the packed records"
     assert torch.equal(ra, rb), "read records (slot, r) differ from the packed records"
-    fa, fb = wa[:, 0, :, 3], wb[:, 0, :, 3]  # event 0 carries the token's overlap flag
-    assert bool(((fa == 1) | (fb == 0)).all()), "record-mode overlap flag missing where the write sets overlap"
-    print(f"overlap flags: record mode {int(fa[:, :T].sum())}, exact {int(fb[:, :T].sum())} of {B * H * T} tokens",
-          flush=True)
+    # event 0 carries the token's overlap flags: bit d - 1 when a written
+    # slot is also written by token t - d (d = 1, 2, 3)
+    fa, fb = wa[:, 0, :T, 3], wb[:, 0, :T, 3]
+    slots = wb[:, :, :T, 0]  # (B*H, K, T), -2 for no-op writes
+    exact = torch.zeros_like(fb)
+    for d in (1, 2, 3):
+        cur, prev = slots[:, :, None, d:], slots[:, None, :, :-d]
+        hit = ((cur == prev) & (cur >= 0)).flatten(1, 2).any(dim=1)
+        exact[:, d:] |= hit.to(exact.dtype) << (d - 1)
+    assert torch.equal(fb, exact), "packed-record overlap flags differ from the exact ones (top-K <= 16)"
+    assert bool(((fa & exact) == exact).all()), "record-mode overlap flag missing where the write sets overlap"
+    print(f"overlap flags (t-1, t-2, t-3): record mode {[int(((fa >> d) & 1).sum()) for d in range(3)]}, "
+          f"exact {[int(((exact >> d) & 1).sum()) for d in range(3)]} of {B * H * T} tokens", flush=True)
     # the flag only selects a reload: both scans give the same bits
     assert torch.equal(y_a, y_b) and torch.equal(slot_a, slot_b) and torch.equal(mass_a, mass_b)
 
