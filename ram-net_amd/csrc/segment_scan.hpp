@@ -59,12 +59,6 @@ __device__ __forceinline__ float event_sum(float v) {
     return v;
 }
 
-// One exchange of a reduce-scatter over lane bit LB, partner = lane ^ (1 <<
-// LB): lanes with the bit clear receive a + a(partner), lanes with it set
-// b + b(partner). Across rows v_permlane16/32_swap trades a's upper half for
-// b's lower half in one instruction, so the two outputs add to the pair sum
-// with no select; within a row, two DPP adds and a bit select (hi = all ones
-// in the lanes with the bit set).
 // a + (lane CTRL of a), for DPP patterns whose source lane always exists or
 // whose missing-source lanes are not used (bound_ctrl: reads 0, no old value)
 template<int CTRL>
@@ -80,6 +74,12 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
     return r;
 }
 
+// One exchange of a reduce-scatter over lane bit LB, partner = lane ^ (1 <<
+// LB): lanes with the bit clear receive a + a(partner), lanes with it set
+// b + b(partner). Across rows v_permlane16/32_swap trades a's upper half for
+// b's lower half in one instruction, so the two outputs add to the pair sum
+// with no select; within a row, two DPP adds and a bit select (hi = all ones
+// in the lanes with the bit set).
 template<int LB>
 __device__ __forceinline__ float scatter_pair(float a, float b, uint32_t hi) {
     if constexpr (LB == 5) {
@@ -848,7 +848,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             write_read(j0, sv[0], rp[0]);
 #pragma unroll
             for (int i = 1; i < G; ++i) {
-                if (flag(j0 + i)) {
+                if (__builtin_expect(flag(j0 + i), 0)) {
                     load_rows(j0 + i, sv[i]);
                     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
                 }
