@@ -633,8 +633,10 @@ __global__ __launch_bounds__(2 * kWave) void autoregressive_steps_kernel(const D
     }
 }
 
-// General shapes: exact LDS search, then sequential row updates.
-template<typename T>
+// General shapes: exact LDS search (STAIR false, NA = pow2 >= A) or the
+// staircase search for wider slot spaces (STAIR true, NA = candidate buffer),
+// then sequential row updates.
+template<typename T, bool STAIR>
 __global__ __launch_bounds__(64) void autoregressive_general_kernel(const DecodeJob job, int NA, int NPD) {
     extern __shared__ float smem[];
     __shared__ int s_flag;
@@ -649,11 +651,16 @@ __global__ __launch_bounds__(64) void autoregressive_general_kernel(const Decode
             store_f32(yrow + c, 0.f);
         return;
     }
+    const int KM = Kw > Kr ? Kw : Kr;
     float *lg = smem;
     float *ex = lg + U * P;
-    float *sv = ex + U * NPD;
+    int *di = reinterpret_cast<int *>(ex + U * NPD);  // staircase only
+    float *sv = STAIR ? reinterpret_cast<float *>(di + U * NPD) : ex + U * NPD;
     int *si = reinterpret_cast<int *>(sv + NA);
-    int *ev_slot = si + NA;            // Kw + Kr
+    float *pv = reinterpret_cast<float *>(si + NA);    // staircase only: KM, KM, KM + 1
+    int *pi = reinterpret_cast<int *>(pv + (STAIR ? KM : 0));
+    int *off = pi + (STAIR ? KM : 0);
+    int *ev_slot = off + (STAIR ? KM + 1 : 0);  // Kw + Kr
     float *ev_val = reinterpret_cast<float *>(ev_slot + Kw + Kr);  // Kw + Kr
     const int shift = h < job.embed_num ? pos_mod(job.position_ids[b], A) : 0;
 
@@ -661,7 +668,11 @@ __global__ __launch_bounds__(64) void autoregressive_general_kernel(const Decode
         const T *ptr = static_cast<const T *>(which ? job.r_addr : job.w_addr) + static_cast<int64_t>(bh) * U * P;
         const int K = which ? Kr : Kw;
         const float re = which ? job.r_re_norm : job.w_re_norm;
-        const bool inactive = block_search_exact(ptr, 1, U, P, A, NA, NPD, lg, ex, sv, si, &s_flag);
+        bool inactive;
+        if constexpr (STAIR)
+            inactive = block_search_stair(ptr, 1, U, P, K, NPD, NA, lg, ex, di, sv, si, pv, pi, off, &s_flag);
+        else
+            inactive = block_search_exact(ptr, 1, U, P, A, NA, NPD, lg, ex, sv, si, &s_flag);
         const float lse = (re != 0.f && !inactive) ? topk_lse_serial(sv, K) : 0.f;
         for (int k = lane; k < K; k += kWave) {
             const int content = inactive ? k : si[k];
@@ -780,11 +791,25 @@ hipError_t launch_typed(const DecodeJob &job, hipStream_t stream, const char **w
     const int NA = pow2_ceil(job.A), NPD = pow2_ceil(job.P);
     const size_t lds = static_cast<size_t>(job.U) * job.P * 4 + static_cast<size_t>(job.U) * NPD * 4 +
                        static_cast<size_t>(NA) * 8 + static_cast<size_t>(job.Kw + job.Kr) * 8;
-    if (lds > 96 * 1024) {
-        *why = "decode step: shape needs P <= 64, top_k <= 16, C <= 256 and A*C*4 < 2^31, or P**U small enough for the exact LDS search (A <= 8192)";
+    if (lds <= 96 * 1024) {
+        hipLaunchKernelGGL((autoregressive_general_kernel<T, false>), grid, dim3(kWave), lds, stream, job, NA, NPD);
+        return hipGetLastError();
+    }
+    // wider slot spaces: the staircase search, any A
+    const int km = std::max(job.Kw, job.Kr);
+    if (km > 128 || NPD > 1024) {
+        *why = "decode step: slot spaces beyond the exact LDS search (A > 8192) take top_k <= 128 and P <= 1024";
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(autoregressive_general_kernel<T>, grid, dim3(kWave), lds, stream, job, NA, NPD);
+    const int NC = stair_buffer(job.P, km, NPD);
+    const size_t lds_s = static_cast<size_t>(job.U) * job.P * 4 + static_cast<size_t>(job.U) * NPD * 8 +
+                         static_cast<size_t>(NC) * 8 + static_cast<size_t>(km) * 8 + static_cast<size_t>(km + 1) * 4 +
+                         static_cast<size_t>(job.Kw + job.Kr) * 8;
+    if (lds_s > 96 * 1024) {
+        *why = "decode step: staircase search scratch exceeds LDS (U * P too large)";
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL((autoregressive_general_kernel<T, true>), grid, dim3(kWave), lds_s, stream, job, NC, NPD);
     return hipGetLastError();
 }
 

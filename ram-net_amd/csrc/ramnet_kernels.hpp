@@ -196,6 +196,9 @@ hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const cha
 hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const char **why);
 // S consecutive decode steps; the inputs, y, position_ids and mask of a
 // DecodeJob carry a leading step dimension (S, ...).
+// Candidate buffer (a power of two) of the staircase address search for
+// radix P, top-K K and NPD = pow2 >= P.
+int stair_buffer(int P, int K, int NPD);
 hipError_t launch_autoregressive_steps(const DecodeJob &job, int S, hipStream_t stream, const char **why);
 
 // Channel-slice width, dynamic LDS bytes and form (1: precomputed gains)

@@ -24,9 +24,12 @@ constexpr float kNegInfF = -__builtin_huge_valf();
 // NPD = pow2 >= P. `ptr` points at digit 0 / radix 0 of the address and
 // consecutive logits are `stride` elements apart. Writes the sorted top
 // entries to sv/si[0..K) and returns the inactive flag (uniform).
+// Loads an address's U x P logits into lg (stride `stride` elements apart)
+// and replaces them by their per-digit log-softmax; ex[U*NPD] is scratch.
+// Sets *flag when a digit is entirely -inf (inactive address).
 template<typename T>
-__device__ bool block_search_exact(const T *ptr, int64_t stride, int U, int P, int A, int NA, int NPD,
-                                   float *lg, float *ex, float *sv, int *si, int *flag) {
+__device__ void block_log_softmax(const T *ptr, int64_t stride, int U, int P, int NPD, float *lg, float *ex,
+                                  int *flag) {
     const int tid = threadIdx.x;
     const int nt = blockDim.x;
     if (tid == 0)
@@ -56,6 +59,50 @@ __device__ bool block_search_exact(const T *ptr, int64_t stride, int U, int P, i
             lg[u * P + p] = (lg[u * P + p] - mx) - ls;
     }
     __syncthreads();
+}
+
+// Bitonic sort of independent runs of n (a power of two) entries, all runs
+// at once: run r holds sv/si[r*n, (r+1)*n); order (score desc, index asc).
+__device__ __forceinline__ void block_sort_runs(float *sv, int *si, int n, int runs) {
+    const int tid = threadIdx.x;
+    const int nt = blockDim.x;
+    const int total = n * runs;
+    for (int k = 2; k <= n; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < total; i += nt) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const int lo = ((i % n) & k) == 0 ? i : l;
+                    const int hi = ((i % n) & k) == 0 ? l : i;
+                    if (before(sv[hi], si[hi], sv[lo], si[lo])) {
+                        const float tv = sv[lo];
+                        const int ti = si[lo];
+                        sv[lo] = sv[hi];
+                        si[lo] = si[hi];
+                        sv[hi] = tv;
+                        si[hi] = ti;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Result of decoding one address: K content slots (before CAPE), the
+// log-domain scores, and whether the address is inactive.
+//
+// Exact search by one workgroup: all A scores in LDS, bitonic sort.
+// Scratch: lg[U*P], ex[U*NPD], sv[NA], si[NA]; NA = pow2 >= A,
+// NPD = pow2 >= P. `ptr` points at digit 0 / radix 0 of the address and
+// consecutive logits are `stride` elements apart. Writes the sorted top
+// entries to sv/si[0..K) and returns the inactive flag (uniform).
+template<typename T>
+__device__ bool block_search_exact(const T *ptr, int64_t stride, int U, int P, int A, int NA, int NPD,
+                                   float *lg, float *ex, float *sv, int *si, int *flag) {
+    const int tid = threadIdx.x;
+    const int nt = blockDim.x;
+    block_log_softmax(ptr, stride, U, P, NPD, lg, ex, flag);
     for (int c = tid; c < NA; c += nt) {
         if (c < A) {
             int rem = c;
@@ -73,25 +120,90 @@ __device__ bool block_search_exact(const T *ptr, int64_t stride, int U, int P, i
         }
     }
     __syncthreads();
-    for (int k = 2; k <= NA; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = tid; i < NA; i += nt) {
-                const int l = i ^ j;
-                if (l > i) {
-                    const int lo = (i & k) == 0 ? i : l;
-                    const int hi = (i & k) == 0 ? l : i;
-                    if (before(sv[hi], si[hi], sv[lo], si[lo])) {
-                        const float tv = sv[lo];
-                        const int ti = si[lo];
-                        sv[lo] = sv[hi];
-                        si[lo] = si[hi];
-                        sv[hi] = tv;
-                        si[hi] = ti;
-                    }
-                }
-            }
-            __syncthreads();
+    block_sort_runs(sv, si, NA, 1);
+    return *flag != 0;
+}
+
+// Candidates of one staircase combination step: prefix entries i < n and
+// digit entries j < P with (i + 1)(j + 1) <= K. Any other pair is preceded,
+// in both digits, by at least K pairs of the staircase.
+__host__ __device__ inline int stair_count(int n, int P, int K) {
+    int c = 0;
+    for (int i = 0; i < n; ++i) {
+        const int m = K / (i + 1);
+        c += m < P ? m : P;
+    }
+    return c;
+}
+
+// Staircase search by one workgroup, for slot spaces of any size: the
+// per-digit log-softmax as above; every digit sorted; the sorted top list of
+// digits 0..d-1 combined with digit d over the staircase candidates and
+// sorted again, digit by digit. Scores are summed ((L_0 + L_1) + L_2) ...
+// like every other path, so the selection agrees with theirs.
+// Scratch: lg[U*P], ex[U*NPD] (then the sorted digit scores), di[U*NPD],
+// sv[NC], si[NC], pv[K], pi[K], off[K + 1]; NC = pow2 >= the largest
+// candidate count (at most stair_count(K, P, K)) and >= NPD.
+// Writes the sorted top entries to sv/si[0..K) and returns the inactive flag.
+template<typename T>
+__device__ bool block_search_stair(const T *ptr, int64_t stride, int U, int P, int K, int NPD, int NC, float *lg,
+                                   float *ex, int *di, float *sv, int *si, float *pv, int *pi, int *off, int *flag) {
+    const int tid = threadIdx.x;
+    const int nt = blockDim.x;
+    block_log_softmax(ptr, stride, U, P, NPD, lg, ex, flag);
+    // every digit sorted: (score, digit value) runs of NPD
+    for (int i = tid; i < U * NPD; i += nt) {
+        const int u = i / NPD, p = i % NPD;
+        ex[i] = p < P ? lg[u * P + p] : kNegInfF;
+        di[i] = p < P ? p : kNoIdx;
+    }
+    __syncthreads();
+    block_sort_runs(ex, di, NPD, U);
+    int n = K < P ? K : P;  // prefix list length
+    for (int c = tid; c < NC; c += nt) {
+        sv[c] = c < n ? ex[c] : kNegInfF;
+        si[c] = c < n ? di[c] : kNoIdx;
+    }
+    __syncthreads();
+    int pw = 1;
+    for (int d = 1; d < U; ++d) {
+        pw *= P;
+        for (int i = tid; i < n; i += nt) {
+            pv[i] = sv[i];
+            pi[i] = si[i];
         }
+        if (tid == 0) {
+            off[0] = 0;
+            for (int i = 0; i < n; ++i) {
+                const int m = K / (i + 1);
+                off[i + 1] = off[i] + (m < P ? m : P);
+            }
+        }
+        __syncthreads();
+        const int count = off[n];
+        const float *dv = ex + d * NPD;
+        const int *dd = di + d * NPD;
+        for (int c = tid; c < NC; c += nt) {
+            if (c < count) {
+                int lo = 0, hi = n - 1;  // the prefix entry i with off[i] <= c < off[i + 1]
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (off[mid] <= c)
+                        lo = mid;
+                    else
+                        hi = mid - 1;
+                }
+                const int j = c - off[lo];
+                sv[c] = pv[lo] + dv[j];
+                si[c] = pi[lo] + dd[j] * pw;
+            } else {
+                sv[c] = kNegInfF;
+                si[c] = kNoIdx;
+            }
+        }
+        __syncthreads();
+        block_sort_runs(sv, si, NC, 1);
+        n = count < K ? count : K;
     }
     return *flag != 0;
 }

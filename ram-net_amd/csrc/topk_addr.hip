@@ -197,8 +197,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FAST && KM 
     }
 }
 
-// Workgroup-per-address exact search (all A scores in LDS).
-template<typename Scalar>
+// Workgroup-per-address search: exact (STAIR false: all A scores in LDS,
+// NA = pow2 >= A) or the staircase search for slot spaces of any size (STAIR
+// true: NA is the candidate buffer NC).
+template<typename Scalar, bool STAIR>
 __global__ __launch_bounds__(256) void topk_addr_bruteforce_kernel(const AddrJob job, int NA, int NPD) {
     extern __shared__ float smem[];
     const AddrSource &src = job.src[blockIdx.y];
@@ -213,14 +215,23 @@ __global__ __launch_bounds__(256) void topk_addr_bruteforce_kernel(const AddrJob
     const int b = static_cast<int>(bh / H);
     const Scalar *base = static_cast<const Scalar *>(src.addr) + bh * static_cast<int64_t>(U * P) * T + tl;
 
+    const int K = src.top_k;
     float *lg = smem;
     float *ex = lg + U * P;
-    float *sv = ex + U * NPD;
+    int *di = reinterpret_cast<int *>(ex + U * NPD);  // staircase only
+    float *sv = STAIR ? reinterpret_cast<float *>(di + U * NPD) : ex + U * NPD;
     int *si = reinterpret_cast<int *>(sv + NA);
+    float *pv = reinterpret_cast<float *>(si + NA);    // staircase only: K each, then K + 1
+    int *pi = reinterpret_cast<int *>(pv + K);
+    int *off = pi + K;
     __shared__ int s_flag;
     __shared__ float s_lse;
-    const bool inactive = block_search_exact(base, static_cast<int64_t>(T), U, P, A, NA, NPD, lg, ex, sv, si, &s_flag);
-    const int K = src.top_k;
+    bool inactive;
+    if constexpr (STAIR)
+        inactive = block_search_stair(base, static_cast<int64_t>(T), U, P, K, NPD, NA, lg, ex, di, sv, si, pv, pi, off,
+                                      &s_flag);
+    else
+        inactive = block_search_exact(base, static_cast<int64_t>(T), U, P, A, NA, NPD, lg, ex, sv, si, &s_flag);
     const int tid = threadIdx.x;
     if (tid == 0)
         s_lse = (src.re_norm != 0.f && !inactive) ? topk_lse_serial(sv, K) : 0.f;
@@ -254,6 +265,18 @@ int pow2_at_least(int x) {
 }
 
 int grid_t(const AddrJob &job) { return job.wrec ? scan_t_pad(job.T) : job.T; }
+
+}  // namespace
+
+// Candidate buffer of the staircase search: a power of two holding every
+// candidate of one step (the prefix list is at most top_k long) and the
+// initial digit list.
+int stair_buffer(int P, int K, int NPD) {
+    const int c = stair_count(K, P, K);
+    return pow2_at_least(c > NPD ? c : NPD);
+}
+
+namespace {
 
 template<typename T, int NP, int KM>
 hipError_t launch_lane(const AddrJob &job, hipStream_t stream) {
@@ -298,17 +321,29 @@ hipError_t launch_typed(const AddrJob &job, hipStream_t stream, const char **why
     const int NA = pow2_at_least(job.A);
     const int NPD = pow2_at_least(job.P);
     const size_t lds = static_cast<size_t>(job.U) * job.P * 4 + static_cast<size_t>(job.U) * NPD * 4 + static_cast<size_t>(NA) * 8;
-    if (lds > 96 * 1024) {
-        *why = "address decoder: shape needs P <= 64 and top_k <= 16, or P**U small enough for the exact LDS search (A <= 8192)";
-        return hipErrorInvalidValue;
-    }
     const int64_t n = static_cast<int64_t>(job.B) * job.H * grid_t(job);
     if (n > 0x7fffffff) {
-        *why = "address decoder: B*H*T too large for the exact search grid";
+        *why = "address decoder: B*H*T too large for the workgroup search grid";
         return hipErrorInvalidValue;
     }
     const dim3 grid(static_cast<unsigned>(n), job.n_src);
-    hipLaunchKernelGGL(topk_addr_bruteforce_kernel<T>, grid, dim3(256), lds, stream, job, NA, NPD);
+    if (lds <= 96 * 1024) {
+        hipLaunchKernelGGL((topk_addr_bruteforce_kernel<T, false>), grid, dim3(256), lds, stream, job, NA, NPD);
+        return hipGetLastError();
+    }
+    // wider slot spaces: the staircase search, any A, top_k <= 128
+    if (kmax > 128 || NPD > 1024) {
+        *why = "address decoder: slot spaces beyond the exact LDS search (A > 8192) take top_k <= 128 and P <= 1024";
+        return hipErrorInvalidValue;
+    }
+    const int NC = stair_buffer(job.P, kmax, NPD);
+    const size_t lds_s = static_cast<size_t>(job.U) * job.P * 4 + static_cast<size_t>(job.U) * NPD * 8 +
+                         static_cast<size_t>(NC) * 8 + static_cast<size_t>(kmax) * 8 + static_cast<size_t>(kmax + 1) * 4;
+    if (lds_s > 96 * 1024) {
+        *why = "address decoder: staircase search scratch exceeds LDS (U * P too large)";
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL((topk_addr_bruteforce_kernel<T, true>), grid, dim3(256), lds_s, stream, job, NC, NPD);
     return hipGetLastError();
 }
 

@@ -69,6 +69,9 @@ DECODER_CASES = [
     (2, 2, 2, 3, 33, 4, 0.5, 1),
     (2, 2, 2, 4, 17, 16, 1.0, 2),      # K == A
     (1, 2, 5, 4, 32, 64, 0.25, 1),     # K > 16: exact LDS search
+    (1, 2, 5, 8, 16, 128, 0.5, 1),     # K > 16, A = 32768 > 8192: staircase workgroup search
+    (1, 1, 7, 4, 24, 32, 0.0, 1),      # K > 16, A = 16384: seven digits
+    (1, 2, 3, 32, 12, 64, 0.25, 0),    # K > 16, A = 32768 at P = 32
     (1, 1, 2, 64, 16, 8, 0.75, 0),     # P = 64
     (1, 2, 4, 7, 9, 12, 0.0, 2),       # odd radix
 ]
@@ -346,6 +349,44 @@ def test_decode_step_matches_oracle(U, P, K, mass_aware, dtype):
     assert oracle.rel_err(m_gpu.cpu(), rmass) <= FP32_TOL
     err = oracle.rel_err(y.cpu(), torch.as_tensor(ry)[:, :, 0])
     assert err <= _out_tol(dtype), f"decode y rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("mass_aware", [False, True])
+@pytest.mark.parametrize("U,P,K", [(5, 8, 32), (3, 32, 128)])
+def test_decode_step_wide_slot_space(U, P, K, mass_aware):
+    """The decode step beyond the exact LDS search (A = 32768 > 8192, top-K
+    above 16): the staircase workgroup search, then the row updates, against
+    the fp64 ranking and the fp64 event loop (reference:
+    ram_attn_topk_autoregressive.cu:309-323 instantiates K up to 128)."""
+    ops = _ops()
+    print(f"decode wide case U={U} P={P} K={K} mass_aware={mass_aware}", flush=True)
+    B, H, C = 2, 2, 16
+    A = P ** U
+    g = torch.Generator().manual_seed(U * 100 + P + K + 7)
+    w = torch.randn(B, H, U, P, generator=g)
+    r = torch.randn(B, H, U, P, generator=g)
+    x = torch.randn(B, H, C, generator=g)
+    gamma = torch.sigmoid(torch.randn(B, H, generator=g))
+    slot = 0.5 * torch.randn(B, H, A, C, generator=g)
+    mass = torch.rand(B, H, A, generator=g) + 0.1
+    pos = torch.randint(0, 1 << 20, (B,), generator=g)
+    s_gpu, m_gpu = slot.to(DEV), mass.to(DEV)
+    y = ops.topk_autoregressive_(w.to(DEV), r.to(DEV), x.to(DEV), gamma.to(DEV), s_gpu, m_gpu, None, 1,
+                                 pos.to(DEV), K, K, 0.25, 0.0, mass_aware, 1e-12)
+    torch.cuda.synchronize()
+    events = []
+    for lg, rn in ((w, 0.25), (r, 0.0)):
+        idx, val = ops.topk_addr_single_forward(lg.unsqueeze(-1).to(DEV), 1, A, pos.view(B, 1).to(DEV), K, rn,
+                                                False, True)
+        stats = oracle.check_topk_indices(idx.cpu(), lg.unsqueeze(-1), 1, pos.view(B, 1), K)
+        assert stats["exempt_slots"] == 0, "near-tie selections; pick another seed"
+        events += [idx.cpu(), val.cpu()]
+    wi, wv, ri, rv = events
+    ry, rslot, rmass = oracle.sparse_gsu_f64(wi, wv, ri, rv, x.double().unsqueeze(2), gamma.double().unsqueeze(-1),
+                                             slot, mass, None, mass_aware, 1e-12)
+    assert oracle.rel_err(s_gpu.cpu(), rslot) <= FP32_TOL
+    assert oracle.rel_err(m_gpu.cpu(), rmass) <= FP32_TOL
+    assert oracle.rel_err(y.cpu(), torch.as_tensor(ry)[:, :, 0]) <= FP32_TOL
 
 
 def call_api(case, sl=slice(None), state=None, **kw):
