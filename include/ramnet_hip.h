@@ -285,7 +285,9 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
  * channel-slice width, LDS bytes per workgroup, and whether it is the
  * precomputed-gain form (a mass pre-pass writes the gain records of the
  * workspace first). Honours RAMNET_SCAN_LAYOUT like the launch does.
- * Returns 1 if the shape is supported (A <= 8190, top-k <= 128), else 0.
+ * Returns 1 if the shape is supported (top-k <= 128; A <= 8190 in one
+ * resident slice, A <= 40958 in the precomputed-gain form split into slot
+ * ranges scanned one launch each), else 0.
  */
 int ramnet_segment_plan(int64_t B, int64_t H, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int dtype,
                         int *slice_channels, int *lds_bytes, int *precomputed_gains);

@@ -679,7 +679,7 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
         RAMNET_REQUIRE(ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(A),
                                             static_cast<int>(C), static_cast<int>(w_top_k), static_cast<int>(r_top_k),
                                             dtype, nullptr, nullptr, &pre),
-                       "segment forward: shape outside the LDS-resident scan (A <= 8190 and top_k <= 128)");
+                       "segment forward: shape outside the LDS-resident scan (A <= 40958 and top_k <= 128)");
         // the decoder records, then the gain records if the launch uses them
         need = ramnet::scan_record_bytes(B, H, T, w_top_k, r_top_k) +
                (pre ? ramnet::scan_gain_bytes(B, H, T, w_top_k, r_top_k) : 0);

@@ -66,7 +66,8 @@ int dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
 struct Plan {
     int vec, epp, np, nw, cs;
     size_t lds;
-    bool pre;  // mass pre-pass + precomputed-gain scan
+    bool pre;     // mass pre-pass + precomputed-gain scan
+    int nr = 1;   // slot ranges, scanned one launch each (precomputed-gain form)
 };
 
 // Cost model of one layout, in cycles per token of one round of resident
@@ -81,17 +82,18 @@ struct Plan {
 constexpr int64_t kChainCycles = 160;
 constexpr int64_t kMassWaveCycles = 230;
 constexpr int64_t kPrePassCycles = 60;
-constexpr int64_t kMassPassLds = 64 * 1024;  // chunk maps (A + 2) * 8 bytes: A <= 8190
+// The mass pre-pass's replay keeps a head's masses in LDS ((A + 2) * 4
+// bytes): the precomputed-gain form reaches A <= 40958.
+constexpr int64_t kMaxPrePassSlots = kLdsPerCu / 4 - 2;
 
-bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, Plan *out) {
-    const int kmax = std::max(Kw, Kr);
-    if (kmax > 2 * kWave)
-        return false;
+// The best layout for slot ranges of AL slots (the whole space when AL == A);
+// forms: mass wave allowed (mass_ok), precomputed gains allowed (pre_ok).
+static bool plan_layout(int B, int H, int AL, int C, int kmax, int elem, int n_cu, bool mass_ok, bool pre_ok,
+                        Plan *out, int64_t *best_cost) {
     const int epp0 = std::min(kWave, std::max(4, pow2_ceil(kmax)));
     bool found = false;
     int64_t best = 0;
-    const bool pre_ok = static_cast<int64_t>(A + 2) * 8 <= kMassPassLds;
-    for (int pre = 0; pre <= (pre_ok ? 1 : 0); ++pre) {
+    for (int pre = mass_ok ? 0 : 1; pre <= (pre_ok ? 1 : 0); ++pre) {
         for (int epp = 4; epp <= kWave; epp <<= 1) {
             const int np = (kmax + epp - 1) / epp;
             if (np > 2 || (np == 2 && epp * 2 < epp0))
@@ -101,7 +103,7 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, P
                     if (!scan_layout_compiled(vec, epp, np, nw, pre))
                         continue;
                     const int cs = nw * (kWave / epp) * vec;
-                    const size_t lds = scan_lds_bytes(A, vec, epp, np, nw, elem, pre);
+                    const size_t lds = scan_lds_bytes(AL, vec, epp, np, nw, elem, pre);
                     const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
                     if (gran > kLdsPerCu)
                         continue;
@@ -127,7 +129,30 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, P
             }
         }
     }
+    *best_cost = best;
     return found;
+}
+
+bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, Plan *out) {
+    const int kmax = std::max(Kw, Kr);
+    if (kmax > 2 * kWave || A < 1)
+        return false;
+    int64_t cost = 0;
+    const bool pre_ok = A <= kMaxPrePassSlots;
+    if (plan_layout(B, H, A, C, kmax, elem, n_cu, true, pre_ok, out, &cost))
+        return true;
+    if (!pre_ok)
+        return false;
+    // Too wide for one resident slice: split the slot space into the fewest
+    // ranges that fit (precomputed-gain form), one launch per range.
+    for (int nr = 2; nr <= 64; ++nr) {
+        const int al = (A + nr - 1) / nr;
+        if (plan_layout(B, H, al, C, kmax, elem, n_cu, false, true, out, &cost)) {
+            out->nr = nr;
+            return true;
+        }
+    }
+    return false;
 }
 
 // Scan records from decoder outputs: one thread per (b*H + h, event, t) with
@@ -514,6 +539,8 @@ int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chun
     nck = std::min(nck, std::max(1, job.T / 64));  // chunks of >= 64 tokens
     while (nck > 1 && static_cast<size_t>(bh) * nck * job.A * sizeof(float2) > scratch_bytes)
         nck /= 2;
+    if (static_cast<int64_t>(job.A + 2) * 8 > kLdsPerCu)
+        nck = 1;  // a chunk's maps do not fit in LDS (A > 20478): one serial replay
     const int len = ((job.T + nck - 1) / nck + 15) / 16 * 16;
     *chunk_len = std::max(16, len);
     return (job.T + *chunk_len - 1) / *chunk_len;
@@ -614,7 +641,7 @@ static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
     }
     const size_t lds = scan_lds_bytes(job.A, vec, epp, np, nw, dtype_bytes(job.dtype), pre != 0);
     if (epp * np < std::max(job.Kw, job.Kr) || static_cast<int64_t>(lds) > kLdsPerCu ||
-        (pre && static_cast<int64_t>(job.A + 2) * 8 > kMassPassLds)) {
+        (pre && job.A > kMaxPrePassSlots)) {
         *why = "RAMNET_SCAN_LAYOUT does not cover top_k or does not fit in LDS";
         return -1;
     }
@@ -629,8 +656,8 @@ static bool pick_plan(const SegmentJob &job, Plan *p, const char **why) {
     if (forced < 0)
         return false;
     if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, dtype_bytes(job.dtype), cu_count(), p)) {
-        *why = "segment forward: shape outside the LDS-resident scan (needs (A*CS + A)*4 bytes <= 160 KiB for some "
-               "slice width and top_k <= 128)";
+        *why = "segment forward: shape outside the LDS-resident scan (A <= 40958 slots, in slot ranges beyond 8190, "
+               "and top_k <= 128)";
         return false;
     }
     return true;
@@ -673,6 +700,8 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     geo.n_units = job.B * job.H * geo.n_slices;
     geo.t_pad = scan_t_pad(job.T);
     geo.n_chunks = (job.T + kChunk - 1) / kChunk;
+    geo.r0 = 0;
+    geo.n_local = job.A;
     if (job.dtype != kF32 && job.dtype != kF16 && job.dtype != kBF16) {
         *why = "segment forward: unsupported dtype";
         return hipErrorInvalidValue;
@@ -688,11 +717,21 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
         if (err != hipSuccess)
             return err;
     }
-    switch (job.dtype) {
-        case kF32: return launch_scan_f32(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream);
-        case kF16: return launch_scan_f16(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream);
-        default: return launch_scan_bf16(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream);
+    // slot ranges in order: the first stores y, the later ones add to it
+    const int al = (job.A + p.nr - 1) / p.nr;
+    for (int r = 0; r < p.nr; ++r) {
+        geo.r0 = r * al;
+        geo.n_local = std::min(al, job.A - geo.r0);
+        hipError_t err;
+        switch (job.dtype) {
+            case kF32: err = launch_scan_f32(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream); break;
+            case kF16: err = launch_scan_f16(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream); break;
+            default: err = launch_scan_bf16(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream); break;
+        }
+        if (err != hipSuccess)
+            return err;
     }
+    return hipSuccess;
 }
 
 }  // namespace ramnet

@@ -32,6 +32,12 @@ struct ScanGeom {
     int n_slices; // ceil(C / CS)
     int n_chunks; // ceil(T / kChunk)
     int t_pad;    // T rounded up to kScanPad (record row length)
+    // Slot range of this launch (precomputed-gain form): slots [r0, r0 +
+    // n_local) are resident, events on other slots act on the dummy rows,
+    // and a launch with r0 > 0 adds its read sums to y instead of storing
+    // them. One range (r0 = 0, n_local = A) unless A is too wide for LDS.
+    int r0;
+    int n_local;
 };
 
 // 1/d refined by one Newton step; gain = w / (m + eps) to ~1 ulp.
@@ -409,10 +415,16 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     const int c0 = (unit - bh * geo.n_slices) * CS;
     const int T = job.T, A = job.A, C = job.C, Kw = job.Kw, Kr = job.Kr, Tp = geo.t_pad;
     const float eps = job.eps;
+    // resident slot range: [r0, r0 + AL) (the whole space but in the
+    // precomputed-gain form's split launches)
+    const int r0 = PRE ? geo.r0 : 0;
+    const int AL = PRE ? geo.n_local : A;
+    const bool ranged = PRE && AL != A;
+    const bool accumulate = PRE && r0 > 0;
 
     float *st = lds + 2 * RS;              // slot 0 of the slice
-    float *ms = lds + (A + 2) * RS + 2;    // mass of slot 0
-    char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(A, RS, PRE);
+    float *ms = lds + (AL + 2) * RS + 2;   // mass of slot 0
+    char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(AL, RS, PRE);
     auto stage_e = [&](int buf) { return reinterpret_cast<StageRec *>(stage0 + buf * kStageBytes); };
     auto stage_x = [&](int buf) { return stage0 + buf * kStageBytes + CH * E * kStageRecBytes; };
     // per token: 1 if its writes may overlap the previous token's
@@ -422,8 +434,8 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
 
     // ---- state slice and masses -> LDS
     {
-        const float *src = job.init_slot + static_cast<int64_t>(bh) * A * C;
-        for (int i = tid; i < A * CS; i += kWave * NWT) {
+        const float *src = job.init_slot + (static_cast<int64_t>(bh) * A + r0) * C;
+        for (int i = tid; i < AL * CS; i += kWave * NWT) {
             const int a = i / CS, c = i - a * CS;
             const bool ok = c0 + c < C;
             const float v = src[static_cast<int64_t>(a) * C + (ok ? c0 + c : 0)];
@@ -748,20 +760,37 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
         // LDS addresses of every event's row (one 24-bit multiply-add each),
         // computed once per chunk, off the token chain. PRE records past T
         // were never written: those tokens act on the dummy rows.
+        auto addresses = [&](auto range_tag) {
+            constexpr bool RANGE = decltype(range_tag)::value;
 #pragma unroll
-        for (int j = 0; j < CH; ++j)
+            for (int j = 0; j < CH; ++j)
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                int wa = rec[p][j].x, ra = rec[p][j].z;
-                if constexpr (PRE && TAIL) {
-                    const bool live = t0 + j < T;
-                    wa = live ? wa : -2;
-                    ra = live ? ra : -1;
-                    rec[p][j].w = live ? rec[p][j].w : 0;
+                for (int p = 0; p < NP; ++p) {
+                    int wa = rec[p][j].x, ra = rec[p][j].z;
+                    if constexpr (PRE && TAIL) {
+                        const bool live = t0 + j < T;
+                        wa = live ? wa : -2;
+                        ra = live ? ra : -1;
+                        rec[p][j].w = live ? rec[p][j].w : 0;
+                    }
+                    if constexpr (RANGE) {
+                        // events on slots outside the resident range act on
+                        // the dummy rows (the no-op slots -2, -1 stay outside)
+                        const int lw = wa - r0, lr = ra - r0;
+                        const bool iw = static_cast<unsigned>(lw) < static_cast<unsigned>(AL);
+                        const bool ir = static_cast<unsigned>(lr) < static_cast<unsigned>(AL);
+                        wa = iw ? lw : -2;
+                        ra = ir ? lr : -1;
+                        rec[p][j].w = ir ? rec[p][j].w : 0;
+                    }
+                    rec[p][j].x = mad24(wa, amul[p], awb[p]);
+                    rec[p][j].z = mad24(ra, amul[p], arb[p]);
                 }
-                rec[p][j].x = mad24(wa, amul[p], awb[p]);
-                rec[p][j].z = mad24(ra, amul[p], arb[p]);
-            }
+        };
+        if (PRE && ranged)
+            addresses(std::true_type{});
+        else
+            addresses(std::false_type{});
         auto row = [&](int a) { return lds_at(static_cast<uint32_t>(a)); };
         auto load_rows = [&](int j, FVec<VEC> (&s)[NP]) {
 #pragma unroll
@@ -864,7 +893,15 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             const int j = EPP <= CH ? q * EPP + ev : ev % CH;
             const int t = t0 + j;
             Scalar *yp = gy + static_cast<int64_t>(t) * C + c0 + cl;
-            if constexpr (FAST) {
+            if (PRE && accumulate) {
+                // a later slot range: add to the earlier ranges' read sums
+                if (t < T) {
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v)
+                        if (FAST || c0 + cl + v < C)
+                            store_out(yp + v, load_f32(yp + v) + ykeep[q].v[v]);
+                }
+            } else if constexpr (FAST) {
                 if (!TAIL || t < T)
                     store_act_vec<Scalar, VEC>(yp, ykeep[q]);
             } else if (t < T) {
@@ -976,8 +1013,8 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
 
     // ---- LDS -> post state (whole workgroup); the masses from slice 0
     {
-        float *dst = job.slot_out + static_cast<int64_t>(bh) * A * C;
-        for (int i = tid; i < A * CS; i += kWave * NWT) {
+        float *dst = job.slot_out + (static_cast<int64_t>(bh) * A + r0) * C;
+        for (int i = tid; i < AL * CS; i += kWave * NWT) {
             const int a = i / CS, c = i - a * CS;
             if (c0 + c < C)
                 dst[static_cast<int64_t>(a) * C + c0 + c] = st[a * RS + c];
@@ -995,7 +1032,7 @@ hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t s
     const unsigned blocks = static_cast<unsigned>(((geo.n_units + 7) / 8) * 8);
     hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST, PRE>), dim3(blocks),
                        dim3(kWave * (NW + (PRE ? 0 : 1))),
-                       scan_lds_bytes(job.A, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar)), PRE), stream, job,
+                       scan_lds_bytes(geo.n_local, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar)), PRE), stream, job,
                        geo);
     return hipGetLastError();
 }

@@ -191,7 +191,9 @@ def test_cuda_path_capacity_asserts():
 def test_scan_plan_envelope():
     """The scan planner (``ramnet_segment_plan``, no device work) accepts every
     shape up to A = 8190 slots and top-K 128 with an LDS footprint within the
-    160 KiB of a CU, and refuses wider slot spaces and top-K beyond 128."""
+    160 KiB of a CU; wider slot spaces up to 40958 in the precomputed-gain
+    form (split into slot ranges); it refuses wider slot spaces still and
+    top-K beyond 128."""
     from ramnet_ops import _native as nat
     for A in (4, 16, 256, 1024, 2401, 4096, 6561, 8100, 8190):
         for C in (1, 7, 16, 100, 128, 512):
@@ -201,8 +203,13 @@ def test_scan_plan_envelope():
                     assert plan is not None, (A, C, K, dtype)
                     cs, lds, _ = plan
                     assert 1 <= cs and 0 < lds <= 160 * 1024, (A, C, K, cs, lds)
+    for A in (8192, 16384, 32768, 40958):
+        for C, K in ((128, 8), (7, 64), (256, 128)):  # B*H*A*C within int32
+            plan = nat.segment_plan(8, 16, A, C, K, K)
+            assert plan is not None and plan[2], (A, C, K, plan)
+            assert 0 < plan[1] <= 160 * 1024, (A, plan)
     assert nat.segment_plan(8, 16, 1024, 128, 8, 129) is None
-    assert nat.segment_plan(8, 16, 8192, 128, 8, 8) is None
+    assert nat.segment_plan(8, 16, 40960, 128, 8, 8) is None
     assert nat.segment_plan(8, 16, 1024, 128, 4, 12) is not None  # Kw != Kr
     assert nat.segment_plan(0, 16, 1024, 128, 8, 8) is None
 

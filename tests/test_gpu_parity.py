@@ -226,6 +226,41 @@ def test_segment_scan_matches_oracle(case, dtype):
     assert err <= _out_tol(dtype), f"y rel err {err:.3e}"
 
 
+WIDE_SEGMENT_CASES = [
+    # B, H, U, P, T, C, Kw, Kr, masked, mass_aware: slot spaces beyond one
+    # resident slice (A > 8190), scanned in slot ranges one launch each
+    (1, 2, 7, 4, 150, 24, 8, 8, True, False),     # A = 16384, partial channel slice, masks
+    (1, 2, 5, 8, 100, 16, 32, 16, False, True),   # A = 32768, Kw != Kr, mass_aware, staircase decoder
+    (2, 1, 3, 32, 70, 8, 8, 8, False, False),     # A = 32768 at P = 32
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", WIDE_SEGMENT_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_segment_scan_wide_slot_space(case, dtype):
+    """The segment forward beyond A = 8190 (the reference's segment path has
+    no slot bound beyond int32): the precomputed-gain scan split into slot
+    ranges, the later ranges adding their read sums to y, against the fp64
+    event loop."""
+    from ramnet_ops import _native as nat
+    B, H, U, P, T, C, Kw, Kr, masked, mass_aware = case
+    A = P ** U
+    plan = nat.segment_plan(B, H, A, C, Kw, Kr, dtype)
+    assert plan is not None and plan[2], (case, plan)
+    print(f"wide segment case {case} {dtype} plan {plan}", flush=True)
+    src, got, ref = _segment_case(B, H, U, P, T, C, Kw, Kr, dtype, masked, mass_aware, seed=T + C + A)
+    y, slot, mass = got
+    ry, rslot, rmass = ref
+    if src.mask is not None:
+        assert bool((y[:, :, ~src.mask[0]] == 0).all()), "masked tokens must read 0"
+        keep = src.mask[0]
+        y, ry = y[:, :, keep], torch.as_tensor(ry)[:, :, keep]
+    assert oracle.rel_err(slot, rslot) <= FP32_TOL, "slot state"
+    assert oracle.rel_err(mass, rmass) <= FP32_TOL, "mass state"
+    err = oracle.rel_err(y, ry)
+    assert err <= _out_tol(dtype), f"y rel err {err:.3e}"
+
+
 # Every compiled lane layout of the segment scan (vec, epp, np, nw), mirrored
 # from RAMNET_SCAN_LAYOUTS in segment_scan.hpp.
 SCAN_LAYOUTS = [
