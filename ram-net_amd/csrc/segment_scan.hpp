@@ -378,9 +378,11 @@ inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem, 
 // its chunks (records, x of its channels, overlap flags) two chunks ahead
 // into registers and stages them in a private LDS region: the waves run
 // without a barrier from the first chunk to the write-back.
-template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
-__global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_kernel(const SegmentJob job,
-                                                                                     const ScanGeom geo) {
+// RANGE (precomputed-gain form only): one slot range of a split slot space
+// (segment_scan_range_kernel); the whole space otherwise.
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE, bool RANGE>
+__device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const ScanGeom &geo) {
+    static_assert(PRE || !RANGE, "slot ranges need the precomputed-gain form");
     constexpr int NWT = NW + (PRE ? 0 : 1);  // waves of the workgroup
     constexpr int LPE = kWave / EPP;
     constexpr int CSW = LPE * VEC;
@@ -416,11 +418,10 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
     const int T = job.T, A = job.A, C = job.C, Kw = job.Kw, Kr = job.Kr, Tp = geo.t_pad;
     const float eps = job.eps;
     // resident slot range: [r0, r0 + AL) (the whole space but in the
-    // precomputed-gain form's split launches)
-    const int r0 = PRE ? geo.r0 : 0;
-    const int AL = PRE ? geo.n_local : A;
-    const bool ranged = PRE && AL != A;
-    const bool accumulate = PRE && r0 > 0;
+    // split launches of a wide one)
+    const int r0 = RANGE ? geo.r0 : 0;
+    const int AL = RANGE ? geo.n_local : A;
+    const bool accumulate = RANGE && r0 > 0;
 
     float *st = lds + 2 * RS;              // slot 0 of the slice
     float *ms = lds + (AL + 2) * RS + 2;   // mass of slot 0
@@ -760,8 +761,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
         // LDS addresses of every event's row (one 24-bit multiply-add each),
         // computed once per chunk, off the token chain. PRE records past T
         // were never written: those tokens act on the dummy rows.
-        auto addresses = [&](auto range_tag) {
-            constexpr bool RANGE = decltype(range_tag)::value;
+        {
 #pragma unroll
             for (int j = 0; j < CH; ++j)
 #pragma unroll
@@ -786,11 +786,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
                     rec[p][j].x = mad24(wa, amul[p], awb[p]);
                     rec[p][j].z = mad24(ra, amul[p], arb[p]);
                 }
-        };
-        if (PRE && ranged)
-            addresses(std::true_type{});
-        else
-            addresses(std::false_type{});
+        }
         auto row = [&](int a) { return lds_at(static_cast<uint32_t>(a)); };
         auto load_rows = [&](int j, FVec<VEC> (&s)[NP]) {
 #pragma unroll
@@ -893,7 +889,7 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
             const int j = EPP <= CH ? q * EPP + ev : ev % CH;
             const int t = t0 + j;
             Scalar *yp = gy + static_cast<int64_t>(t) * C + c0 + cl;
-            if (PRE && accumulate) {
+            if (RANGE && accumulate) {
                 // a later slot range: add to the earlier ranges' read sums
                 if (t < T) {
 #pragma unroll
@@ -1028,8 +1024,28 @@ __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_ker
 }
 
 template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
+__global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_kernel(const SegmentJob job,
+                                                                                     const ScanGeom geo) {
+    segment_scan_body<Scalar, VEC, EPP, NP, NW, MA, FAST, PRE, false>(job, geo);
+}
+
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
+__global__ __launch_bounds__(kWave * NW) void segment_scan_range_kernel(const SegmentJob job, const ScanGeom geo) {
+    segment_scan_body<Scalar, VEC, EPP, NP, NW, MA, FAST, true, true>(job, geo);
+}
+
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
 hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t stream) {
     const unsigned blocks = static_cast<unsigned>(((geo.n_units + 7) / 8) * 8);
+    if constexpr (PRE) {
+        if (geo.n_local != job.A) {
+            hipLaunchKernelGGL((segment_scan_range_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST>), dim3(blocks),
+                               dim3(kWave * NW),
+                               scan_lds_bytes(geo.n_local, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar)), true),
+                               stream, job, geo);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST, PRE>), dim3(blocks),
                        dim3(kWave * (NW + (PRE ? 0 : 1))),
                        scan_lds_bytes(geo.n_local, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar)), PRE), stream, job,
