@@ -284,7 +284,9 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
  * layout a segment-scan launch of this shape uses on the current device --
  * channel-slice width, LDS bytes per workgroup, and whether it is the
  * precomputed-gain form (a mass pre-pass writes the gain records of the
- * workspace first). Honours RAMNET_SCAN_LAYOUT like the launch does.
+ * workspace first). Honours RAMNET_SCAN_LAYOUT like the launch does. The
+ * answer is for a 4096-token call: a much shorter call may take the
+ * mass-wave form instead (the workspace size does not depend on the form).
  * Returns 1 if the shape is supported (top-k <= 128; A <= 8190 in one
  * resident slice, A <= 40958 in the precomputed-gain form split into slot
  * ranges scanned one launch each), else 0.

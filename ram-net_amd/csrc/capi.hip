@@ -612,14 +612,19 @@ int ramnet_topk_autoregressive_steps_(const void *w_addr, const void *r_addr, co
     return finish(err, why, "topk_autoregressive_steps_ launch");
 }
 
+// The query has no token count: it answers for a call of kPlanQueryTokens
+// tokens (the form can differ for much shorter calls, where the mass-wave
+// form's saving of the pre-pass launches decides).
+constexpr int kPlanQueryTokens = 4096;
+
 int ramnet_segment_plan(int64_t B, int64_t H, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int dtype,
                         int *slice_channels, int *lds_bytes, int *precomputed_gains) {
     if (B <= 0 || H <= 0 || A <= 0 || A >= kAddressLimit || C <= 0 || w_top_k <= 0 || r_top_k <= 0 ||
         !valid_dtype(dtype) || !fits_int({B * H * A * C, B * H * (A + 2)}))
         return 0;
-    return ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(A), static_cast<int>(C),
-                                static_cast<int>(w_top_k), static_cast<int>(r_top_k), dtype, slice_channels,
-                                lds_bytes, precomputed_gains);
+    return ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), kPlanQueryTokens, static_cast<int>(A),
+                                static_cast<int>(C), static_cast<int>(w_top_k), static_cast<int>(r_top_k), dtype,
+                                slice_channels, lds_bytes, precomputed_gains);
 }
 
 // ---- prefill forward without a workspace argument
@@ -676,9 +681,9 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
                                      B * H * (T + ramnet::kScanPad) * (w_top_k + r_top_k)});
     if (plausible) {
         int pre = 0;
-        RAMNET_REQUIRE(ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(A),
-                                            static_cast<int>(C), static_cast<int>(w_top_k), static_cast<int>(r_top_k),
-                                            dtype, nullptr, nullptr, &pre),
+        RAMNET_REQUIRE(ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T),
+                                            static_cast<int>(A), static_cast<int>(C), static_cast<int>(w_top_k),
+                                            static_cast<int>(r_top_k), dtype, nullptr, nullptr, &pre),
                        "segment forward: shape outside the LDS-resident scan (A <= 40958 and top_k <= 128)");
         // the decoder records, then the gain records if the launch uses them
         need = ramnet::scan_record_bytes(B, H, T, w_top_k, r_top_k) +

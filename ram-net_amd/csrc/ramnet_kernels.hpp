@@ -203,7 +203,7 @@ hipError_t launch_autoregressive_steps(const DecodeJob &job, int S, hipStream_t 
 
 // Channel-slice width, dynamic LDS bytes and form (1: precomputed gains)
 // that a segment-scan launch of this shape uses on the current device.
-int segment_plan(int B, int H, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre);
+int segment_plan(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre);
 
 // Mass pre-pass in record-keeping mode: the records stay as they are and
 // `aux` receives the per-event quantities. `maps` holds the chunk maps

@@ -74,22 +74,25 @@ struct Plan {
 // workgroups: a wave's token loop is bound by its dependency chain (LDS
 // read -> update -> LDS write, ~kChainCycles) or by the issue of its VALU
 // work (~10 + 6 * VEC * NP instructions, 4 cycles each, shared by the waves
-// on one SIMD), whichever is longer. Total = rounds * per-token cycles. In
-// the mass-wave form the mass wave's own chain (mass update, gain, staging:
-// ~kMassWaveCycles per token) paces the state waves; the precomputed-gain
-// form instead pays for its pre-pass, chunked over time across the GPU
-// (~kPrePassCycles per token). Measured per-token figures on MI355X.
+// on one SIMD), whichever is longer. Total = T * rounds * per-token cycles.
+// In the mass-wave form the mass wave's own chain (mass update, gain,
+// staging: ~kMassWaveCycles per token) paces the state waves; the
+// precomputed-gain form instead pays for its pre-pass, chunked over time
+// across the GPU (~kPrePassCycles per token), plus its three extra launches
+// (~kPrePassLaunchCycles, which decide short calls). Measured on MI355X.
 constexpr int64_t kChainCycles = 160;
 constexpr int64_t kMassWaveCycles = 230;
 constexpr int64_t kPrePassCycles = 60;
+constexpr int64_t kPrePassLaunchCycles = 45000;
 // The mass pre-pass's replay keeps a head's masses in LDS ((A + 2) * 4
 // bytes): the precomputed-gain form reaches A <= 40958.
 constexpr int64_t kMaxPrePassSlots = kLdsPerCu / 4 - 2;
 
 // The best layout for slot ranges of AL slots (the whole space when AL == A);
 // forms: mass wave allowed (mass_ok), precomputed gains allowed (pre_ok).
-static bool plan_layout(int B, int H, int AL, int C, int kmax, int elem, int n_cu, bool mass_ok, bool pre_ok,
+static bool plan_layout(int B, int H, int AL, int C, int kmax, int elem, int n_cu, int T, bool mass_ok, bool pre_ok,
                         Plan *out, int64_t *best_cost) {
+    const int64_t tt = std::max(1, T);
     const int epp0 = std::min(kWave, std::max(4, pow2_ceil(kmax)));
     bool found = false;
     int64_t best = 0;
@@ -113,13 +116,17 @@ static bool plan_layout(int B, int H, int AL, int C, int kmax, int elem, int n_c
                     const int64_t resident = std::min<int64_t>(per_cu, (units + n_cu - 1) / n_cu);
                     const int64_t waves_per_simd = (resident * nw + 3) / 4;
                     const int64_t issue = 4 * (10 + 6 * vec * np) * waves_per_simd;
-                    int64_t cost = rounds * std::max(pre ? kChainCycles : kMassWaveCycles, issue);
+                    int64_t cost = tt * rounds * std::max(pre ? kChainCycles : kMassWaveCycles, issue);
                     if (C % cs != 0)
                         cost = cost * 3 / 2;  // partial slices take the guarded path
                     if (pre)
-                        cost += kPrePassCycles;
-                    const bool better = !found || cost < best ||
-                                        (cost == best && (nw > out->nw || (nw == out->nw && cs > out->cs)));
+                        cost += tt * kPrePassCycles + kPrePassLaunchCycles;
+                    // ties: fewer channels per lane (less work per wave), then
+                    // more waves, then wider slices
+                    const bool better =
+                        !found || cost < best ||
+                        (cost == best && (vec < out->vec || (vec == out->vec && (nw > out->nw ||
+                                                                                 (nw == out->nw && cs > out->cs)))));
                     if (better) {
                         *out = {vec, epp, np, nw, cs, lds, pre != 0};
                         best = cost;
@@ -133,13 +140,13 @@ static bool plan_layout(int B, int H, int AL, int C, int kmax, int elem, int n_c
     return found;
 }
 
-bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, Plan *out) {
+bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, int T, Plan *out) {
     const int kmax = std::max(Kw, Kr);
     if (kmax > 2 * kWave || A < 1)
         return false;
     int64_t cost = 0;
     const bool pre_ok = A <= kMaxPrePassSlots;
-    if (plan_layout(B, H, A, C, kmax, elem, n_cu, true, pre_ok, out, &cost))
+    if (plan_layout(B, H, A, C, kmax, elem, n_cu, T, true, pre_ok, out, &cost))
         return true;
     if (!pre_ok)
         return false;
@@ -147,7 +154,7 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, P
     // ranges that fit (precomputed-gain form), one launch per range.
     for (int nr = 2; nr <= 64; ++nr) {
         const int al = (A + nr - 1) / nr;
-        if (plan_layout(B, H, al, C, kmax, elem, n_cu, false, true, out, &cost)) {
+        if (plan_layout(B, H, al, C, kmax, elem, n_cu, T, false, true, out, &cost)) {
             out->nr = nr;
             return true;
         }
@@ -655,7 +662,7 @@ static bool pick_plan(const SegmentJob &job, Plan *p, const char **why) {
     const int forced = layout_override(job, p, why);
     if (forced < 0)
         return false;
-    if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, dtype_bytes(job.dtype), cu_count(), p)) {
+    if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, dtype_bytes(job.dtype), cu_count(), job.T, p)) {
         *why = "segment forward: shape outside the LDS-resident scan (A <= 40958 slots, in slot ranges beyond 8190, "
                "and top_k <= 128)";
         return false;
@@ -663,10 +670,11 @@ static bool pick_plan(const SegmentJob &job, Plan *p, const char **why) {
     return true;
 }
 
-int segment_plan(int B, int H, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre) {
+int segment_plan(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre) {
     SegmentJob job{};
     job.B = B;
     job.H = H;
+    job.T = T;
     job.A = A;
     job.C = C;
     job.Kw = Kw;
