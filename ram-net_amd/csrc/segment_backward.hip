@@ -146,6 +146,14 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     constexpr int NXE = CH * CSW;                  // x (and Dy) elements per chunk
     constexpr int XPL = (NXE + kWave - 1) / kWave;
     constexpr int GX = EPP < CH ? EPP : CH;        // tokens per batched grad_x store
+    // Reductions by reduce-scatter over the tokens of a group (one exchange
+    // per token instead of an all-reduce and a select per token): over the
+    // LPE channel lanes of an event (lane bits 0 .. log2(LPE) - 1) for the
+    // read dots and Dg, over the EPP event lanes (the bits above) for Dx
+    // when a chunk holds EPP tokens.
+    constexpr int LOGL = __builtin_ctz(LPE);
+    constexpr bool XSC = EPP <= CH;
+    constexpr int NXS = XSC ? EPP : 1;
     // The chunk's event records and activations, loaded once per chunk
     // (one element per lane) and read back per token as LDS broadcasts.
     __shared__ int4 stw[NREC];   // write records {slot, g, matched read weight, mass}
@@ -169,6 +177,14 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     const int lane = static_cast<int>(threadIdx.x);
     const int e = lane / LPE, q = lane % LPE;
     const int c0 = sub * CSW + q * VEC;  // first channel of this lane
+    uint32_t hi[6];
+    hi[0] = bit_mask<1>(lane);
+    hi[1] = bit_mask<2>(lane);
+    hi[2] = bit_mask<4>(lane);
+    hi[3] = bit_mask<8>(lane);
+    hi[4] = bit_mask<16>(lane);
+    hi[5] = bit_mask<32>(lane);
+    auto opq = [](float v) { return __uint_as_float(opaque(__float_as_uint(v))); };
     float *rows = st + 2 * CSW;
     const Scalar *xs = static_cast<const Scalar *>(fj.x);
     const Scalar *dys = static_cast<const Scalar *>(job.grad_y);
@@ -270,9 +286,15 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
 #pragma unroll
             for (int p = 0; p < NP; ++p)
                 sw[p] = lds_vec(rows + wsl[0][p] * CSW + q * VEC);
-            float keep[NP];  // d_j of token (group start + q), stored once per LPE tokens
-            // d_j of token j: the dot of its read rows with Dy_t, reduced over
-            // the event's lanes and kept by lane q = j % LPE
+            // d_j of token j: the dot of its read rows with Dy_t; the lane's
+            // partials of a group of LPE tokens are reduced over the event's
+            // lanes at once, leaving token (group start + q) in lane q
+            float rdp[NP][LPE];
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+                for (int m = 0; m < LPE; ++m)
+                    rdp[p][m] = 0.f;
             auto read_dot = [&](int j, const FVec<VEC> (&sr)[NP]) {
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
@@ -280,14 +302,15 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
 #pragma unroll
                     for (int v = 0; v < VEC; ++v)
                         part = fmaf(sr[p].v[v], dyv[j][v], part);
-                    part = event_sum<LPE>(part);
-                    keep[p] = q == j % LPE ? part : keep[p];
+                    rdp[p][j % LPE] = opq(part);
                 }
                 if (j % LPE == LPE - 1) {
                     const int tg = ci * CH + j - (LPE - 1) + q;  // this lane's token of the group
 #pragma unroll
-                    for (int p = 0; p < NP; ++p)
-                        drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
+                    for (int p = 0; p < NP; ++p) {
+                        event_scatter<LOGL - 1, 0, LPE>(rdp[p], hi);
+                        drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = rdp[p][0];
+                    }
                 }
             };
             FVec<VEC> sr[NP];  // read rows of the previous token, reduced one token late
@@ -336,8 +359,10 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
             if (T - ci * CH < CH && (T - ci * CH) % LPE != 0) {  // ragged last group
                 const int n = T - ci * CH, tg = ci * CH + n / LPE * LPE + q;
 #pragma unroll
-                for (int p = 0; p < NP; ++p)
-                    drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
+                for (int p = 0; p < NP; ++p) {
+                    event_scatter<LOGL - 1, 0, LPE>(rdp[p], hi);
+                    drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = rdp[p][0];
+                }
             }
             cur = nxt;
         }
@@ -392,8 +417,19 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                 for (int v = 0; v < VEC; ++v)
                     dyv[j][v] = sdy[j * CSW + q * VEC + v];
             }
-            float keep[NP];       // Dg of token (group start - q), stored once per LPE tokens
+            float dgp_[NP][LPE];  // Dg partials of a group of LPE tokens (token group start - m)
+            float dxp[VEC][NXS];  // Dx partials of a group of EPP tokens (reduce-scatter form)
             float keep_x[VEC];    // Dx of token (group start - e), stored once per GX tokens
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+                for (int m = 0; m < LPE; ++m)
+                    dgp_[p][m] = 0.f;
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+#pragma unroll
+                for (int m = 0; m < NXS; ++m)
+                    dxp[v][m] = 0.f;
             // rows of the current token, loaded before the previous token's
             // reductions (after its stores)
             FVec<VEC> dr[NP], dw[NP];
@@ -447,22 +483,36 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                             dw[p] = lds_vec(rows + wsl[j + 1][p] * CSW + q * VEC);
                     }
 #pragma unroll
-                    for (int p = 0; p < NP; ++p) {
-                        const float sp = event_sum<LPE>(part[p]);
-                        keep[p] = q == j % LPE ? sp : keep[p];
-                    }
+                    for (int p = 0; p < NP; ++p)
+                        dgp_[p][j % LPE] = opq(part[p]);
                     if (j % LPE == LPE - 1 || (TL && t == 0)) {
                         const int tg = t + (j % LPE) - q;  // this lane's token of the group
+#pragma unroll
+                        for (int p = 0; p < NP; ++p)
+                            event_scatter<LOGL - 1, 0, LPE>(dgp_[p], hi);
                         if (tg >= t) {
 #pragma unroll
                             for (int p = 0; p < NP; ++p)
-                                dgp[static_cast<int64_t>(tg) * KP + p * EPP + e] = keep[p];
+                                dgp[static_cast<int64_t>(tg) * KP + p * EPP + e] = dgp_[p][0];
                         }
                     }
+                    if constexpr (XSC) {
 #pragma unroll
-                    for (int v = 0; v < VEC; ++v) {
-                        const float sx = strided_sum<LPE>(dx[v]);
-                        keep_x[v] = e == j % GX ? sx : keep_x[v];
+                        for (int v = 0; v < VEC; ++v)
+                            dxp[v][j % GX] = opq(dx[v]);
+                        if (j % GX == GX - 1 || (TL && t == 0)) {
+#pragma unroll
+                            for (int v = 0; v < VEC; ++v) {
+                                event_scatter<__builtin_ctz(NXS) - 1, LOGL, NXS>(dxp[v], hi);
+                                keep_x[v] = dxp[v][0];
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < VEC; ++v) {
+                            const float sx = strided_sum<LPE>(dx[v]);
+                            keep_x[v] = e == j % GX ? sx : keep_x[v];
+                        }
                     }
                     if (j % GX == GX - 1 || (TL && t == 0)) {
                         const int tg = t + (j % GX) - e;  // this lane's token of the group
