@@ -229,8 +229,13 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
         for (int i = 0; i < RPL; ++i) {
             const int idx = lane + kWave * i;
             if (NREC % kWave == 0 || idx < NREC) {
+                // padding slots get the no-op records; selected bitwise, as a
+                // branch around the copy would wait for every outstanding access
                 const int k = idx % KP;
-                stw[idx] = k < Kw ? pf.w[i] : make_int4(-2, 0, 0, 0);
+                const uint32_t mw = k < Kw ? ~0u : 0u;
+                const int4 w = pf.w[i];
+                stw[idx] = make_int4(static_cast<int>(bfi(mw, w.x, static_cast<uint32_t>(-2))), static_cast<int>(bfi(mw, w.y, 0)),
+                                     static_cast<int>(bfi(mw, w.z, 0)), static_cast<int>(bfi(mw, w.w, 0)));
                 str[idx] = k < Kr ? pf.r[i] : make_int2(-1, 0);
             }
         }
@@ -248,6 +253,19 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     auto lds_vec = [&](const float *p) { return lds_load<VEC>(p); };
     const int nck = (T + CH - 1) / CH;
 
+    // A chunk's results stay in registers and are stored at the start of the
+    // next chunk, before its prefetch, so a wait for prefetched data never
+    // waits on stores just issued; and the chunk loop runs two chunks per
+    // iteration with swapped buffers, as a copy of a register with a load
+    // pending waits for every outstanding access.
+    constexpr int NG = CH / LPE;   // groups of LPE tokens per chunk (read dots, Dg)
+    constexpr int NGX = CH / GX;   // groups of GX tokens per chunk (Dx)
+    static_assert(CH % LPE == 0 && CH % GX == 0, "a chunk holds whole groups");
+    // Wide lanes at two passes (more than 32 saved floats per chunk) would
+    // spill with the held-back saved rows and the paired chunk buffers: those
+    // store the saved rows as they go and loop over single chunks.
+    constexpr bool HOLD = CH * NP * VEC <= 32;
+
     // ---- forward over t: s in LDS; save x - s before each write, d_j per read
     for (int i = lane; i < (A + 2) * CSW; i += kWave) {
         const int a = i / CSW - 2, c = sub * CSW + i % CSW;
@@ -256,10 +274,43 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     __syncthreads();
     {
         using Tag = std::true_type;
-        Pre cur, nxt;
-        prefetch(0, cur, Tag{});
-        for (int ci = 0; ci < nck; ++ci) {
+        struct Out {
+            FVec<VEC> d[HOLD ? CH : 1][NP];  // x - s of each write row, per token
+            float dr[NG][NP];     // d_j of token (group start + q)
+        };
+        Out out;
+        auto flush = [&](int ci) {
+            const int n = min(CH, T - ci * CH);
+            float *dc = dlt + static_cast<int64_t>(ci) * CH * KP * CSW;
+            float *rc = drp + (static_cast<int64_t>(ci) * CH + q) * KP + e;  // rows padded to whole chunks
+            auto put = [&](auto full_tag) {
+                constexpr bool FULL = decltype(full_tag)::value;
+                if constexpr (HOLD) {
+#pragma unroll
+                    for (int j = 0; j < CH; ++j)
+                        if (FULL || j < n) {
+#pragma unroll
+                            for (int p = 0; p < NP; ++p)
+                                lds_store<VEC>(dc + (j * KP + p * EPP) * CSW, out.d[j][p]);
+                        }
+                }
+#pragma unroll
+                for (int g = 0; g < NG; ++g)
+                    if (FULL || g * LPE < n) {
+#pragma unroll
+                        for (int p = 0; p < NP; ++p)
+                            rc[g * LPE * KP + p * EPP] = out.dr[g][p];
+                    }
+            };
+            if (n == CH)
+                put(std::true_type{});
+            else
+                put(std::false_type{});
+        };
+        auto chunk = [&](int ci, Pre &cur, Pre &nxt) {
             stage(cur, Tag{});
+            if (ci > 0)
+                flush(ci - 1);
             prefetch(min(ci + 1, nck - 1), nxt, Tag{});
             // the chunk's records and activations for this lane, read back in
             // one batch, so that each token costs one LDS round trip
@@ -305,11 +356,10 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     rdp[p][j % LPE] = opq(part);
                 }
                 if (j % LPE == LPE - 1) {
-                    const int tg = ci * CH + j - (LPE - 1) + q;  // this lane's token of the group
 #pragma unroll
                     for (int p = 0; p < NP; ++p) {
                         event_scatter<LOGL - 1, 0, LPE>(rdp[p], hi);
-                        drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = rdp[p][0];
+                        out.dr[j / LPE][p] = rdp[p][0];
                     }
                 }
             };
@@ -332,7 +382,10 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                             s.v[v] = fmaf(wg[j][p], d.v[v], s.v[v]);
                         }
                         lds_store<VEC>(rows + wsl[j][p] * CSW + q * VEC, s);
-                        lds_store<VEC>(dlt + (static_cast<int64_t>(t) * KP + p * EPP) * CSW, d);
+                        if constexpr (HOLD)
+                            out.d[j][p] = d;
+                        else
+                            lds_store<VEC>(dlt + (static_cast<int64_t>(t) * KP + p * EPP) * CSW, d);
                     }
                     FVec<VEC> srn[NP];
 #pragma unroll
@@ -356,16 +409,32 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                 tokens(std::false_type{});
             else
                 tokens(std::true_type{});
-            if (T - ci * CH < CH && (T - ci * CH) % LPE != 0) {  // ragged last group
-                const int n = T - ci * CH, tg = ci * CH + n / LPE * LPE + q;
+            if constexpr (LPE > 1) {
+                if (T - ci * CH < CH && (T - ci * CH) % LPE != 0) {  // ragged last group
+                    const int gl = (T - ci * CH) / LPE;
 #pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    event_scatter<LOGL - 1, 0, LPE>(rdp[p], hi);
-                    drp[static_cast<int64_t>(tg) * KP + p * EPP + e] = rdp[p][0];
+                    for (int p = 0; p < NP; ++p) {
+                        event_scatter<LOGL - 1, 0, LPE>(rdp[p], hi);
+#pragma unroll
+                        for (int g = 0; g < NG; ++g)
+                            if (g == gl)
+                                out.dr[g][p] = rdp[p][0];
+                    }
                 }
             }
-            cur = nxt;
+        };
+        Pre pa, pb;
+        prefetch(0, pa, Tag{});
+        for (int ci = 0; ci < nck; ci += HOLD ? 2 : 1) {
+            chunk(ci, pa, pb);
+            if constexpr (HOLD) {
+                if (ci + 1 < nck)
+                    chunk(ci + 1, pb, pa);
+            } else {
+                pa = pb;
+            }
         }
+        flush(nck - 1);
     }
     __syncthreads();
 
@@ -390,13 +459,46 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     raw_load_vec<VEC>(dlt + (static_cast<int64_t>(t) * KP + p * EPP) * CSW, sv.v[j] + p * VEC);
             }
         };
-        Pre cur, nxt;
-        Saved scur, snxt;
-        prefetch(0, cur, Tag{});
-        load_saved(0, scur);
+        struct Out {
+            float dg[NG][NP];    // Dg of token (group start - q)
+            float gx[NGX][VEC];  // Dx of token (group start - e)
+        };
+        Out out;
         float *gx = job.grad_x + static_cast<int64_t>(bh) * T * C;
-        for (int ci = 0; ci < nck; ++ci) {
+        auto flush = [&](int ci) {
+            const int n = min(CH, T - ci * CH);
+            const int t0 = T - 1 - ci * CH;  // the chunk's first token; group g's in this lane: t0 - g * LPE - q (Dg), t0 - g * GX - e (Dx)
+            auto put = [&](auto full_tag) {
+                constexpr bool FULL = decltype(full_tag)::value;
+#pragma unroll
+                for (int g = 0; g < NG; ++g)
+                    if (FULL || g * LPE + q < n) {
+                        const int64_t tg = t0 - g * LPE - q;
+#pragma unroll
+                        for (int p = 0; p < NP; ++p)
+                            dgp[tg * KP + p * EPP + e] = out.dg[g][p];
+                    }
+                if (e < GX) {
+#pragma unroll
+                    for (int g = 0; g < NGX; ++g)
+                        if (FULL || g * GX + e < n) {
+                            const int64_t tg = t0 - g * GX - e;
+#pragma unroll
+                            for (int v = 0; v < VEC; ++v)
+                                if (c0 + v < C)
+                                    gx[tg * C + c0 + v] = out.gx[g][v];
+                        }
+                }
+            };
+            if (n == CH)
+                put(std::true_type{});
+            else
+                put(std::false_type{});
+        };
+        auto chunk = [&](int ci, Pre &cur, Pre &nxt, Saved &scur, Saved &snxt) {
             stage(cur, Tag{});
+            if (ci > 0)
+                flush(ci - 1);
             prefetch(min(ci + 1, nck - 1), nxt, Tag{});
             load_saved(min(ci + 1, nck - 1), snxt);
             int wsl[CH][NP], rsl[CH][NP];
@@ -419,17 +521,19 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
             }
             float dgp_[NP][LPE];  // Dg partials of a group of LPE tokens (token group start - m)
             float dxp[VEC][NXS];  // Dx partials of a group of EPP tokens (reduce-scatter form)
-            float keep_x[VEC];    // Dx of token (group start - e), stored once per GX tokens
+            float keep_x[VEC];    // Dx of token (group start - e) (all-reduce form)
 #pragma unroll
             for (int p = 0; p < NP; ++p)
 #pragma unroll
                 for (int m = 0; m < LPE; ++m)
                     dgp_[p][m] = 0.f;
 #pragma unroll
-            for (int v = 0; v < VEC; ++v)
+            for (int v = 0; v < VEC; ++v) {
+                keep_x[v] = 0.f;
 #pragma unroll
                 for (int m = 0; m < NXS; ++m)
                     dxp[v][m] = 0.f;
+            }
             // rows of the current token, loaded before the previous token's
             // reductions (after its stores)
             FVec<VEC> dr[NP], dw[NP];
@@ -486,14 +590,10 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     for (int p = 0; p < NP; ++p)
                         dgp_[p][j % LPE] = opq(part[p]);
                     if (j % LPE == LPE - 1 || (TL && t == 0)) {
-                        const int tg = t + (j % LPE) - q;  // this lane's token of the group
 #pragma unroll
-                        for (int p = 0; p < NP; ++p)
+                        for (int p = 0; p < NP; ++p) {
                             event_scatter<LOGL - 1, 0, LPE>(dgp_[p], hi);
-                        if (tg >= t) {
-#pragma unroll
-                            for (int p = 0; p < NP; ++p)
-                                dgp[static_cast<int64_t>(tg) * KP + p * EPP + e] = dgp_[p][0];
+                            out.dg[j / LPE][p] = dgp_[p][0];
                         }
                     }
                     if constexpr (XSC) {
@@ -504,7 +604,7 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
 #pragma unroll
                             for (int v = 0; v < VEC; ++v) {
                                 event_scatter<__builtin_ctz(NXS) - 1, LOGL, NXS>(dxp[v], hi);
-                                keep_x[v] = dxp[v][0];
+                                out.gx[j / GX][v] = dxp[v][0];
                             }
                         }
                     } else {
@@ -513,14 +613,10 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                             const float sx = strided_sum<LPE>(dx[v]);
                             keep_x[v] = e == j % GX ? sx : keep_x[v];
                         }
-                    }
-                    if (j % GX == GX - 1 || (TL && t == 0)) {
-                        const int tg = t + (j % GX) - e;  // this lane's token of the group
-                        if (tg >= t && e < GX) {
+                        if (j % GX == GX - 1 || (TL && t == 0)) {
 #pragma unroll
                             for (int v = 0; v < VEC; ++v)
-                                if (c0 + v < C)
-                                    gx[static_cast<int64_t>(tg) * C + c0 + v] = keep_x[v];
+                                out.gx[j / GX][v] = keep_x[v];
                         }
                     }
                 }
@@ -529,9 +625,22 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                 tokens(std::false_type{});
             else
                 tokens(std::true_type{});
-            cur = nxt;
-            scur = snxt;
+        };
+        Pre pa, pb;
+        Saved sa, sb;
+        prefetch(0, pa, Tag{});
+        load_saved(0, sa);
+        for (int ci = 0; ci < nck; ci += HOLD ? 2 : 1) {
+            chunk(ci, pa, pb, sa, sb);
+            if constexpr (HOLD) {
+                if (ci + 1 < nck)
+                    chunk(ci + 1, pb, pa, sb, sa);
+            } else {
+                pa = pb;
+                sa = sb;
+            }
         }
+        flush(nck - 1);
     }
     __syncthreads();
     for (int i = lane; i < A * CSW; i += kWave) {
