@@ -32,6 +32,7 @@ CASES = [
     (1, 2, 2, 16, 40, 64, 8, 8, F16, False, True),
     (1, 2, 2, 32, 24, 300, 16, 16, F32, False, False),  # C > 16 slices of 4: wider lanes
     (1, 2, 2, 90, 20, 12, 8, 8, F32, True, True),     # A = 8100: 8-channel slices do not fit, 16 event lanes
+    (1, 2, 2, 4, 45, 16, 8, 8, F32, False, False),    # A = 16: neighbouring tokens share slots (row reloads)
 ]
 
 
