@@ -256,18 +256,33 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
 // accesses carry the slot dependency from token to token. Tokens go in pairs
 // like the scan's mass wave: the second token's masses are read before the
 // first token's writes and again only when the two write sets may overlap.
+//
+// Lanes past max(Kw, Kr) stand in for the last event lane of their half
+// (same records, same results, same stores), so that every memory access of
+// a token is made by the whole wave: no branch around a load or a store,
+// which would make the compiler's memory-counter waits drain everything
+// outstanding, the just-issued prefetch and the stores included.
 template<int MP>
 struct MassLanes {
     static constexpr int CH = MP <= 1 ? 16 : MP == 2 ? 8 : 4;  // tokens per fetch
-    int ev[MP];   // this lane's event (clamped for loads)
-    bool on[MP];  // whether it is a real event
+    int ev[MP];    // this lane's event (clamped for loads)
+    int evw[MP];   // its write event and read event, each clamped (every lane loads both)
+    int evr[MP];
+    bool on[MP];   // whether it is a real event
+    bool act[MP];  // whether it acts: a real event, or a stand-in for the half's last event lane
+    int es[MP];    // the event it stores (lanes past max(Kw, Kr) repeat the last one's store)
     __device__ MassLanes(int lane, int Kw, int Kr) {
         const int hl = lane & 31;
+        const int ek = max(Kw, Kr);
 #pragma unroll
         for (int p = 0; p < MP; ++p) {
             const int e = p * 32 + hl;
+            es[p] = min(e, ek - 1);
             on[p] = lane < 32 ? e < Kw : e < Kr;
-            ev[p] = lane < 32 ? min(e, Kw - 1) : min(e, Kr - 1);
+            act[p] = lane < 32 ? es[p] < Kw : es[p] < Kr;
+            evw[p] = min(e, Kw - 1);
+            evr[p] = min(e, Kr - 1);
+            ev[p] = lane < 32 ? evw[p] : evr[p];
         }
     }
 };
@@ -276,18 +291,19 @@ struct MassRecs {
     int4 w[MP][CH];
     int2 r[MP][CH];
 };
-template<int MP, int CH>
+// The chunk's records from token t0 on: write records for every lane, and
+// read records too unless WONLY.
+template<bool WONLY, int MP, int CH>
 __device__ __forceinline__ void mass_fetch(const MassLanes<MP> &ln, const WriteRec *gw, const ReadRec *gr, int t_pad,
-                                           int t0, bool wlane, MassRecs<MP, CH> &c) {
+                                           int t0, MassRecs<MP, CH> &c) {
 #pragma unroll
     for (int p = 0; p < MP; ++p)
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
             const int t = min(t0 + j, t_pad - 1);
-            if (wlane)
-                c.w[p][j] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ln.ev[p]) * t_pad + t);
-            else
-                c.r[p][j] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(ln.ev[p]) * t_pad + t);
+            c.w[p][j] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ln.evw[p]) * t_pad + t);
+            if constexpr (!WONLY)
+                c.r[p][j] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(ln.evr[p]) * t_pad + t);
         }
 }
 
@@ -311,25 +327,35 @@ __global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob 
     const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad;
     const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
     const int nc = (t_end - t_begin + CH - 1) / CH;
-    MassRecs<MP, CH> cur, nxt;  // read lanes fetch (unused) read records: in bounds for Kr > Kw
-    mass_fetch(ln, gw, gr, t_pad, t_begin, wlane, cur);
-    for (int ci = 0; ci < nc; ++ci) {
-        mass_fetch(ln, gw, gr, t_pad, t_begin + min(ci + 1, nc - 1) * CH, wlane, nxt);
-        __builtin_amdgcn_sched_barrier(0);
+    auto run = [&](int ci, const MassRecs<MP, CH> &c) {
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
                 const bool act = wlane && ln.on[p] && t_begin + ci * CH + j < t_end;
-                const int a = act ? cur.w[p][j].x : -2;
-                const float w = act ? __int_as_float(cur.w[p][j].y) : 0.f;
-                const float al = act ? __int_as_float(cur.w[p][j].z) : 1.f;
+                const int a = act ? c.w[p][j].x : -2;
+                const float w = act ? __int_as_float(c.w[p][j].y) : 0.f;
+                const float al = act ? __int_as_float(c.w[p][j].z) : 1.f;
                 const float2 m = mp[a];
                 mp[a] = make_float2(al * m.x, fmaf(al, m.y, w));
             }
         }
+    };
+    // two chunks per iteration with swapped buffers: a copy of registers
+    // with loads pending would wait for every outstanding load
+    MassRecs<MP, CH> ca, cb;
+    mass_fetch<true>(ln, gw, gr, t_pad, t_begin, ca);
+    for (int ci = 0; ci < nc; ci += 2) {
+        mass_fetch<true>(ln, gw, gr, t_pad, t_begin + min(ci + 1, nc - 1) * CH, cb);
         __builtin_amdgcn_sched_barrier(0);
-        cur = nxt;
+        run(ci, ca);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ci + 1 >= nc)
+            break;
+        mass_fetch<true>(ln, gw, gr, t_pad, t_begin + min(ci + 2, nc - 1) * CH, ca);
+        __builtin_amdgcn_sched_barrier(0);
+        run(ci + 1, cb);
+        __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
     float2 *dst = maps + (static_cast<int64_t>(bh) * nck + ck) * A;
@@ -402,7 +428,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
     auto run = [&](int t0, const MassRecs<MP, CH> &c) {
         auto wev = [&](int p, int j, int &a, float &w, float &al) {
-            const bool act = wlane && ln.on[p] && t0 + j < t_end;
+            const bool act = wlane && ln.act[p] && t0 + j < t_end;
             a = act ? c.w[p][j].x : -2;
             w = act ? __int_as_float(c.w[p][j].y) : 0.f;
             al = act ? __int_as_float(c.w[p][j].z) : 1.f;
@@ -416,14 +442,6 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 const float m2 = fmaf(al[p], m[p], w[p]);
                 ms[a[p]] = m2;
                 gn[p] = scan_gain(w[p], m2 + eps);
-                if constexpr (!AUX) {
-                    // every event below max(Kw, Kr) gets a record; past Kw it is
-                    // the no-op write (slot -2, gain 0)
-                    const int e = p * 32 + hl;
-                    if (wlane && e < ek && live)
-                        *reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(t) * ek + e].wslot) =
-                            make_int2(a[p], __float_as_int(gn[p]));
-                }
             }
             {
                 int rb[MP];
@@ -431,14 +449,15 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 float sr = 0.f, srm = 0.f;
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
-                    const bool act = !wlane && ln.on[p] && live;
+                    const bool act = !wlane && ln.act[p] && live;
                     rb[p] = act ? c.r[p][j].x : -1;
                     rr[p] = act ? __int_as_float(c.r[p][j].y) : 0.f;
                     mm[p] = 0.f;
                     if constexpr (MA || AUX) {
                         mm[p] = ms[rb[p]];  // post-write mass
-                        sr += rr[p];
-                        srm += rr[p] * mm[p];
+                        const float rs = ln.on[p] ? rr[p] : 0.f;  // stand-ins add nothing
+                        sr += rs;
+                        srm += rs * mm[p];
                     }
                 }
                 float scale = 1.f;
@@ -457,11 +476,13 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                             aux.rev[o] = make_int4(rb[p], __float_as_int(re[p]), __float_as_int(mm[p]), 0);
                         }
                     } else {
-                        // past Kr: the no-op read (slot -1, weight 0)
-                        const int e = p * 32 + hl;
-                        if (!wlane && e < ek && live)
-                            *reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(t) * ek + e].rslot) =
-                                make_int2(rb[p], __float_as_int(re[p]));
+                        // every event below max(Kw, Kr) gets a record (past Kw
+                        // the no-op write: slot -2, gain 0; past Kr the no-op
+                        // read: slot -1, weight 0); write lanes store its first
+                        // half, read lanes its second. Tokens past the end
+                        // store no-op records into the padding rows.
+                        int2 *dst = reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(t) * ek + ln.es[p]]) + (wlane ? 0 : 1);
+                        *dst = wlane ? make_int2(a[p], __float_as_int(gn[p])) : make_int2(rb[p], __float_as_int(re[p]));
                     }
                 }
                 if constexpr (AUX) {
@@ -516,15 +537,21 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
         }
     };
     const int nc = (t_end - t_begin + CH - 1) / CH;
-    MassRecs<MP, CH> cur, nxt;
-    mass_fetch(ln, gw, gr, t_pad, t_begin, wlane, cur);
-    for (int ci = 0; ci < nc; ++ci) {
-        // the next loads stay ahead of this part's mass chain
-        mass_fetch(ln, gw, gr, t_pad, t_begin + min(ci + 1, nc - 1) * CH, wlane, nxt);
+    // the next chunk's loads stay ahead of this chunk's mass chain; two
+    // chunks per iteration with swapped buffers (no copy of pending loads)
+    MassRecs<MP, CH> ca, cb;
+    mass_fetch<false>(ln, gw, gr, t_pad, t_begin, ca);
+    for (int ci = 0; ci < nc; ci += 2) {
+        mass_fetch<false>(ln, gw, gr, t_pad, t_begin + min(ci + 1, nc - 1) * CH, cb);
         __builtin_amdgcn_sched_barrier(0);
-        run(t_begin + ci * CH, cur);
+        run(t_begin + ci * CH, ca);
         __builtin_amdgcn_sched_barrier(0);
-        cur = nxt;
+        if (ci + 1 >= nc)
+            break;
+        mass_fetch<false>(ln, gw, gr, t_pad, t_begin + min(ci + 2, nc - 1) * CH, ca);
+        __builtin_amdgcn_sched_barrier(0);
+        run(t_begin + (ci + 1) * CH, cb);
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (!starts) {
         __syncthreads();
