@@ -312,7 +312,9 @@ template<int MP>
 __global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob job, float2 *maps, int t_pad,
                                                               int chunk_len) {
     using L = MassLanes<MP>;
-    constexpr int CH = L::CH;
+    // half the replay's fetch: fewer registers, more resident waves to
+    // cover the record loads' latency
+    constexpr int CH = L::CH / 2;
     extern __shared__ __align__(16) float2 cm[];
     const int bh = blockIdx.x, ck = blockIdx.y, nck = gridDim.y;
     const int lane = static_cast<int>(threadIdx.x);
@@ -345,18 +347,19 @@ __global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob 
     // with loads pending would wait for every outstanding load
     MassRecs<MP, CH> ca, cb;
     mass_fetch<true>(ln, gw, gr, t_pad, t_begin, ca);
-    for (int ci = 0; ci < nc; ci += 2) {
-        mass_fetch<true>(ln, gw, gr, t_pad, t_begin + min(ci + 1, nc - 1) * CH, cb);
+    int ci = 0;
+    for (; ci + 1 < nc; ci += 2) {
+        mass_fetch<true>(ln, gw, gr, t_pad, t_begin + (ci + 1) * CH, cb);
         __builtin_amdgcn_sched_barrier(0);
         run(ci, ca);
         __builtin_amdgcn_sched_barrier(0);
-        if (ci + 1 >= nc)
-            break;
         mass_fetch<true>(ln, gw, gr, t_pad, t_begin + min(ci + 2, nc - 1) * CH, ca);
         __builtin_amdgcn_sched_barrier(0);
         run(ci + 1, cb);
         __builtin_amdgcn_sched_barrier(0);
     }
+    if (ci < nc)
+        run(ci, ca);
     __syncthreads();
     float2 *dst = maps + (static_cast<int64_t>(bh) * nck + ck) * A;
     for (int a = lane; a < A; a += kWave)
@@ -390,7 +393,8 @@ template<bool MA, int MP, bool AUX = false>
 __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, int t_pad, int chunk_len,
                                                             const float2 *starts, const MassAux aux) {
     using L = MassLanes<MP>;
-    constexpr int CH = L::CH;
+    // half the fetch of the records: fewer registers, more resident waves
+    constexpr int CH = L::CH / 2;
     extern __shared__ __align__(16) float lds[];
     const int bh = blockIdx.x, ck = blockIdx.y, nck = gridDim.y;
     const int lane = static_cast<int>(threadIdx.x);
