@@ -565,16 +565,21 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     }
 }
 
-// Time chunks of the mass passes: about four waves per SIMD (the per-token
-// chain is latency-bound, so more waves per SIMD pay for the extra maps).
-constexpr int kReplayChunkFactor = 4;
+// Time chunks of the mass passes: about kMassChunkTokens tokens each, or
+// shorter (down to 64 tokens) until the (b, h, chunk) waves put one wave on
+// every SIMD. Measured on MI355X, mass pre-pass + scan: config 2 (128
+// heads, T = 4096) 0.81 ms at chunks of 128 tokens, 0.79 at 256, 0.81 at
+// 512; config 4 (32 heads, T = 8192) 1.44 at 64 and 128, 1.42 at 256. The
+// training step's backward replay is also fastest at 256.
+constexpr int kReplayChunkFactor = 1;
+constexpr int kMassChunkTokens = 256;
 
-// Chunks of the mass pre-pass: enough (b, h, chunk) waves to fill the GPU,
-// chunks a multiple of 16 tokens, and maps that fit the scratch buffer.
+// Chunks of the mass pre-pass: as above, chunks a multiple of 16 tokens,
+// and maps that fit the scratch buffer.
 int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chunk_len) {
     const int64_t bh = static_cast<int64_t>(job.B) * job.H;
-    int nck = static_cast<int>(std::max<int64_t>(1, (4 * n_cu + bh - 1) / bh));
-    nck = std::min(nck, std::max(1, job.T / 64));  // chunks of >= 64 tokens
+    const int fill = static_cast<int>(std::min<int64_t>((4 * n_cu + bh - 1) / bh, std::max(1, job.T / 64)));
+    int nck = std::max((job.T + kMassChunkTokens - 1) / kMassChunkTokens, std::max(1, fill));
     while (nck > 1 && static_cast<size_t>(bh) * nck * job.A * sizeof(float2) > scratch_bytes)
         nck /= 2;
     if (static_cast<int64_t>(job.A + 2) * 8 > kLdsPerCu)
