@@ -342,8 +342,14 @@ __host__ __device__ constexpr size_t scan_stage_offset(int A, int rs, bool pre =
     return ((static_cast<size_t>(A + 2) * rs + (pre ? 0 : static_cast<size_t>(A + 2))) * 4 + 15) / 16 * 16;
 }
 // Tokens per chunk: 16, or 8 when more than 64 events per token would make
-// the double-buffered stage outgrow LDS.
-__host__ __device__ constexpr int scan_chunk_len(int events) { return events > 64 ? 8 : kChunk; }
+// the double-buffered stage outgrow LDS. The precomputed-gain form with at
+// most 8 events per token takes 32: its per-chunk work (fetch, deposit, row
+// addresses, y stores) is spread over twice the tokens for a few KB more of
+// private stage (config 2: segment stage 0.80 -> 0.78 ms). The records are
+// padded to whole 32-token chunks either way.
+__host__ __device__ constexpr int scan_chunk_len(int events, bool pre = false) {
+    return events > 64 ? 8 : (pre && events <= 8) ? 2 * kChunk : kChunk;
+}
 
 // PRE: gains precomputed by the mass pre-pass (no mass column; the state
 // waves stream their records from global memory and stage only x, one
@@ -351,7 +357,7 @@ __host__ __device__ constexpr int scan_chunk_len(int events) { return events > 6
 // wave, the StageRec it produces, x and the overlap flags.
 inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem, bool pre = false) {
     const int cs = nw * (kWave / epp) * vec;
-    const int ch = scan_chunk_len(epp * np);
+    const int ch = scan_chunk_len(epp * np, pre);
     const size_t state = scan_stage_offset(A, scan_row_stride(vec, cs), pre);
     const size_t x = static_cast<size_t>(cs) * (ch * elem + 16);
     if (pre)  // one private stage per wave: its records and its channels' x
@@ -390,7 +396,7 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
     constexpr int RS = scan_row_stride(VEC, CS);
     constexpr int NST = kWave * NW;           // state threads
     constexpr int E = EPP * NP;               // event lanes per token
-    constexpr int CH = scan_chunk_len(E);     // tokens per chunk
+    constexpr int CH = scan_chunk_len(E, PRE);  // tokens per chunk
     constexpr int MP = (E + 31) / 32;         // mass-wave passes (32 events each)
     constexpr int ES = static_cast<int>(sizeof(Scalar));
     constexpr int XRB = CH * ES + 16;  // staged x row: CH elements + 16 bytes against bank conflicts
