@@ -4,12 +4,21 @@
 // content index asc); both parts are packed into one unsigned key so that a
 // compare-exchange is a max/min pair:
 //   digit keys      16-bit inputs: ord16(logit) << 16 | (0xFFFF - digit)
-//                   fp32 inputs:   ord32(logit) << 32 | (0xFFFFFFFF - digit)
-//   prefix keys     ord32(score) << 32 | (0xFFFFFFFF - content index)
+//                   fp32 inputs:   ord32(logit) << 31 | (0x7FFFFFFF - digit)
+//   prefix keys     ord32(score) << 31 | (0x7FFFFFFF - content index)
 // where ord maps a float's bits to an unsigned integer with the same order
 // (-0 is folded onto +0 first so that equal values compare equal). Within a
 // digit, log_softmax is a monotone shift of the logits, so ordering by logit
 // orders by log-probability. Key 0 marks "no candidate".
+//
+// The 64-bit keys stay below 2^63, so read as IEEE doubles they are
+// non-negative and ordered as the integers are; a 64-bit compare-exchange
+// is then one v_max_f64 and one v_min_f64 instead of a 64-bit compare and
+// four selects. The exponent field of a key is bits 30..20 of its ord32
+// value: it is all ones or all zeros only for NaN inputs (positive NaNs
+// from 0x7FE00000 up, negative ones from 0xFFE00000 up), whose keys would
+// read as NaN or subnormal doubles; -inf, finite values and +inf give
+// normal doubles, and key 0 reads as +0.
 //
 // Search (U digits, top-KM lists): the sorted top-KM of each digit is
 // combined with the sorted top-KM prefix list over the staircase
@@ -43,11 +52,18 @@ __device__ __forceinline__ void ce_desc(uint32_t &a, uint32_t &b) {
     a = hi;
     b = lo;
 }
+__device__ __forceinline__ uint32_t key_max(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) {
+    uint64_t r;
+    asm("v_max_f64 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ void ce_desc(uint64_t &a, uint64_t &b) {
-    const bool sw = b > a;
-    const uint64_t t = a;
-    a = sw ? b : a;
-    b = sw ? t : b;
+    uint64_t hi, lo;
+    asm("v_max_f64 %0, %1, %2" : "=v"(hi) : "v"(a), "v"(b));
+    asm("v_min_f64 %0, %1, %2" : "=v"(lo) : "v"(a), "v"(b));
+    a = hi;
+    b = lo;
 }
 
 // Bitonic sort (descending) of keys [OFF, OFF + N); N a power of two.
@@ -76,8 +92,7 @@ template<int KM, int OFF, typename K, int M>
 __device__ __forceinline__ void merge_top(K (&a)[KM], const K (&b)[M]) {
 #pragma unroll
     for (int i = 0; i < KM; ++i) {
-        const K x = b[OFF + KM - 1 - i];
-        a[i] = a[i] > x ? a[i] : x;
+        a[i] = key_max(a[i], b[OFF + KM - 1 - i]);
     }
 #pragma unroll
     for (int j = KM >> 1; j > 0; j >>= 1) {
@@ -174,7 +189,7 @@ __device__ __forceinline__ DigitKey<Scalar> digit_key(uint32_t bits, int p) {
     if constexpr (sizeof(Scalar) == 2)
         return (ord16(bits) << 16) | (0xFFFFu - static_cast<uint32_t>(p));
     else
-        return (static_cast<uint64_t>(ord32(bits)) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(p));
+        return (static_cast<uint64_t>(ord32(bits)) << 31) | (0x7FFFFFFFu - static_cast<uint32_t>(p));
 }
 template<typename Scalar>
 __device__ __forceinline__ void digit_unkey(DigitKey<Scalar> k, float &x, int &p) {
@@ -182,13 +197,13 @@ __device__ __forceinline__ void digit_unkey(DigitKey<Scalar> k, float &x, int &p
         x = bits_value<Scalar>(unord16(k >> 16));
         p = static_cast<int>(0xFFFFu - (k & 0xFFFFu));
     } else {
-        x = __uint_as_float(unord32(static_cast<uint32_t>(k >> 32)));
-        p = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(k));
+        x = __uint_as_float(unord32(static_cast<uint32_t>(k >> 31)));
+        p = static_cast<int>(0x7FFFFFFFu - (static_cast<uint32_t>(k) & 0x7FFFFFFFu));
     }
 }
 
 __device__ __forceinline__ uint64_t prefix_key(float s, int c) {
-    return (static_cast<uint64_t>(ord32(__float_as_uint(s))) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(c));
+    return (static_cast<uint64_t>(ord32(__float_as_uint(s))) << 31) | (0x7FFFFFFFu - static_cast<uint32_t>(c));
 }
 
 // One digit: sorted top-KM log-probabilities (lv) and digit values (dv),
@@ -301,8 +316,8 @@ __device__ __forceinline__ void combine_prefix(float (&sv)[KM], int (&cv)[KM], u
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
         ok[k] = top[k] != 0 ? ~0u : 0u;
-        sv[k] = __uint_as_float(unord32(static_cast<uint32_t>(top[k] >> 32)));
-        cv[k] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(top[k]));
+        sv[k] = __uint_as_float(unord32(static_cast<uint32_t>(top[k] >> 31)));
+        cv[k] = static_cast<int>(0x7FFFFFFFu - (static_cast<uint32_t>(top[k]) & 0x7FFFFFFFu));
     }
 }
 
