@@ -163,14 +163,15 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, i
 }
 
 // Scan records from decoder outputs: one thread per (b*H + h, event, t) with
-// t < T_pad. Writes keep positive weights; reads were stored negated.
-template<typename Scalar>
+// t < T_pad. Writes keep positive weights; reads were stored negated. KF:
+// write events compared per token for the overlap flags (8 or 16, >= Kw).
+template<typename Scalar, int KF>
 __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, int t_pad) {
     const int Kt = job.Kw + job.Kr;
     const int64_t n = static_cast<int64_t>(job.B) * job.H * Kt * t_pad;
-    const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (gid >= n)
-        return;
+    const int64_t gid0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const bool in = gid0 < n;
+    const int64_t gid = in ? gid0 : n - 1;  // lanes past the end follow along (the flags' shuffles)
     const int t = static_cast<int>(gid % t_pad);
     const int64_t rest = gid / t_pad;
     const int k = static_cast<int>(rest % Kt);
@@ -184,42 +185,51 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
     const float g = load_f32(static_cast<const Scalar *>(job.gamma) + static_cast<int64_t>(bh) * T + tl);
     const uint8_t *mp = job.mask ? job.mask + static_cast<int64_t>(b) * T + tl : &kScanAllValid;
     const bool live = t < T && *mp != 0 && static_cast<unsigned>(a) < static_cast<unsigned>(A);
+    // Event 0 carries the token's overlap flags, which the scan reads: bit
+    // d - 1 set if a slot this token writes is also written by token t - d
+    // (d = 1, 2, 3). Computed exactly for top-K up to 16 (assumed for wider
+    // top-K), by whole waves: each lane reads its own token's write slots and
+    // takes those of tokens t - d from the lane d back (the same row of the
+    // grid when t >= d), reading them itself in the wave's first d lanes.
+    int ov = 7;
+    if (__ballot(in && k == 0 && job.Kw <= 16) != 0) {
+        // slot written by write event kk of token tt (tt < T), or -1
+        auto written = [&](int tt, int kk) {
+            const int64_t s = (static_cast<int64_t>(bh) * Kt + kk) * T + tt;
+            const int aa = job.addr_idx[s] - bh * A;
+            const uint8_t *m = job.mask ? job.mask + static_cast<int64_t>(b) * T + tt : &kScanAllValid;
+            return *m != 0 && static_cast<unsigned>(aa) < static_cast<unsigned>(A) && job.addr_val[s] != 0.f ? aa
+                                                                                                              : -1;
+        };
+        const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+        int cur[KF];
+#pragma unroll
+        for (int i = 0; i < KF; ++i)
+            cur[i] = i < job.Kw && t < T ? written(t, i) : -1;
+        ov = 0;
+#pragma unroll
+        for (int d = 1; d <= 3; ++d) {
+            bool hit = false;
+#pragma unroll
+            for (int i = 0; i < KF; ++i) {
+                int x = __shfl_up(cur[i], d);
+                if (t < d || t >= T)
+                    x = -1;
+                else if (lane < d)
+                    x = i < job.Kw ? written(t - d, i) : -1;
+#pragma unroll
+                for (int j = 0; j < KF; ++j)
+                    hit = hit || (x >= 0 && x == cur[j]);
+            }
+            if (hit)
+                ov |= 1 << (d - 1);
+        }
+    }
+    if (!in)
+        return;
     if (k < job.Kw) {
         const bool act = live && v != 0.f;
-        // Event 0 carries the token's overlap flags, which the scan reads:
-        // bit d - 1 set if a slot this token writes is also written by token
-        // t - d (d = 1, 2, 3). Computed exactly for top-K up to 16; assumed
-        // for wider top-K.
-        int ov = 7;
-        if (k == 0 && job.Kw <= 16) {
-            ov = 0;
-            if (t < T) {
-                // slot written by write event kk of token tt (tt < T), or -1
-                auto written = [&](int tt, int kk) {
-                    const int64_t s = (static_cast<int64_t>(bh) * Kt + kk) * T + tt;
-                    const int aa = job.addr_idx[s] - bh * A;
-                    const uint8_t *m = job.mask ? job.mask + static_cast<int64_t>(b) * T + tt : &kScanAllValid;
-                    return *m != 0 && static_cast<unsigned>(aa) < static_cast<unsigned>(A) && job.addr_val[s] != 0.f
-                               ? aa : -1;
-                };
-                int cur[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    cur[i] = i < job.Kw ? written(t, i) : -1;
-                for (int d = 1; d <= 3 && d <= t; ++d) {
-                    bool hit = false;
-                    for (int i = 0; i < job.Kw; ++i) {
-                        const int x = written(t - d, i);
-#pragma unroll
-                        for (int j = 0; j < 16; ++j)
-                            hit = hit || (x >= 0 && x == cur[j]);
-                    }
-                    if (hit)
-                        ov |= 1 << (d - 1);
-                }
-            }
-        }
-        const float overlap = __int_as_float(ov);
+        const float overlap = __int_as_float(k == 0 && job.Kw <= 16 ? ov : 7);
         WriteRec rec{-2, 0.f, 1.f, overlap};
         if (act)
             rec = WriteRec{a, v, gsu_alpha(v, g), overlap};
@@ -654,6 +664,15 @@ hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *m
                           : launch_mass_pass<false, true>(job, t_pad, n, maps, maps_bytes, aux, stream);
 }
 
+template<typename Scalar>
+hipError_t launch_pack(const PackJob &job, unsigned blocks, int t_pad, hipStream_t stream) {
+    if (job.Kw <= 8)
+        hipLaunchKernelGGL((pack_records_kernel<Scalar, 8>), dim3(blocks), dim3(256), 0, stream, job, t_pad);
+    else
+        hipLaunchKernelGGL((pack_records_kernel<Scalar, 16>), dim3(blocks), dim3(256), 0, stream, job, t_pad);
+    return hipGetLastError();
+}
+
 hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const char **why) {
     const int t_pad = scan_t_pad(job.T);
     const int64_t n = static_cast<int64_t>(job.B) * job.H * (job.Kw + job.Kr) * t_pad;
@@ -661,12 +680,11 @@ hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const cha
         return hipSuccess;
     const unsigned blocks = static_cast<unsigned>((n + 255) / 256);
     switch (job.dtype) {
-        case kF32: hipLaunchKernelGGL(pack_records_kernel<float>, dim3(blocks), dim3(256), 0, stream, job, t_pad); break;
-        case kF16: hipLaunchKernelGGL(pack_records_kernel<_Float16>, dim3(blocks), dim3(256), 0, stream, job, t_pad); break;
-        case kBF16: hipLaunchKernelGGL(pack_records_kernel<bf16_t>, dim3(blocks), dim3(256), 0, stream, job, t_pad); break;
+        case kF32: return launch_pack<float>(job, blocks, t_pad, stream);
+        case kF16: return launch_pack<_Float16>(job, blocks, t_pad, stream);
+        case kBF16: return launch_pack<bf16_t>(job, blocks, t_pad, stream);
         default: *why = "record packing: unsupported dtype"; return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 // RAMNET_SCAN_LAYOUT="vec,epp,np,nw[,pre]" replaces the planner's choice (tests
