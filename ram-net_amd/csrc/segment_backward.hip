@@ -664,9 +664,20 @@ __global__ __launch_bounds__(256) void segment_bwd_sum_kernel(const float *part,
     const int64_t bh = bt / T;
     const int64_t stride = static_cast<int64_t>(BH) * t_pad * KP;
     const float *src = part + (bh * t_pad + t) * KP + k;
-    float s = src[0];
-    for (int u = 1; u < n_sub; ++u)
-        s += src[u * stride];
+    // eight loads in flight at a time (clamped into range, so unconditional),
+    // added in slice order
+    float s = 0.f;
+    for (int u0 = 0; u0 < n_sub; u0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            v[j] = src[static_cast<int64_t>(min(u0 + j, n_sub - 1)) * stride];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int u = u0 + j;
+            s = u == 0 ? v[j] : u < n_sub ? s + v[j] : s;
+        }
+    }
     out[i] = s;
 }
 
