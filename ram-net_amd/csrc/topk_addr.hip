@@ -381,15 +381,23 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
     };
     float dsum = 0.f, vsum = 0.f;
     float D[KM > 0 ? KM : 1];
+    float wk[KM > 0 ? KM : 1];
     int c[KM > 0 ? KM : 1];
     if constexpr (KM > 0) {
+        // every lane loads all KM events (clamped to the last one), so the
+        // loads issue together instead of one branch and wait each
 #pragma unroll
         for (int k = 0; k < KM; ++k) {
             const bool on = k < K;
-            D[k] = on ? dscore(on ? k : 0) : 0.f;
-            c[k] = on ? content(on ? k : 0) : -1;
+            const int kc = on ? k : K - 1;
+            const float w = weight(kc);
+            const float d = job.grad_val[row0 + static_cast<int64_t>(kc) * T] * w;
+            const int ck = content(kc);
+            wk[k] = on ? w : 0.f;
+            D[k] = on ? d : 0.f;
+            c[k] = on ? ck : -1;
             dsum += D[k];
-            vsum += on ? weight(k) : 0.f;
+            vsum += wk[k];
         }
     } else {
         for (int k = 0; k < K; ++k) {
@@ -406,7 +414,7 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
         if (renorm) {
 #pragma unroll
             for (int k = 0; k < KM; ++k)
-                D[k] = k < K ? D[k] - re * (weight(k) / vsum) * dsum : 0.f;
+                D[k] = k < K ? D[k] - re * (wk[k] / vsum) * dsum : 0.f;
         }
     }
     const float dsoft = (1.f - re) * dsum;
@@ -460,10 +468,16 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
             return g;
         };
         if constexpr (PR > 0) {
+            if (P == PR) {  // the common case: stores without a branch each
 #pragma unroll
-            for (int q = 0; q < PR; ++q)
-                if (q < P)
+                for (int q = 0; q < PR; ++q)
                     store_f32(gu + static_cast<int64_t>(q) * T, grad_of(q) - xr[q] * scale);
+            } else {
+#pragma unroll
+                for (int q = 0; q < PR; ++q)
+                    if (q < P)
+                        store_f32(gu + static_cast<int64_t>(q) * T, grad_of(q) - xr[q] * scale);
+            }
         } else {
             for (int q = 0; q < P; ++q) {
                 const float sm = live ? expf(load_f32(xu + static_cast<int64_t>(q) * T) - mx) : 0.f;
@@ -477,10 +491,13 @@ template<typename T>
 hipError_t launch_backward_typed(const AddrBwdJob &job, hipStream_t stream) {
     const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
     const dim3 grid(static_cast<unsigned>((n + 255) / 256)), blk(256);
-    const bool reg = job.P <= 32;  // a digit's logits fit in registers
+    // a digit's logits fit in registers up to P = 32; P = 16 has its own
+    // instance, whose stores need no per-logit branch
 #define RAMNET_ADDR_BWD(KM)                                                                          \
     do {                                                                                             \
-        if (reg)                                                                                     \
+        if (job.P == 16)                                                                             \
+            hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 16>), grid, blk, 0, stream, job);   \
+        else if (job.P <= 32)                                                                        \
             hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 32>), grid, blk, 0, stream, job);   \
         else                                                                                         \
             hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 0>), grid, blk, 0, stream, job);    \
