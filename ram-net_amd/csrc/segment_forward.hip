@@ -272,8 +272,11 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
 // a token is made by the whole wave: no branch around a load or a store,
 // which would make the compiler's memory-counter waits drain everything
 // outstanding, the just-issued prefetch and the stores included.
-template<int MP>
+// HALF: lanes per half (write lanes, then read lanes); 32, or fewer when a
+// wave carries several (b, h) units, each on 2 * HALF consecutive lanes.
+template<int MP, int HALF = 32>
 struct MassLanes {
+    static_assert(HALF == 32 || MP == 1, "units narrower than a wave take one pass of events");
     static constexpr int CH = MP <= 1 ? 16 : MP == 2 ? 8 : 4;  // tokens per fetch
     int ev[MP];    // this lane's event (clamped for loads)
     int evw[MP];   // its write event and read event, each clamped (every lane loads both)
@@ -282,17 +285,18 @@ struct MassLanes {
     bool act[MP];  // whether it acts: a real event, or a stand-in for the half's last event lane
     int es[MP];    // the event it stores (lanes past max(Kw, Kr) repeat the last one's store)
     __device__ MassLanes(int lane, int Kw, int Kr) {
-        const int hl = lane & 31;
+        const int hl = lane % HALF;
+        const bool wl = (lane / HALF) % 2 == 0;
         const int ek = max(Kw, Kr);
 #pragma unroll
         for (int p = 0; p < MP; ++p) {
             const int e = p * 32 + hl;
             es[p] = min(e, ek - 1);
-            on[p] = lane < 32 ? e < Kw : e < Kr;
-            act[p] = lane < 32 ? es[p] < Kw : es[p] < Kr;
+            on[p] = wl ? e < Kw : e < Kr;
+            act[p] = wl ? es[p] < Kw : es[p] < Kr;
             evw[p] = min(e, Kw - 1);
             evr[p] = min(e, Kr - 1);
-            ev[p] = lane < 32 ? evw[p] : evr[p];
+            ev[p] = wl ? evw[p] : evr[p];
         }
     }
 };
@@ -303,8 +307,8 @@ struct MassRecs {
 };
 // The chunk's records from token t0 on: write records for every lane, and
 // read records too unless WONLY.
-template<bool WONLY, int MP, int CH>
-__device__ __forceinline__ void mass_fetch(const MassLanes<MP> &ln, const WriteRec *gw, const ReadRec *gr, int t_pad,
+template<bool WONLY, int MP, int CH, int HALF>
+__device__ __forceinline__ void mass_fetch(const MassLanes<MP, HALF> &ln, const WriteRec *gw, const ReadRec *gr, int t_pad,
                                            int t0, MassRecs<MP, CH> &c) {
 #pragma unroll
     for (int p = 0; p < MP; ++p)
@@ -395,35 +399,49 @@ __global__ __launch_bounds__(256) void mass_chunk_scan_kernel(const SegmentJob j
     job.mass_out[i] = m;
 }
 
-// Step 3: one wave per (b, h, chunk), from m_start (the maps after step 2,
-// or the initial mass when there is one chunk). With AUX the records stay
-// as they are and the per-event quantities go to `aux` instead (the forward
-// replay of the segment backward).
-template<bool MA, int MP, bool AUX = false>
+// Step 3: one wave per NU (b, h) units of one chunk, from m_start (the maps
+// after step 2, or the initial mass when there is one chunk). With AUX the
+// records stay as they are and the per-event quantities go to `aux` instead
+// (the forward replay of the segment backward). NU > 1 (at most 32 / NU
+// events per token): unit u takes lanes [u * 64 / NU, (u + 1) * 64 / NU),
+// so every lane of a record load or gain store serves an event; the units
+// past the last (b, h) repeat it (same records, same values stored).
+template<bool MA, int MP, bool AUX = false, int NU = 1>
 __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, int t_pad, int chunk_len,
                                                             const float2 *starts, const MassAux aux) {
-    using L = MassLanes<MP>;
+    static_assert(NU == 1 || (MP == 1 && !AUX), "several units per wave: one pass of events, no AUX");
+    constexpr int HALF = kWave / NU / 2;
+    using L = MassLanes<MP, HALF>;
     // half the fetch of the records: fewer registers, more resident waves
     constexpr int CH = L::CH / 2;
     extern __shared__ __align__(16) float lds[];
-    const int bh = blockIdx.x, ck = blockIdx.y, nck = gridDim.y;
+    const int n_bh = job.B * job.H;
+    const int ck = blockIdx.y, nck = gridDim.y;
     const int lane = static_cast<int>(threadIdx.x);
-    const int hl = lane & 31;
-    const bool wlane = lane < 32;
+    const int unit = lane / (2 * HALF);
+    const int bh = min(static_cast<int>(blockIdx.x) * NU + unit, n_bh - 1);
+    const int hl = lane % HALF;
+    const bool wlane = (lane / HALF) % 2 == 0;
     const int A = job.A, Kw = job.Kw, Kr = job.Kr;
     const float eps = job.eps;
-    float *ms = lds + 2;  // ms[-2], ms[-1]: the no-op slots of padding records
-    if (starts) {
-        const float2 *src = starts + (static_cast<int64_t>(bh) * nck + ck) * A;
-        for (int a = lane; a < A; a += kWave)
-            ms[a] = src[a].x;
-    } else {
-        const float *src = job.init_mass + static_cast<int64_t>(bh) * A;
-        for (int a = lane; a < A; a += kWave)
-            ms[a] = src[a];
+    // unit v's masses at lds + v * (A + 2) + 2; [-2], [-1]: the no-op slots of padding records
+    float *ms = lds + unit * (A + 2) + 2;
+#pragma unroll
+    for (int v = 0; v < NU; ++v) {
+        const int bv = min(static_cast<int>(blockIdx.x) * NU + v, n_bh - 1);
+        float *mv = lds + v * (A + 2) + 2;
+        if (starts) {
+            const float2 *src = starts + (static_cast<int64_t>(bv) * nck + ck) * A;
+            for (int a = lane; a < A; a += kWave)
+                mv[a] = src[a].x;
+        } else {
+            const float *src = job.init_mass + static_cast<int64_t>(bv) * A;
+            for (int a = lane; a < A; a += kWave)
+                mv[a] = src[a];
+        }
+        if (lane < 2)
+            mv[lane - 2] = 1.f;
     }
-    if (lane < 2)
-        lds[lane] = 1.f;
     // AUX: per slot, the token whose read last posted there and its weight
     int *rtag = reinterpret_cast<int *>(lds + A + 2);
     float *rval = lds + 2 * A + 2;
@@ -476,8 +494,8 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 }
                 float scale = 1.f;
                 if constexpr (MA) {
-                    sr = event_sum<32>(sr);
-                    srm = event_sum<32>(srm);
+                    sr = event_sum<HALF>(sr);
+                    srm = event_sum<HALF>(srm);
                     scale = sr / (srm + eps);
                 }
                 float re[MP];
@@ -531,7 +549,12 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
 #pragma unroll
         for (int j0 = 0; j0 < CH; j0 += 2) {
             const int j1 = j0 + 1;
-            const int ov = __builtin_amdgcn_readfirstlane(c.w[0][j1].w) & 1;  // shares a slot with token j0
+            // token j1 shares a slot with token j0 (in any unit: event 0's record carries the flag)
+            int ov;
+            if constexpr (NU == 1)
+                ov = __builtin_amdgcn_readfirstlane(c.w[0][j1].w) & 1;
+            else
+                ov = __ballot(lane % (2 * HALF) == 0 && (c.w[0][j1].w & 1) != 0) != 0;
             int a0[MP], a1[MP];
             float w0[MP], w1[MP], al0[MP], al1[MP], m0[MP], m1[MP];
 #pragma unroll
@@ -569,9 +592,14 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     }
     if (!starts) {
         __syncthreads();
-        float *mdst = job.mass_out + static_cast<int64_t>(bh) * A;
-        for (int a = lane; a < A; a += kWave)
-            mdst[a] = ms[a];
+#pragma unroll
+        for (int v = 0; v < NU; ++v) {
+            const int bv = min(static_cast<int>(blockIdx.x) * NU + v, n_bh - 1);
+            const float *mv = lds + v * (A + 2) + 2;
+            float *mdst = job.mass_out + static_cast<int64_t>(bv) * A;
+            for (int a = lane; a < A; a += kWave)
+                mdst[a] = mv[a];
+        }
     }
 }
 
@@ -599,8 +627,36 @@ int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chun
     return (job.T + *chunk_len - 1) / *chunk_len;
 }
 
-// LDS of the replay kernel: the masses (and with AUX the read tag table).
-size_t mass_lds_bytes(int A, bool aux) { return static_cast<size_t>(A + 2) * 4 + (aux ? static_cast<size_t>(A) * 8 : 0); }
+// LDS of the replay kernel: the masses of its NU units (and with AUX the
+// read tag table).
+size_t mass_lds_bytes(int A, bool aux, int nu = 1) {
+    return static_cast<size_t>(A + 2) * 4 * nu + (aux ? static_cast<size_t>(A) * 8 : 0);
+}
+
+// The replay kernel with NU units per wave: (b, h) units of a chunk in
+// groups of NU.
+template<bool MA, int MP, bool AUX, int NU>
+void launch_replay_units(const SegmentJob &job, int t_pad, int len, int nck, const float2 *starts, const MassAux &aux,
+                         hipStream_t stream) {
+    const unsigned groups = static_cast<unsigned>((job.B * job.H + NU - 1) / NU);
+    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX, NU>), dim3(groups, static_cast<unsigned>(nck)), dim3(kWave),
+                       mass_lds_bytes(job.A, AUX, NU), stream, job, t_pad, len, starts, aux);
+}
+
+// Units per replay wave: four when a token has at most 8 events and the
+// four units' masses take at most 64 KB of LDS, else one. Measured on
+// MI355X: config 2 (K = 8) segment stage 0.762 -> 0.755 ms with four units;
+// config 4 (K = 16) 1.420 -> 1.433 ms with two (so one there), and both
+// slower with the time chunks halved to keep the wave count.
+template<bool MA, int MP, bool AUX>
+void launch_mass_replay_nu(const SegmentJob &job, int t_pad, int len, int nck, const float2 *starts,
+                           const MassAux &aux, hipStream_t stream) {
+    if constexpr (MP == 1 && !AUX) {
+        if (std::max(job.Kw, job.Kr) <= 8 && mass_lds_bytes(job.A, false, 4) <= 64 * 1024)
+            return launch_replay_units<MA, MP, AUX, 4>(job, t_pad, len, nck, starts, aux, stream);
+    }
+    launch_replay_units<MA, MP, AUX, 1>(job, t_pad, len, nck, starts, aux, stream);
+}
 
 // `maps` is scratch for the chunk maps (maps_bytes of it); the final masses
 // go to job.mass_out.
@@ -611,8 +667,7 @@ hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void 
     const int nck = mass_chunks(job, maps_bytes, n_cu, &len);
     const unsigned bh = static_cast<unsigned>(job.B * job.H);
     if (nck <= 1) {
-        hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, 1), dim3(kWave), mass_lds_bytes(job.A, AUX),
-                           stream, job, t_pad, job.T, nullptr, aux);
+        launch_mass_replay_nu<MA, MP, AUX>(job, t_pad, job.T, 1, nullptr, aux, stream);
         return hipGetLastError();
     }
     auto *maps = static_cast<float2 *>(maps_buf);
@@ -621,8 +676,7 @@ hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void 
     const int64_t n = static_cast<int64_t>(bh) * job.A;
     hipLaunchKernelGGL(mass_chunk_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, job,
                        maps, nck);
-    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX>), dim3(bh, nck), dim3(kWave), mass_lds_bytes(job.A, AUX),
-                       stream, job, t_pad, len, maps, aux);
+    launch_mass_replay_nu<MA, MP, AUX>(job, t_pad, len, nck, maps, aux, stream);
     return hipGetLastError();
 }
 

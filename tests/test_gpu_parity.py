@@ -320,6 +320,26 @@ def test_mass_prepass_time_chunks(mass_aware, monkeypatch):
     assert oracle.rel_err(y[:, :, keep], ry[:, :, keep]) <= FP32_TOL
 
 
+@pytest.mark.parametrize("bh,T", [((1, 3), 45), ((3, 2), 45), ((1, 3), 700), ((5, 1), 300)])
+def test_mass_prepass_partial_unit_group(bh, T, monkeypatch):
+    """With at most 8 events per token the pre-pass replay packs four (b, h)
+    units into a wave; B * H not a multiple of four leaves a wave whose last
+    units repeat the last (b, h). One time chunk (the replay writes the final
+    masses per unit) and several, against the fp64 oracle."""
+    B, H = bh
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", "1,8,1,4,1")
+    for mass_aware in (False, True):
+        print(f"pre-pass unit groups B={B} H={H} T={T} mass_aware={mass_aware}", flush=True)
+        src, got, ref = _segment_case(B, H, 2, 16, T, 64, 8, 6, torch.float32, True, mass_aware, seed=7 + T + B)
+        y, slot, mass = got
+        ry, rslot, rmass = ref
+        ry = torch.as_tensor(ry)
+        assert oracle.rel_err(slot, rslot) <= FP32_TOL
+        assert oracle.rel_err(mass, rmass) <= FP32_TOL
+        keep = src.mask[0]
+        assert oracle.rel_err(y[:, :, keep], ry[:, :, keep]) <= FP32_TOL
+
+
 @pytest.mark.parametrize("re_norm", [(0.0, 0.0), (1.0, 1.0), (0.25, 0.75)])
 def test_api_matches_dense_reference(re_norm):
     """random_access_memory_attention vs the dense restatement of the reference (config 1 shape)."""
