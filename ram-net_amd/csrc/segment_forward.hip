@@ -321,22 +321,29 @@ __device__ __forceinline__ void mass_fetch(const MassLanes<MP, HALF> &ln, const 
         }
 }
 
-// Step 1: one wave per (b, h, chunk); LDS holds (a, b) per slot.
-template<int MP>
+// Step 1: one wave per NU (b, h) units of one chunk (NU > 1: lanes as in
+// the replay, unit u on lanes [u * 64 / NU, (u + 1) * 64 / NU), the units
+// past the last (b, h) repeating it); LDS holds (a, b) per slot and unit.
+template<int MP, int NU = 1>
 __global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob job, float2 *maps, int t_pad,
                                                               int chunk_len) {
-    using L = MassLanes<MP>;
+    static_assert(NU == 1 || MP == 1, "several units per wave: one pass of events");
+    constexpr int HALF = kWave / NU / 2;
+    using L = MassLanes<MP, HALF>;
     // half the replay's fetch: fewer registers, more resident waves to
     // cover the record loads' latency
     constexpr int CH = L::CH / 2;
     extern __shared__ __align__(16) float2 cm[];
-    const int bh = blockIdx.x, ck = blockIdx.y, nck = gridDim.y;
+    const int n_bh = job.B * job.H;
+    const int ck = blockIdx.y, nck = gridDim.y;
     const int lane = static_cast<int>(threadIdx.x);
-    const bool wlane = lane < 32;
+    const int bh = min(static_cast<int>(blockIdx.x) * NU + lane / (2 * HALF), n_bh - 1);
+    const bool wlane = (lane / HALF) % 2 == 0;
     const int A = job.A, Kw = job.Kw, Kr = job.Kr;
-    float2 *mp = cm + 2;  // mp[-2]: the no-op slot of padding records
-    for (int a = lane - 2; a < A; a += kWave)
-        mp[a] = make_float2(1.f, 0.f);
+    // unit v's maps at cm + v * (A + 2) + 2; [-2]: the no-op slot of padding records
+    float2 *mp = cm + (lane / (2 * HALF)) * (A + 2) + 2;
+    for (int a = lane; a < NU * (A + 2); a += kWave)
+        cm[a] = make_float2(1.f, 0.f);
     __syncthreads();
     const L ln(lane, Kw, Kr);
     const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * t_pad;
@@ -375,9 +382,14 @@ __global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob 
     if (ci < nc)
         run(ci, ca);
     __syncthreads();
-    float2 *dst = maps + (static_cast<int64_t>(bh) * nck + ck) * A;
-    for (int a = lane; a < A; a += kWave)
-        dst[a] = mp[a];
+#pragma unroll
+    for (int v = 0; v < NU; ++v) {
+        const int bv = min(static_cast<int>(blockIdx.x) * NU + v, n_bh - 1);
+        const float2 *mv = cm + v * (A + 2) + 2;
+        float2 *dst = maps + (static_cast<int64_t>(bv) * nck + ck) * A;
+        for (int a = lane; a < A; a += kWave)
+            dst[a] = mv[a];
+    }
 }
 
 // Step 2: one thread per (b, h, slot); the map of chunk c is replaced by
@@ -671,8 +683,12 @@ hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void 
         return hipGetLastError();
     }
     auto *maps = static_cast<float2 *>(maps_buf);
-    hipLaunchKernelGGL((mass_chunk_map_kernel<MP>), dim3(bh, nck), dim3(kWave), static_cast<size_t>(job.A + 2) * 8,
-                       stream, job, maps, t_pad, len);
+    if (MP == 1 && std::max(job.Kw, job.Kr) <= 8 && static_cast<size_t>(job.A + 2) * 8 * 4 <= 64 * 1024)
+        hipLaunchKernelGGL((mass_chunk_map_kernel<1, 4>), dim3((bh + 3) / 4, nck), dim3(kWave),
+                           static_cast<size_t>(job.A + 2) * 8 * 4, stream, job, maps, t_pad, len);
+    else
+        hipLaunchKernelGGL((mass_chunk_map_kernel<MP>), dim3(bh, nck), dim3(kWave),
+                           static_cast<size_t>(job.A + 2) * 8, stream, job, maps, t_pad, len);
     const int64_t n = static_cast<int64_t>(bh) * job.A;
     hipLaunchKernelGGL(mass_chunk_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, job,
                        maps, nck);
