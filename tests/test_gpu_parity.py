@@ -320,17 +320,20 @@ def test_mass_prepass_time_chunks(mass_aware, monkeypatch):
     assert oracle.rel_err(y[:, :, keep], ry[:, :, keep]) <= FP32_TOL
 
 
-@pytest.mark.parametrize("bh,T", [((1, 3), 45), ((3, 2), 45), ((1, 3), 700), ((5, 1), 300)])
-def test_mass_prepass_partial_unit_group(bh, T, monkeypatch):
-    """With at most 8 events per token the pre-pass replay packs four (b, h)
+@pytest.mark.parametrize("bh,T,P", [((1, 3), 45, 16), ((3, 2), 45, 16), ((1, 3), 700, 16), ((5, 1), 300, 16),
+                                    ((1, 3), 700, 63)])
+def test_mass_prepass_partial_unit_group(bh, T, P, monkeypatch):
+    """With at most 8 events per token the pre-pass kernels pack four (b, h)
     units into a wave; B * H not a multiple of four leaves a wave whose last
     units repeat the last (b, h). One time chunk (the replay writes the final
-    masses per unit) and several, against the fp64 oracle."""
+    masses per unit) and several, against the fp64 oracle. P = 63 (A = 3969):
+    the four-unit replay at 63.5 KB of LDS beside one-unit chunk maps."""
     B, H = bh
-    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", "1,8,1,4,1")
+    # a precomputed-gain layout whose slice fits in LDS at this A
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", "1,8,1,4,1" if P == 16 else "1,16,1,2,1")
     for mass_aware in (False, True):
-        print(f"pre-pass unit groups B={B} H={H} T={T} mass_aware={mass_aware}", flush=True)
-        src, got, ref = _segment_case(B, H, 2, 16, T, 64, 8, 6, torch.float32, True, mass_aware, seed=7 + T + B)
+        print(f"pre-pass unit groups B={B} H={H} T={T} P={P} mass_aware={mass_aware}", flush=True)
+        src, got, ref = _segment_case(B, H, 2, P, T, 64, 8, 6, torch.float32, True, mass_aware, seed=7 + T + B)
         y, slot, mass = got
         ry, rslot, rmass = ref
         ry = torch.as_tensor(ry)
