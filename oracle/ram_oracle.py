@@ -204,9 +204,9 @@ def sparse_gsu_f64(w_idx, w_val, r_idx, r_val, x, gamma, init_slot, init_mass, m
     f = np.float64
     x = np.asarray(x, dtype=f)
     B, H, T, C = x.shape
-    S = np.array(init_slot, dtype=f).reshape(B * H, -1, C)
+    S = np.asarray(init_slot, dtype=f).copy().reshape(B * H, -1, C)
     A = S.shape[1]
-    M = np.array(init_mass, dtype=f).reshape(B * H, A)
+    M = np.asarray(init_mass, dtype=f).copy().reshape(B * H, A)
     g = np.asarray(gamma, dtype=f).reshape(B * H, T)
     xs = x.reshape(B * H, T, C)
     wi = np.asarray(w_idx, dtype=np.int64).reshape(B * H, -1, T)
@@ -264,9 +264,9 @@ def sparse_gsu_backward_f64(w_idx, w_val, r_idx, r_val, x, gamma, init_slot, ini
     f = np.float64
     x = np.asarray(x, dtype=f)
     B, H, T, C = x.shape
-    S = np.array(init_slot, dtype=f).reshape(B * H, -1, C)
+    S = np.asarray(init_slot, dtype=f).copy().reshape(B * H, -1, C)
     A = S.shape[1]
-    M = np.array(init_mass, dtype=f).reshape(B * H, A)
+    M = np.asarray(init_mass, dtype=f).copy().reshape(B * H, A)
     g = np.asarray(gamma, dtype=f).reshape(B * H, T)
     xs = x.reshape(B * H, T, C)
     dys = np.asarray(grad_y, dtype=f).reshape(B * H, T, C)
@@ -305,8 +305,8 @@ def sparse_gsu_backward_f64(w_idx, w_val, r_idx, r_val, x, gamma, init_slot, ini
             S[rows, a] = s + gain[:, None] * delta[t, k]
         m_read[t] = M[rows[:, None], ri[:, :, t]].T
     # reverse: S holds the final state and is rolled back token by token
-    Ds = np.zeros_like(S) if grad_slot is None else np.array(grad_slot, dtype=f).reshape(B * H, A, C)
-    Dm = np.zeros_like(M) if grad_mass is None else np.array(grad_mass, dtype=f).reshape(B * H, A)
+    Ds = np.zeros_like(S) if grad_slot is None else np.asarray(grad_slot, dtype=f).copy().reshape(B * H, A, C)
+    Dm = np.zeros_like(M) if grad_mass is None else np.asarray(grad_mass, dtype=f).copy().reshape(B * H, A)
     d_w = np.zeros((B * H, Kw, T), dtype=f)
     d_r = np.zeros((B * H, Kr, T), dtype=f)
     d_x = np.zeros((B * H, T, C), dtype=f)
