@@ -284,9 +284,10 @@ struct MassLanes {
     bool on[MP];   // whether it is a real event
     bool act[MP];  // whether it acts: a real event, or a stand-in for the half's last event lane
     int es[MP];    // the event it stores (lanes past max(Kw, Kr) repeat the last one's store)
+    bool wl;       // a write lane (else a read lane)
     __device__ MassLanes(int lane, int Kw, int Kr) {
         const int hl = lane % HALF;
-        const bool wl = (lane / HALF) % 2 == 0;
+        wl = (lane / HALF) % 2 == 0;
         const int ek = max(Kw, Kr);
 #pragma unroll
         for (int p = 0; p < MP; ++p) {
@@ -305,8 +306,10 @@ struct MassRecs {
     int4 w[MP][CH];
     int2 r[MP][CH];
 };
-// The chunk's records from token t0 on: write records for every lane, and
-// read records too unless WONLY.
+// The chunk's records from token t0 on: WONLY, the write record in every
+// lane; else one 16-byte load per lane and token, the write record in the
+// write lanes (c.w) and, in the read lanes, the aligned pair of read records
+// holding token t's (c.r; t_pad is even and the rows 16-byte aligned).
 template<bool WONLY, int MP, int CH, int HALF>
 __device__ __forceinline__ void mass_fetch(const MassLanes<MP, HALF> &ln, const WriteRec *gw, const ReadRec *gr, int t_pad,
                                            int t0, MassRecs<MP, CH> &c) {
@@ -315,9 +318,16 @@ __device__ __forceinline__ void mass_fetch(const MassLanes<MP, HALF> &ln, const 
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
             const int t = min(t0 + j, t_pad - 1);
-            c.w[p][j] = *reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ln.evw[p]) * t_pad + t);
-            if constexpr (!WONLY)
-                c.r[p][j] = *reinterpret_cast<const int2 *>(gr + static_cast<int64_t>(ln.evr[p]) * t_pad + t);
+            const WriteRec *pw = gw + static_cast<int64_t>(ln.evw[p]) * t_pad + t;
+            if constexpr (WONLY) {
+                c.w[p][j] = *reinterpret_cast<const int4 *>(pw);
+            } else {
+                const ReadRec *pr = gr + static_cast<int64_t>(ln.evr[p]) * t_pad + (t & ~1);
+                const int4 q = *reinterpret_cast<const int4 *>(ln.wl ? static_cast<const void *>(pw)
+                                                                     : static_cast<const void *>(pr));
+                c.w[p][j] = q;
+                c.r[p][j] = (t & 1) ? make_int2(q.z, q.w) : make_int2(q.x, q.y);
+            }
         }
 }
 
