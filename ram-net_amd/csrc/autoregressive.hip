@@ -64,6 +64,14 @@ __device__ __forceinline__ void lane_event(float v, int c, bool inactive, int K,
     o = o < 0 ? o + A : o;
     slot = li < K ? o : 0;
     val = li < K && !inactive ? expf(v - re_norm * lse) : 0.f;
+    // Hide from the optimiser that slot and weight are 0 on lanes past K.
+    // Later stages read event 0 with v_readlane on exactly those lanes
+    // (`lane < Kw ? own slot : event 0's slot`); hipcc 7.2 turned that select
+    // into a branch over the lanes past Kw, rebuilt the slot there as the
+    // constant 0 and read lane 0 of it, so those lanes stored event 0's mass
+    // into slot 0. The barrier is volatile so that it stays here, where every
+    // lane executes it.
+    asm volatile("" : "+v"(slot), "+v"(val));
 }
 
 // Value of `v` on lane L (L uniform; a constant after unrolling), as a

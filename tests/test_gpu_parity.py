@@ -371,7 +371,7 @@ def test_api_matches_dense_reference(re_norm):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mass_aware", [False, True])
-@pytest.mark.parametrize("U,P,K", [(2, 32, 8), (2, 4, 16), (3, 16, 16), (5, 4, 32)])
+@pytest.mark.parametrize("U,P,K", [(2, 32, 8), (2, 4, 16), (3, 16, 16), (5, 4, 32), (2, 32, 64), (5, 4, 128)])
 def test_decode_step_matches_oracle(U, P, K, mass_aware, dtype):
     ops = _ops()
     print(f"decode case U={U} P={P} K={K} mass_aware={mass_aware} {dtype}", flush=True)
@@ -407,6 +407,47 @@ def test_decode_step_matches_oracle(U, P, K, mass_aware, dtype):
     assert oracle.rel_err(m_gpu.cpu(), rmass) <= FP32_TOL
     err = oracle.rel_err(y.cpu(), torch.as_tensor(ry)[:, :, 0])
     assert err <= _out_tol(dtype), f"decode y rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("C", [64, 128, 256])
+@pytest.mark.parametrize("U,P,Kw,Kr", [(2, 4, 4, 12), (2, 4, 12, 4), (2, 32, 8, 16), (2, 32, 16, 8), (2, 64, 3, 5),
+                                       (2, 64, 8, 4), (2, 16, 12, 12)])
+def test_decode_step_unequal_top_k(U, P, Kw, Kr, C, dtype):
+    """One decode step with Kw != Kr (or top-k below the kernel's event
+    count) on the fast kernels that search each address over the whole wave
+    (P > 32, or staircases of more than 32 candidates). Lanes past Kw repeat
+    event 0's mass store; a build whose compiler folded that repeat's slot to
+    0 stored event 0's mass into slot 0, so every slot's mass and row, and y,
+    are compared with the fp64 event loop."""
+    ops = _ops()
+    print(f"decode step U={U} P={P} Kw={Kw} Kr={Kr} C={C} {dtype}", flush=True)
+    B, H = 3, 2
+    A = P ** U
+    g = torch.Generator().manual_seed(U * 1000 + P * 10 + Kw + 3 * Kr + C)
+    w = torch.randn(B, H, U, P, generator=g).to(dtype)
+    r = torch.randn(B, H, U, P, generator=g).to(dtype)
+    x = torch.randn(B, H, C, generator=g).to(dtype)
+    gamma = torch.sigmoid(torch.randn(B, H, generator=g)).to(dtype)
+    slot = 0.5 * torch.randn(B, H, A, C, generator=g)
+    mass = torch.rand(B, H, A, generator=g) + 0.1
+    pos = torch.randint(0, 8192, (B,), generator=g)
+    s_gpu, m_gpu = slot.to(DEV), mass.to(DEV)
+    y = ops.topk_autoregressive_(w.to(DEV), r.to(DEV), x.to(DEV), gamma.to(DEV), s_gpu, m_gpu, None, 1,
+                                 pos.to(DEV), Kw, Kr, 0.0, 0.0, False, 1e-12)
+    torch.cuda.synchronize()
+    events = []
+    for lg, K in ((w, Kw), (r, Kr)):
+        idx, val = ops.topk_addr_single_forward(lg.unsqueeze(-1).to(DEV), 1, A, pos.view(B, 1).to(DEV), K, 0.0,
+                                                False, True)
+        oracle.check_topk_indices(idx.cpu(), lg.unsqueeze(-1), 1, pos.view(B, 1), K)
+        events += [idx.cpu(), val.cpu()]
+    wi, wv, ri, rv = events
+    ry, rslot, rmass = oracle.sparse_gsu_f64(wi, wv, ri, rv, x.double().unsqueeze(2), gamma.double().unsqueeze(-1),
+                                             slot, mass, None, False, 1e-12)
+    assert oracle.rel_err(m_gpu.cpu(), rmass) <= FP32_TOL, "mass state after the step"
+    assert oracle.rel_err(s_gpu.cpu(), rslot) <= FP32_TOL, "slot state after the step"
+    assert oracle.rel_err(y.cpu(), torch.as_tensor(ry)[:, :, 0]) <= _out_tol(dtype)
 
 
 @pytest.mark.parametrize("mass_aware", [False, True])

@@ -44,6 +44,8 @@ EPS = 1e-12
 # U, P, C, T (reference SHAPE_CASES: partial template widths and a long sequence)
 SHAPE_CASES = ((4, 3, 29, 1024), (4, 5, 47, 33), (4, 7, 65, 128), (5, 4, 32, 1024))
 TOP_K_RE_NORM_SETTINGS = ((0.0, 0.0), (1.0, 1.0), (0.25, 0.75), (0.75, 0.25))
+# reference ram_attention_helpers.py:14
+TOP_K_SETTINGS = ((4, 4), (8, 8), (4, 12), (16, 16), (32, 32), (64, 64), (128, 128))
 
 
 @dataclass(frozen=True)
@@ -294,3 +296,36 @@ def test_inplace_forms_match_dense_oracle(op, mass_aware):
     ref = run_oracle(case, re_norm=re_norm, mass_aware=mass_aware, grad=False, dense=True)
     assert not torch.equal(got[0][1], case.init_slot), "the state was not updated in place"
     assert_pairs(op, got, ref, case.mask, FP32_TOL)
+
+
+@pytest.mark.parametrize("top_k", TOP_K_SETTINGS, ids=lambda k: "K{}-{}".format(*k))
+def test_autoregressive_matches_parallel(top_k):
+    """Single-token decode steps (the fused decode op, one call per token,
+    state carried in place) == one parallel call, and == the fp64 event loop
+    on the decoder's selection, over the reference's top-K range at A = 1024
+    (order 5, radix 4), every re-norm setting and mass_aware, without and
+    with per-row masks (reference test_ram_attention_behavior.py:90-109).
+    fp32 rel <= 1e-5; masked tokens read exactly 0 in both paths."""
+    case = make_ram_case(batch=3, heads=4, order=5, channels=16, seq_len=65, masked=False, seed=31)
+    mask = torch.ones(3, 65, dtype=torch.bool)
+    mask[0, ::3] = False
+    mask[1, 1::4] = False
+    mask[2, 2::5] = False
+    mask[:, 7::16] = False
+    positions = (mask.long().cumsum(-1) - 1).masked_fill(~mask, 0)
+    masked = replace(case, mask=mask, position_ids=positions)
+    for re_norm in TOP_K_RE_NORM_SETTINGS:
+        for mass_aware in (False, True):
+            for name, inputs in (("plain", case), ("masked", masked)):
+                label = f"AR == PARALLEL top_k={top_k} re_norm={re_norm} mass_aware={mass_aware} {name}"
+                print(label, flush=True)
+                ar, _ = run_gpu(inputs, top_k=top_k, re_norm=re_norm, mass_aware=mass_aware, chunk=1, grad=False)
+                par, _ = run_gpu(inputs, top_k=top_k, re_norm=re_norm, mass_aware=mass_aware, grad=False)
+                ref, _ = run_oracle(inputs, top_k=top_k, re_norm=re_norm, mass_aware=mass_aware, grad=False)
+                for what, other in (("parallel", par), ("fp64 event loop", ref)):
+                    for tname, a, b in zip(("y", "slot", "mass"), ar, other):
+                        err = oracle.rel_err(a, b)
+                        assert err <= FP32_TOL, f"{label}: {tname} vs {what} rel err {err:.3e}"
+                if inputs.mask is not None:
+                    off = ~inputs.mask[:, None, :, None].expand_as(ar[0])
+                    assert bool((ar[0][off] == 0).all()), f"{label}: masked tokens must read 0"
