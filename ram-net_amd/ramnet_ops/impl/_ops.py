@@ -63,6 +63,17 @@ def _check_slots(op: str, U: int, P: int, A: int) -> None:
         raise RuntimeError(f"{op}: the slot count A={A} must equal P**U = {P}**{U}")
 
 
+def _check_decode_dtypes(op: str, w_addr: Tensor, r_addr: Tensor, x: Tensor) -> None:
+    """The decode kernels read the logits in x's dtype, as the reference
+    requires (check_address with x's scalar type,
+    ram_attn_topk_autoregressive.cu:32-34,216): logits of another dtype
+    raise RuntimeError before any launch."""
+    _code(x)
+    for name, t in (("w_addr", w_addr), ("r_addr", r_addr)):
+        if t.dtype != x.dtype:
+            raise RuntimeError(f"{op}: Tensor {name} dtype mismatch: expect {x.dtype}, but got {t.dtype}")
+
+
 def _require_given(name: str, **tensors: Tensor) -> None:
     """Required tensor arguments (the dispatcher passes None through to a
     Python operator); the reference's native checks raise RuntimeError."""
@@ -514,6 +525,7 @@ def topk_autoregressive_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma: Tenso
                   slot=(slot, (B, H, A, C)), mass=(mass, (B, H, A)), position_ids=(position_ids, (B,)),
                   mask=(None if mask is None or mask.numel() == 0 else mask, (B,)))
     _require_state(op, slot, mass)
+    _check_decode_dtypes(op, w_addr, r_addr, x)
     w_addr, r_addr, x = w_addr.contiguous(), r_addr.contiguous(), x.contiguous()
     gamma = gamma.to(dtype=x.dtype).contiguous()
     pos = position_ids.to(device=x.device, dtype=torch.int32).contiguous()
@@ -553,6 +565,7 @@ def topk_autoregressive_steps_(w_addr: Tensor, r_addr: Tensor, x: Tensor, gamma:
                   slot=(slot, (B, H, A, C)), mass=(mass, (B, H, A)), position_ids=(position_ids, (S, B)),
                   mask=(None if mask is None or mask.numel() == 0 else mask, (S, B)))
     _require_state(op, slot, mass)
+    _check_decode_dtypes(op, w_addr, r_addr, x)
     w_addr, r_addr, x = w_addr.contiguous(), r_addr.contiguous(), x.contiguous()
     gamma = gamma.to(dtype=x.dtype).contiguous()
     pos = position_ids.to(device=x.device, dtype=torch.int32).contiguous()

@@ -105,3 +105,29 @@ def test_fused_and_decode_ops_reject_mis_shaped_tensors():
         w_, r_, x_, g_, s_, m_, mk, p_ = args
         _raises(ops.topk_autoregressive_, w_, r_, x_, g_, s_.clone(), m_.clone(), mk, 0, p_, K, K, 0.0, 0.0, False,
                 1e-12)
+
+
+def test_decode_ops_reject_logits_of_another_dtype():
+    """The decode kernels read the logits in x's dtype: bf16 or fp16 logits
+    with fp32 values (or the other way round) raise RuntimeError before any
+    launch, as the reference's check_address does
+    (ram_attn_topk_autoregressive.cu:32-34,216)."""
+    ops = _ops()
+    S = 3
+    slot, mass = _t(B, H, A, C), _t(B, H, A)
+    empty = torch.empty(0, dtype=torch.bool, device=DEV)
+    for xd, ld in ((torch.float32, torch.bfloat16), (torch.float32, torch.float16), (torch.bfloat16, torch.float32)):
+        x, g = _t(B, H, C, dtype=xd), _t(B, H, dtype=xd)
+        good, bad = _t(B, H, U, P, dtype=xd), _t(B, H, U, P, dtype=ld)
+        pd = _t(B, dtype=torch.int32)
+        for w_, r_ in ((bad, good), (good, bad), (bad, bad)):
+            with pytest.raises(RuntimeError, match="dtype mismatch"):
+                ops.topk_autoregressive_(w_, r_, x, g, slot.clone(), mass.clone(), empty, 0, pd, K, K, 0.0, 0.0,
+                                         False, 1e-12)
+        xs, gs = _t(S, B, H, C, dtype=xd), _t(S, B, H, dtype=xd)
+        gs_, bs_ = _t(S, B, H, U, P, dtype=xd), _t(S, B, H, U, P, dtype=ld)
+        ps = _t(S, B, dtype=torch.int32)
+        for w_, r_ in ((bs_, gs_), (gs_, bs_)):
+            with pytest.raises(RuntimeError, match="dtype mismatch"):
+                ops.topk_autoregressive_steps_(w_, r_, xs, gs, slot.clone(), mass.clone(), empty, 0, ps, K, K, 0.0,
+                                               0.0, False, 1e-12)
