@@ -256,8 +256,9 @@ int ramnet_topk_autoregressive_steps_(const void *w_addr, const void *r_addr, co
                                       float w_re_norm, float r_re_norm, int mass_aware, float eps, void *y,
                                       void *stream);
 
-/* Bytes of the per-GPU scratch of ramnet_ram_attn_forward_noalloc (128 MiB). */
-#define RAMNET_NOALLOC_SCRATCH_BYTES (128LL << 20)
+/* Bytes of the per-GPU scratch of ramnet_ram_attn_forward_noalloc (192 MiB:
+ * config 2, B=8 H=16 T=4096 K=8 in the precomputed-gain form, needs 160 MiB). */
+#define RAMNET_NOALLOC_SCRATCH_BYTES (192LL << 20)
 
 /*
  * ramnet_ram_attn_forward without a workspace argument. No counterpart in
@@ -268,7 +269,10 @@ int ramnet_topk_autoregressive_steps_(const void *w_addr, const void *r_addr, co
  * library runs on, held until the process ends. A shape whose records
  * (B*H*T_pad*(16*w_top_k + 8*r_top_k) bytes, plus B*H*T_pad*16*max(w_top_k,
  * r_top_k) when the scan uses the precomputed-gain form) exceed it returns
- * RAMNET_EINVAL. Every call on one GPU shares that GPU's array: calls that
+ * RAMNET_EINVAL. The array is part of the library's device code: loading
+ * the library's code on a GPU reserves RAMNET_NOALLOC_SCRATCH_BYTES of that
+ * GPU's memory until the process ends, whether or not this entry point is
+ * ever called. Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, other threads) race, and the caller
  * must order them. Other arguments and results as ramnet_ram_attn_forward.
  */

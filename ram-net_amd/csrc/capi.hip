@@ -675,7 +675,7 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
     void *ws = nullptr;
     int64_t need = 0;
     // sizes the scan's own checks accept (anything else fails there first)
-    const bool plausible = B > 0 && H > 0 && T > 0 && C > 0 && A > 0 && A < kAddressLimit && w_top_k > 0 &&
+    const bool plausible = B > 0 && H > 0 && T >= 0 && C > 0 && A > 0 && A < kAddressLimit && w_top_k > 0 &&
                            r_top_k > 0 && w_top_k <= A && r_top_k <= A && valid_dtype(dtype) &&
                            fits_int({B * H * A * C, B * H * (A + 2), B * H * T * C,
                                      B * H * (T + ramnet::kScanPad) * (w_top_k + r_top_k)});
@@ -684,7 +684,7 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
         RAMNET_REQUIRE(ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T),
                                             static_cast<int>(A), static_cast<int>(C), static_cast<int>(w_top_k),
                                             static_cast<int>(r_top_k), dtype, nullptr, nullptr, &pre),
-                       "segment forward: shape outside the LDS-resident scan (A <= 40958 and top_k <= 128)");
+                       "ram_attn_forward_noalloc: shape outside the LDS-resident scan (A <= 40958 and top_k <= 128)");
         // the decoder records, then the gain records if the launch uses them
         need = ramnet::scan_record_bytes(B, H, T, w_top_k, r_top_k) +
                (pre ? ramnet::scan_gain_bytes(B, H, T, w_top_k, r_top_k) : 0);
@@ -693,6 +693,8 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
                                            " bytes of records, more than the " +
                                            std::to_string(static_cast<long long>(RAMNET_NOALLOC_SCRATCH_BYTES)) +
                                            "-byte scratch; use ramnet_ram_attn_forward with a workspace");
+        // T == 0 reads no records, but the launch still takes the scratch as
+        // its workspace (the precomputed-gain form refuses a null one)
         if (int rc = scratch_address(&ws))
             return rc;
     }

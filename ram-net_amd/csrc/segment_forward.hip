@@ -31,6 +31,7 @@
 #include "segment_scan.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 
@@ -48,17 +49,27 @@ int pow2_ceil(int x) {
     return p;
 }
 
+// CU count of the current device, looked up once per device. Concurrent
+// first calls may both query the runtime; they store the same value.
+constexpr int kCuCacheDevices = 64;
+std::atomic<int> g_cu_count[kCuCacheDevices];
+
 int cu_count() {
-    static int cached = 0;
-    if (cached == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-            cached = n;
-        else
-            cached = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+        return 256;
+    const bool cacheable = dev < kCuCacheDevices;
+    if (cacheable) {
+        const int c = g_cu_count[dev].load(std::memory_order_relaxed);
+        if (c > 0)
+            return c;
     }
-    return cached;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    if (cacheable)
+        g_cu_count[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 int dtype_bytes(int dtype) { return dtype == kF32 ? 4 : 2; }
@@ -767,6 +778,15 @@ hipError_t launch_pack_records(const PackJob &job, hipStream_t stream, const cha
     }
 }
 
+namespace {
+// dst = src over n floats: the state copy of a call without tokens.
+__global__ __launch_bounds__(256) void state_copy_kernel(float *dst, const float *src, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n)
+        dst[i] = src[i];
+}
+}  // namespace
+
 // RAMNET_SCAN_LAYOUT="vec,epp,np,nw[,pre]" replaces the planner's choice (tests
 // sweep every compiled layout with it; also a tuning knob). The layout must
 // be compiled, cover max(Kw, Kr) events and fit in LDS.
@@ -833,6 +853,17 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     Plan p{};
     if (!pick_plan(job, &p, why))
         return hipErrorInvalidValue;
+    if (job.T == 0) {
+        // no events: the final state is the initial state (a kernel, not a
+        // copy, so that callers may capture the call in a graph)
+        const int64_t ns = static_cast<int64_t>(job.B) * job.H * job.A;
+        if (job.slot_out != job.init_slot)
+            hipLaunchKernelGGL(state_copy_kernel, dim3(static_cast<unsigned>((ns * job.C + 255) / 256)), dim3(256), 0,
+                               stream, job.slot_out, job.init_slot, ns * job.C);
+        hipLaunchKernelGGL(state_copy_kernel, dim3(static_cast<unsigned>((ns + 255) / 256)), dim3(256), 0, stream,
+                           job.mass_out, job.init_mass, ns);
+        return hipGetLastError();
+    }
     if (p.pre && !job.gain) {
         *why = "segment forward: the precomputed-gain layout needs the gain records of the scan workspace";
         return hipErrorInvalidValue;

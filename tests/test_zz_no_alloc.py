@@ -6,8 +6,11 @@ same kernels with a caller workspace) on the same inputs: outputs and post
 state must be identical bits. Two calls in a row, the second on a smaller
 input (the scratch keeps the first call's records, which the second must not
 read), then a slot space wide enough for the precomputed-gain form (whose
-gain records also live in the scratch), and a shape beyond the scratch, which
-is refused on the host before anything is launched.
+gain records also live in the scratch), the full config-2 shape (which plans
+the precomputed-gain form and needs 160 MiB of the 192 MiB scratch), calls
+without tokens or without batch rows, one call captured in a HIP graph and
+replayed on fresh inputs, and a shape beyond the scratch, which is refused
+on the host before anything is launched.
 """
 from __future__ import annotations
 
@@ -28,13 +31,17 @@ def _nat():
     return _native
 
 
-def _run(nat, case, K, E, re_norm, mass_aware, noalloc):
-    d = case.to(DEV)
-    B, H, U, P, T, C = case.shape
+def _launch(nat, d, U, P, K, E, re_norm, mass_aware, noalloc, out=None):
+    """One forward call on device inputs ``d`` (a case already on the GPU);
+    returns (y, slot, mass), written into ``out`` if given."""
+    B, H, _, _, T = d.w_addr.shape
+    C = d.values.shape[-1]
     A = P ** U
     pos = d.position_ids.to(torch.int32).contiguous()
     mask = None if d.mask is None else d.mask.to(torch.uint8).contiguous()
-    slot, mass, y = torch.empty_like(d.init_slot), torch.empty_like(d.init_mass), torch.empty_like(d.values)
+    if out is None:
+        out = (torch.empty_like(d.values), torch.empty_like(d.init_slot), torch.empty_like(d.init_mass))
+    y, slot, mass = out
     code = nat.DTYPE_CODES[d.values.dtype]
     stream = torch.cuda.current_stream().cuda_stream
     args = [d.w_addr.data_ptr(), d.r_addr.data_ptr(), d.values.data_ptr(), d.gamma.data_ptr(), code, nat.ptr(mask), E,
@@ -43,10 +50,16 @@ def _run(nat, case, K, E, re_norm, mass_aware, noalloc):
     if noalloc:
         nat.call("ramnet_ram_attn_forward_noalloc", *args, stream)
     else:
-        ws = torch.empty(nat.scan_workspace_bytes(B, H, T, *K), dtype=torch.uint8, device=DEV)
+        ws = torch.empty(max(1, nat.scan_workspace_bytes(B, H, T, *K)), dtype=torch.uint8, device=DEV)
         nat.call("ramnet_ram_attn_forward", *args, ws.data_ptr(), ws.numel(), stream)
+    return out
+
+
+def _run(nat, case, K, E, re_norm, mass_aware, noalloc):
+    U, P = case.shape[2], case.shape[3]
+    out = _launch(nat, case.to(DEV), U, P, K, E, re_norm, mass_aware, noalloc)
     torch.cuda.synchronize()
-    return y.cpu(), slot.cpu(), mass.cpu()
+    return tuple(t.cpu() for t in out)
 
 
 def _same(nat, case, K, E, re_norm, mass_aware, label):
@@ -75,8 +88,80 @@ def test_noalloc_precomputed_gain_form(monkeypatch):
     _same(nat, case, (8, 8), 1, (0.0, 0.0), True, "precomputed-gain form: A=4096 T=700")
 
 
+def test_noalloc_config2_shape():
+    """Config 2 (B=8, H=16, T=4096, A=1024, K=8, bf16, CAPE on half the
+    heads, zero initial state) plans the precomputed-gain form: 96 MiB of
+    decoder records plus 64 MiB of gain records in the scratch."""
+    nat = _nat()
+    B, H, U, P, T, C, K, E = 8, 16, 2, 32, 4096, 128, 8, 8
+    A = P ** U
+    assert nat.segment_plan(B, H, A, C, K, K, torch.bfloat16)[2]
+    g = torch.Generator(device=DEV).manual_seed(84)
+    bf = dict(device=DEV, dtype=torch.bfloat16)
+    from ram_cases import RamCase
+    d = RamCase(torch.randn(B, H, U, P, T, generator=g, **bf), torch.randn(B, H, U, P, T, generator=g, **bf),
+                torch.randn(B, H, T, C, generator=g, **bf),
+                torch.sigmoid(torch.randn(B, H, T, generator=g, device=DEV) - 1).to(torch.bfloat16),
+                torch.zeros(B, H, A, C, device=DEV), torch.full((B, H, A), 1.0 / A, device=DEV),
+                torch.arange(T, device=DEV).view(1, T).expand(B, T).contiguous(), None)
+    print("no-allocation forward: config 2, B=8 H=16 T=4096 A=1024 K=8 bf16", flush=True)
+    got = _launch(nat, d, U, P, (K, K), E, (0.0, 0.0), False, True)
+    want = _launch(nat, d, U, P, (K, K), E, (0.0, 0.0), False, False)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("y", "slot", "mass"), got, want):
+        assert torch.equal(a, b), f"config 2: {name} differs from ramnet_ram_attn_forward"
+    assert bool(torch.isfinite(got[0]).all()) and float(got[1].abs().max()) > 0
+
+
+def test_noalloc_empty_calls():
+    """No tokens: the post state is a copy of the initial state, in both scan
+    forms (A = 32768 takes the precomputed-gain form in slot ranges). No
+    batch rows: nothing to do, and the call succeeds as the workspace entry
+    point does."""
+    nat = _nat()
+    for (U, P, C, K) in ((2, 16, 24, (4, 4)), (3, 32, 16, (8, 8))):
+        case = make_case(B=2, H=3, U=U, P=P, T=0, C=C, dtype=torch.bfloat16, seed=85)
+        print(f"no-allocation forward: T=0, A={P ** U}", flush=True)
+        for noalloc in (True, False):
+            y, slot, mass = _run(nat, case, K, 1, (0.0, 0.0), False, noalloc)
+            assert y.numel() == 0
+            assert torch.equal(slot, case.init_slot) and torch.equal(mass, case.init_mass)
+    case = make_case(B=0, H=2, U=2, P=4, T=40, C=8, seed=86)
+    print("no-allocation forward: B=0", flush=True)
+    y, slot, mass = _run(nat, case, (4, 4), 0, (0.0, 0.0), False, True)
+    assert y.numel() == slot.numel() == mass.numel() == 0
+
+
+def test_noalloc_graph_capture_replays():
+    """One call captured in a HIP graph (the library allocates nothing and
+    issues no memset), replayed three times on fresh inputs written into the
+    captured tensors, with eager work and a synchronisation between the
+    replays: every replay is bit-equal to the workspace entry point's eager
+    call on the same inputs."""
+    nat = _nat()
+    B, H, U, P, T, C, K = 2, 4, 2, 16, 300, 64, (8, 8)
+    static = make_case(B=B, H=H, U=U, P=P, T=T, C=C, dtype=torch.bfloat16, seed=87, masked=True).to(DEV)
+    out = (torch.empty_like(static.values), torch.empty_like(static.init_slot), torch.empty_like(static.init_mass))
+    _launch(nat, static, U, P, K, 2, (0.0, 0.0), False, True, out)  # first call on the device: scratch lookup
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _launch(nat, static, U, P, K, 2, (0.0, 0.0), False, True, out)
+    for rep in range(3):
+        print(f"no-allocation forward: graph replay {rep}", flush=True)
+        fresh = make_case(B=B, H=H, U=U, P=P, T=T, C=C, dtype=torch.bfloat16, seed=88 + rep, masked=True).to(DEV)
+        for name in ("w_addr", "r_addr", "values", "gamma", "init_slot", "init_mass", "position_ids", "mask"):
+            getattr(static, name).copy_(getattr(fresh, name))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _launch(nat, fresh, U, P, K, 2, (0.0, 0.0), False, False)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("y", "slot", "mass"), out, want):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from the eager workspace call"
+
+
 def test_noalloc_refuses_shapes_beyond_the_scratch():
-    """Records of B=8, H=16, T=16384, K=8 need 403 MB, more than the 128 MiB
+    """Records of B=8, H=16, T=16384, K=8 need 671 MB, more than the 192 MiB
     scratch: refused with a message before any launch (the pointers are
     never dereferenced)."""
     nat = _nat()
@@ -87,4 +172,4 @@ def test_noalloc_refuses_shapes_beyond_the_scratch():
     rc = nat.lib().ramnet_ram_attn_forward_noalloc(*args)
     assert rc == nat.RAMNET_EINVAL
     msg = nat.lib().ramnet_last_error().decode()
-    assert "scratch" in msg and str(128 << 20) in msg, msg
+    assert "scratch" in msg and str(192 << 20) in msg, msg
