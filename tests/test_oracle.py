@@ -121,6 +121,31 @@ def test_index_checker_rejects_a_planted_mistake():
         oracle.check_topk_indices(bad, case.w_addr, 1, case.position_ids, 4)
 
 
+@pytest.mark.parametrize("t_chunk", [1, 5, 256])
+def test_index_checker_rejects_mistakes_in_any_time_chunk(t_chunk):
+    """The checker walks tokens in chunks: a wrong slot, a duplicated slot
+    and an index outside its head's range are caught whichever chunk holds
+    them, on CAPE and plain heads."""
+    case = make_case(2, 2, 2, 8, 17, 4, seed=22)
+    pos = case.position_ids * 3 + 5  # CAPE shifts beyond A
+    idx, _ = oracle.dense_topk_addr(case.w_addr, 1, pos, 4)
+    st = oracle.check_topk_indices(idx, case.w_addr, 1, pos, 4, t_chunk=t_chunk)
+    assert st["addresses"] == 2 * 2 * 17
+    _, order = oracle.topk_f64(case.w_addr, 64)
+    for b, h, t in ((0, 0, 0), (1, 1, 16), (1, 0, 9)):
+        base = (b * 2 + h) * 64
+        shift = int(pos[b, t]) if h < 1 else 0
+        wrong = idx.clone()
+        wrong[b, h, 2, t] = base + (int(order[b, h, t, 50]) - shift) % 64  # the 51st-ranked slot
+        dup = idx.clone()
+        dup[b, h, 3, t] = dup[b, h, 0, t]
+        out = idx.clone()
+        out[b, h, 1, t] = base + 64 if (b, h) != (1, 1) else base - 1
+        for bad in (wrong, dup, out):
+            with pytest.raises(AssertionError):
+                oracle.check_topk_indices(bad, case.w_addr, 1, pos, 4, t_chunk=t_chunk)
+
+
 def test_index_checker_exempts_exact_ties():
     addr = torch.zeros(1, 1, 2, 4, 2)  # all 16 slots tie
     idx = torch.tensor([[[[15, 3], [2, 7], [9, 1], [4, 0]]]], dtype=torch.int32)
