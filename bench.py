@@ -13,9 +13,13 @@ of ``topk_autoregressive_steps_``) under ``decode.multi_step``. Timings give
 the median, min and max over repetitions. Config 1 (fp32, one fused forward
 call) is reported under ``config1``.
 
-``roofline`` is for the dominant kernel (the segment scan): algorithmic bytes
-of the event model per launch / the kernel's average duration measured with
-HIP events on the stream it runs on. ``cpu_baseline`` times the CPU
+``roofline`` is for the dominant stage (the segment stage: mass pre-pass and
+segment scan, one C-ABI call), timed with HIP events on the stream it runs
+on: ``achieved`` / ``frac`` are its counter-measured HBM bytes per call
+(rocprofv3, ``--traffic-summary``) over that time against the HBM peak;
+``bound`` names what binds it (LDS: the slot state stays on chip), with the
+slot-row bytes it moves through LDS priced against an LDS read peak measured
+in the same run, and the event ("active state") model's figure beside them. ``cpu_baseline`` times the CPU
 restatement of the reference's dense PyTorch algorithm on a bounded sample of
 the same config-2 inputs (rank 0, N=1 only); ``cpu_baselines`` does the same
 for config 1 (in full), config 3 (32 consecutive decode steps) and config 4
@@ -24,6 +28,7 @@ for config 1 (in full), config 3 (32 consecutive decode steps) and config 4
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S]
        [--no-cpu-baseline] [--no-stress] [--no-lm] [--lm-tokens N]
        [--only prefill|decode|stress|lm|train] [--no-train] [--copy-probe MIB]
+       [--traffic-summary DIR]
 
 Config 4 (B=4, H=8, T=8192, U=3, P=16 -> A=4096, K=16) and its tie-heavy
 variant (decoder logits quantised to multiples of 0.25) are timed the same
@@ -39,6 +44,8 @@ it is the calibration kernel of known traffic for the byte counters.
 from __future__ import annotations
 
 import argparse
+import csv
+import hashlib
 import json
 import os
 import platform
@@ -53,9 +60,15 @@ for _p in (os.path.join(REPO, "ram-net_amd"), REPO, os.path.join(REPO, "tests"))
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
-# Calibrated HBM bytes per segment-scan dispatch at config 2, from the
-# rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in profiles/.
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "segment_scan_traffic_c2.json")
+# Counter-measured HBM bytes per call of the prefill stages at configs 2 and
+# 4: rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this script, calibrated on
+# a copy of known size and written by `bench.py --traffic-summary DIR`. The
+# file records a digest of the kernel sources it was measured with; a line
+# built from other sources reports it as stale.
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "segment_stage_traffic.json")
+TRAFFIC_SOURCES = ("segment_scan.hpp", "segment_forward.hip", "segment_scan_bf16.hip", "ramnet_kernels.hpp",
+                   "ramnet_device.hpp", "topk_addr.hip", "lane_search.hpp", "capi.hip")
+PROBE_LIB = os.path.join(REPO, "ram-net_amd", "ramnet_ops", "_lib", "libramnet_lds_probe.so")
 METRIC = "prefill tokens/s (T=4096) + decode tokens/s (B=64); % HBM roofline"
 
 # config 2 (prefill), config 3 (decode), config 4 (stress prefill; tie-heavy
@@ -74,6 +87,102 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def source_digest() -> str:
+    """Digest of the kernel sources the prefill traffic depends on."""
+    h = hashlib.sha256()
+    for name in TRAFFIC_SOURCES:
+        with open(os.path.join(REPO, "ram-net_amd", "csrc", name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
+def load_traffic() -> dict | None:
+    """The counter-measured traffic file, with ``current`` telling whether it
+    was measured on the kernel sources of this tree."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        tr = json.load(f)
+    tr["current"] = tr.get("source_digest") == source_digest()
+    return tr
+
+
+def lds_read_peak(dev, reps=5) -> dict | None:
+    """LDS read bandwidth of the whole GPU, measured live: a conflict-free
+    ds_read_b128 stream (csrc/lds_probe.hip), five workgroups of 256 threads
+    per CU, timed with HIP events on the stream it runs on; best of ``reps``."""
+    import ctypes
+    if not os.path.exists(PROBE_LIB):
+        return None
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.ramnet_lds_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.ramnet_lds_probe.restype = ctypes.c_int
+    lib.ramnet_lds_probe_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.ramnet_lds_probe_bytes.restype = ctypes.c_int64
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks, iters = 5 * n_cu, 4096
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    best = None
+    for _ in range(reps + 1):  # the first launch warms up
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rc = lib.ramnet_lds_probe(blocks, iters, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream))
+        e1.record()
+        torch.cuda.synchronize()
+        if rc != 0:
+            return None
+        ms = e0.elapsed_time(e1)
+        best = ms if best is None else min(best, ms)
+    nbytes = lib.ramnet_lds_probe_bytes(blocks, iters)
+    return {"gbs": nbytes / (best / 1e3) / 1e9, "cus": n_cu, "bytes": nbytes, "ms": best,
+            "kernel": "lds_read_probe_kernel (ds_read_b128, no bank conflicts)"}
+
+
+def traffic_summary(out_dir: str) -> int:
+    """Write TRAFFIC_FILE from rocprofv3 runs in ``out_dir``: for w in
+    (prefill, stress), ``<w>_trace`` (--kernel-trace --stats) and
+    ``<w>_FETCH_SIZE`` / ``<w>_WRITE_SIZE`` (--pmc) of ``bench.py --only <w>
+    --copy-probe 1024``. FETCH_SIZE and WRITE_SIZE (KiB per dispatch,
+    medians) are scaled by what they read for the 1 GiB copy."""
+    import statistics
+    stage_names = ("segment_scan_kernel", "segment_mass_kernel", "mass_chunk_map_kernel", "mass_chunk_scan_kernel")
+
+    def counters(path):
+        vals = {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return {k: statistics.median(v) for k, v in vals.items()}
+
+    res = {"source_digest": source_digest(), "unit": "bytes per call", "configs": {}}
+    for w, name in (("prefill", "config2"), ("stress", "config4")):
+        fe = counters(os.path.join(out_dir, f"{w}_FETCH_SIZE", "run_counter_collection.csv"))
+        wr = counters(os.path.join(out_dir, f"{w}_WRITE_SIZE", "run_counter_collection.csv"))
+        fs = 1048576.0 / next(v for k, v in fe.items() if "copyBuffer" in k)
+        ws = 1048576.0 / next(v for k, v in wr.items() if "copyBuffer" in k)
+        with open(os.path.join(out_dir, f"{w}_trace", "run_kernel_stats.csv")) as f:
+            trace = {r["Name"]: float(r["AverageNs"]) / 1e3 for r in csv.DictReader(f)}
+        part = {"scan": 0.0, "prepass": 0.0, "decoder": 0.0}
+        times = {"scan": 0.0, "prepass": 0.0, "decoder": 0.0}
+        for k, v in fe.items():
+            which = ("scan" if "segment_scan_kernel" in k else "prepass" if any(n in k for n in stage_names)
+                     else "decoder" if "topk_addr" in k else None)
+            if which is None:
+                continue
+            part[which] += (v * fs + wr.get(k, 0.0) * ws) * 1024
+            times[which] += next((t for n, t in trace.items() if n == k), 0.0)
+        res["configs"][name] = {
+            "scan_bytes": part["scan"], "prepass_bytes": part["prepass"], "decoder_bytes": part["decoder"],
+            "stage_bytes": part["scan"] + part["prepass"], "step_bytes": sum(part.values()),
+            "scan_traced_us": times["scan"], "stage_traced_us": times["scan"] + times["prepass"],
+            "decoder_traced_us": times["decoder"], "fetch_scale": fs, "write_scale": ws}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res))
+    return 0
+
+
 def event_model_bytes(U, P, C, K, H, s_a=2) -> dict:
     """Algorithmic bytes per token-head of the event ("active state") model.
 
@@ -83,7 +192,10 @@ def event_model_bytes(U, P, C, K, H, s_a=2) -> dict:
     op = 2 * U * P * s_a + C * s_a + s_a + C * s_a + 4.0 / H + K * (2 * C * 4 + 2 * 4) + K * C * 4
     # the segment scan itself: decoded (idx, val) pairs instead of logits
     seg = op - 2 * U * P * s_a - 4.0 / H + 2 * K * 8
-    return {"op": op, "segment": seg}
+    # the slot rows the scan moves through LDS (its state stays there): each
+    # write loads and stores a row of C fp32, each read loads one
+    lds = K * 2 * C * 4 + K * C * 4
+    return {"op": op, "segment": seg, "lds_rows": lds}
 
 
 def make_prefill_inputs(dev, c=C2):
@@ -153,6 +265,10 @@ def bench_prefill(steps, warmup, dev, c=C2):
     n_th = B * H * T
     seg_bytes = per["segment"] * n_th + state_io
     op_bytes = per["op"] * n_th + state_io
+    # compulsory HBM bytes of a step: logits, x, gamma and positions read
+    # once, y written once, the zero initial state read and the final state
+    # written once
+    floor_bytes = (B * H * T * (2 * U * P * 2 + C * 2 + 2 + C * 2) + B * T * 4 + state_io)
     tokens = B * T
     return {
         "host": host,
@@ -165,6 +281,8 @@ def bench_prefill(steps, warmup, dev, c=C2):
         "segment_ms_stats": stats(seg_ms),
         "decoder_ms_stats": stats(dec_ms),
         "segment_bytes": seg_bytes,
+        "lds_row_bytes": per["lds_rows"] * n_th,
+        "floor_bytes": floor_bytes,
         "op_bytes": op_bytes,
         "op_roofline_frac": (op_bytes / (ms_per_step / 1e3)) / (HBM_PEAK_GBS * 1e9),
         "bytes_per_token_head": per,
@@ -588,7 +706,11 @@ def main(argv=None) -> int:
     ap.add_argument("--lm-tokens", type=int, default=C5["new"])
     ap.add_argument("--no-stress", action="store_true", help="skip the config-4 stress prefill lines")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB")
+    ap.add_argument("--traffic-summary", default=None, metavar="DIR",
+                    help="write the counter-measured traffic file from rocprofv3 runs in DIR, then exit")
     args = ap.parse_args(argv)
+    if args.traffic_summary:
+        return traffic_summary(args.traffic_summary)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the operator shards over (batch, head) "
@@ -618,6 +740,7 @@ def main(argv=None) -> int:
         pre = bench_prefill(args.steps, args.warmup, dev)
         log(f"prefill: {pre['ms_per_step']:.3f} ms/step, segment {pre['segment_ms']:.3f} ms, "
             f"decoder {pre['decoder_ms']:.3f} ms")
+    traffic = load_traffic()
     stress = {}
     stress_host = None
     if args.only == "stress" or (args.only is None and not args.no_stress):
@@ -637,9 +760,17 @@ def main(argv=None) -> int:
                 "tokens_per_s": st["tokens_per_s"], "ms_per_step": st["ms_per_step"],
                 "step_ms_stats": st["step_ms_stats"], "segment_ms_stats": st["segment_ms_stats"],
                 "decoder_ms": st["decoder_ms"], "segment_ms": st["segment_ms"],
-                "op_roofline_frac": st["op_roofline_frac"],
-                "segment_roofline_frac": seg_gbs / HBM_PEAK_GBS, "op_bytes_per_step": st["op_bytes"],
+                "event_model_op_frac": st["op_roofline_frac"],
+                "event_model_segment_frac": seg_gbs / HBM_PEAK_GBS, "op_bytes_per_step": st["op_bytes"],
+                "floor_bytes_per_step": st["floor_bytes"],
             }
+            tr = traffic.get("configs", {}).get("config4") if traffic and name == "config4" else None
+            if tr:
+                stress[name]["hbm_counter"] = {
+                    "stage_bytes": tr["stage_bytes"], "step_bytes": tr["step_bytes"],
+                    "stage_gbs": tr["stage_bytes"] / (st["segment_ms"] / 1e3) / 1e9,
+                    "stage_frac": tr["stage_bytes"] / (st["segment_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS,
+                    "step_vs_floor": tr["step_bytes"] / st["floor_bytes"], "current": traffic["current"]}
             log(f"stress: {name} {st['ms_per_step']:.3f} ms/step = {st['tokens_per_s'] / 1e6:.1f} M tokens/s, "
                 f"segment {st['segment_ms']:.3f} ms, decoder {st['decoder_ms']:.3f} ms")
     train = None
@@ -663,16 +794,13 @@ def main(argv=None) -> int:
         log(f"config 1: {c1['ms_per_call']['median']:.3f} ms per call")
 
     if pre is not None:
-        seg_gbs = pre["segment_bytes"] / (pre["segment_ms"] / 1e3) / 1e9
-        traffic = None
-        if os.path.exists(TRAFFIC_FILE):
-            with open(TRAFFIC_FILE) as f:
-                tr = json.load(f)
-            counter_gbs = tr["traffic_bytes"] / (pre["segment_ms"] / 1e3) / 1e9
-            traffic = {"bytes": tr["traffic_bytes"], "kernel": tr["kernel"],
-                       "scan_bytes": tr.get("scan_bytes"), "prepass_bytes": tr.get("prepass_bytes"),
-                       "counter_gbs": counter_gbs, "counter_frac": counter_gbs / HBM_PEAK_GBS,
-                       "source": "profiles/segment_scan_traffic_c2.json"}
+        seg_s = pre["segment_ms"] / 1e3
+        event_gbs = pre["segment_bytes"] / seg_s / 1e9
+        tr = traffic["configs"]["config2"] if traffic else None
+        hbm_bytes = tr["stage_bytes"] if tr else None
+        hbm_gbs = None if tr is None else hbm_bytes / seg_s / 1e9
+        lds_peak = lds_read_peak(dev)
+        lds_gbs = pre["lds_row_bytes"] / seg_s / 1e9
         out.update({
             "value": pre["tokens_per_s"],
             "unit": "tokens/s",
@@ -693,27 +821,46 @@ def main(argv=None) -> int:
                 "segment_length": 128,
             },
             "roofline": {
-                "bound": "hbm",
-                # the timed region is the whole segment stage (one C-ABI call):
-                # the mass pre-pass kernels, then segment_scan_kernel; the
-                # event model counts every row the ops touch in HBM, which the
-                # LDS-resident scan does not re-read, so frac can pass 1 (the
-                # counter-measured bytes are in traffic / traffic_detail)
+                # The dominant stage is the segment stage (one C-ABI call: the
+                # mass pre-pass kernels, then segment_scan_kernel), timed live
+                # with HIP events. achieved / frac: its HBM bytes per call as
+                # rocprofv3's FETCH_SIZE / WRITE_SIZE count them (calibrated on
+                # a copy), over that time, against the HBM peak. It does not
+                # bind: the slot state stays in LDS for the whole call, and
+                # the scan is bound by its per-token LDS round trips ("lds"
+                # below: the slot rows it moves through LDS against the LDS
+                # read peak measured in this run).
+                "bound": "lds",
+                "peak_resource": "hbm",
                 "kernel": "segment stage: mass pre-pass + segment_scan_kernel",
-                "achieved": seg_gbs,
+                "achieved": hbm_gbs,
                 "peak": HBM_PEAK_GBS,
                 "unit": "GB/s",
-                "frac": seg_gbs / HBM_PEAK_GBS,
-                "traffic": None if traffic is None else traffic["bytes"],
-                "traffic_detail": traffic,
-                "algorithmic_bytes": pre["segment_bytes"],
+                "frac": None if hbm_gbs is None else hbm_gbs / HBM_PEAK_GBS,
+                "traffic": hbm_bytes,
+                "traffic_current": None if traffic is None else traffic["current"],
+                "traffic_source": os.path.relpath(TRAFFIC_FILE, REPO),
                 "kernel_ms": pre["segment_ms"],
                 "kernel_ms_stats": pre["segment_ms_stats"],
+                "event_model_bytes": pre["segment_bytes"],
+                "event_model_gbs": event_gbs,
+                "event_model_frac": event_gbs / HBM_PEAK_GBS,
+                "lds": {
+                    "row_bytes": pre["lds_row_bytes"],
+                    "achieved_gbs": lds_gbs,
+                    "peak_gbs": None if lds_peak is None else lds_peak["gbs"],
+                    "frac": None if lds_peak is None else lds_gbs / lds_peak["gbs"],
+                    "peak_probe": lds_peak,
+                },
+                "step_hbm": None if tr is None else {
+                    "bytes": tr["step_bytes"], "floor_bytes": pre["floor_bytes"],
+                    "vs_floor": tr["step_bytes"] / pre["floor_bytes"],
+                    "decoder_bytes": tr["decoder_bytes"], "stage_bytes": tr["stage_bytes"]},
             },
             "prefill": {
                 "tokens_per_s": pre["tokens_per_s"],
                 "step_ms_stats": pre["step_ms_stats"],
-                "op_roofline_frac": pre["op_roofline_frac"],
+                "event_model_op_frac": pre["op_roofline_frac"],
                 "decoder_ms": pre["decoder_ms"],
                 "segment_ms": pre["segment_ms"],
                 "op_bytes_per_step": pre["op_bytes"],

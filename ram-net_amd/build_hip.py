@@ -2,7 +2,9 @@
 
 Each HIP translation unit is compiled in parallel into ``_build/`` and the
 objects are linked into ``ramnet_ops/_lib/libramnet_hip.so``. Packed-FP32
-instruction selection is disabled for device code.
+instruction selection is disabled for device code. The benchmark's LDS
+bandwidth probe (``csrc/lds_probe.hip``) is linked into a library of its own,
+``ramnet_ops/_lib/libramnet_lds_probe.so``; no operator uses it.
 
 Usage: python ram-net_amd/build_hip.py [--jobs N] [--verbose]
 """
@@ -22,6 +24,8 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "ramnet_ops", "_lib")
 LIB = os.path.join(LIB_DIR, "libramnet_hip.so")
+PROBE_LIB = os.path.join(LIB_DIR, "libramnet_lds_probe.so")
+PROBE_SOURCE = "lds_probe.hip"
 
 SOURCES = ("topk_addr.hip", "segment_forward.hip", "segment_scan_f32.hip", "segment_scan_f16.hip",
            "segment_scan_bf16.hip", "segment_backward.hip", "autoregressive.hip", "capi.hip")
@@ -70,17 +74,19 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     cc = hipcc()
     objs = []
     cmds = []
-    for src in SOURCES:
+    for src in SOURCES + (PROBE_SOURCE,):
         obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         cmds.append([cc, *common_flags(), "-c", os.path.join(CSRC, src), "-o", obj])
+    probe_obj = objs.pop()
     jobs = jobs or min(len(cmds), os.cpu_count() or 1)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         for fut in [pool.submit(_run, c, verbose) for c in cmds]:
             fut.result()
-    tmp = LIB + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
-    os.replace(tmp, LIB)
+    for lib, lib_objs in ((LIB, objs), (PROBE_LIB, [probe_obj])):
+        tmp = lib + ".tmp"
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *lib_objs, "-o", tmp], verbose)
+        os.replace(tmp, lib)
     return LIB
 
 
