@@ -108,13 +108,29 @@ int ramnet_topk_addr_backward(const int32_t *idx, const float *val, const void *
 
 /*
  * Bytes of device workspace the segment scan needs for B x H heads, T tokens
- * and the given top-k: the decoder's per-event records (T padded to 32),
- * then the gain records the precomputed-gain form writes. A scan only reads
- * the decoder records, so the same records can be scanned again. The 32-bit
- * form returns -1 when the size does not fit an int.
+ * and the given top-k when it keeps a head's slot slice resident in one
+ * piece (every shape up to A = 8190 slots): the decoder's per-event records
+ * (T padded to 32), then the gain records the precomputed-gain form writes.
+ * A scan only reads the decoder records, so the same records can be scanned
+ * again. The 32-bit form returns -1 when the size does not fit an int. No
+ * counterpart in the reference, which allocates inside its ops
+ * (ram_attn_ops.cpp:251-253); ramnet_segment_workspace_bytes sizes any shape.
  */
 int ramnet_scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k);
 int64_t ramnet_scan_workspace_bytes64(int64_t B, int64_t H, int64_t T, int64_t w_top_k, int64_t r_top_k);
+
+/*
+ * Bytes of device workspace of the segment forward entry points
+ * (ramnet_topk_segment_forward(_), ramnet_segment_scan,
+ * ramnet_ram_attn_forward) for this exact shape and activation dtype: the
+ * records above, plus, when the slot space is too wide for one resident
+ * slice and is scanned in slot ranges with 16-bit activations,
+ * B*H*T*C fp32 read sums carried from range to range (y is rounded once,
+ * from the whole sum). -1 for shapes the scan does not take. No counterpart
+ * in the reference (it allocates inside its ops, ram_attn_ops.cpp:251-253).
+ */
+int64_t ramnet_segment_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
+                                       int64_t r_top_k, int dtype);
 
 /*
  * Gated sparse update and top-K read over a whole sequence, returning a new
@@ -130,8 +146,9 @@ int64_t ramnet_scan_workspace_bytes64(int64_t B, int64_t H, int64_t T, int64_t w
  *   slot_out/mass_out   (B, H, A, C) / (B, H, A) fp32; slot_out may alias
  *                       init_slot, mass_out must not alias init_mass
  *   y                   (B, H, T, C) `dtype`; masked tokens get 0
- *   workspace           >= ramnet_scan_workspace_bytes(B, H, T, w, r) bytes
- *                       of device memory, overwritten by the call
+ *   workspace           >= ramnet_segment_workspace_bytes(B, H, T, A, C, w, r,
+ *                       dtype) bytes of device memory, overwritten by the
+ *                       call
  */
 int ramnet_topk_segment_forward(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
                                 int dtype, const uint8_t *mask, const float *init_slot, const float *init_mass,
@@ -292,8 +309,9 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
  * answer is for a 4096-token call: a much shorter call may take the
  * mass-wave form instead (the workspace size does not depend on the form).
  * Returns 1 if the shape is supported (top-k <= 128; A <= 8190 in one
- * resident slice, A <= 40958 in the precomputed-gain form split into slot
- * ranges scanned one launch each), else 0.
+ * resident slice, wider slot spaces in the precomputed-gain form split into
+ * at most 4096 slot ranges scanned one launch each, within the int32 limits
+ * B*H*A*C < 2**31), else 0.
  */
 int ramnet_segment_plan(int64_t B, int64_t H, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k, int dtype,
                         int *slice_channels, int *lds_bytes, int *precomputed_gains);

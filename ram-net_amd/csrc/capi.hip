@@ -226,6 +226,28 @@ static int64_t scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t Kw,
     return ramnet::scan_record_bytes(B, H, T, Kw, Kr) + ramnet::scan_gain_bytes(B, H, T, Kw, Kr);
 }
 
+// fp32 read sums that a scan in slot ranges carries from range to range
+// (B*H*T*C floats after the gain records), when y is 16-bit (fp32 y holds
+// them itself). `plan_ok` is false for shapes the scan does not take.
+static int64_t range_sum_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t Kw, int64_t Kr,
+                               int dtype, bool *plan_ok = nullptr) {
+    int ranges = 1;
+    const bool ok = B > 0 && H > 0 && T >= 0 && A > 0 && A < kAddressLimit && C > 0 && Kw > 0 && Kr > 0 &&
+                    valid_dtype(dtype) && fits_int({B * H * A * C, B * H * (A + 2), B * H * T * C}) &&
+                    ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T),
+                                         static_cast<int>(A), static_cast<int>(C), static_cast<int>(Kw),
+                                         static_cast<int>(Kr), dtype, nullptr, nullptr, nullptr, &ranges);
+    if (plan_ok)
+        *plan_ok = ok;
+    return ok && ranges > 1 && dtype != RAMNET_F32 ? B * H * T * C * 4 : 0;
+}
+
+// The whole workspace of a segment forward of this shape.
+static int64_t segment_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t Kw,
+                                       int64_t Kr, int dtype) {
+    return scan_workspace_bytes(B, H, T, Kw, Kr) + range_sum_bytes(B, H, T, A, C, Kw, Kr, dtype);
+}
+
 // Checks shared by the segment entry points; fills the scan job.
 // `need` is the workspace the caller's entry point requires (-1: the scan's).
 static int segment_checks(const void *x, const void *gamma, int dtype, const float *init_slot, const float *init_mass,
@@ -246,9 +268,9 @@ static int segment_checks(const void *x, const void *gamma, int dtype, const flo
                    "mass_out must not alias init_mass");
     RAMNET_REQUIRE(T == 0 || (x && gamma && y), "null tensor pointer");
     if (need < 0)
-        need = scan_workspace_bytes(B, H, T, w_top_k, r_top_k);
+        need = segment_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k, dtype);
     RAMNET_REQUIRE(workspace_bytes >= need && (T == 0 || workspace),
-                   "workspace too small: see ramnet_scan_workspace_bytes");
+                   "workspace too small: see ramnet_segment_workspace_bytes");
     return RAMNET_OK;
 }
 
@@ -264,6 +286,11 @@ static ramnet::SegmentJob make_segment_job(const void *x, int dtype, const float
     const int64_t r_bytes = B * H * t_pad * r_top_k * static_cast<int64_t>(sizeof(ramnet::ReadRec));
     job.rrec = reinterpret_cast<const ramnet::ReadRec *>(ws + w_bytes);
     job.gain = reinterpret_cast<ramnet::GainRec *>(const_cast<char *>(ws) + w_bytes + r_bytes);
+    // fp32 read sums of a scan in slot ranges: y itself, or after the gain records
+    if (y && B * T > 0)
+        job.yacc = dtype == RAMNET_F32 ? static_cast<float *>(y)
+                                       : reinterpret_cast<float *>(const_cast<char *>(ws) +
+                                                                   scan_workspace_bytes(B, H, T, w_top_k, r_top_k));
     job.x = x;
     job.init_slot = init_slot;
     job.init_mass = init_mass;
@@ -338,6 +365,17 @@ int64_t ramnet_scan_workspace_bytes64(int64_t B, int64_t H, int64_t T, int64_t w
     if (B < 0 || H < 0 || T < 0 || w_top_k < 0 || r_top_k < 0)
         return -1;
     return scan_workspace_bytes(B, H, T, w_top_k, r_top_k);
+}
+
+int64_t ramnet_segment_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
+                                       int64_t r_top_k, int dtype) {
+    if (B < 0 || H < 0 || T < 0 || w_top_k < 0 || r_top_k < 0 || A <= 0 || C <= 0 || !valid_dtype(dtype))
+        return -1;
+    if (B * H * T == 0)
+        return scan_workspace_bytes(B, H, T, w_top_k, r_top_k);
+    bool ok = false;
+    const int64_t extra = range_sum_bytes(B, H, T, A, C, w_top_k, r_top_k, dtype, &ok);
+    return ok ? scan_workspace_bytes(B, H, T, w_top_k, r_top_k) + extra : -1;
 }
 
 int ramnet_topk_segment_forward(const int32_t *addr_idx, const float *addr_val, const void *x, const void *gamma,
@@ -684,10 +722,11 @@ int ramnet_ram_attn_forward_noalloc(const void *w_addr, const void *r_addr, cons
         RAMNET_REQUIRE(ramnet::segment_plan(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T),
                                             static_cast<int>(A), static_cast<int>(C), static_cast<int>(w_top_k),
                                             static_cast<int>(r_top_k), dtype, nullptr, nullptr, &pre),
-                       "ram_attn_forward_noalloc: shape outside the LDS-resident scan (A <= 40958 and top_k <= 128)");
-        // the decoder records, then the gain records if the launch uses them
-        need = ramnet::scan_record_bytes(B, H, T, w_top_k, r_top_k) +
-               (pre ? ramnet::scan_gain_bytes(B, H, T, w_top_k, r_top_k) : 0);
+                       "ram_attn_forward_noalloc: shape outside the LDS-resident scan (top_k <= 128)");
+        // the decoder records; the precomputed-gain form adds the gain
+        // records and, in slot ranges with 16-bit y, the fp32 read sums
+        need = pre ? segment_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k, dtype)
+                   : ramnet::scan_record_bytes(B, H, T, w_top_k, r_top_k);
         if (need > RAMNET_NOALLOC_SCRATCH_BYTES)
             return fail(RAMNET_EINVAL, "ram_attn_forward_noalloc: this shape needs " + std::to_string(need) +
                                            " bytes of records, more than the " +

@@ -117,6 +117,10 @@ struct SegmentJob {
     float *slot_out;          // (B, H, A, C); may alias init_slot
     float *mass_out;          // (B, H, A); may alias init_mass
     void *y;                  // (B, H, T, C) in dtype
+    // (B, H, T, C) fp32 read sums carried from one slot range to the next
+    // when the scan is split into slot ranges: y itself for fp32 y, else a
+    // workspace buffer (so y is rounded once, from the full sum)
+    float *yacc;
     int dtype;
     int B, H, T, A, C, Kw, Kr;
     int mass_aware;
@@ -201,9 +205,11 @@ hipError_t launch_autoregressive(const DecodeJob &job, hipStream_t stream, const
 int stair_buffer(int P, int K, int NPD);
 hipError_t launch_autoregressive_steps(const DecodeJob &job, int S, hipStream_t stream, const char **why);
 
-// Channel-slice width, dynamic LDS bytes and form (1: precomputed gains)
-// that a segment-scan launch of this shape uses on the current device.
-int segment_plan(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre);
+// Channel-slice width, dynamic LDS bytes, form (1: precomputed gains) and
+// number of slot ranges that a segment-scan launch of this shape uses on the
+// current device.
+int segment_plan(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre,
+                 int *ranges = nullptr);
 
 // Mass pre-pass in record-keeping mode: the records stay as they are and
 // `aux` receives the per-event quantities. `maps` holds the chunk maps

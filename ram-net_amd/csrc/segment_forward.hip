@@ -96,8 +96,11 @@ constexpr int64_t kMassWaveCycles = 230;
 constexpr int64_t kPrePassCycles = 60;
 constexpr int64_t kPrePassLaunchCycles = 45000;
 // The mass pre-pass's replay keeps a head's masses in LDS ((A + 2) * 4
-// bytes): the precomputed-gain form reaches A <= 40958.
+// bytes): up to A = 40958 in one piece, chunked over time; wider slot spaces
+// run it per slot range of at most that many slots (segment_mass_range_kernel).
 constexpr int64_t kMaxPrePassSlots = kLdsPerCu / 4 - 2;
+// Slot ranges of one scan: at most this many launches.
+constexpr int kMaxScanRanges = 4096;
 
 // The best layout for slot ranges of AL slots (the whole space when AL == A);
 // forms: mass wave allowed (mass_ok), precomputed gains allowed (pre_ok).
@@ -156,14 +159,14 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, i
     if (kmax > 2 * kWave || A < 1)
         return false;
     int64_t cost = 0;
-    const bool pre_ok = A <= kMaxPrePassSlots;
-    if (plan_layout(B, H, A, C, kmax, elem, n_cu, T, true, pre_ok, out, &cost))
+    if (plan_layout(B, H, A, C, kmax, elem, n_cu, T, true, true, out, &cost))
         return true;
-    if (!pre_ok)
-        return false;
     // Too wide for one resident slice: split the slot space into the fewest
-    // ranges that fit (precomputed-gain form), one launch per range.
-    for (int nr = 2; nr <= 64; ++nr) {
+    // ranges that fit (precomputed-gain form), one launch per range. A slice
+    // row holds at least one channel plus a pad (8 bytes), so no range is
+    // wider than kLdsPerCu / 8 slots: the search starts at that bound.
+    for (int nr = std::max(2, static_cast<int>(static_cast<int64_t>(A) * 8 / kLdsPerCu)); nr <= kMaxScanRanges;
+         ++nr) {
         const int al = (A + nr - 1) / nr;
         if (plan_layout(B, H, al, C, kmax, elem, n_cu, T, false, true, out, &cost)) {
             out->nr = nr;
@@ -717,6 +720,148 @@ hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void 
     return hipGetLastError();
 }
 
+// Wide slot spaces (A > kMaxPrePassSlots): the mass pre-pass of one slot
+// range [r0, r0 + AL) of every (b, h), one wave per (b, h) over the whole
+// sequence (no time chunks), launched once per range. The range's masses live
+// in LDS; events on other slots act on the no-op slots. Every range sees
+// every event, and each half of a gain record is written by one range: the
+// write half by the range holding the write slot, the read half by the range
+// holding the read slot, and the halves of no-op events (slot < 0: masked,
+// inactive, or past top-k) by range 0. Mass-aware reads store r m (m: the
+// post-write mass of their slot); mass_read_scale_kernel turns them into
+// effective weights once every range has run. Lanes as in
+// segment_mass_kernel: write events on lanes 0..31, read events on 32..63.
+template<bool MA, int MP>
+__global__ __launch_bounds__(kWave) void segment_mass_range_kernel(const SegmentJob job, int t_pad, int r0, int AL) {
+    using L = MassLanes<MP>;
+    constexpr int CH = L::CH;
+    extern __shared__ __align__(16) float lds[];
+    const int bh = static_cast<int>(blockIdx.x);
+    const int lane = static_cast<int>(threadIdx.x);
+    const int hl = lane % 32;
+    const int A = job.A, Kw = job.Kw, Kr = job.Kr, T = job.T;
+    const float eps = job.eps;
+    float *ms = lds + 2;  // ms[-2], ms[-1]: the no-op slots
+    {
+        const float *src = job.init_mass + static_cast<int64_t>(bh) * A + r0;
+        for (int a = lane; a < AL; a += kWave)
+            ms[a] = src[a];
+        if (lane < 2)
+            lds[lane] = 1.f;
+    }
+    __syncthreads();
+    const L ln(lane, Kw, Kr);
+    const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * t_pad;
+    const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad;
+    const int ek = max(Kw, Kr);
+    GainRec *gg = job.gain + static_cast<int64_t>(bh) * ek * t_pad;
+    const bool first = r0 == 0;
+    for (int t0 = 0; t0 < T; t0 += CH) {
+        MassRecs<MP, CH> c;
+        mass_fetch<false>(ln, gw, gr, t_pad, t0, c);
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int t = t0 + j;
+            if (t >= T)
+                break;
+            // writes of token t on the range's slots
+            int wa[MP];
+            bool win[MP];
+            float gn[MP];
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                wa[p] = ln.wl && ln.on[p] ? c.w[p][j].x : -2;
+                const int loc = wa[p] - r0;
+                win[p] = wa[p] >= 0 && static_cast<unsigned>(loc) < static_cast<unsigned>(AL);
+                const int li = win[p] ? loc : -2;
+                const float w = win[p] ? __int_as_float(c.w[p][j].y) : 0.f;
+                const float al = win[p] ? __int_as_float(c.w[p][j].z) : 1.f;
+                const float m2 = fmaf(al, ms[li], w);
+                ms[li] = m2;
+                gn[p] = scan_gain(w, m2 + eps);
+            }
+            // then its reads (LDS keeps the wave's accesses in order: the
+            // masses read are the post-write ones)
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                const int e = p * 32 + hl;
+                const int rb = !ln.wl && ln.on[p] ? c.r[p][j].x : -1;
+                const int loc = rb - r0;
+                const bool rin = rb >= 0 && static_cast<unsigned>(loc) < static_cast<unsigned>(AL);
+                const float r = rin ? __int_as_float(c.r[p][j].y) : 0.f;
+                const float mr = MA ? ms[rin ? loc : -1] : 1.f;
+                if (e < ek) {
+                    int2 *dst = reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(t) * ek + e]) + (ln.wl ? 0 : 1);
+                    if (ln.wl) {
+                        if (wa[p] >= 0 ? win[p] : first)
+                            *dst = make_int2(wa[p] >= 0 ? wa[p] : -2, __float_as_int(wa[p] >= 0 ? gn[p] : 0.f));
+                    } else if (rb >= 0 ? rin : first) {
+                        *dst = make_int2(rb >= 0 ? rb : -1, __float_as_int(rb >= 0 ? (MA ? r * mr : r) : 0.f));
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    float *mdst = job.mass_out + static_cast<int64_t>(bh) * A + r0;
+    for (int a = lane; a < AL; a += kWave)
+        mdst[a] = ms[a];
+}
+
+// Mass-aware reads after the ranged pre-pass: per (b, h, token), with S_r the
+// sum of the token's read weights and S_m the sum of the stored r m, each
+// read's effective weight is r m S_r / (S_m + eps), as the chunked pre-pass
+// computes it.
+__global__ __launch_bounds__(256) void mass_read_scale_kernel(const SegmentJob job, int t_pad) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(job.B) * job.H * job.T)
+        return;
+    const int64_t bh = i / job.T;
+    const int t = static_cast<int>(i - bh * job.T);
+    const int Kr = job.Kr, ek = max(job.Kw, job.Kr);
+    const ReadRec *rr = job.rrec + bh * Kr * t_pad + t;
+    GainRec *g = job.gain + (bh * t_pad + t) * ek;
+    float sr = 0.f, sm = 0.f;
+    for (int k = 0; k < Kr; ++k) {
+        sr += rr[static_cast<int64_t>(k) * t_pad].r;
+        sm += g[k].r;
+    }
+    const float scale = sr / (sm + job.eps);
+    for (int k = 0; k < Kr; ++k)
+        g[k].r *= scale;
+}
+
+// The pre-pass of a slot space wider than kMaxPrePassSlots: ranges of at
+// most that many slots, in order, then the mass-aware read weights.
+hipError_t launch_mass_ranges(const SegmentJob &job, int t_pad, hipStream_t stream) {
+    const int nr = static_cast<int>((job.A + kMaxPrePassSlots - 1) / kMaxPrePassSlots);
+    const int al = (job.A + nr - 1) / nr;
+    const int kmax = std::max(job.Kw, job.Kr);
+    const dim3 grid(static_cast<unsigned>(job.B * job.H));
+    for (int r = 0; r < nr; ++r) {
+        const int r0 = r * al, n = std::min(al, job.A - r0);
+        const size_t lds = static_cast<size_t>(n + 2) * 4;
+#define RAMNET_MASS_RANGE(MA, MP) \
+    hipLaunchKernelGGL((segment_mass_range_kernel<MA, MP>), grid, dim3(kWave), lds, stream, job, t_pad, r0, n)
+        if (job.mass_aware) {
+            if (kmax <= 32) RAMNET_MASS_RANGE(true, 1);
+            else if (kmax <= 64) RAMNET_MASS_RANGE(true, 2);
+            else RAMNET_MASS_RANGE(true, 4);
+        } else {
+            if (kmax <= 32) RAMNET_MASS_RANGE(false, 1);
+            else if (kmax <= 64) RAMNET_MASS_RANGE(false, 2);
+            else RAMNET_MASS_RANGE(false, 4);
+        }
+#undef RAMNET_MASS_RANGE
+    }
+    if (job.mass_aware) {
+        const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
+        hipLaunchKernelGGL(mass_read_scale_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                           job, t_pad);
+    }
+    return hipGetLastError();
+}
+
 template<bool MA, bool AUX>
 hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, int n_cu, void *maps, size_t maps_bytes,
                             const MassAux &aux, hipStream_t stream) {
@@ -817,14 +962,15 @@ static bool pick_plan(const SegmentJob &job, Plan *p, const char **why) {
     if (forced < 0)
         return false;
     if (!forced && !make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, dtype_bytes(job.dtype), cu_count(), job.T, p)) {
-        *why = "segment forward: shape outside the LDS-resident scan (A <= 40958 slots, in slot ranges beyond 8190, "
-               "and top_k <= 128)";
+        *why = "segment forward: shape outside the LDS-resident scan (top_k <= 128; slot spaces wider than one "
+               "resident slice are scanned in at most 4096 slot ranges)";
         return false;
     }
     return true;
 }
 
-int segment_plan(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre) {
+int segment_plan(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, int *cs, int *lds_bytes, int *pre,
+                 int *ranges) {
     SegmentJob job{};
     job.B = B;
     job.H = H;
@@ -844,6 +990,8 @@ int segment_plan(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, i
         *lds_bytes = static_cast<int>(p.lds);
     if (pre)
         *pre = p.pre ? 1 : 0;
+    if (ranges)
+        *ranges = p.nr;
     return 1;
 }
 
@@ -879,22 +1027,32 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
         *why = "segment forward: unsupported dtype";
         return hipErrorInvalidValue;
     }
+    if (p.nr > 1 && !job.yacc) {
+        *why = "segment forward: a scan in slot ranges needs fp32 read sums (y for fp32 y, else workspace)";
+        return hipErrorInvalidValue;
+    }
     if (p.pre) {
-        // the chunk maps use y as scratch: the scan overwrites it afterwards
-        const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);
-        const MassAux none{};
-        const int n = kReplayChunkFactor * cu_count();
-        const hipError_t err =
-            job.mass_aware ? launch_mass_pass<true, false>(job, geo.t_pad, n, job.y, y_bytes, none, stream)
-                           : launch_mass_pass<false, false>(job, geo.t_pad, n, job.y, y_bytes, none, stream);
+        hipError_t err;
+        if (job.A > kMaxPrePassSlots) {
+            err = launch_mass_ranges(job, geo.t_pad, stream);
+        } else {
+            // the chunk maps use y as scratch: the scan overwrites it afterwards
+            const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);
+            const MassAux none{};
+            const int n = kReplayChunkFactor * cu_count();
+            err = job.mass_aware ? launch_mass_pass<true, false>(job, geo.t_pad, n, job.y, y_bytes, none, stream)
+                                 : launch_mass_pass<false, false>(job, geo.t_pad, n, job.y, y_bytes, none, stream);
+        }
         if (err != hipSuccess)
             return err;
     }
-    // slot ranges in order: the first stores y, the later ones add to it
+    // slot ranges in order: each adds its read sums to the fp32 sums of the
+    // ranges before it, and the last stores y
     const int al = (job.A + p.nr - 1) / p.nr;
     for (int r = 0; r < p.nr; ++r) {
         geo.r0 = r * al;
         geo.n_local = std::min(al, job.A - geo.r0);
+        geo.last = r == p.nr - 1 ? 1 : 0;
         hipError_t err;
         switch (job.dtype) {
             case kF32: err = launch_scan_f32(job, geo, p.vec, p.epp, p.np, p.nw, p.pre, stream); break;

@@ -33,11 +33,13 @@ struct ScanGeom {
     int n_chunks; // ceil(T / kChunk)
     int t_pad;    // T rounded up to kScanPad (record row length)
     // Slot range of this launch (precomputed-gain form): slots [r0, r0 +
-    // n_local) are resident, events on other slots act on the dummy rows,
-    // and a launch with r0 > 0 adds its read sums to y instead of storing
-    // them. One range (r0 = 0, n_local = A) unless A is too wide for LDS.
+    // n_local) are resident and events on other slots act on the dummy rows.
+    // The ranges run in order; each adds its read sums to the fp32 sums of
+    // the ranges before it (job.yacc), and the last (last != 0) stores y. One
+    // range (r0 = 0, n_local = A) unless A is too wide for LDS.
     int r0;
     int n_local;
+    int last;
 };
 
 // 1/d refined by one Newton step; gain = w / (m + eps) to ~1 ulp.
@@ -427,7 +429,7 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
     // split launches of a wide one)
     const int r0 = RANGE ? geo.r0 : 0;
     const int AL = RANGE ? geo.n_local : A;
-    const bool accumulate = RANGE && r0 > 0;
+    const bool first_range = r0 == 0, last_range = geo.last != 0;
 
     float *st = lds + 2 * RS;              // slot 0 of the slice
     float *ms = lds + (AL + 2) * RS + 2;   // mass of slot 0
@@ -905,13 +907,21 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
             const int j = EPP <= CH ? q * EPP + ev : ev % CH;
             const int t = t0 + j;
             Scalar *yp = gy + static_cast<int64_t>(t) * C + c0 + cl;
-            if (RANGE && accumulate) {
-                // a later slot range: add to the earlier ranges' read sums
+            if constexpr (RANGE) {
+                // slot ranges: the read sums of the ranges so far stay fp32
+                // in yacc; the last range adds its own and stores y
                 if (t < T) {
+                    float *ap = job.yacc + (static_cast<int64_t>(bh) * T + t) * C + c0 + cl;
 #pragma unroll
-                    for (int v = 0; v < VEC; ++v)
-                        if (FAST || c0 + cl + v < C)
-                            store_out(yp + v, load_f32(yp + v) + ykeep[q].v[v]);
+                    for (int v = 0; v < VEC; ++v) {
+                        if (FAST || c0 + cl + v < C) {
+                            const float sum = (first_range ? 0.f : ap[v]) + ykeep[q].v[v];
+                            if (last_range)
+                                store_out(yp + v, sum);
+                            else
+                                ap[v] = sum;
+                        }
+                    }
                 }
             } else if constexpr (FAST) {
                 if (!TAIL || t < T)

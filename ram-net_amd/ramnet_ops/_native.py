@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple[type, list]] = {
         _c_ptr, _c_i64, _c_i64, _c_float, _c_float, _c_ptr, _c_ptr, _c_ptr]),
     "ramnet_scan_workspace_bytes64": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "ramnet_scan_workspace_bytes": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "ramnet_segment_workspace_bytes": (_c_i64, [_c_i64] * 7 + [_c_int]),
     "ramnet_topk_segment_forward": (_c_int, [
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_float, _c_ptr, _c_i64, _c_ptr]),
@@ -140,6 +141,13 @@ def segment_plan(B: int, H: int, A: int, C: int, w_top_k: int, r_top_k: int,
 def scan_workspace_bytes(B: int, H: int, T: int, w_top_k: int, r_top_k: int) -> int:
     """Device workspace (bytes) the segment scan needs for these sizes."""
     return int(lib().ramnet_scan_workspace_bytes64(B, H, T, w_top_k, r_top_k))
+
+
+def segment_workspace_bytes(B: int, H: int, T: int, A: int, C: int, w_top_k: int, r_top_k: int,
+                            dtype: torch.dtype) -> int:
+    """Device workspace (bytes) of the segment forward entry points for this
+    exact shape (-1: a shape the scan does not take)."""
+    return int(lib().ramnet_segment_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k, DTYPE_CODES[dtype]))
 
 
 def segment_backward_workspace_bytes(B: int, H: int, T: int, A: int, C: int, w_top_k: int, r_top_k: int) -> int:

@@ -277,10 +277,12 @@ def _segment_args(x, gamma, mask):
     return x, gamma, mask
 
 
-def _workspace(x: Tensor, B: int, H: int, T: int, w_top_k: int, r_top_k: int) -> Tensor:
-    """Per-call scan workspace (per-event records) from torch's caching allocator."""
-    return torch.empty(max(1, nat.scan_workspace_bytes(B, H, T, w_top_k, r_top_k)), dtype=torch.uint8,
-                       device=x.device)
+def _workspace(x: Tensor, B: int, H: int, T: int, A: int, C: int, w_top_k: int, r_top_k: int) -> Tensor:
+    """Per-call scan workspace (per-event records; fp32 read sums of a scan in
+    slot ranges) from torch's caching allocator. A shape the scan does not
+    take gets a minimal buffer: the native call then refuses it."""
+    n = nat.segment_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k, x.dtype) if x.dtype in nat.DTYPE_CODES else -1
+    return torch.empty(max(1, n), dtype=torch.uint8, device=x.device)
 
 
 @torch.library.custom_op(f"{_NS}::topk_segment_forward", mutates_args=(), device_types="cuda")
@@ -298,7 +300,7 @@ def topk_segment_forward(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: T
     slot = torch.empty_like(init_slot)
     mass = torch.empty_like(init_mass)
     y = torch.empty_like(x)
-    ws = _workspace(x, B, H, T, w_top_k, r_top_k)
+    ws = _workspace(x, B, H, T, A, C, w_top_k, r_top_k)
     with torch.cuda.device(x.device):
         nat.call("ramnet_topk_segment_forward", addr_idx.data_ptr(), addr_val.data_ptr(), x.data_ptr(),
                  gamma.data_ptr(), _code(x), nat.ptr(mask), init_slot.data_ptr(), init_mass.data_ptr(),
@@ -415,7 +417,7 @@ def topk_segment_forward_(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: 
     # masses, so every slice reads the masses from a snapshot
     mass_in = mass.clone()
     y = torch.empty_like(x)
-    ws = _workspace(x, B, H, T, w_top_k, r_top_k)
+    ws = _workspace(x, B, H, T, A, C, w_top_k, r_top_k)
     with torch.cuda.device(x.device):
         nat.call("ramnet_topk_segment_forward_", addr_idx.data_ptr(), addr_val.data_ptr(), x.data_ptr(),
                  gamma.data_ptr(), _code(x), nat.ptr(mask), slot.data_ptr(), mass.data_ptr(), mass_in.data_ptr(),
@@ -455,7 +457,7 @@ def _ram_attn_call(w_addr, r_addr, x, gamma, mask, embed_num, position_ids, init
     x, gamma, mask = _segment_args(x, gamma, mask)
     pos = position_ids.to(device=x.device, dtype=torch.int32).contiguous()
     y = torch.empty_like(x)
-    ws = _workspace(x, B, H, T, w_top_k, r_top_k)
+    ws = _workspace(x, B, H, T, A, C, w_top_k, r_top_k)
     with torch.cuda.device(x.device):
         nat.call("ramnet_ram_attn_forward", w_addr.data_ptr(), r_addr.data_ptr(), x.data_ptr(), gamma.data_ptr(),
                  _code(x), nat.ptr(mask), embed_num, pos.data_ptr(), init_slot.data_ptr(), init_mass.data_ptr(),

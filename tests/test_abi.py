@@ -191,9 +191,9 @@ def test_cuda_path_capacity_asserts():
 def test_scan_plan_envelope():
     """The scan planner (``ramnet_segment_plan``, no device work) accepts every
     shape up to A = 8190 slots and top-K 128 with an LDS footprint within the
-    160 KiB of a CU; wider slot spaces up to 40958 in the precomputed-gain
-    form (split into slot ranges); it refuses wider slot spaces still and
-    top-K beyond 128."""
+    160 KiB of a CU; wider slot spaces in the precomputed-gain form (split
+    into slot ranges), as far as the int32 limit B*H*A*C < 2**31 allows; it
+    refuses top-K beyond 128 and shapes past the int32 limits."""
     from ramnet_ops import _native as nat
     for A in (4, 16, 256, 1024, 2401, 4096, 6561, 8100, 8190):
         for C in (1, 7, 16, 100, 128, 512):
@@ -203,15 +203,37 @@ def test_scan_plan_envelope():
                     assert plan is not None, (A, C, K, dtype)
                     cs, lds, _ = plan
                     assert 1 <= cs and 0 < lds <= 160 * 1024, (A, C, K, cs, lds)
-    for A in (8192, 16384, 32768, 40958):
-        for C, K in ((128, 8), (7, 64), (256, 128)):  # B*H*A*C within int32
-            plan = nat.segment_plan(8, 16, A, C, K, K)
+    for A in (8192, 16384, 32768, 40958, 40960, 65536, 1 << 17):
+        for C, K in ((128, 8), (7, 64), (256, 128)):
+            B = max(1, min(8, (2 ** 31 - 1) // (16 * A * C)))
+            plan = nat.segment_plan(B, 16, A, C, K, K)
             assert plan is not None and plan[2], (A, C, K, plan)
             assert 0 < plan[1] <= 160 * 1024, (A, plan)
+    assert nat.segment_plan(1, 1, 1 << 20, 16, 8, 8) is not None
     assert nat.segment_plan(8, 16, 1024, 128, 8, 129) is None
-    assert nat.segment_plan(8, 16, 40960, 128, 8, 8) is None
+    assert nat.segment_plan(8, 16, 1 << 20, 128, 8, 8) is None  # B*H*A*C beyond int32
     assert nat.segment_plan(8, 16, 1024, 128, 4, 12) is not None  # Kw != Kr
     assert nat.segment_plan(0, 16, 1024, 128, 8, 8) is None
+
+
+def test_segment_workspace_query():
+    """``ramnet_segment_workspace_bytes`` sizes the forward's workspace for
+    the exact shape: the records and gain records of
+    ``ramnet_scan_workspace_bytes`` for a slot space held in one slice; a
+    scan in slot ranges with 16-bit activations adds B*H*T*C fp32 read sums
+    (fp32 activations keep them in y); -1 for shapes the scan refuses."""
+    from ramnet_ops import _native as nat
+    for (B, H, T, A, C, K) in ((8, 16, 4096, 1024, 128, 8), (2, 3, 33, 4096, 7, 16), (1, 2, 100, 8190, 24, 64)):
+        for dtype in (torch.float32, torch.float16, torch.bfloat16):
+            assert nat.segment_workspace_bytes(B, H, T, A, C, K, K, dtype) == nat.scan_workspace_bytes(B, H, T, K, K)
+    B, H, T, A, C, K = 1, 2, 300, 65536, 24, 8
+    base = nat.scan_workspace_bytes(B, H, T, K, K)
+    assert nat.segment_workspace_bytes(B, H, T, A, C, K, K, torch.float32) == base
+    for dtype in (torch.float16, torch.bfloat16):
+        assert nat.segment_workspace_bytes(B, H, T, A, C, K, K, dtype) == base + B * H * T * C * 4
+    assert nat.segment_workspace_bytes(B, H, 0, A, C, K, K, torch.bfloat16) == nat.scan_workspace_bytes(B, H, 0, K, K)
+    assert nat.segment_workspace_bytes(B, H, T, A, C, K, 129, torch.bfloat16) == -1
+    assert nat.segment_workspace_bytes(8, 16, T, 1 << 20, 128, K, K, torch.bfloat16) == -1
 
 
 def test_scan_plan_follows_shape_and_override(monkeypatch):

@@ -232,6 +232,10 @@ WIDE_SEGMENT_CASES = [
     (1, 2, 7, 4, 150, 24, 8, 8, True, False),     # A = 16384, partial channel slice, masks
     (1, 2, 5, 8, 100, 16, 32, 16, False, True),   # A = 32768, Kw != Kr, mass_aware, staircase decoder
     (2, 1, 3, 32, 70, 8, 8, 8, False, False),     # A = 32768 at P = 32
+    # beyond 40958 slots the mass pre-pass also runs in slot ranges
+    (1, 2, 4, 16, 120, 24, 8, 8, True, False),    # A = 65536, masks
+    (1, 1, 4, 16, 90, 20, 16, 32, False, True),   # A = 65536, Kw != Kr, mass_aware (weights scaled after the ranges)
+    (1, 1, 3, 64, 60, 8, 8, 8, False, True),      # A = 262144: seven pre-pass ranges, mass_aware
 ]
 
 
@@ -240,8 +244,9 @@ WIDE_SEGMENT_CASES = [
 def test_segment_scan_wide_slot_space(case, dtype):
     """The segment forward beyond A = 8190 (the reference's segment path has
     no slot bound beyond int32): the precomputed-gain scan split into slot
-    ranges, the later ranges adding their read sums to y, against the fp64
-    event loop."""
+    ranges, each adding its read sums to the fp32 sums of the ranges before
+    it, and beyond 40958 slots the mass pre-pass split into slot ranges too,
+    against the fp64 event loop."""
     from ramnet_ops import _native as nat
     B, H, U, P, T, C, Kw, Kr, masked, mass_aware = case
     A = P ** U
@@ -259,6 +264,25 @@ def test_segment_scan_wide_slot_space(case, dtype):
     assert oracle.rel_err(mass, rmass) <= FP32_TOL, "mass state"
     err = oracle.rel_err(y, ry)
     assert err <= _out_tol(dtype), f"y rel err {err:.3e}"
+
+
+def test_segment_scan_ranges_round_y_once():
+    """bf16 y of a scan split into many slot ranges is the fp32 sum of every
+    range's reads, rounded once: each element lies within half a bf16 ulp of
+    the fp64 event loop (2**-8 of its magnitude, plus fp32 noise). Rounding
+    y after every range, as a bf16 running sum would, breaks that bound."""
+    from ramnet_ops import _native as nat
+    B, H, U, P, T, C, K = 1, 2, 4, 16, 160, 24, 8
+    A = P ** U
+    plan = nat.segment_plan(B, H, A, C, K, K, torch.bfloat16)
+    assert plan is not None and plan[2]
+    print(f"rounding case A={A} plan {plan}", flush=True)
+    src, got, ref = _segment_case(B, H, U, P, T, C, K, K, torch.bfloat16, False, False, seed=91)
+    y = got[0].double()
+    ry = torch.as_tensor(ref[0])
+    bound = 2.0 ** -8 * ry.abs() + 1e-5 * ry.abs().max()
+    excess = (y - ry).abs() - bound
+    assert float(excess.max()) <= 0, f"y beyond one bf16 rounding by {float(excess.max()):.3e}"
 
 
 # Every compiled lane layout of the segment scan (vec, epp, np, nw), mirrored
