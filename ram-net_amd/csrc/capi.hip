@@ -536,7 +536,8 @@ int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val,
         return rc;
     if (B == 0)
         return RAMNET_OK;
-    RAMNET_REQUIRE(need >= 0, "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A <= 13652)");
+    RAMNET_REQUIRE(need >= 0, "segment backward: shape outside the LDS-resident scan (top_k <= 128 and a slot "
+                              "slice in LDS: A <= 37870, or 34798 beyond 64 events)");
     RAMNET_REQUIRE(workspace_bytes >= need && workspace,
                    "workspace too small: see ramnet_segment_backward_workspace_bytes");
     RAMNET_REQUIRE(T == 0 || (addr_idx && addr_val && grad_y && grad_addr_val && grad_gamma), "null tensor pointer");

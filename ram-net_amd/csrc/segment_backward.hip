@@ -54,6 +54,9 @@ namespace {
 
 constexpr int64_t kBwdLdsLimit = 160 * 1024;
 constexpr int kBwdMaxSlices = 16;
+// The Dm chain keeps one float per slot in LDS ((A + 2) * 4 bytes); the
+// forward mass replay runs in slot ranges where its tag tables do not fit.
+constexpr int64_t kBwdMaxMassSlots = kBwdLdsLimit / 4 - 2;
 
 int pow2_at_least(int x) {
     int p = 1;
@@ -82,8 +85,8 @@ constexpr int64_t bwd_stage_bytes(int epp, int np, int vec) {
 // then take more event lanes per pass (fewer channels per wave).
 bool bwd_plan(int A, int C, int Kw, int Kr, BwdPlan *p) {
     const int kmax = std::max(Kw, Kr);
-    // the mass replay keeps a mass and a read tag and weight per slot in LDS
-    if (kmax > 2 * kWave || A <= 0 || C <= 0 || static_cast<int64_t>(A) * 12 + 8 > kBwdLdsLimit)
+    // the Dm chain keeps one float per slot in LDS
+    if (kmax > 2 * kWave || A <= 0 || C <= 0 || A > kBwdMaxMassSlots)
         return false;
     for (int epp = std::min(kWave, std::max(8, pow2_at_least(kmax))); epp <= kWave; epp *= 2) {
         const int np = (kmax + epp - 1) / epp;
@@ -1035,7 +1038,8 @@ hipError_t launch_segment_backward(const SegmentBwdJob &job, hipStream_t stream,
         return hipSuccess;
     BwdPlan p{};
     if (!bwd_plan(fj.A, fj.C, fj.Kw, fj.Kr, &p)) {
-        *why = "segment backward: shape outside the LDS-resident scan (top_k <= 128 and A <= 13652)";
+        *why = "segment backward: shape outside the LDS-resident scan (top_k <= 128 and a slot slice in LDS: "
+               "A <= 37870, or 34798 beyond 64 events)";
         return hipErrorInvalidValue;
     }
     if (fj.T == 0) {

@@ -99,6 +99,10 @@ constexpr int64_t kPrePassLaunchCycles = 45000;
 // bytes): up to A = 40958 in one piece, chunked over time; wider slot spaces
 // run it per slot range of at most that many slots (segment_mass_range_kernel).
 constexpr int64_t kMaxPrePassSlots = kLdsPerCu / 4 - 2;
+// Its record-keeping mode (the segment backward) also holds a read tag and
+// weight per slot, (A + 2) * 4 + (A + 1) * 8 bytes: A <= 13652 in one piece,
+// slot ranges beyond.
+constexpr int64_t kMaxAuxSlots = (kLdsPerCu - 16) / 12;
 // Slot ranges of one scan: at most this many launches.
 constexpr int kMaxScanRanges = 4096;
 
@@ -720,19 +724,25 @@ hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void 
     return hipGetLastError();
 }
 
-// Wide slot spaces (A > kMaxPrePassSlots): the mass pre-pass of one slot
-// range [r0, r0 + AL) of every (b, h), one wave per (b, h) over the whole
-// sequence (no time chunks), launched once per range. The range's masses live
+// Wide slot spaces: the mass pre-pass of one slot range [r0, r0 + AL) of
+// every (b, h), one wave per (b, h) over the whole sequence (no time
+// chunks), launched once per range in range order. The range's masses live
 // in LDS; events on other slots act on the no-op slots. Every range sees
-// every event, and each half of a gain record is written by one range: the
-// write half by the range holding the write slot, the read half by the range
+// every event, and each event's output is written by one range: the write
+// half by the range holding the write slot, the read half by the range
 // holding the read slot, and the halves of no-op events (slot < 0: masked,
 // inactive, or past top-k) by range 0. Mass-aware reads store r m (m: the
 // post-write mass of their slot); mass_read_scale_kernel turns them into
 // effective weights once every range has run. Lanes as in
 // segment_mass_kernel: write events on lanes 0..31, read events on 32..63.
-template<bool MA, int MP>
-__global__ __launch_bounds__(kWave) void segment_mass_range_kernel(const SegmentJob job, int t_pad, int r0, int AL) {
+// The forward (AUX false) writes gain records and runs beyond
+// kMaxPrePassSlots; the record-keeping mode of the segment backward (AUX
+// true: the per-event quantities of MassAux, with the tag table that matches
+// each write to the same token's read of its slot) runs beyond
+// kMaxAuxSlots.
+template<bool MA, int MP, bool AUX>
+__global__ __launch_bounds__(kWave) void segment_mass_range_kernel(const SegmentJob job, int t_pad, int r0, int AL,
+                                                                  const MassAux aux) {
     using L = MassLanes<MP>;
     constexpr int CH = L::CH;
     extern __shared__ __align__(16) float lds[];
@@ -742,19 +752,27 @@ __global__ __launch_bounds__(kWave) void segment_mass_range_kernel(const Segment
     const int A = job.A, Kw = job.Kw, Kr = job.Kr, T = job.T;
     const float eps = job.eps;
     float *ms = lds + 2;  // ms[-2], ms[-1]: the no-op slots
+    // AUX: per slot, the token whose read last posted there and its weight
+    // ([-1]: where lanes without a read post)
+    int *rtag = reinterpret_cast<int *>(lds + AL + 2) + 1;
+    float *rval = lds + 2 * AL + 4;
     {
         const float *src = job.init_mass + static_cast<int64_t>(bh) * A + r0;
         for (int a = lane; a < AL; a += kWave)
             ms[a] = src[a];
         if (lane < 2)
             lds[lane] = 1.f;
+        if constexpr (AUX) {
+            for (int a = lane - 1; a < AL; a += kWave)
+                rtag[a] = -1;
+        }
     }
     __syncthreads();
     const L ln(lane, Kw, Kr);
     const WriteRec *gw = job.wrec + static_cast<int64_t>(bh) * Kw * t_pad;
     const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad;
     const int ek = max(Kw, Kr);
-    GainRec *gg = job.gain + static_cast<int64_t>(bh) * ek * t_pad;
+    GainRec *gg = AUX ? nullptr : job.gain + static_cast<int64_t>(bh) * ek * t_pad;
     const bool first = r0 == 0;
     for (int t0 = 0; t0 < T; t0 += CH) {
         MassRecs<MP, CH> c;
@@ -765,38 +783,64 @@ __global__ __launch_bounds__(kWave) void segment_mass_range_kernel(const Segment
             if (t >= T)
                 break;
             // writes of token t on the range's slots
-            int wa[MP];
+            int wa[MP], wl[MP];
             bool win[MP];
-            float gn[MP];
+            float gn[MP], mb[MP];
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
                 wa[p] = ln.wl && ln.on[p] ? c.w[p][j].x : -2;
                 const int loc = wa[p] - r0;
                 win[p] = wa[p] >= 0 && static_cast<unsigned>(loc) < static_cast<unsigned>(AL);
-                const int li = win[p] ? loc : -2;
+                wl[p] = win[p] ? loc : -2;
                 const float w = win[p] ? __int_as_float(c.w[p][j].y) : 0.f;
                 const float al = win[p] ? __int_as_float(c.w[p][j].z) : 1.f;
-                const float m2 = fmaf(al, ms[li], w);
-                ms[li] = m2;
+                mb[p] = ms[wl[p]];
+                const float m2 = fmaf(al, mb[p], w);
+                ms[wl[p]] = m2;
                 gn[p] = scan_gain(w, m2 + eps);
             }
             // then its reads (LDS keeps the wave's accesses in order: the
             // masses read are the post-write ones)
+            int rb[MP], rl[MP];
+            bool rin[MP];
+            float re[MP], mr[MP];
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                rb[p] = !ln.wl && ln.on[p] ? c.r[p][j].x : -1;
+                const int loc = rb[p] - r0;
+                rin[p] = rb[p] >= 0 && static_cast<unsigned>(loc) < static_cast<unsigned>(AL);
+                rl[p] = rin[p] ? loc : -1;
+                const float r = rin[p] ? __int_as_float(c.r[p][j].y) : 0.f;
+                mr[p] = MA || AUX ? ms[rl[p]] : 1.f;
+                re[p] = MA ? r * mr[p] : r;
+                if constexpr (AUX) {
+                    rtag[rl[p]] = t;
+                    rval[rl[p]] = re[p];
+                }
+            }
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
                 const int e = p * 32 + hl;
-                const int rb = !ln.wl && ln.on[p] ? c.r[p][j].x : -1;
-                const int loc = rb - r0;
-                const bool rin = rb >= 0 && static_cast<unsigned>(loc) < static_cast<unsigned>(AL);
-                const float r = rin ? __int_as_float(c.r[p][j].y) : 0.f;
-                const float mr = MA ? ms[rin ? loc : -1] : 1.f;
-                if (e < ek) {
+                if constexpr (AUX) {
+                    // the weight of this token's read of the write's slot, if any
+                    const int sl = win[p] ? wl[p] : -1;
+                    const float rmatch = win[p] && rtag[sl] == t ? rval[sl] : 0.f;
+                    const int64_t tb = static_cast<int64_t>(bh) * T + t;
+                    if (ln.wl) {
+                        if (e < Kw && (wa[p] >= 0 ? win[p] : first))
+                            aux.wev[tb * Kw + e] = make_int4(wa[p] >= 0 ? wa[p] : -2, __float_as_int(gn[p]),
+                                                             __float_as_int(rmatch), __float_as_int(mb[p]));
+                    } else if (e < Kr && (rb[p] >= 0 ? rin[p] : first)) {
+                        aux.rev[tb * Kr + e] = make_int4(rb[p] >= 0 ? rb[p] : -1, __float_as_int(re[p]),
+                                                         __float_as_int(mr[p]), 0);
+                    }
+                } else if (e < ek) {
                     int2 *dst = reinterpret_cast<int2 *>(&gg[static_cast<int64_t>(t) * ek + e]) + (ln.wl ? 0 : 1);
                     if (ln.wl) {
                         if (wa[p] >= 0 ? win[p] : first)
                             *dst = make_int2(wa[p] >= 0 ? wa[p] : -2, __float_as_int(wa[p] >= 0 ? gn[p] : 0.f));
-                    } else if (rb >= 0 ? rin : first) {
-                        *dst = make_int2(rb >= 0 ? rb : -1, __float_as_int(rb >= 0 ? (MA ? r * mr : r) : 0.f));
+                    } else if (rb[p] >= 0 ? rin[p] : first) {
+                        *dst = make_int2(rb[p] >= 0 ? rb[p] : -1, __float_as_int(rb[p] >= 0 ? re[p] : 0.f));
                     }
                 }
             }
@@ -811,38 +855,56 @@ __global__ __launch_bounds__(kWave) void segment_mass_range_kernel(const Segment
 // Mass-aware reads after the ranged pre-pass: per (b, h, token), with S_r the
 // sum of the token's read weights and S_m the sum of the stored r m, each
 // read's effective weight is r m S_r / (S_m + eps), as the chunked pre-pass
-// computes it.
-__global__ __launch_bounds__(256) void mass_read_scale_kernel(const SegmentJob job, int t_pad) {
+// computes it. AUX: the same for the backward's per-event records (the read
+// weights and each write's matched read weight).
+template<bool AUX>
+__global__ __launch_bounds__(256) void mass_read_scale_kernel(const SegmentJob job, int t_pad, const MassAux aux) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<int64_t>(job.B) * job.H * job.T)
         return;
     const int64_t bh = i / job.T;
     const int t = static_cast<int>(i - bh * job.T);
-    const int Kr = job.Kr, ek = max(job.Kw, job.Kr);
+    const int Kw = job.Kw, Kr = job.Kr, ek = max(Kw, Kr);
     const ReadRec *rr = job.rrec + bh * Kr * t_pad + t;
-    GainRec *g = job.gain + (bh * t_pad + t) * ek;
     float sr = 0.f, sm = 0.f;
-    for (int k = 0; k < Kr; ++k) {
-        sr += rr[static_cast<int64_t>(k) * t_pad].r;
-        sm += g[k].r;
+    if constexpr (AUX) {
+        int4 *rv = aux.rev + i * Kr;
+        for (int k = 0; k < Kr; ++k) {
+            sr += rr[static_cast<int64_t>(k) * t_pad].r;
+            sm += __int_as_float(rv[k].y);
+        }
+        const float scale = sr / (sm + job.eps);
+        for (int k = 0; k < Kr; ++k)
+            rv[k].y = __float_as_int(__int_as_float(rv[k].y) * scale);
+        int4 *wv = aux.wev + i * Kw;
+        for (int k = 0; k < Kw; ++k)
+            wv[k].z = __float_as_int(__int_as_float(wv[k].z) * scale);
+    } else {
+        GainRec *g = job.gain + (bh * t_pad + t) * ek;
+        for (int k = 0; k < Kr; ++k) {
+            sr += rr[static_cast<int64_t>(k) * t_pad].r;
+            sm += g[k].r;
+        }
+        const float scale = sr / (sm + job.eps);
+        for (int k = 0; k < Kr; ++k)
+            g[k].r *= scale;
     }
-    const float scale = sr / (sm + job.eps);
-    for (int k = 0; k < Kr; ++k)
-        g[k].r *= scale;
 }
 
-// The pre-pass of a slot space wider than kMaxPrePassSlots: ranges of at
-// most that many slots, in order, then the mass-aware read weights.
-hipError_t launch_mass_ranges(const SegmentJob &job, int t_pad, hipStream_t stream) {
-    const int nr = static_cast<int>((job.A + kMaxPrePassSlots - 1) / kMaxPrePassSlots);
+// The pre-pass in slot ranges of at most `max_al` slots, in order, then the
+// mass-aware read weights.
+template<bool AUX>
+hipError_t launch_mass_ranges(const SegmentJob &job, int t_pad, int64_t max_al, const MassAux &aux,
+                              hipStream_t stream) {
+    const int nr = static_cast<int>((job.A + max_al - 1) / max_al);
     const int al = (job.A + nr - 1) / nr;
     const int kmax = std::max(job.Kw, job.Kr);
     const dim3 grid(static_cast<unsigned>(job.B * job.H));
     for (int r = 0; r < nr; ++r) {
         const int r0 = r * al, n = std::min(al, job.A - r0);
-        const size_t lds = static_cast<size_t>(n + 2) * 4;
+        const size_t lds = static_cast<size_t>(n + 2) * 4 + (AUX ? static_cast<size_t>(n + 1) * 8 : 0);
 #define RAMNET_MASS_RANGE(MA, MP) \
-    hipLaunchKernelGGL((segment_mass_range_kernel<MA, MP>), grid, dim3(kWave), lds, stream, job, t_pad, r0, n)
+    hipLaunchKernelGGL((segment_mass_range_kernel<MA, MP, AUX>), grid, dim3(kWave), lds, stream, job, t_pad, r0, n, aux)
         if (job.mass_aware) {
             if (kmax <= 32) RAMNET_MASS_RANGE(true, 1);
             else if (kmax <= 64) RAMNET_MASS_RANGE(true, 2);
@@ -856,8 +918,8 @@ hipError_t launch_mass_ranges(const SegmentJob &job, int t_pad, hipStream_t stre
     }
     if (job.mass_aware) {
         const int64_t n = static_cast<int64_t>(job.B) * job.H * job.T;
-        hipLaunchKernelGGL(mass_read_scale_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
-                           job, t_pad);
+        hipLaunchKernelGGL((mass_read_scale_kernel<AUX>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                           stream, job, t_pad, aux);
     }
     return hipGetLastError();
 }
@@ -895,6 +957,8 @@ hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *m
     if (static_cast<int64_t>(job.B) * job.H * job.T == 0)
         return hipSuccess;
     const int t_pad = scan_t_pad(job.T);
+    if (job.A > kMaxAuxSlots)
+        return launch_mass_ranges<true>(job, t_pad, kMaxAuxSlots, aux, stream);
     const int n = kReplayChunkFactor * cu_count();
     return job.mass_aware ? launch_mass_pass<true, true>(job, t_pad, n, maps, maps_bytes, aux, stream)
                           : launch_mass_pass<false, true>(job, t_pad, n, maps, maps_bytes, aux, stream);
@@ -1034,7 +1098,7 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     if (p.pre) {
         hipError_t err;
         if (job.A > kMaxPrePassSlots) {
-            err = launch_mass_ranges(job, geo.t_pad, stream);
+            err = launch_mass_ranges<false>(job, geo.t_pad, kMaxPrePassSlots, MassAux{}, stream);
         } else {
             // the chunk maps use y as scratch: the scan overwrites it afterwards
             const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);

@@ -116,6 +116,46 @@ def test_segment_backward_matches_oracle(case):
             assert torch.equal(a, b)
 
 
+WIDE_CASES = [
+    # B, H, U, P, T, C, Kw, Kr, dtype, masked, mass_aware: slot spaces beyond
+    # 13652, where the forward replay's tag tables run in slot ranges
+    (1, 2, 7, 4, 50, 8, 8, 8, F32, False, True),      # A = 16384, mass_aware
+    (1, 2, 3, 32, 60, 8, 8, 8, F32, True, False),     # A = 32768, masked tokens
+    (1, 1, 3, 32, 50, 12, 16, 8, F32, False, True),   # A = 32768, Kw != Kr, mass_aware
+    (1, 1, 5, 8, 40, 8, 100, 70, F32, True, True),    # A = 32768, two 64-event passes
+    (1, 2, 3, 32, 40, 8, 8, 8, BF16, False, False),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_segment_backward_wide_slot_space(case):
+    """The segment backward beyond A = 13652 (the reference's is bounded only
+    by int32): the forward mass replay in record-keeping mode split into slot
+    ranges (mass-aware weights scaled per token afterwards), the slice scan
+    with one channel per wave, against the fp64 state-reconstruction oracle
+    on the GPU's events."""
+    B, H, U, P, T, C, Kw, Kr, dtype, masked, mass_aware = case
+    ops = _ops()
+    print(f"wide segment backward case {case}", flush=True)
+    d = _inputs(B, H, U, P, T, C, Kw, Kr, dtype, masked, seed=B * 1000 + T * 10 + C + Kw + 7)
+    A = d["A"]
+    idx, val = ops.topk_addr_forward(d["w"].to(DEV), d["r"].to(DEV), 1, A, d["pos"].to(DEV).int(), Kw, Kr, 0.0, 0.0)
+    mask = None if d["mask"] is None else d["mask"].to(DEV)
+    got = ops.topk_segment_backward(idx, val, d["x"].to(DEV), d["gamma"].to(DEV), d["slot"].to(DEV),
+                                    d["mass"].to(DEV), mask, d["Dy"].to(DEV), d["Ds"].to(DEV), d["Dm"].to(DEV),
+                                    Kw, Kr, mass_aware, 1e-12)
+    torch.cuda.synchronize()
+    got = [t.cpu() for t in got]
+    wi, wv, ri, rv = oracle.split_events(idx.cpu(), val.cpu(), Kw)
+    ref = oracle.sparse_gsu_backward_f64(wi, wv, ri, rv, d["x"].double(), d["gamma"].double(), d["slot"], d["mass"],
+                                         d["Dy"].double(), d["Ds"], d["Dm"], d["mask"], mass_aware, 1e-12)
+    tol = _tol(dtype)
+    names = ("D_w", "D_r", "D_x", "D_gamma", "D_init_slot", "D_init_mass")
+    mine = (got[0][:, :, :Kw], got[0][:, :, Kw:], got[1], got[2], got[3], got[4])
+    for name, a, b in zip(names, mine, ref):
+        _check(name, a, torch.as_tensor(b), tol)
+
+
 def test_segment_backward_deterministic_and_optional_grads():
     """Two calls give identical bits; absent final-state gradients act as zeros."""
     ops = _ops()
