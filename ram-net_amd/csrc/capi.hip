@@ -221,9 +221,11 @@ int ramnet_topk_addr_forward(const void *w_addr, const void *r_addr, int dtype, 
     return finish(err, why, "topk_addr_forward launch");
 }
 
-// Decoder records, then the gain records of the precomputed-gain scan.
+// Decoder records, then the gain records of the precomputed-gain scan and
+// the paired scan's flags.
 static int64_t scan_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t Kw, int64_t Kr) {
-    return ramnet::scan_record_bytes(B, H, T, Kw, Kr) + ramnet::scan_gain_bytes(B, H, T, Kw, Kr);
+    return ramnet::scan_record_bytes(B, H, T, Kw, Kr) + ramnet::scan_gain_bytes(B, H, T, Kw, Kr) +
+           ramnet::scan_flag_bytes(B, H, T);
 }
 
 // fp32 read sums that a scan in slot ranges carries from range to range
@@ -286,6 +288,8 @@ static ramnet::SegmentJob make_segment_job(const void *x, int dtype, const float
     const int64_t r_bytes = B * H * t_pad * r_top_k * static_cast<int64_t>(sizeof(ramnet::ReadRec));
     job.rrec = reinterpret_cast<const ramnet::ReadRec *>(ws + w_bytes);
     job.gain = reinterpret_cast<ramnet::GainRec *>(const_cast<char *>(ws) + w_bytes + r_bytes);
+    job.flags = reinterpret_cast<int *>(const_cast<char *>(ws) + w_bytes + r_bytes +
+                                        ramnet::scan_gain_bytes(B, H, T, w_top_k, r_top_k));
     // fp32 read sums of a scan in slot ranges: y itself, or after the gain records
     if (y && B * T > 0)
         job.yacc = dtype == RAMNET_F32 ? static_cast<float *>(y)
@@ -544,6 +548,7 @@ int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val,
     ramnet::SegmentJob fj = make_segment_job(x, dtype, init_slot, init_mass, nullptr, nullptr, nullptr, B, H, T, A, C,
                                              w_top_k, r_top_k, mass_aware, eps, workspace);
     fj.gain = nullptr;  // the backward's own buffers follow the records
+    fj.flags = nullptr;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const char *why = nullptr;
     if (T > 0) {

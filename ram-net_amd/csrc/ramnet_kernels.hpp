@@ -30,8 +30,9 @@ struct AddrSource {
 // (B*H, Kw, T_pad), read records (B*H, Kr, T_pad), then the gain records of
 // the precomputed-gain scan (B*H, T_pad, max(Kw, Kr)) of GainRec, token-major
 // so that the events of one token, which the scan's lanes load together,
-// are contiguous. The decoder records are never modified after they are
-// written, so one set of records can be scanned any number of times.
+// are contiguous, then the paired scan's flags (B*H, T_pad) of int. The
+// decoder records are never modified after they are written, so one set of
+// records can be scanned any number of times.
 constexpr int kScanChunk = 16;
 constexpr int kScanPad = 2 * kScanChunk;
 struct WriteRec {
@@ -67,6 +68,10 @@ inline int64_t scan_record_bytes(int64_t B, int64_t H, int64_t T, int64_t Kw, in
 }
 inline int64_t scan_gain_bytes(int64_t B, int64_t H, int64_t T, int64_t Kw, int64_t Kr) {
     return B * H * scan_t_pad64(T) * (Kw > Kr ? Kw : Kr) * static_cast<int64_t>(sizeof(GainRec));
+}
+// The paired scan's read-after-write flags, one int per (b, h, padded token).
+inline int64_t scan_flag_bytes(int64_t B, int64_t H, int64_t T) {
+    return B * H * scan_t_pad64(T) * static_cast<int64_t>(sizeof(int));
 }
 
 // Decode one or two address tensors (write and read) sharing a shape.
@@ -121,6 +126,10 @@ struct SegmentJob {
     // when the scan is split into slot ranges: y itself for fp32 y, else a
     // workspace buffer (so y is rounded once, from the full sum)
     float *yacc;
+    // (B*H, T_pad) per token: 1 if one of its write slots is a read slot of
+    // the token before (or if that is not known), else 0. Written by the mass
+    // pre-pass for the paired scan (segment_scan_pair.hpp); null otherwise.
+    int *flags;
     int dtype;
     int B, H, T, A, C, Kw, Kr;
     int mass_aware;

@@ -29,9 +29,11 @@
 #include "ramnet_device.hpp"
 #include "ramnet_kernels.hpp"
 #include "segment_scan.hpp"
+#include "segment_scan_pair.hpp"
 
 #include <algorithm>
 #include <atomic>
+#include <climits>
 #include <cstdio>
 #include <cstdlib>
 
@@ -79,6 +81,7 @@ struct Plan {
     size_t lds;
     bool pre;     // mass pre-pass + precomputed-gain scan
     int nr = 1;   // slot ranges, scanned one launch each (precomputed-gain form)
+    int tp = 1;   // tokens per wave step: 2 = the paired scan (precomputed-gain form, one range)
 };
 
 // Cost model of one layout, in cycles per token of one round of resident
@@ -92,6 +95,20 @@ struct Plan {
 // across the GPU (~kPrePassCycles per token), plus its three extra launches
 // (~kPrePassLaunchCycles, which decide short calls). Measured on MI355X.
 constexpr int64_t kChainCycles = 160;
+// The paired scan (two tokens per wave step, segment_scan_pair.hpp): its
+// chain per pair, hazard steps included, per token, with one wave per SIMD
+// and one channel per lane; a second channel per lane adds kPairVecCycles,
+// each further wave sharing a SIMD kPairSharedCycles (they contend for the
+// LDS, whose bank conflicts grow with the rows a pass touches), and the
+// pre-pass's read-after-write flags kPairFlagCycles. Measured on MI355X, in
+// the units of kChainCycles (one-token scan: ~190 cycles per token and
+// round): config 4, 2 one-token waves per CU or 4 paired, scan 1.33 -> 1.06
+// ms; config 2, 4 one-token waves per CU or 8 paired, 0.654 -> 0.67 ms, or 4
+// paired with two channels per lane, 0.70 ms.
+constexpr int64_t kPairChainCycles = 130;
+constexpr int64_t kPairVecCycles = 40;
+constexpr int64_t kPairSharedCycles = 35;
+constexpr int64_t kPairFlagCycles = 15;
 constexpr int64_t kMassWaveCycles = 230;
 constexpr int64_t kPrePassCycles = 60;
 constexpr int64_t kPrePassLaunchCycles = 45000;
@@ -105,15 +122,61 @@ constexpr int64_t kMaxPrePassSlots = kLdsPerCu / 4 - 2;
 constexpr int64_t kMaxAuxSlots = (kLdsPerCu - 16) / 12;
 // Slot ranges of one scan: at most this many launches.
 constexpr int kMaxScanRanges = 4096;
+// The paired scan's pre-pass also keeps a tag per slot for its read-after-
+// write flags: (A + 2) * 4 + (A + 3) * 4 bytes.
+constexpr int64_t kMaxPairSlots = (kLdsPerCu - 20) / 8;
+// The paired scan reads a head's gain records through a buffer resource of
+// at most 2^31 - 1 bytes.
+static bool pair_records_fit(int kmax, int T) {
+    return static_cast<int64_t>(kmax) * scan_t_pad(std::max(T, 0)) * 16 <= INT_MAX;
+}
 
 // The best layout for slot ranges of AL slots (the whole space when AL == A);
 // forms: mass wave allowed (mass_ok), precomputed gains allowed (pre_ok).
-static bool plan_layout(int B, int H, int AL, int C, int kmax, int elem, int n_cu, int T, bool mass_ok, bool pre_ok,
-                        Plan *out, int64_t *best_cost) {
+static bool plan_layout(int B, int H, int AL, int A_full, int C, int kmax, int elem, int n_cu, int T, bool mass_ok,
+                        bool pre_ok, Plan *out, int64_t *best_cost) {
     const int64_t tt = std::max(1, T);
     const int epp0 = std::min(kWave, std::max(4, pow2_ceil(kmax)));
     bool found = false;
     int64_t best = 0;
+    // paired scan: the precomputed-gain form over the whole slot space, one
+    // pass of events
+    if (pre_ok && AL == A_full && AL <= kMaxPairSlots && pair_records_fit(kmax, T)) {
+        for (int epp = 2; epp <= kWave / 2; epp <<= 1) {
+            if (epp < kmax)
+                continue;
+            for (int nw = 8; nw >= 1; nw >>= 1) {
+                for (int vec = 4; vec >= 1; vec >>= 1) {
+                    if (!scan_pair_layout_compiled(vec, epp, nw))
+                        continue;
+                    const int cs = nw * (kWave / 2 / epp) * vec;
+                    const size_t lds = scan_pair_lds_bytes(AL, vec, epp, nw, elem, kLdsPerCu);
+                    const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
+                    if (gran > kLdsPerCu)
+                        continue;
+                    const int64_t units = static_cast<int64_t>(B) * H * ((C + cs - 1) / cs);
+                    const int64_t per_cu = std::min<int64_t>(kLdsPerCu / gran, std::max(1, 16 / nw));
+                    const int64_t rounds = (units + per_cu * n_cu - 1) / (per_cu * n_cu);
+                    const int64_t resident = std::min<int64_t>(per_cu, (units + n_cu - 1) / n_cu);
+                    const int64_t waves_per_simd = (resident * nw + 3) / 4;
+                    // per token: half a pair's chain, or half its issue
+                    const int64_t issue = 4 * (12 + 6 * vec) * waves_per_simd / 2;
+                    const int64_t chain =
+                        kPairChainCycles + kPairVecCycles * (vec - 1) + kPairSharedCycles * (waves_per_simd - 1);
+                    int64_t cost = tt * rounds * std::max(chain, issue);
+                    if (C % cs != 0)
+                        cost = cost * 3 / 2;
+                    cost += tt * (kPrePassCycles + kPairFlagCycles) + kPrePassLaunchCycles;
+                    if (!found || cost < best) {
+                        *out = {vec, epp, 1, nw, cs, lds, true};
+                        out->tp = 2;
+                        best = cost;
+                        found = true;
+                    }
+                }
+            }
+        }
+    }
     for (int pre = mass_ok ? 0 : 1; pre <= (pre_ok ? 1 : 0); ++pre) {
         for (int epp = 4; epp <= kWave; epp <<= 1) {
             const int np = (kmax + epp - 1) / epp;
@@ -147,6 +210,7 @@ static bool plan_layout(int B, int H, int AL, int C, int kmax, int elem, int n_c
                                                                                  (nw == out->nw && cs > out->cs)))));
                     if (better) {
                         *out = {vec, epp, np, nw, cs, lds, pre != 0};
+                        out->tp = 1;
                         best = cost;
                         found = true;
                     }
@@ -163,7 +227,7 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, i
     if (kmax > 2 * kWave || A < 1)
         return false;
     int64_t cost = 0;
-    if (plan_layout(B, H, A, C, kmax, elem, n_cu, T, true, true, out, &cost))
+    if (plan_layout(B, H, A, A, C, kmax, elem, n_cu, T, true, true, out, &cost))
         return true;
     // Too wide for one resident slice: split the slot space into the fewest
     // ranges that fit (precomputed-gain form), one launch per range. A slice
@@ -172,7 +236,7 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, i
     for (int nr = std::max(2, static_cast<int>(static_cast<int64_t>(A) * 8 / kLdsPerCu)); nr <= kMaxScanRanges;
          ++nr) {
         const int al = (A + nr - 1) / nr;
-        if (plan_layout(B, H, al, C, kmax, elem, n_cu, T, false, true, out, &cost)) {
+        if (plan_layout(B, H, al, A, C, kmax, elem, n_cu, T, false, true, out, &cost)) {
             out->nr = nr;
             return true;
         }
@@ -446,10 +510,16 @@ __global__ __launch_bounds__(256) void mass_chunk_scan_kernel(const SegmentJob j
 // events per token): unit u takes lanes [u * 64 / NU, (u + 1) * 64 / NU),
 // so every lane of a record load or gain store serves an event; the units
 // past the last (b, h) repeat it (same records, same values stored).
-template<bool MA, int MP, bool AUX = false, int NU = 1>
+// FL: also the read-after-write flags of the paired scan (job.flags): per
+// token, whether one of its write slots is a read slot of the token before.
+// Each token's reads post the token under their slots in an LDS tag table;
+// the next token's writes look their slots up. The first token of a chunk
+// (whose predecessor another chunk replays) is flagged.
+template<bool MA, int MP, bool AUX = false, int NU = 1, bool FL = false>
 __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, int t_pad, int chunk_len,
                                                             const float2 *starts, const MassAux aux) {
     static_assert(NU == 1 || (MP == 1 && !AUX), "several units per wave: one pass of events, no AUX");
+    static_assert(!(FL && AUX), "flags: the forward pre-pass only");
     constexpr int HALF = kWave / NU / 2;
     using L = MassLanes<MP, HALF>;
     // half the fetch of the records: fewer registers, more resident waves
@@ -489,6 +559,14 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
         for (int a = lane; a < A; a += kWave)
             rtag[a] = -1;
     }
+    // FL: unit v's tags at ftag + v * (A + 3) + 3: [-2] where no-op writes
+    // look (never posted), [-1] where no-op reads post ([-3] unused)
+    int *ftag = reinterpret_cast<int *>(lds + NU * (A + 2));
+    int *tg = ftag + unit * (A + 3) + 3;
+    if constexpr (FL) {
+        for (int a = lane; a < NU * (A + 3); a += kWave)
+            ftag[a] = INT_MIN;
+    }
     __syncthreads();
 
     const L ln(lane, Kw, Kr);
@@ -498,7 +576,11 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     const int ek = max(Kw, Kr);
     GainRec *gg = AUX ? nullptr : job.gain + static_cast<int64_t>(bh) * ek * t_pad;
     const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
+    int *gfl = FL ? job.flags + static_cast<int64_t>(bh) * t_pad : nullptr;
     auto run = [&](int t0, const MassRecs<MP, CH> &c) {
+        // FL: per token of the chunk, the tag each pass's write slot holds
+        // (compared once the chunk is done, off the mass chain)
+        int tgv[CH][MP];
         auto wev = [&](int p, int j, int &a, float &w, float &al) {
             const bool act = wlane && ln.act[p] && t0 + j < t_end;
             a = act ? c.w[p][j].x : -2;
@@ -508,21 +590,49 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
         auto finish = [&](int j, const int (&a)[MP], const float (&w)[MP], const float (&al)[MP], float (&m)[MP]) {
             const int t = t0 + j;
             const bool live = t < t_end;
+            int rb[MP];
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                const bool act = !wlane && ln.act[p] && live;
+                rb[p] = act ? c.r[p][j].x : -1;
+            }
+            if constexpr (FL) {
+                // the tags this token's write slots hold, before its own
+                // reads post theirs (read lanes look at a slot never posted).
+                // The tags are posted by other lanes (the read lanes of the
+                // token before, and of this token): the barriers keep the
+                // compiler from moving these loads above the one's stores or
+                // below the other's.
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int p = 0; p < MP; ++p)
+                    tgv[j][p] = tg[wlane ? a[p] : -2];
+                __builtin_amdgcn_wave_barrier();
+            }
             float gn[MP];
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
                 const float m2 = fmaf(al[p], m[p], w[p]);
-                ms[a[p]] = m2;
+                if constexpr (FL) {
+                    // one store: the write lanes' masses, the read lanes' tags
+                    float *dst = wlane ? &ms[a[p]] : reinterpret_cast<float *>(&tg[rb[p]]);
+                    *dst = wlane ? m2 : __int_as_float(t);
+                } else {
+                    ms[a[p]] = m2;
+                }
                 gn[p] = scan_gain(w[p], m2 + eps);
             }
+            // (FL: the read lanes stored their tags, not into the masses,
+            // above; the barrier keeps their post-write mass loads below
+            // the write lanes' mass stores)
+            if constexpr (FL && MA)
+                __builtin_amdgcn_wave_barrier();
             {
-                int rb[MP];
                 float rr[MP], mm[MP];
                 float sr = 0.f, srm = 0.f;
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
                     const bool act = !wlane && ln.act[p] && live;
-                    rb[p] = act ? c.r[p][j].x : -1;
                     rr[p] = act ? __int_as_float(c.r[p][j].y) : 0.f;
                     mm[p] = 0.f;
                     if constexpr (MA || AUX) {
@@ -612,6 +722,26 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
             }
             finish(j1, a1, w1, al1, m1);
         }
+        if constexpr (FL) {
+            // per token: a hit in any write lane of this lane's unit; lane hl
+            // stores token t0 + hl's flag (lanes past the chunk's tokens
+            // repeat the last one's store)
+            const int ubase = unit * 2 * HALF;
+            uint32_t rwm = 0;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                bool hit = false;
+#pragma unroll
+                for (int p = 0; p < MP; ++p)
+                    hit = hit || (wlane && ln.on[p] && tgv[j][p] == t0 + j - 1);
+                const uint64_t hb = __ballot(hit);
+                const bool unit_hit = ((hb >> ubase) & ((1ull << HALF) - 1)) != 0;
+                const bool first = t0 + j == t_begin && t_begin > 0;
+                rwm |= unit_hit || first ? 1u << j : 0u;
+            }
+            const int jj = min(hl, min(CH, t_end - t0) - 1);
+            gfl[t0 + jj] = static_cast<int>((rwm >> jj) & 1u);
+        }
     };
     const int nc = (t_end - t_begin + CH - 1) / CH;
     // the next chunk's loads stay ahead of this chunk's mass chain; two
@@ -668,9 +798,10 @@ int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chun
 }
 
 // LDS of the replay kernel: the masses of its NU units (and with AUX the
-// read tag table).
-size_t mass_lds_bytes(int A, bool aux, int nu = 1) {
-    return static_cast<size_t>(A + 2) * 4 * nu + (aux ? static_cast<size_t>(A) * 8 : 0);
+// read tag table, with FL the flag tag tables).
+size_t mass_lds_bytes(int A, bool aux, int nu = 1, bool fl = false) {
+    return static_cast<size_t>(A + 2) * 4 * nu + (aux ? static_cast<size_t>(A) * 8 : 0) +
+           (fl ? static_cast<size_t>(A + 3) * 4 * nu : 0);
 }
 
 // The replay kernel with NU units per wave: (b, h) units of a chunk in
@@ -679,8 +810,17 @@ template<bool MA, int MP, bool AUX, int NU>
 void launch_replay_units(const SegmentJob &job, int t_pad, int len, int nck, const float2 *starts, const MassAux &aux,
                          hipStream_t stream) {
     const unsigned groups = static_cast<unsigned>((job.B * job.H + NU - 1) / NU);
-    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX, NU>), dim3(groups, static_cast<unsigned>(nck)), dim3(kWave),
-                       mass_lds_bytes(job.A, AUX, NU), stream, job, t_pad, len, starts, aux);
+    const bool fl = !AUX && job.flags;
+    const dim3 grid(groups, static_cast<unsigned>(nck));
+    if constexpr (!AUX) {
+        if (fl) {
+            hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX, NU, true>), grid, dim3(kWave),
+                               mass_lds_bytes(job.A, AUX, NU, true), stream, job, t_pad, len, starts, aux);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX, NU>), grid, dim3(kWave), mass_lds_bytes(job.A, AUX, NU), stream,
+                       job, t_pad, len, starts, aux);
 }
 
 // Units per replay wave: four when a token has at most 8 events and the
@@ -692,7 +832,7 @@ template<bool MA, int MP, bool AUX>
 void launch_mass_replay_nu(const SegmentJob &job, int t_pad, int len, int nck, const float2 *starts,
                            const MassAux &aux, hipStream_t stream) {
     if constexpr (MP == 1 && !AUX) {
-        if (std::max(job.Kw, job.Kr) <= 8 && mass_lds_bytes(job.A, false, 4) <= 64 * 1024)
+        if (std::max(job.Kw, job.Kr) <= 8 && mass_lds_bytes(job.A, false, 4, job.flags != nullptr) <= 64 * 1024)
             return launch_replay_units<MA, MP, AUX, 4>(job, t_pad, len, nck, starts, aux, stream);
     }
     launch_replay_units<MA, MP, AUX, 1>(job, t_pad, len, nck, starts, aux, stream);
@@ -996,26 +1136,34 @@ __global__ __launch_bounds__(256) void state_copy_kernel(float *dst, const float
 }
 }  // namespace
 
-// RAMNET_SCAN_LAYOUT="vec,epp,np,nw[,pre]" replaces the planner's choice (tests
-// sweep every compiled layout with it; also a tuning knob). The layout must
-// be compiled, cover max(Kw, Kr) events and fit in LDS.
+// RAMNET_SCAN_LAYOUT="vec,epp,np,nw[,pre[,tp]]" replaces the planner's
+// choice (tests sweep every compiled layout with it; also a tuning knob).
+// tp = 2 names a paired layout (pre = 1, np = 1; epp events per half wave).
+// The layout must be compiled, cover max(Kw, Kr) events and fit in LDS.
 static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
     const char *env = std::getenv("RAMNET_SCAN_LAYOUT");
     if (!env || !*env)
         return 0;
-    int vec = 0, epp = 0, np = 0, nw = 0, pre = 0;
-    const int n = std::sscanf(env, "%d,%d,%d,%d,%d", &vec, &epp, &np, &nw, &pre);
-    if ((n != 4 && n != 5) || (pre != 0 && pre != 1) || !scan_layout_compiled(vec, epp, np, nw, pre != 0)) {
-        *why = "RAMNET_SCAN_LAYOUT names no compiled layout (vec,epp,np,nw[,pre])";
+    int vec = 0, epp = 0, np = 0, nw = 0, pre = 0, tp = 1;
+    const int n = std::sscanf(env, "%d,%d,%d,%d,%d,%d", &vec, &epp, &np, &nw, &pre, &tp);
+    const bool pair = n == 6 && tp == 2;
+    const bool named = pair ? pre == 1 && np == 1 && scan_pair_layout_compiled(vec, epp, nw)
+                            : (n >= 4 && n <= 6) && (pre == 0 || pre == 1) && tp == 1 &&
+                                  scan_layout_compiled(vec, epp, np, nw, pre != 0);
+    if (!named) {
+        *why = "RAMNET_SCAN_LAYOUT names no compiled layout (vec,epp,np,nw[,pre[,tp]])";
         return -1;
     }
-    const size_t lds = scan_lds_bytes(job.A, vec, epp, np, nw, dtype_bytes(job.dtype), pre != 0);
+    const size_t lds = pair ? scan_pair_lds_bytes(job.A, vec, epp, nw, dtype_bytes(job.dtype), kLdsPerCu)
+                            : scan_lds_bytes(job.A, vec, epp, np, nw, dtype_bytes(job.dtype), pre != 0);
     if (epp * np < std::max(job.Kw, job.Kr) || static_cast<int64_t>(lds) > kLdsPerCu ||
-        (pre && job.A > kMaxPrePassSlots)) {
+        (pre && job.A > kMaxPrePassSlots) ||
+        (pair && (job.A > kMaxPairSlots || !pair_records_fit(std::max(job.Kw, job.Kr), job.T)))) {
         *why = "RAMNET_SCAN_LAYOUT does not cover top_k or does not fit in LDS";
         return -1;
     }
-    *p = {vec, epp, np, nw, nw * (kWave / epp) * vec, lds, pre != 0};
+    *p = {vec, epp, np, nw, nw * (kWave / (pair ? 2 : 1) / epp) * vec, lds, pre != 0};
+    p->tp = pair ? 2 : 1;
     return 1;
 }
 
@@ -1080,6 +1228,14 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
         *why = "segment forward: the precomputed-gain layout needs the gain records of the scan workspace";
         return hipErrorInvalidValue;
     }
+    if (p.tp == 2 && !job.flags) {
+        *why = "segment forward: the paired layout needs the flags of the scan workspace";
+        return hipErrorInvalidValue;
+    }
+    // the pre-pass writes the paired scan's flags only when it runs
+    SegmentJob pj = job;
+    if (p.tp != 2)
+        pj.flags = nullptr;
     ScanGeom geo{};
     geo.n_slices = (job.C + p.cs - 1) / p.cs;
     geo.n_units = job.B * job.H * geo.n_slices;
@@ -1104,11 +1260,18 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
             const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);
             const MassAux none{};
             const int n = kReplayChunkFactor * cu_count();
-            err = job.mass_aware ? launch_mass_pass<true, false>(job, geo.t_pad, n, job.y, y_bytes, none, stream)
-                                 : launch_mass_pass<false, false>(job, geo.t_pad, n, job.y, y_bytes, none, stream);
+            err = job.mass_aware ? launch_mass_pass<true, false>(pj, geo.t_pad, n, job.y, y_bytes, none, stream)
+                                 : launch_mass_pass<false, false>(pj, geo.t_pad, n, job.y, y_bytes, none, stream);
         }
         if (err != hipSuccess)
             return err;
+    }
+    if (p.tp == 2) {
+        switch (job.dtype) {
+            case kF32: return launch_scan_pair_f32(pj, geo, p.vec, p.epp, p.nw, kLdsPerCu, stream);
+            case kF16: return launch_scan_pair_f16(pj, geo, p.vec, p.epp, p.nw, kLdsPerCu, stream);
+            default: return launch_scan_pair_bf16(pj, geo, p.vec, p.epp, p.nw, kLdsPerCu, stream);
+        }
     }
     // slot ranges in order: each adds its read sums to the fp32 sums of the
     // ranges before it, and the last stores y

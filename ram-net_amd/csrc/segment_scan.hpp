@@ -40,6 +40,7 @@ struct ScanGeom {
     int r0;
     int n_local;
     int last;
+    int row_stride;  // floats per slot row of the paired scan (segment_scan_pair.hpp)
 };
 
 // 1/d refined by one Newton step; gain = w / (m + eps) to ~1 ulp.

@@ -1,12 +1,18 @@
 // Segment scan kernels for float activations (one translation unit per dtype
 // so the lane-layout instantiations compile in parallel).
 #include "segment_scan.hpp"
+#include "segment_scan_pair.hpp"
 
 namespace ramnet {
 
 hipError_t launch_scan_f32(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, int nw, bool pre,
                           hipStream_t stream) {
     return scan_dispatch<float>(job, geo, vec, epp, np, nw, pre, stream);
+}
+
+hipError_t launch_scan_pair_f32(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int nw,
+                               int64_t lds_limit, hipStream_t stream) {
+    return scan_pair_dispatch<float>(job, geo, vec, epp, nw, lds_limit, stream);
 }
 
 }  // namespace ramnet

@@ -67,8 +67,9 @@ def test_workspace_size_formula():
     for B, H, T, kw, kr in ((8, 16, 4096, 8, 8), (1, 1, 1, 1, 1), (2, 3, 33, 4, 12), (1, 2, 0, 3, 3)):
         t_pad = (T + 31) // 32 * 32
         # write records (16 B) and read records (8 B), then one 16-byte gain
-        # record per (event, token) for the precomputed-gain scan
-        want = B * H * t_pad * (kw * 16 + kr * 8) + B * H * t_pad * max(kw, kr) * 16
+        # record per (event, token) for the precomputed-gain scan, then one
+        # int of read-after-write flags per token for the paired scan
+        want = B * H * t_pad * (kw * 16 + kr * 8) + B * H * t_pad * max(kw, kr) * 16 + B * H * t_pad * 4
         assert lib.ramnet_scan_workspace_bytes64(B, H, T, kw, kr) == want
     assert lib.ramnet_scan_workspace_bytes(1 << 20, 64, 1 << 20, 8, 8) == -1  # > int32
 

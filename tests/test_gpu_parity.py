@@ -295,11 +295,19 @@ SCAN_LAYOUTS = [
 ] + [  # precomputed-gain form (mass pre-pass), from RAMNET_SCAN_PRE_LAYOUTS
     (1, 8, 1, 2, 1), (1, 8, 1, 4, 1), (1, 16, 1, 2, 1), (1, 16, 1, 4, 1), (1, 32, 1, 2, 1), (1, 64, 1, 2, 1),
     (1, 64, 2, 1, 1),
+] + [  # paired form (two tokens per wave step; epp events per half wave), from RAMNET_SCAN_PAIR_LAYOUTS
+    (1, 8, 1, 4, 1, 2), (1, 8, 1, 8, 1, 2), (1, 16, 1, 4, 1, 2), (1, 16, 1, 8, 1, 2), (2, 8, 1, 4, 1, 2),
+    (2, 16, 1, 2, 1, 2), (2, 16, 1, 4, 1, 2),
 ]
+PAIR_LAYOUTS = [l for l in SCAN_LAYOUTS if len(l) == 6]
+
+
+def _layout_id(l):
+    return "v{}e{}n{}w{}".format(*l) + ("p" if len(l) > 4 else "") + ("2" if len(l) > 5 else "")
 
 
 @pytest.mark.parametrize("partial", [False, True], ids=["full_slices", "partial_slice"])
-@pytest.mark.parametrize("layout", SCAN_LAYOUTS, ids=lambda l: "v{}e{}n{}w{}".format(*l) + ("p" if len(l) > 4 else ""))
+@pytest.mark.parametrize("layout", SCAN_LAYOUTS, ids=_layout_id)
 def test_segment_scan_every_layout(layout, partial, monkeypatch):
     """Each layout, forced through RAMNET_SCAN_LAYOUT, against the fp64 sparse
     oracle: top-K filling every event lane (writes) and all but one (reads),
@@ -308,7 +316,7 @@ def test_segment_scan_every_layout(layout, partial, monkeypatch):
     vec, epp, np_, nw = layout[:4]
     kmax = epp * np_
     U, P = (4, 4) if kmax > 64 else (3, 4)
-    cs = nw * (64 // epp) * vec
+    cs = nw * ((32 if len(layout) > 5 else 64) // epp) * vec
     C = 2 * cs + (0 if not partial else (-3 if cs > 3 else 1))  # partial: last slice ends inside C
     Kw, Kr = kmax, max(1, kmax - 1)
     monkeypatch.setenv("RAMNET_SCAN_LAYOUT", ",".join(map(str, layout)))
@@ -325,6 +333,43 @@ def test_segment_scan_every_layout(layout, partial, monkeypatch):
         assert oracle.rel_err(mass, rmass) <= FP32_TOL, f"mass state, layout {layout}"
         err = oracle.rel_err(y, ry)
         assert err <= _out_tol(dtype), f"y rel err {err:.3e}, layout {layout}"
+
+
+# Slot spaces small enough that most pairs of tokens collide: the paired
+# scan's in-order pairs (the odd token writes a slot the even token writes or
+# reads), its reloads after a group's first pair, and runs of clean pairs.
+PAIR_HAZARD_CASES = [
+    # B, H, U, P, T, C, Kw, Kr, masked, mass_aware
+    (2, 2, 2, 4, 77, 64, 8, 8, True, False),      # A = 16, K = 8: nearly every pair in order
+    (1, 3, 3, 4, 200, 32, 8, 5, False, True),     # A = 64
+    (2, 1, 2, 16, 301, 48, 6, 8, True, True),     # A = 256, partial slice
+    (1, 2, 3, 6, 1100, 64, 16, 16, False, False),  # A = 216, K = 16, several pre-pass chunks
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", PAIR_LAYOUTS, ids=_layout_id)
+@pytest.mark.parametrize("case", PAIR_HAZARD_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_paired_scan_hazards(case, layout, dtype, monkeypatch):
+    """Each paired layout, forced through RAMNET_SCAN_LAYOUT, against the
+    fp64 sparse oracle on slot spaces where the two tokens of a pair collide
+    most of the time."""
+    B, H, U, P, T, C, Kw, Kr, masked, mass_aware = case
+    if max(Kw, Kr) > layout[1]:
+        pytest.skip("top-k beyond the layout's events per half wave")
+    monkeypatch.setenv("RAMNET_SCAN_LAYOUT", ",".join(map(str, layout)))
+    print(f"paired hazards {case} layout {layout} {dtype}", flush=True)
+    src, got, ref = _segment_case(B, H, U, P, T, C, Kw, Kr, dtype, masked, mass_aware, seed=T + C + layout[1])
+    y, slot, mass = got
+    ry, rslot, rmass = ref
+    ry = torch.as_tensor(ry)
+    if src.mask is not None:
+        assert bool((y[:, :, ~src.mask[0]] == 0).all()), "masked tokens must read 0"
+        y, ry = y[:, :, src.mask[0]], ry[:, :, src.mask[0]]
+    assert oracle.rel_err(slot, rslot) <= FP32_TOL, f"slot state, layout {layout}"
+    assert oracle.rel_err(mass, rmass) <= FP32_TOL, f"mass state, layout {layout}"
+    err = oracle.rel_err(y, ry)
+    assert err <= _out_tol(dtype), f"y rel err {err:.3e}, layout {layout}"
 
 
 @pytest.mark.parametrize("mass_aware", [False, True])
