@@ -150,7 +150,7 @@ static bool plan_layout(int B, int H, int AL, int A_full, int C, int kmax, int e
                     if (!scan_pair_layout_compiled(vec, epp, nw))
                         continue;
                     const int cs = nw * (kWave / 2 / epp) * vec;
-                    const size_t lds = scan_pair_lds_bytes(AL, vec, epp, nw, elem, kLdsPerCu);
+                    const size_t lds = scan_pair_lds_bytes(AL, vec, epp, nw, elem);
                     const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
                     if (gran > kLdsPerCu)
                         continue;
@@ -1154,7 +1154,7 @@ static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
         *why = "RAMNET_SCAN_LAYOUT names no compiled layout (vec,epp,np,nw[,pre[,tp]])";
         return -1;
     }
-    const size_t lds = pair ? scan_pair_lds_bytes(job.A, vec, epp, nw, dtype_bytes(job.dtype), kLdsPerCu)
+    const size_t lds = pair ? scan_pair_lds_bytes(job.A, vec, epp, nw, dtype_bytes(job.dtype))
                             : scan_lds_bytes(job.A, vec, epp, np, nw, dtype_bytes(job.dtype), pre != 0);
     if (epp * np < std::max(job.Kw, job.Kr) || static_cast<int64_t>(lds) > kLdsPerCu ||
         (pre && job.A > kMaxPrePassSlots) ||
@@ -1268,9 +1268,9 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
     }
     if (p.tp == 2) {
         switch (job.dtype) {
-            case kF32: return launch_scan_pair_f32(pj, geo, p.vec, p.epp, p.nw, kLdsPerCu, stream);
-            case kF16: return launch_scan_pair_f16(pj, geo, p.vec, p.epp, p.nw, kLdsPerCu, stream);
-            default: return launch_scan_pair_bf16(pj, geo, p.vec, p.epp, p.nw, kLdsPerCu, stream);
+            case kF32: return launch_scan_pair_f32(pj, geo, p.vec, p.epp, p.nw, stream);
+            case kF16: return launch_scan_pair_f16(pj, geo, p.vec, p.epp, p.nw, stream);
+            default: return launch_scan_pair_bf16(pj, geo, p.vec, p.epp, p.nw, stream);
         }
     }
     // slot ranges in order: each adds its read sums to the fp32 sums of the

@@ -40,7 +40,6 @@ struct ScanGeom {
     int r0;
     int n_local;
     int last;
-    int row_stride;  // floats per slot row of the paired scan (segment_scan_pair.hpp)
 };
 
 // 1/d refined by one Newton step; gain = w / (m + eps) to ~1 ulp.
@@ -326,7 +325,8 @@ __device__ const uint8_t kScanAllValid = 1;
 
 // Row stride (floats) of the LDS slot slice: one pad float per row spreads
 // rows over banks; VEC-wide rows keep VEC-float alignment.
-constexpr int scan_row_stride(int vec, int cs) { return cs + (vec == 1 ? 1 : vec); }
+__host__ __device__ constexpr int scan_row_stride(int vec, int cs) { return cs + (vec == 1 ? 1 : vec); }
+
 // Staged event: {write slot, gain, read slot, read weight}.
 struct StageRec {
     int wslot;
@@ -767,12 +767,13 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
             for (int v = 0; v < VEC; ++v)
                 ykeep[q].v[v] = 0.f;
         auto flag = [&](int j) { return ((fm >> j) & 1u) != 0; };
-        // LDS addresses of every event's row (one 24-bit multiply-add each),
-        // computed once per chunk, off the token chain. PRE records past T
-        // were never written: those tokens act on the dummy rows.
-        {
-#pragma unroll
-            for (int j = 0; j < CH; ++j)
+        // LDS addresses of the rows of token j's events (a 24-bit
+        // multiply-add each). The first group's are
+        // computed before the token loop, each later group's during the
+        // group before it, where they fill the wait for that group's rows.
+        // PRE records past T were never written: those tokens act on the
+        // dummy rows.
+        auto addresses = [&](int j) {
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
                     int wa = rec[p][j].x, ra = rec[p][j].z;
@@ -795,7 +796,7 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
                     rec[p][j].x = mad24(wa, amul[p], awb[p]);
                     rec[p][j].z = mad24(ra, amul[p], arb[p]);
                 }
-        }
+        };
         auto row = [&](int a) { return lds_at(static_cast<uint32_t>(a)); };
         auto load_rows = [&](int j, FVec<VEC> (&s)[NP]) {
 #pragma unroll
@@ -869,6 +870,9 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
         static_assert(CH % G == 0, "chunks hold whole token groups");
         FVec<VEC> rp[G][NP];
 #pragma unroll
+        for (int i = 0; i < G; ++i)
+            addresses(i);
+#pragma unroll
         for (int j0 = 0; j0 < CH; j0 += G) {
             FVec<VEC> sv[G][NP];
 #pragma unroll
@@ -878,6 +882,11 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
 #pragma unroll
                 for (int i = 0; i < G; ++i)
                     reduce(j0 - G + i, rp[i]);
+            }
+            if (j0 + G < CH) {
+#pragma unroll
+                for (int i = 0; i < G; ++i)
+                    addresses(j0 + G + i);
             }
             // Up to 8 events per token, a group whose tokens meet none of
             // their group's earlier ones skips the per-token checks (config

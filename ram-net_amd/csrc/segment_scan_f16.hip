@@ -11,8 +11,8 @@ hipError_t launch_scan_f16(const SegmentJob &job, const ScanGeom &geo, int vec, 
 }
 
 hipError_t launch_scan_pair_f16(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int nw,
-                               int64_t lds_limit, hipStream_t stream) {
-    return scan_pair_dispatch<_Float16>(job, geo, vec, epp, nw, lds_limit, stream);
+                               hipStream_t stream) {
+    return scan_pair_dispatch<_Float16>(job, geo, vec, epp, nw, stream);
 }
 
 }  // namespace ramnet

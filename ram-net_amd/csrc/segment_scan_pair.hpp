@@ -47,26 +47,11 @@ constexpr int scan_pair_chunk_len(int epp) { return 2 * epp < 32 ? 2 * epp : 32;
 __host__ __device__ constexpr size_t scan_pair_stage_bytes(int vec, int epp, int nw, int elem) {
     return static_cast<size_t>(nw) * (kWave / 2 / epp) * vec * 2 * ((scan_pair_chunk_len(epp) / 2) * elem + 16);
 }
-// Row stride (floats) of the paired scan's slot slice. A lane group reads
-// 4 / VEC consecutive channels of a row per token, so a row stride of
-// 4 (mod 8) floats starts every row's window of them at one of 16 aligned
-// bank groups: the rows of one LDS pass then collide less often than at a
-// stride of one pad float (config 2, 8 rows of 4 channels per half wave:
-// 2.07 against 2.35 bank cycles per pass, by simulation of random slots).
-// It takes 4 pad floats per row, so it applies when they fit in LDS.
-__host__ __device__ constexpr int scan_pair_row_stride(int A, int vec, int cs, int epp, int nw, int elem,
-                                                       int64_t lds_limit) {
-    return scan_stage_offset(A, cs + 4, true) + scan_pair_stage_bytes(vec, epp, nw, elem) <=
-                   static_cast<size_t>(lds_limit)
-               ? cs + 4
-               : scan_row_stride(vec, cs);
-}
 // LDS of one workgroup: the slot slice with its two dummy rows, then the
 // staged x.
-inline size_t scan_pair_lds_bytes(int A, int vec, int epp, int nw, int elem, int64_t lds_limit) {
+inline size_t scan_pair_lds_bytes(int A, int vec, int epp, int nw, int elem) {
     const int cs = nw * (kWave / 2 / epp) * vec;
-    const int rs = scan_pair_row_stride(A, vec, cs, epp, nw, elem, lds_limit);
-    return scan_stage_offset(A, rs, true) + scan_pair_stage_bytes(vec, epp, nw, elem);
+    return scan_stage_offset(A, scan_row_stride(vec, cs), true) + scan_pair_stage_bytes(vec, epp, nw, elem);
 }
 
 template<typename Scalar, int VEC, int EPP, int NW, bool FAST>
@@ -101,7 +86,7 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_pair_kernel(const Seg
     const int c0 = (unit - bh * geo.n_slices) * CS;
     const int T = job.T, A = job.A, C = job.C, Tp = geo.t_pad;
     const int EK = job.Kw > job.Kr ? job.Kw : job.Kr;
-    const int RS = geo.row_stride;
+    constexpr int RS = scan_row_stride(VEC, CS);
 
     float *st = lds + 2 * RS;  // slot 0 of the slice; rows -2 (dummy write) and -1 (zero read) in front
     char *stage0 = reinterpret_cast<char *>(lds) + scan_stage_offset(A, RS, true);
@@ -221,8 +206,10 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_pair_kernel(const Seg
                 return half_bits_to_f<Scalar>((wd >> (16 * (s % 2))) & 0xffffu);
         };
         auto &rec = f.rec;
-#pragma unroll
-        for (int s = 0; s < NPS; ++s) {
+        // row addresses of pair s; the first group's before the pair loop,
+        // each later group's during the group before it, where they fill the
+        // wait for that group's rows
+        auto addresses = [&](int s) {
             int wa = rec[s].x, ra = rec[s].z;
             if constexpr (TAIL) {
                 const bool live = t0 + 2 * s + tp < T;
@@ -232,7 +219,7 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_pair_kernel(const Seg
             }
             rec[s].x = mad24(wa, amul, awb);
             rec[s].z = mad24(ra, amul, arb);
-        }
+        };
         auto row = [&](int a) { return lds_at(static_cast<uint32_t>(a)); };
         auto write = [&](int s, const FVec<VEC> &sv, int addr) {
             const float g = __int_as_float(rec[s].y);
@@ -287,6 +274,8 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_pair_kernel(const Seg
                 part[v][s] = __uint_as_float(opaque(__float_as_uint(wgt * rv.v[v])));
         };
         FVec<VEC> rp[2];
+        addresses(0);
+        addresses(1);
 #pragma unroll
         for (int s0 = 0; s0 < NPS; s0 += 2) {
             FVec<VEC> sv0, sv1;
@@ -295,6 +284,10 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_pair_kernel(const Seg
             if (s0 > 0) {
                 reduce(s0 - 2, rp[0]);
                 reduce(s0 - 1, rp[1]);
+            }
+            if (s0 + 2 < NPS) {
+                addresses(s0 + 2);
+                addresses(s0 + 3);
             }
             pair(s0, sv0, rp[0]);
             if (__builtin_expect(((m_rel >> (2 * s0 + 2)) & 3u) != 0, 0)) {
@@ -372,17 +365,11 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_pair_kernel(const Seg
     }
 }
 
-// lds_limit: the LDS a workgroup may take (it decides the row stride, which
-// the kernel reads from the launch geometry).
 template<typename Scalar, int VEC, int EPP, int NW, bool FAST>
-hipError_t launch_scan_pair(const SegmentJob &job, const ScanGeom &geo_in, int64_t lds_limit, hipStream_t stream) {
-    constexpr int CS = NW * (kWave / 2 / EPP) * VEC;
-    constexpr int ES = static_cast<int>(sizeof(Scalar));
-    ScanGeom geo = geo_in;
-    geo.row_stride = scan_pair_row_stride(job.A, VEC, CS, EPP, NW, ES, lds_limit);
+hipError_t launch_scan_pair(const SegmentJob &job, const ScanGeom &geo, hipStream_t stream) {
     const unsigned blocks = static_cast<unsigned>(((geo.n_units + 7) / 8) * 8);
     hipLaunchKernelGGL((segment_scan_pair_kernel<Scalar, VEC, EPP, NW, FAST>), dim3(blocks), dim3(kWave * NW),
-                       scan_pair_lds_bytes(job.A, VEC, EPP, NW, ES, lds_limit), stream, job, geo);
+                       scan_pair_lds_bytes(job.A, VEC, EPP, NW, static_cast<int>(sizeof(Scalar))), stream, job, geo);
     return hipGetLastError();
 }
 
@@ -390,14 +377,14 @@ hipError_t launch_scan_pair(const SegmentJob &job, const ScanGeom &geo_in, int64
 #define RAMNET_SCAN_PAIR_LAYOUTS(X) X(1, 8, 4) X(1, 8, 8) X(1, 16, 4) X(1, 16, 8) X(2, 8, 4) X(2, 16, 2) X(2, 16, 4)
 
 template<typename Scalar>
-hipError_t scan_pair_dispatch(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int nw, int64_t lds_limit,
+hipError_t scan_pair_dispatch(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int nw,
                               hipStream_t stream) {
     const int cs = nw * (kWave / 2 / epp) * vec;
     const bool fast = job.C % cs == 0;
 #define RAMNET_SCAN_PAIR_CASE(V, E, W)                                                                  \
     if (vec == V && epp == E && nw == W)                                                                \
-        return fast ? launch_scan_pair<Scalar, V, E, W, true>(job, geo, lds_limit, stream)              \
-                    : launch_scan_pair<Scalar, V, E, W, false>(job, geo, lds_limit, stream);
+        return fast ? launch_scan_pair<Scalar, V, E, W, true>(job, geo, stream)              \
+                    : launch_scan_pair<Scalar, V, E, W, false>(job, geo, stream);
     RAMNET_SCAN_PAIR_LAYOUTS(RAMNET_SCAN_PAIR_CASE)
 #undef RAMNET_SCAN_PAIR_CASE
     return hipErrorInvalidValue;
@@ -410,8 +397,8 @@ inline bool scan_pair_layout_compiled(int vec, int epp, int nw) {
     return false;
 }
 
-hipError_t launch_scan_pair_f32(const SegmentJob &, const ScanGeom &, int, int, int, int64_t, hipStream_t);
-hipError_t launch_scan_pair_f16(const SegmentJob &, const ScanGeom &, int, int, int, int64_t, hipStream_t);
-hipError_t launch_scan_pair_bf16(const SegmentJob &, const ScanGeom &, int, int, int, int64_t, hipStream_t);
+hipError_t launch_scan_pair_f32(const SegmentJob &, const ScanGeom &, int, int, int, hipStream_t);
+hipError_t launch_scan_pair_f16(const SegmentJob &, const ScanGeom &, int, int, int, hipStream_t);
+hipError_t launch_scan_pair_bf16(const SegmentJob &, const ScanGeom &, int, int, int, hipStream_t);
 
 }  // namespace ramnet
