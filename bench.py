@@ -66,8 +66,10 @@ HBM_PEAK_GBS = 8000.0
 # file records a digest of the kernel sources it was measured with; a line
 # built from other sources reports it as stale.
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "segment_stage_traffic.json")
-TRAFFIC_SOURCES = ("segment_scan.hpp", "segment_forward.hip", "segment_scan_bf16.hip", "ramnet_kernels.hpp",
-                   "ramnet_device.hpp", "topk_addr.hip", "lane_search.hpp", "capi.hip")
+TRAFFIC_SOURCES = ("segment_scan.hpp", "segment_scan_pair.hpp", "segment_forward.hip", "segment_scan_bf16.hip",
+                   "ramnet_kernels.hpp", "ramnet_device.hpp", "topk_addr.hip", "lane_search.hpp", "capi.hip")
+# the scan kernels of the segment stage (one-token, paired, slot-range forms)
+SCAN_KERNELS = ("segment_scan_kernel", "segment_scan_pair_kernel", "segment_scan_range_kernel")
 PROBE_LIB = os.path.join(REPO, "ram-net_amd", "ramnet_ops", "_lib", "libramnet_lds_probe.so")
 METRIC = "prefill tokens/s (T=4096) + decode tokens/s (B=64); % HBM roofline"
 
@@ -146,7 +148,7 @@ def traffic_summary(out_dir: str) -> int:
     --copy-probe 1024``. FETCH_SIZE and WRITE_SIZE (KiB per dispatch,
     medians) are scaled by what they read for the 1 GiB copy."""
     import statistics
-    stage_names = ("segment_scan_kernel", "segment_mass_kernel", "mass_chunk_map_kernel", "mass_chunk_scan_kernel")
+    stage_names = SCAN_KERNELS + ("segment_mass_kernel", "mass_chunk_map_kernel", "mass_chunk_scan_kernel")
 
     def counters(path):
         vals = {}
@@ -166,7 +168,7 @@ def traffic_summary(out_dir: str) -> int:
         part = {"scan": 0.0, "prepass": 0.0, "decoder": 0.0}
         times = {"scan": 0.0, "prepass": 0.0, "decoder": 0.0}
         for k, v in fe.items():
-            which = ("scan" if "segment_scan_kernel" in k else "prepass" if any(n in k for n in stage_names)
+            which = ("scan" if any(n in k for n in SCAN_KERNELS) else "prepass" if any(n in k for n in stage_names)
                      else "decoder" if "topk_addr" in k else None)
             if which is None:
                 continue

@@ -110,9 +110,10 @@ int ramnet_topk_addr_backward(const int32_t *idx, const float *val, const void *
  * Bytes of device workspace the segment scan needs for B x H heads, T tokens
  * and the given top-k when it keeps a head's slot slice resident in one
  * piece (every shape up to A = 8190 slots): the decoder's per-event records
- * (T padded to 32), then the gain records the precomputed-gain form writes.
- * A scan only reads the decoder records, so the same records can be scanned
- * again. The 32-bit form returns -1 when the size does not fit an int. No
+ * (T padded to 32), then the gain records the precomputed-gain form writes,
+ * then one int per token of the read-after-write flags its paired layout
+ * uses. A scan only reads the decoder records, so the same records can be
+ * scanned again. The 32-bit form returns -1 when the size does not fit an int. No
  * counterpart in the reference, which allocates inside its ops
  * (ram_attn_ops.cpp:251-253); ramnet_segment_workspace_bytes sizes any shape.
  */
@@ -274,7 +275,7 @@ int ramnet_topk_autoregressive_steps_(const void *w_addr, const void *r_addr, co
                                       void *stream);
 
 /* Bytes of the per-GPU scratch of ramnet_ram_attn_forward_noalloc (192 MiB:
- * config 2, B=8 H=16 T=4096 K=8 in the precomputed-gain form, needs 160 MiB). */
+ * config 2, B=8 H=16 T=4096 K=8 in the precomputed-gain form, needs 162 MiB). */
 #define RAMNET_NOALLOC_SCRATCH_BYTES (192LL << 20)
 
 /*
@@ -284,8 +285,8 @@ int ramnet_topk_autoregressive_steps_(const void *w_addr, const void *r_addr, co
  * hipMalloc). It allocates nothing: the per-event records live in a
  * file-scope device array of RAMNET_NOALLOC_SCRATCH_BYTES, one per GPU the
  * library runs on, held until the process ends. A shape whose records
- * (B*H*T_pad*(16*w_top_k + 8*r_top_k) bytes, plus B*H*T_pad*16*max(w_top_k,
- * r_top_k) when the scan uses the precomputed-gain form) exceed it returns
+ * (B*H*T_pad*(16*w_top_k + 8*r_top_k) bytes, plus B*H*T_pad*(16*max(w_top_k,
+ * r_top_k) + 4) when the scan uses the precomputed-gain form) exceed it returns
  * RAMNET_EINVAL. The array is part of the library's device code: loading
  * the library's code on a GPU reserves RAMNET_NOALLOC_SCRATCH_BYTES of that
  * GPU's memory until the process ends, whether or not this entry point is

@@ -7,7 +7,7 @@ state must be identical bits. Two calls in a row, the second on a smaller
 input (the scratch keeps the first call's records, which the second must not
 read), then a slot space wide enough for the precomputed-gain form (whose
 gain records also live in the scratch), the full config-2 shape (which plans
-the precomputed-gain form and needs 160 MiB of the 192 MiB scratch), calls
+the precomputed-gain form and needs 162 MiB of the 192 MiB scratch), calls
 without tokens or without batch rows, one call captured in a HIP graph and
 replayed on fresh inputs, and a shape beyond the scratch, which is refused
 on the host before anything is launched.
