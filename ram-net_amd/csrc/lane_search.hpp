@@ -31,6 +31,7 @@
 
 #include <stdint.h>
 #include <type_traits>
+#include <utility>
 
 namespace ramnet {
 
@@ -66,25 +67,52 @@ __device__ __forceinline__ void ce_desc(uint64_t &a, uint64_t &b) {
     b = lo;
 }
 
-// Bitonic sort (descending) of keys [OFF, OFF + N); N a power of two.
-template<int N, int OFF, typename K, int M>
-__device__ __forceinline__ void sort_desc(K (&k)[M]) {
-#pragma unroll
-    for (int kk = 2; kk <= N; kk <<= 1) {
-#pragma unroll
-        for (int j = kk >> 1; j > 0; j >>= 1) {
-#pragma unroll
-            for (int i = 0; i < N; ++i) {
-                const int l = i ^ j;
-                if (l > i) {
-                    if ((i & kk) == 0)
-                        ce_desc(k[OFF + i], k[OFF + l]);
-                    else
-                        ce_desc(k[OFF + l], k[OFF + i]);
-                }
+// Batcher's odd-even merge sort network on N = 2^n keys, generated at
+// compile time: comparator c orders positions (a[c], b[c]), a < b. It takes
+// 19 compare-exchanges for 8 keys and 63 for 16, where the bitonic network
+// takes 24 and 80.
+template<int N>
+struct SortNet {
+    int a[N * N > 0 ? N * N : 1] = {};
+    int b[N * N > 0 ? N * N : 1] = {};
+    int n = 0;
+    constexpr SortNet() { sort_range(0, N - 1); }
+    constexpr void merge(int lo, int hi, int r) {
+        const int step = r * 2;
+        if (step < hi - lo) {
+            merge(lo, hi, step);
+            merge(lo + r, hi, step);
+            for (int i = lo + r; i < hi - r; i += step) {
+                a[n] = i;
+                b[n] = i + r;
+                ++n;
             }
+        } else {
+            a[n] = lo;
+            b[n] = lo + r;
+            ++n;
         }
     }
+    constexpr void sort_range(int lo, int hi) {
+        if (hi - lo >= 1) {
+            const int mid = lo + (hi - lo) / 2;
+            sort_range(lo, mid);
+            sort_range(mid + 1, hi);
+            merge(lo, hi, 1);
+        }
+    }
+};
+template<int N, int OFF, typename K, int M, int... C>
+__device__ __forceinline__ void sort_net_apply(K (&k)[M], std::integer_sequence<int, C...>) {
+    constexpr SortNet<N> net{};
+    (ce_desc(k[OFF + net.a[C]], k[OFF + net.b[C]]), ...);
+}
+
+// Descending sort of keys [OFF, OFF + N); N a power of two.
+template<int N, int OFF, typename K, int M>
+__device__ __forceinline__ void sort_desc(K (&k)[M]) {
+    if constexpr (N > 1)
+        sort_net_apply<N, OFF>(k, std::make_integer_sequence<int, SortNet<N>().n>{});
 }
 
 // a <- sorted top-KM of sorted a and the sorted group [OFF, OFF + KM) of b.
@@ -292,27 +320,124 @@ __device__ __forceinline__ bool digit_top(const Load &load, int u, int P_, float
     return live;
 }
 
+// The staircase row merge. Row i of the staircase (prefix i with digit
+// entries j < KM / (i + 1)) is already sorted: the prefix score is fixed and
+// the digit's log-probabilities descend with j (equal sums from distinct
+// log-probabilities, where fp32 rounding absorbs their difference, can
+// break the content-index order of a tie, which the parity bar allows). So
+// the top KM of the staircase is a merge of sorted lists, not a sort: rows
+// [LO, HI) are merged recursively, each list padded with empty keys to a
+// power of two, keeping the top KM. KM = 16: about half the compare-
+// exchanges of sorting the 50 candidates in groups.
+template<int KM>
+constexpr int stair_row_len(int i) { return KM / (i + 1); }
+constexpr int pow2_up(int n) { return n <= 1 ? 1 : 2 * pow2_up((n + 1) / 2); }
+template<int KM, int LO, int HI>
+constexpr int stair_list_len() {
+    if constexpr (HI - LO == 1) {
+        return pow2_up(stair_row_len<KM>(LO));
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        constexpr int A = stair_list_len<KM, LO, MID>(), B = stair_list_len<KM, MID, HI>();
+        constexpr int L = 2 * (A > B ? A : B);
+        return L < KM ? L : KM;
+    }
+}
+template<int N>
+struct KeyList {
+    uint64_t k[N];
+};
+// Descending bitonic merge of a bitonic list of N (a power of two).
+template<int N>
+__device__ __forceinline__ void bitonic_merge_desc(uint64_t (&k)[N]) {
+#pragma unroll
+    for (int j = N >> 1; j > 0; j >>= 1) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int l = i ^ j;
+            if (l > i)
+                ce_desc(k[i], k[l]);
+        }
+    }
+}
+// Top min(KM, 2 max(NA, NB)) of two sorted lists, sorted. Entries of the
+// shorter list past its length are empty and take no compare.
+template<int KM, int NA, int NB>
+__device__ __forceinline__ auto merge_lists(const KeyList<NA> &a, const KeyList<NB> &b) {
+    if constexpr (NA < NB) {
+        return merge_lists<KM, NB, NA>(b, a);
+    } else {
+        constexpr int L = 2 * NA <= KM ? 2 * NA : KM;
+        KeyList<L> out;
+        if constexpr (L == 2 * NA) {
+            // a then reversed b: bitonic; its first stage pairs a[i] with b[NA - 1 - i]
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                const int jb = NA - 1 - i;
+                if (jb < NB) {
+                    uint64_t x = a.k[i], y = b.k[jb];
+                    ce_desc(x, y);
+                    out.k[i] = x;
+                    out.k[NA + i] = y;
+                } else {
+                    out.k[i] = a.k[i];
+                    out.k[NA + i] = 0;
+                }
+            }
+            KeyList<NA> lo, hi;
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                hi.k[i] = out.k[i];
+                lo.k[i] = out.k[NA + i];
+            }
+            bitonic_merge_desc<NA>(hi.k);
+            bitonic_merge_desc<NA>(lo.k);
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                out.k[i] = hi.k[i];
+                out.k[NA + i] = lo.k[i];
+            }
+        } else {
+            // NA == KM: the larger of a[i] and b[KM - 1 - i] are the top KM, bitonic
+#pragma unroll
+            for (int i = 0; i < KM; ++i) {
+                const int jb = KM - 1 - i;
+                out.k[i] = jb < NB ? key_max(a.k[i], b.k[jb]) : a.k[i];
+            }
+            bitonic_merge_desc<KM>(out.k);
+        }
+        return out;
+    }
+}
+// Candidate keys of staircase rows [LO, HI), merged.
+template<int KM, int LO, int HI, typename RowKey>
+__device__ __forceinline__ KeyList<stair_list_len<KM, LO, HI>()> stair_rows(const RowKey &key) {
+    if constexpr (HI - LO == 1) {
+        constexpr int N = stair_list_len<KM, LO, HI>();
+        KeyList<N> r;
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+            r.k[j] = j < stair_row_len<KM>(LO) ? key(LO, j) : 0;
+        return r;
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        return merge_lists<KM>(stair_rows<KM, LO, MID>(key), stair_rows<KM, MID, HI>(key));
+    }
+}
+
 // Prefix (score sv, content cv) x digit (lv, dv) over the staircase ->
 // sorted top-KM new prefix. `stride` is P^u of the digit.
 template<int KM>
 __device__ __forceinline__ void combine_prefix(float (&sv)[KM], int (&cv)[KM], uint32_t (&ok)[KM],
                                                const float (&lv)[KM], const int (&dv)[KM], const uint32_t (&dok)[KM],
                                                int stride) {
-    constexpr int NC = stair_count<KM>();
-    constexpr int NG = (NC + KM - 1) / KM * KM;
-    uint64_t cand[NG];
-#pragma unroll
-    for (int n = 0; n < NG; ++n) {
-        if (n < NC) {
-            const int i = stair_i<KM>(n), j = stair_j<KM>(n);
-            const uint64_t m = ok[i] & dok[j];
-            cand[n] = prefix_key(sv[i] + lv[j], cv[i] + stride * dv[j]) & ((m << 32) | m);
-        } else {
-            cand[n] = 0;
-        }
-    }
-    uint64_t top[KM];
-    top_keys<KM>(cand, top);
+    auto key = [&](int i, int j) -> uint64_t {
+        const uint64_t m = ok[i] & dok[j];
+        return prefix_key(sv[i] + lv[j], cv[i] + stride * dv[j]) & ((m << 32) | m);
+    };
+    const auto merged = stair_rows<KM, 0, KM>(key);
+    static_assert(stair_list_len<KM, 0, KM>() == KM, "the staircase merge keeps KM keys");
+    const uint64_t(&top)[KM] = merged.k;
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
         ok[k] = top[k] != 0 ? ~0u : 0u;
