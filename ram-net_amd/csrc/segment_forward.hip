@@ -249,15 +249,18 @@ bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, i
 // write events compared per token for the overlap flags (8 or 16, >= Kw).
 template<typename Scalar, int KF>
 __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, int t_pad) {
-    const int Kt = job.Kw + job.Kr;
-    const int64_t n = static_cast<int64_t>(job.B) * job.H * Kt * t_pad;
-    const int64_t gid0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    // 32-bit index arithmetic: the host checks that B*H*T_pad*(Kw + Kr) fits
+    // an int (a 64-bit division costs far more than the rest of a thread)
+    const uint32_t Kt = static_cast<uint32_t>(job.Kw + job.Kr);
+    const uint32_t n = static_cast<uint32_t>(job.B) * static_cast<uint32_t>(job.H) * Kt * static_cast<uint32_t>(t_pad);
+    const uint32_t gid0 = blockIdx.x * blockDim.x + threadIdx.x;
     const bool in = gid0 < n;
-    const int64_t gid = in ? gid0 : n - 1;  // lanes past the end follow along (the flags' shuffles)
-    const int t = static_cast<int>(gid % t_pad);
-    const int64_t rest = gid / t_pad;
-    const int k = static_cast<int>(rest % Kt);
-    const int bh = static_cast<int>(rest / Kt);
+    const uint32_t gid = in ? gid0 : n - 1;  // lanes past the end follow along (in the ballot)
+    const uint32_t rest = gid / static_cast<uint32_t>(t_pad);
+    const int t = static_cast<int>(gid - rest * static_cast<uint32_t>(t_pad));
+    const uint32_t bhu = rest / Kt;
+    const int k = static_cast<int>(rest - bhu * Kt);
+    const int bh = static_cast<int>(bhu);
     const int b = bh / job.H;
     const int T = job.T, A = job.A;
     const int tl = t < T ? t : T - 1;
@@ -270,35 +273,41 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
     // Event 0 carries the token's overlap flags, which the scan reads: bit
     // d - 1 set if a slot this token writes is also written by token t - d
     // (d = 1, 2, 3). Computed exactly for top-K up to 16 (assumed for wider
-    // top-K), by whole waves: each lane reads its own token's write slots and
-    // takes those of tokens t - d from the lane d back (the same row of the
-    // grid when t >= d), reading them itself in the wave's first d lanes.
+    // top-K), by whole waves: each lane reads the write slots of its own
+    // token and of the three before it. Every load is issued
+    // unconditionally from clamped indices (neighbouring lanes read the same
+    // records, from cache): a load under a lane condition would be waited
+    // for inside its branch, one round trip at a time.
     int ov = 7;
     if (__ballot(in && k == 0 && job.Kw <= 16) != 0) {
-        // slot written by write event kk of token tt (tt < T), or -1
+        // slot written by write event kk of token tt, or -1
         auto written = [&](int tt, int kk) {
             const int64_t s = (static_cast<int64_t>(bh) * Kt + kk) * T + tt;
             const int aa = job.addr_idx[s] - bh * A;
-            const uint8_t *m = job.mask ? job.mask + static_cast<int64_t>(b) * T + tt : &kScanAllValid;
-            return *m != 0 && static_cast<unsigned>(aa) < static_cast<unsigned>(A) && job.addr_val[s] != 0.f ? aa
-                                                                                                              : -1;
+            return static_cast<unsigned>(aa) < static_cast<unsigned>(A) && job.addr_val[s] != 0.f ? aa : -1;
         };
-        const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+        auto unmasked = [&](int tt) {
+            const uint8_t *m = job.mask ? job.mask + static_cast<int64_t>(b) * T + tt : &kScanAllValid;
+            return *m != 0;
+        };
+        const int kl = job.Kw - 1;
         int cur[KF];
+        const bool mine = t < T && unmasked(tl);
 #pragma unroll
-        for (int i = 0; i < KF; ++i)
-            cur[i] = i < job.Kw && t < T ? written(t, i) : -1;
+        for (int i = 0; i < KF; ++i) {
+            const int x = written(tl, min(i, kl));
+            cur[i] = i < job.Kw && mine ? x : -1;
+        }
         ov = 0;
 #pragma unroll
         for (int d = 1; d <= 3; ++d) {
+            const int tq = tl - d > 0 ? tl - d : 0;
+            const bool theirs = t < T && t >= d && unmasked(tq);
             bool hit = false;
 #pragma unroll
             for (int i = 0; i < KF; ++i) {
-                int x = __shfl_up(cur[i], d);
-                if (t < d || t >= T)
-                    x = -1;
-                else if (lane < d)
-                    x = i < job.Kw ? written(t - d, i) : -1;
+                int x = written(tq, min(i, kl));
+                x = i < job.Kw && theirs ? x : -1;
 #pragma unroll
                 for (int j = 0; j < KF; ++j)
                     hit = hit || (x >= 0 && x == cur[j]);
@@ -320,6 +329,99 @@ __global__ __launch_bounds__(256) void pack_records_kernel(const PackJob job, in
         const float r = -v;
         const bool act = live && r != 0.f;
         job.rrec[(static_cast<int64_t>(bh) * job.Kr + (k - job.Kw)) * t_pad + t] = act ? ReadRec{a, r} : ReadRec{-1, 0.f};
+    }
+}
+
+// The same records, one thread per (b*H + h, t) with t < T_pad, for top-K up
+// to KE (8 or 16) on both sides: every load of a token -- its events, and
+// the write events of the three tokens before it for the overlap flags -- is
+// issued up front from clamped indices, then its Kw + Kr records are stored.
+// A thread per event (above) leaves each thread one load and one store, so
+// its waves sit on memory latency (config 2: 88 us a call).
+template<typename Scalar, int KE>
+__global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob job, int t_pad) {
+    const uint32_t n = static_cast<uint32_t>(job.B) * static_cast<uint32_t>(job.H) * static_cast<uint32_t>(t_pad);
+    const uint32_t gid0 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid0 >= n)
+        return;
+    const uint32_t bhu = gid0 / static_cast<uint32_t>(t_pad);
+    const int t = static_cast<int>(gid0 - bhu * static_cast<uint32_t>(t_pad));
+    const int bh = static_cast<int>(bhu);
+    const int b = bh / job.H;
+    const int T = job.T, A = job.A, Kw = job.Kw, Kr = job.Kr, Kt = Kw + Kr;
+    const int tl = t < T ? t : T - 1;
+    const int32_t *ip = job.addr_idx + static_cast<int64_t>(bh) * Kt * T;
+    const float *vp = job.addr_val + static_cast<int64_t>(bh) * Kt * T;
+    const uint8_t *mrow = job.mask ? job.mask + static_cast<int64_t>(b) * T : nullptr;
+    auto unmasked = [&](int tt) { return *(mrow ? mrow + tt : &kScanAllValid) != 0; };
+    // this token's events (write events 0..Kw-1, then read events), clamped
+    int ia[2 * KE];
+    float va[2 * KE];
+#pragma unroll
+    for (int e = 0; e < 2 * KE; ++e) {
+        const int k = e < KE ? min(e, Kw - 1) : Kw + min(e - KE, Kr - 1);
+        ia[e] = ip[static_cast<int64_t>(k) * T + tl];
+        va[e] = vp[static_cast<int64_t>(k) * T + tl];
+    }
+    // the write slots of tokens t - 1, t - 2, t - 3 (clamped to token 0)
+    int pa[3][KE];
+    bool pon[3];
+    float pv[3][KE];
+#pragma unroll
+    for (int d = 1; d <= 3; ++d) {
+        const int tq = tl - d > 0 ? tl - d : 0;
+        pon[d - 1] = t < T && t >= d && unmasked(tq);
+#pragma unroll
+        for (int e = 0; e < KE; ++e) {
+            const int k = min(e, Kw - 1);
+            pa[d - 1][e] = ip[static_cast<int64_t>(k) * T + tq];
+            pv[d - 1][e] = vp[static_cast<int64_t>(k) * T + tq];
+        }
+    }
+    const float g = load_f32(static_cast<const Scalar *>(job.gamma) + static_cast<int64_t>(bh) * T + tl);
+    const bool live = t < T && unmasked(tl);
+    const int base = bh * A;
+    // slot written by event e (or -1): in range, with a nonzero weight
+    auto wslot = [&](int a, float v) {
+        const int o = a - base;
+        return static_cast<unsigned>(o) < static_cast<unsigned>(A) && v != 0.f ? o : -1;
+    };
+    int ov = 0;
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        bool hit = false;
+#pragma unroll
+        for (int i = 0; i < KE; ++i) {
+            const int x = i < Kw && pon[d] ? wslot(pa[d][i], pv[d][i]) : -1;
+#pragma unroll
+            for (int j = 0; j < KE; ++j) {
+                const int y = j < Kw && live ? wslot(ia[j], va[j]) : -1;
+                hit = hit || (x >= 0 && x == y);
+            }
+        }
+        ov |= hit ? 1 << d : 0;
+    }
+    const float overlap = __int_as_float(ov);
+#pragma unroll
+    for (int e = 0; e < KE; ++e) {
+        if (e < Kw) {
+            const int a = ia[e] - base;
+            const float v = va[e];
+            const bool act = live && static_cast<unsigned>(a) < static_cast<unsigned>(A) && v != 0.f;
+            WriteRec rec{-2, 0.f, 1.f, overlap};
+            if (act)
+                rec = WriteRec{a, v, gsu_alpha(v, g), overlap};
+            job.wrec[(static_cast<int64_t>(bh) * Kw + e) * t_pad + t] = rec;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < KE; ++e) {
+        if (e < Kr) {
+            const int a = ia[KE + e] - base;
+            const float r = -va[KE + e];  // reads were stored negated
+            const bool act = live && static_cast<unsigned>(a) < static_cast<unsigned>(A) && r != 0.f;
+            job.rrec[(static_cast<int64_t>(bh) * Kr + e) * t_pad + t] = act ? ReadRec{a, r} : ReadRec{-1, 0.f};
+        }
     }
 }
 
@@ -1106,10 +1208,19 @@ hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *m
 
 template<typename Scalar>
 hipError_t launch_pack(const PackJob &job, unsigned blocks, int t_pad, hipStream_t stream) {
-    if (job.Kw <= 8)
+    const int ke = std::max(job.Kw, job.Kr);
+    if (ke <= 16) {
+        const int64_t n = static_cast<int64_t>(job.B) * job.H * t_pad;
+        const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+        if (ke <= 8)
+            hipLaunchKernelGGL((pack_token_records_kernel<Scalar, 8>), grid, dim3(256), 0, stream, job, t_pad);
+        else
+            hipLaunchKernelGGL((pack_token_records_kernel<Scalar, 16>), grid, dim3(256), 0, stream, job, t_pad);
+    } else if (job.Kw <= 8) {
         hipLaunchKernelGGL((pack_records_kernel<Scalar, 8>), dim3(blocks), dim3(256), 0, stream, job, t_pad);
-    else
+    } else {
         hipLaunchKernelGGL((pack_records_kernel<Scalar, 16>), dim3(blocks), dim3(256), 0, stream, job, t_pad);
+    }
     return hipGetLastError();
 }
 
