@@ -81,10 +81,11 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
 template<typename Scalar, int NP, int KM, bool FAST>
 // Occupancy: the per-lane search holds its digit in registers (about 210
 // VGPRs unconstrained, two waves per SIMD). Capping it at 168 (three waves)
-// costs a few spills and hides more of the sort chains' latency; the FAST
-// form with K <= 8 fits 128 (four waves) with a few spills (config 2
-// decoder: 0.092 -> 0.088 ms).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(FAST && KM <= 8 ? 4 : 3))) void topk_addr_lane_kernel(
+// hides more of the sort chains' latency at the cost of a few spills at
+// K = 16. With the staircase merge, config 2 (K = 8) fits 168 without
+// spilling, and measures faster there than capped at 128 with a few spills
+// (four waves per SIMD): 0.086 -> 0.081 ms.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void topk_addr_lane_kernel(
     const AddrJob job) {
     const AddrSource &src = job.src[blockIdx.y];
     const int T = job.T, H = job.H, U = job.U, P = job.P, A = job.A;
