@@ -294,11 +294,15 @@ def bench_prefill(steps, warmup, dev, c=C2):
 def bench_train(steps, warmup, dev, c=C2):
     """One training step of the operator at a prefill config: the
     differentiable forward (decoder ops ``topk_addr_forward`` +
-    ``topk_segment_forward``) and its backward (``topk_segment_backward`` +
-    ``topk_addr_backward``), the op sequence autograd runs for
-    ``random_access_memory_attention``. Gradients of y come in as N(0,1)
-    bf16; the final-state gradients are zero (None)."""
+    ``topk_segment_forward_saved``, which keeps the rows its backward needs)
+    and its backward (``topk_segment_backward_saved`` + ``topk_addr_backward``),
+    the op sequence autograd runs for ``random_access_memory_attention`` at
+    this shape (the recompute pair ``topk_segment_forward`` /
+    ``topk_segment_backward`` where the saved pair does not apply).
+    Gradients of y come in as N(0,1) bf16; the final-state gradients are zero
+    (None)."""
     import ramnet_ops  # noqa: F401
+    from ramnet_ops import _native as nat
     ops = torch.ops.ramnet_ops
     B, H, T, C, U, P, K = c["B"], c["H"], c["T"], c["C"], c["U"], c["P"], c["K"]
     A = P ** U
@@ -310,14 +314,24 @@ def bench_train(steps, warmup, dev, c=C2):
     dy = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16).to(dev)
     shape = [B, H, U, P, A, T]
 
+    saved_pair = nat.segment_saved_bytes(B, H, T, A, C, K, K, d["x"].dtype) >= 0
+
     def step(ev):
         ev[0].record()
         idx, val = ops.topk_addr_forward(d["w"], d["r"], E, A, d["pos"], K, K, 0.0, 0.0)
         ev[1].record()
-        ops.topk_segment_forward(idx, val, d["x"], d["gamma"], slot0, mass0, None, K, K, False, 1e-12)
-        ev[2].record()
-        dval = ops.topk_segment_backward(idx, val, d["x"], d["gamma"], slot0, mass0, None, dy, None, None, K, K,
-                                         False, 1e-12)[0]
+        if saved_pair:
+            saved = ops.topk_segment_forward_saved(idx, val, d["x"], d["gamma"], slot0, mass0, None, K, K, False,
+                                                   1e-12)[3]
+            ev[2].record()
+            dval = ops.topk_segment_backward_saved(val, d["x"], d["gamma"], slot0, mass0, saved, dy, None, None, K,
+                                                   K, False, 1e-12)[0]
+            del saved
+        else:
+            ops.topk_segment_forward(idx, val, d["x"], d["gamma"], slot0, mass0, None, K, K, False, 1e-12)
+            ev[2].record()
+            dval = ops.topk_segment_backward(idx, val, d["x"], d["gamma"], slot0, mass0, None, dy, None, None, K, K,
+                                             False, 1e-12)[0]
         ev[3].record()
         ops.topk_addr_backward(idx, val, d["w"], d["r"], dval, E, d["pos"], K, K, 0.0, 0.0, shape, d["w"].dtype)
         ev[4].record()
@@ -338,6 +352,8 @@ def bench_train(steps, warmup, dev, c=C2):
         "workload": f"config {c.get('name', 2)} training step of the operator: decoder + segment forward, segment "
                     f"backward + decoder backward; B={B}, H={H}, T={T}, d_v={C}, A={A}, K={K}, bf16 activations, "
                     "gradient of y ~ N(0,1), none on the final state",
+        "segment_pair": "saved rows (topk_segment_forward_saved / topk_segment_backward_saved)" if saved_pair
+                        else "recompute (topk_segment_forward / topk_segment_backward)",
         "ms_per_step": ms,
         "tokens_per_s": B * T / (ms / 1e3),
         "decoder_forward_ms": stage[0],

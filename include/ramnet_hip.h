@@ -201,6 +201,49 @@ int64_t ramnet_segment_backward_workspace_bytes(int64_t B, int64_t H, int64_t T,
                                                 int64_t w_top_k, int64_t r_top_k);
 
 /*
+ * Training pair with saved rows: a forward that keeps what the backward
+ * would otherwise recompute, and the backward that uses it. No counterpart
+ * in the reference, whose backward reconstructs the forward
+ * (ram_attn_segment_parallel.cu:418-606); the outputs are those of
+ * ramnet_topk_segment_forward and ramnet_topk_segment_backward
+ * (ram_attn_bind.cpp:65-82) on the same inputs, to fp32 rounding. For
+ * training callers with memory to spare: the saved buffer holds the scan
+ * records plus two fp32 arrays of B*H*T_pad*kp*C*4 bytes (x - s before each
+ * write, the row of each read; kp = max(Kw, Kr) rounded up to the backward's
+ * event slots, T_pad = T rounded up to 32): 4.4 GB at B=8, H=16, T=4096,
+ * C=128, K=8. One backward pass over the sequence then replaces the
+ * backward's replay of the forward.
+ *
+ * ramnet_segment_saved_bytes: bytes of the saved buffer, or -1 where the pair
+ * does not apply (the forward must run a one-token precomputed-gain scan
+ * over the whole slot space with whole channel slices; B, T > 0). Callers
+ * fall back to ramnet_topk_segment_forward/_backward there.
+ * ramnet_topk_segment_forward_save: arguments of ramnet_topk_segment_forward
+ * plus `saved` (written; kept unchanged until the backward).
+ * ramnet_topk_segment_backward_saved: arguments of
+ * ramnet_topk_segment_backward without addr_idx and mask (the records are in
+ * `saved`), plus `saved`; its workspace is
+ * ramnet_segment_backward_saved_workspace_bytes(...) bytes.
+ */
+int64_t ramnet_segment_saved_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
+                                   int64_t r_top_k, int dtype);
+int ramnet_topk_segment_forward_save(const int32_t *addr_idx, const float *addr_val, const void *x,
+                                     const void *gamma, int dtype, const uint8_t *mask, const float *init_slot,
+                                     const float *init_mass, float *slot_out, float *mass_out, void *y, int64_t B,
+                                     int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k,
+                                     int mass_aware, float eps, void *workspace, int64_t workspace_bytes, void *saved,
+                                     int64_t saved_bytes, void *stream);
+int64_t ramnet_segment_backward_saved_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                                                      int64_t w_top_k, int64_t r_top_k);
+int ramnet_topk_segment_backward_saved(const float *addr_val, const void *x, const void *gamma, int dtype,
+                                       const float *init_slot, const float *init_mass, const void *grad_y,
+                                       const float *grad_slot, const float *grad_mass, float *grad_addr_val,
+                                       float *grad_x, float *grad_gamma, float *grad_init_slot, float *grad_init_mass,
+                                       int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
+                                       int64_t r_top_k, int mass_aware, float eps, const void *saved,
+                                       int64_t saved_bytes, void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
  * The two stages of ramnet_ram_attn_forward, for callers that schedule or
  * time them separately. ramnet_topk_addr_records runs both address decoders
  * and writes the scan's per-event records into `workspace` (CAPE, mask,

@@ -576,6 +576,122 @@ int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val,
     return finish(err, why, "topk_segment_backward launch");
 }
 
+// ---- training pair with saved rows. The saved buffer holds the scan
+// records, then x - s of every write row and every read row, in the
+// backward's channel slices (SavedRows), each part 256-byte aligned.
+static bool saved_layout(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t Kw, int64_t Kr, int dtype,
+                         ramnet::SavedRows *geo, int64_t *rec_bytes, int64_t *row_bytes) {
+    if (B <= 0 || H <= 0 || T <= 0 || A <= 0 || A >= kAddressLimit || C <= 0 || Kw <= 0 || Kr <= 0 || Kw > A ||
+        Kr > A || !valid_dtype(dtype) ||
+        !fits_int({B * H * A * C, B * H * (A + 2), B * H * T * C, B * H * (T + ramnet::kScanPad) * (Kw + Kr)}))
+        return false;
+    if (backward_workspace_bytes(B, H, T, A, C, Kw, Kr) < 0 ||
+        !ramnet::segment_saved_slices(static_cast<int>(A), static_cast<int>(C), static_cast<int>(Kw),
+                                      static_cast<int>(Kr), geo) ||
+        !ramnet::segment_forward_can_save(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T),
+                                          static_cast<int>(A), static_cast<int>(C), static_cast<int>(Kw),
+                                          static_cast<int>(Kr), dtype, *geo))
+        return false;
+    *rec_bytes = (ramnet::scan_record_bytes(B, H, T, Kw, Kr) + 255) / 256 * 256;
+    *row_bytes = (B * H * geo->n_sub * ramnet::scan_t_pad64(T) * geo->kp * geo->csw * 4 + 255) / 256 * 256;
+    return true;
+}
+
+int64_t ramnet_segment_saved_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
+                                   int64_t r_top_k, int dtype) {
+    ramnet::SavedRows geo{};
+    int64_t rec = 0, rows = 0;
+    return saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &rec, &rows) ? rec + 2 * rows : -1;
+}
+
+int ramnet_topk_segment_forward_save(const int32_t *addr_idx, const float *addr_val, const void *x,
+                                     const void *gamma, int dtype, const uint8_t *mask, const float *init_slot,
+                                     const float *init_mass, float *slot_out, float *mass_out, void *y, int64_t B,
+                                     int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k, int64_t r_top_k,
+                                     int mass_aware, float eps, void *workspace, int64_t workspace_bytes, void *saved,
+                                     int64_t saved_bytes, void *stream) {
+    if (int rc = segment_checks(x, gamma, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C, w_top_k,
+                                r_top_k, eps, workspace, workspace_bytes))
+        return rc;
+    ramnet::SavedRows geo{};
+    int64_t rec = 0, rows = 0;
+    RAMNET_REQUIRE(saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &rec, &rows),
+                   "topk_segment_forward_save: no saved-row form for this shape (ramnet_segment_saved_bytes < 0)");
+    RAMNET_REQUIRE(saved && saved_bytes >= rec + 2 * rows, "saved buffer too small: see ramnet_segment_saved_bytes");
+    RAMNET_REQUIRE(addr_idx && addr_val, "null tensor pointer");
+    ramnet::SegmentJob job = make_segment_job(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C,
+                                              w_top_k, r_top_k, mass_aware, eps, workspace);
+    char *sv = static_cast<char *>(saved);
+    job.wrec = reinterpret_cast<const ramnet::WriteRec *>(sv);
+    job.rrec = reinterpret_cast<const ramnet::ReadRec *>(sv + B * H * ramnet::scan_t_pad64(T) * w_top_k *
+                                                               static_cast<int64_t>(sizeof(ramnet::WriteRec)));
+    geo.w = reinterpret_cast<float *>(sv + rec);
+    geo.r = reinterpret_cast<float *>(sv + rec + rows);
+    job.save = geo;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const char *why = nullptr;
+    hipError_t err = pack_decoded(job, addr_idx, addr_val, gamma, mask, s, &why);
+    if (err == hipSuccess)
+        err = ramnet::launch_segment_forward(job, s, &why);
+    return finish(err, why, "topk_segment_forward_save launch");
+}
+
+int64_t ramnet_segment_backward_saved_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C,
+                                                      int64_t w_top_k, int64_t r_top_k) {
+    if (backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k) < 0)
+        return -1;
+    return ramnet::segment_backward_layout(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T),
+                                           static_cast<int>(A), static_cast<int>(C), static_cast<int>(w_top_k),
+                                           static_cast<int>(r_top_k), nullptr, nullptr, true);
+}
+
+int ramnet_topk_segment_backward_saved(const float *addr_val, const void *x, const void *gamma, int dtype,
+                                       const float *init_slot, const float *init_mass, const void *grad_y,
+                                       const float *grad_slot, const float *grad_mass, float *grad_addr_val,
+                                       float *grad_x, float *grad_gamma, float *grad_init_slot, float *grad_init_mass,
+                                       int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
+                                       int64_t r_top_k, int mass_aware, float eps, const void *saved,
+                                       int64_t saved_bytes, void *workspace, int64_t workspace_bytes, void *stream) {
+    const int64_t need = ramnet_segment_backward_saved_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k);
+    if (int rc = segment_checks(x, gamma, dtype, init_slot, init_mass, grad_init_slot, grad_init_mass, grad_x, B, H,
+                                T, A, C, w_top_k, r_top_k, eps, workspace, workspace_bytes, need < 0 ? 0 : need))
+        return rc;
+    ramnet::SavedRows geo{};
+    int64_t rec = 0, rows = 0;
+    RAMNET_REQUIRE(need >= 0 && saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &rec, &rows),
+                   "topk_segment_backward_saved: no saved-row form for this shape (ramnet_segment_saved_bytes < 0)");
+    RAMNET_REQUIRE(saved && saved_bytes >= rec + 2 * rows, "saved buffer too small: see ramnet_segment_saved_bytes");
+    RAMNET_REQUIRE(workspace_bytes >= need && workspace,
+                   "workspace too small: see ramnet_segment_backward_saved_workspace_bytes");
+    RAMNET_REQUIRE(addr_val && grad_y && grad_addr_val && grad_gamma, "null tensor pointer");
+    // the records were packed into the saved buffer by the forward
+    ramnet::SegmentJob fj = make_segment_job(x, dtype, init_slot, init_mass, nullptr, nullptr, nullptr, B, H, T, A, C,
+                                             w_top_k, r_top_k, mass_aware, eps, const_cast<void *>(saved));
+    fj.gain = nullptr;
+    fj.flags = nullptr;
+    ramnet::SegmentBwdJob job{};
+    job.fwd = fj;
+    job.addr_val = addr_val;
+    job.gamma = gamma;
+    job.grad_y = grad_y;
+    job.grad_slot = grad_slot;
+    job.grad_mass = grad_mass;
+    job.grad_val = grad_addr_val;
+    job.grad_x = grad_x;
+    job.grad_gamma = grad_gamma;
+    job.grad_init_slot = grad_init_slot;
+    job.grad_init_mass = grad_init_mass;
+    ramnet::segment_backward_layout(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T), static_cast<int>(A),
+                                    static_cast<int>(C), static_cast<int>(w_top_k), static_cast<int>(r_top_k),
+                                    static_cast<char *>(workspace), &job, true);
+    const char *sv = static_cast<const char *>(saved);
+    job.delta = reinterpret_cast<float *>(const_cast<char *>(sv) + rec);
+    job.saved_r = reinterpret_cast<const float *>(sv + rec + rows);
+    const char *why = nullptr;
+    const hipError_t err = ramnet::launch_segment_backward(job, static_cast<hipStream_t>(stream), &why);
+    return finish(err, why, "topk_segment_backward_saved launch");
+}
+
 // Checks and job of one decode step (S = 1) or S steps of one shape.
 static int decode_job(const void *w_addr, const void *r_addr, const void *x, const void *gamma, int dtype,
                       float *slot, float *mass, const uint8_t *mask, int64_t embed_num, const int32_t *position_ids,

@@ -111,6 +111,16 @@ struct AddrBwdJob {
     float sign;
 };
 
+// Rows a training forward saves for the segment backward, laid out in the
+// backward's channel slices: (B*H*n_sub, T_pad, kp, csw) floats each, n_sub
+// slices of csw channels (a power of two), kp padded event slots per token,
+// T_pad = scan_t_pad(T) (the padding tokens' rows are written, never read).
+struct SavedRows {
+    float *w;  // per write event: x_t - s before the write; null: nothing saved
+    float *r;  // per read event: the row read, after the token's writes
+    int n_sub, kp, csw;
+};
+
 // Time-sequential gated sparse update + top-K read over a whole sequence.
 struct SegmentJob {
     const WriteRec *wrec;     // (B*H, Kw, T_pad) scan records
@@ -130,6 +140,7 @@ struct SegmentJob {
     // the token before (or if that is not known), else 0. Written by the mass
     // pre-pass for the paired scan (segment_scan_pair.hpp); null otherwise.
     int *flags;
+    SavedRows save;           // rows for the segment backward (save.w null: none)
     int dtype;
     int B, H, T, A, C, Kw, Kr;
     int mass_aware;
@@ -159,7 +170,8 @@ struct SegmentBwdJob {
     float *grad_gamma;        // (B, H, T)
     float *grad_init_slot;    // (B, H, A, C)
     float *grad_init_mass;    // (B, H, A)
-    float *delta;             // (B*H*n_sub, T, KP, CSW) x - s before each write (KP: padded event count)
+    float *delta;             // (B*H*n_sub, T_pad, KP, CSW) x - s before each write (KP: padded event count)
+    const float *saved_r;     // same layout: the rows read, saved by the forward (then delta too); else null
     float *dr_part;           // (n_sub, B*H, T_pad, KP) per-slice read dot products
     float *dg_part;           // (n_sub, B*H, T_pad, KP) per-slice gain gradients
     float *dr_sum;            // (B*H, T, Kr) read dot products d_j
@@ -234,7 +246,17 @@ hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *m
 // and returns their total size in bytes (-1: shape not supported); with a
 // null `base` it only sizes. The launch expects the scan records already
 // packed into job.fwd's workspace.
-int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int Kr, char *base, SegmentBwdJob *job);
+// With `saved`, the rows x - s come from the forward (SavedRows) and the
+// layout holds no buffer for them.
+int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int Kr, char *base, SegmentBwdJob *job,
+                                bool saved = false);
+// The channel slices (n_sub, kp, csw) in which a forward saves rows for the
+// backward of this shape; false where the backward takes no saved rows.
+bool segment_saved_slices(int A, int C, int Kw, int Kr, SavedRows *geo);
+// Whether a forward of this shape can save rows in those slices on the
+// current device (a one-token precomputed-gain scan over the whole slot
+// space, with whole channel slices).
+bool segment_forward_can_save(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, const SavedRows &geo);
 hipError_t launch_segment_backward(const SegmentBwdJob &job, hipStream_t stream, const char **why);
 
 }  // namespace ramnet

@@ -138,7 +138,10 @@ __device__ __forceinline__ void raw_load_vec(const float *p, uint32_t *out) {
     }
 }
 
-template<typename Scalar, int EPP, int NP, int VEC>
+// SAVED: the forward saved the rows x - s and the read rows (job.delta,
+// job.saved_r), so the forward pass over t is skipped and the backward pass
+// also forms the read dot products d_j from the saved read rows.
+template<typename Scalar, int EPP, int NP, int VEC, bool SAVED>
 __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBwdJob job, int n_sub) {
     constexpr int LPE = kWave / EPP;               // lanes per event (consecutive: channel groups)
     constexpr int CSW = LPE * VEC;
@@ -195,7 +198,9 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     // per-slice partial sums of this unit: [t][KP]
     float *drp = job.dr_part + (static_cast<int64_t>(sub) * BH + bh) * t_pad * KP;
     float *dgp = job.dg_part + (static_cast<int64_t>(sub) * BH + bh) * t_pad * KP;
-    float *dlt = job.delta + static_cast<int64_t>(unit) * T * KP * CSW + e * CSW + q * VEC;  // + (t * KP + p * EPP) * CSW
+    // the rows x - s: (unit, T_pad, KP, CSW), the forward's padded token count
+    float *dlt = job.delta + static_cast<int64_t>(unit) * scan_t_pad(T) * KP * CSW + e * CSW + q * VEC;  // + (t * KP + p * EPP) * CSW
+    const float *dlr = SAVED ? job.saved_r + (dlt - job.delta) : nullptr;  // saved read rows, same layout
 
     struct Pre {
         int4 w[RPL];
@@ -270,6 +275,7 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     constexpr bool HOLD = CH * NP * VEC <= 32;
 
     // ---- forward over t: s in LDS; save x - s before each write, d_j per read
+    if constexpr (!SAVED) {
     for (int i = lane; i < (A + 2) * CSW; i += kWave) {
         const int a = i / CSW - 2, c = sub * CSW + i % CSW;
         st[i] = (a >= 0 && c < C) ? fj.init_slot[(static_cast<int64_t>(bh) * A + a) * C + c] : 0.f;
@@ -440,6 +446,7 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
         flush(nck - 1);
     }
     __syncthreads();
+    }
 
     // ---- backward over t: Ds in LDS
     for (int i = lane; i < (A + 2) * CSW; i += kWave) {
@@ -449,22 +456,30 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     __syncthreads();
     {
         using Tag = std::false_type;
-        // the saved rows x - s of this lane's write events, per token of a chunk
+        // the saved rows x - s of this lane's write events (and with SAVED the
+        // read rows of its read events), per token of a chunk
+        constexpr int NSR = SAVED ? CH : 1;
         struct Saved {
             uint32_t v[CH][NP * VEC];
+            uint32_t r[NSR][NP * VEC];
         };
         auto load_saved = [&](int ci, Saved &sv) {
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int t = token(ci, j, Tag{});
 #pragma unroll
-                for (int p = 0; p < NP; ++p)
-                    raw_load_vec<VEC>(dlt + (static_cast<int64_t>(t) * KP + p * EPP) * CSW, sv.v[j] + p * VEC);
+                for (int p = 0; p < NP; ++p) {
+                    const int64_t o = (static_cast<int64_t>(t) * KP + p * EPP) * CSW;
+                    raw_load_vec<VEC>(dlt + o, sv.v[j] + p * VEC);
+                    if constexpr (SAVED)
+                        raw_load_vec<VEC>(dlr + o, sv.r[j] + p * VEC);
+                }
             }
         };
         struct Out {
             float dg[NG][NP];    // Dg of token (group start - q)
             float gx[NGX][VEC];  // Dx of token (group start - e)
+            float dr[SAVED ? NG : 1][NP];  // SAVED: d_j of token (group start - q)
         };
         Out out;
         float *gx = job.grad_x + static_cast<int64_t>(bh) * T * C;
@@ -478,8 +493,11 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     if (FULL || g * LPE + q < n) {
                         const int64_t tg = t0 - g * LPE - q;
 #pragma unroll
-                        for (int p = 0; p < NP; ++p)
+                        for (int p = 0; p < NP; ++p) {
                             dgp[tg * KP + p * EPP + e] = out.dg[g][p];
+                            if constexpr (SAVED)
+                                drp[tg * KP + p * EPP + e] = out.dr[g][p];
+                        }
                     }
                 if (e < GX) {
 #pragma unroll
@@ -523,13 +541,17 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
                     dyv[j][v] = sdy[j * CSW + q * VEC + v];
             }
             float dgp_[NP][LPE];  // Dg partials of a group of LPE tokens (token group start - m)
+            float rdp_[SAVED ? NP : 1][LPE];  // SAVED: d_j partials, grouped as Dg's
             float dxp[VEC][NXS];  // Dx partials of a group of EPP tokens (reduce-scatter form)
             float keep_x[VEC];    // Dx of token (group start - e) (all-reduce form)
 #pragma unroll
             for (int p = 0; p < NP; ++p)
 #pragma unroll
-                for (int m = 0; m < LPE; ++m)
+                for (int m = 0; m < LPE; ++m) {
                     dgp_[p][m] = 0.f;
+                    if constexpr (SAVED)
+                        rdp_[p][m] = 0.f;
+                }
 #pragma unroll
             for (int v = 0; v < VEC; ++v) {
                 keep_x[v] = 0.f;
@@ -592,11 +614,26 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
 #pragma unroll
                     for (int p = 0; p < NP; ++p)
                         dgp_[p][j % LPE] = opq(part[p]);
+                    if constexpr (SAVED) {
+                        // d_j of this token: its saved read rows with Dy_t
+#pragma unroll
+                        for (int p = 0; p < NP; ++p) {
+                            float pr = 0.f;
+#pragma unroll
+                            for (int v = 0; v < VEC; ++v)
+                                pr = fmaf(__uint_as_float(scur.r[j][p * VEC + v]), dyv[j][v], pr);
+                            rdp_[p][j % LPE] = opq(pr);
+                        }
+                    }
                     if (j % LPE == LPE - 1 || (TL && t == 0)) {
 #pragma unroll
                         for (int p = 0; p < NP; ++p) {
                             event_scatter<LOGL - 1, 0, LPE>(dgp_[p], hi);
                             out.dg[j / LPE][p] = dgp_[p][0];
+                            if constexpr (SAVED) {
+                                event_scatter<LOGL - 1, 0, LPE>(rdp_[p], hi);
+                                out.dr[j / LPE][p] = rdp_[p][0];
+                            }
                         }
                     }
                     if constexpr (XSC) {
@@ -914,16 +951,28 @@ __global__ __launch_bounds__(256) void segment_bwd_mass_scan_kernel(const Segmen
     job.grad_init_mass[i] = D;
 }
 
-template<typename Scalar, int EPP, int NP>
-hipError_t launch_bwd_scan_vec(const SegmentBwdJob &job, const BwdPlan &p, hipStream_t stream) {
+template<typename Scalar, int EPP, int NP, bool SAVED>
+hipError_t launch_bwd_scan_saved(const SegmentBwdJob &job, const BwdPlan &p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((job.fwd.B * job.fwd.H * p.n_sub + 7) / 8 * 8));
     const size_t lds = static_cast<size_t>(p.lds);
     switch (p.vec) {
-        case 1: hipLaunchKernelGGL((segment_bwd_scan_kernel<Scalar, EPP, NP, 1>), grid, dim3(kWave), lds, stream, job, p.n_sub); break;
-        case 2: hipLaunchKernelGGL((segment_bwd_scan_kernel<Scalar, EPP, NP, 2>), grid, dim3(kWave), lds, stream, job, p.n_sub); break;
-        default: hipLaunchKernelGGL((segment_bwd_scan_kernel<Scalar, EPP, NP, 4>), grid, dim3(kWave), lds, stream, job, p.n_sub); break;
+        case 1: hipLaunchKernelGGL((segment_bwd_scan_kernel<Scalar, EPP, NP, 1, SAVED>), grid, dim3(kWave), lds, stream, job, p.n_sub); break;
+        case 2: hipLaunchKernelGGL((segment_bwd_scan_kernel<Scalar, EPP, NP, 2, SAVED>), grid, dim3(kWave), lds, stream, job, p.n_sub); break;
+        default: hipLaunchKernelGGL((segment_bwd_scan_kernel<Scalar, EPP, NP, 4, SAVED>), grid, dim3(kWave), lds, stream, job, p.n_sub); break;
     }
     return hipGetLastError();
+}
+
+// Saved rows are taken with one pass of events (segment_saved_slices).
+template<typename Scalar, int EPP, int NP>
+hipError_t launch_bwd_scan_vec(const SegmentBwdJob &job, const BwdPlan &p, hipStream_t stream) {
+    if constexpr (NP == 1) {
+        if (job.saved_r)
+            return launch_bwd_scan_saved<Scalar, EPP, NP, true>(job, p, stream);
+    } else if (job.saved_r) {
+        return hipErrorInvalidValue;
+    }
+    return launch_bwd_scan_saved<Scalar, EPP, NP, false>(job, p, stream);
 }
 
 template<typename Scalar>
@@ -998,7 +1047,8 @@ int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
 }  // namespace
 
-int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int Kr, char *base, SegmentBwdJob *job) {
+int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int Kr, char *base, SegmentBwdJob *job,
+                                bool saved) {
     BwdPlan p{};
     if (!bwd_plan(A, C, Kw, Kr, &p))
         return -1;
@@ -1015,7 +1065,7 @@ int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int K
     const int64_t maps_bytes = mass_replay_scratch_bytes(B, H, T, A);
     char *maps = take(maps_bytes);
     const int64_t kp = p.epp * p.np, ch = bwd_chunk(p.epp, p.np, p.vec), t_pad = (T + ch - 1) / ch * ch;
-    char *delta = take(bh * p.n_sub * T * kp * p.csw * 4);
+    char *delta = saved ? nullptr : take(bh * p.n_sub * scan_t_pad64(T) * kp * p.csw * 4);
     char *dr = take(p.n_sub * bh * t_pad * kp * 4), *dg = take(p.n_sub * bh * t_pad * kp * 4);
     char *drs = take(nr * 4), *dgs = take(nw * 4);
     if (job) {
@@ -1023,13 +1073,27 @@ int64_t segment_backward_layout(int B, int H, int T, int A, int C, int Kw, int K
         job->mass_scratch = reinterpret_cast<float *>(mass);
         job->maps = maps;
         job->maps_bytes = static_cast<size_t>(maps_bytes);
-        job->delta = reinterpret_cast<float *>(delta);
+        if (!saved)
+            job->delta = reinterpret_cast<float *>(delta);
         job->dr_part = reinterpret_cast<float *>(dr);
         job->dg_part = reinterpret_cast<float *>(dg);
         job->dr_sum = reinterpret_cast<float *>(drs);
         job->dg_sum = reinterpret_cast<float *>(dgs);
     }
     return off;
+}
+
+bool segment_saved_slices(int A, int C, int Kw, int Kr, SavedRows *geo) {
+    BwdPlan p{};
+    // whole slices only (the forward stores every channel of a slice), and one
+    // pass of events (two-pass layouts would spill the saved read rows)
+    if (!bwd_plan(A, C, Kw, Kr, &p) || C % p.csw != 0 || p.np != 1)
+        return false;
+    geo->w = geo->r = nullptr;
+    geo->n_sub = p.n_sub;
+    geo->kp = p.epp * p.np;
+    geo->csw = p.csw;
+    return true;
 }
 
 hipError_t launch_segment_backward(const SegmentBwdJob &job, hipStream_t stream, const char **why) {

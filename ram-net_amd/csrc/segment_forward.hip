@@ -131,17 +131,29 @@ static bool pair_records_fit(int kmax, int T) {
     return static_cast<int64_t>(kmax) * scan_t_pad(std::max(T, 0)) * 16 <= INT_MAX;
 }
 
+// A forward that saves rows for the backward (SavedRows sv) runs a one-token
+// precomputed-gain layout with one channel per lane and whole slices, whose
+// event lanes fit in the backward's kp slots; a head's saved rows are
+// addressed with 32-bit byte offsets.
+static bool save_fits(const SavedRows &sv, int T) {
+    return static_cast<int64_t>(sv.n_sub) * scan_t_pad(std::max(T, 1)) * sv.kp * sv.csw * 4 <= INT_MAX;
+}
+static bool save_layout_ok(const SavedRows *sv, int vec, int epp, int np, int cs, int C) {
+    return !sv || (vec == 1 && epp * np <= sv->kp && C % cs == 0);
+}
+
 // The best layout for slot ranges of AL slots (the whole space when AL == A);
-// forms: mass wave allowed (mass_ok), precomputed gains allowed (pre_ok).
+// forms: mass wave allowed (mass_ok), precomputed gains allowed (pre_ok);
+// sv: the layout saves rows in those slices.
 static bool plan_layout(int B, int H, int AL, int A_full, int C, int kmax, int elem, int n_cu, int T, bool mass_ok,
-                        bool pre_ok, Plan *out, int64_t *best_cost) {
+                        bool pre_ok, Plan *out, int64_t *best_cost, const SavedRows *sv = nullptr) {
     const int64_t tt = std::max(1, T);
     const int epp0 = std::min(kWave, std::max(4, pow2_ceil(kmax)));
     bool found = false;
     int64_t best = 0;
     // paired scan: the precomputed-gain form over the whole slot space, one
     // pass of events
-    if (pre_ok && AL == A_full && AL <= kMaxPairSlots && pair_records_fit(kmax, T)) {
+    if (!sv && pre_ok && AL == A_full && AL <= kMaxPairSlots && pair_records_fit(kmax, T)) {
         for (int epp = 2; epp <= kWave / 2; epp <<= 1) {
             if (epp < kmax)
                 continue;
@@ -187,6 +199,8 @@ static bool plan_layout(int B, int H, int AL, int A_full, int C, int kmax, int e
                     if (!scan_layout_compiled(vec, epp, np, nw, pre))
                         continue;
                     const int cs = nw * (kWave / epp) * vec;
+                    if (!save_layout_ok(sv, vec, epp, np, cs, C))
+                        continue;
                     const size_t lds = scan_lds_bytes(AL, vec, epp, np, nw, elem, pre);
                     const int64_t gran = (static_cast<int64_t>(lds) + kLdsGranule - 1) / kLdsGranule * kLdsGranule;
                     if (gran > kLdsPerCu)
@@ -222,11 +236,15 @@ static bool plan_layout(int B, int H, int AL, int A_full, int C, int kmax, int e
     return found;
 }
 
-bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, int T, Plan *out) {
+bool make_plan(int B, int H, int A, int C, int Kw, int Kr, int elem, int n_cu, int T, Plan *out,
+               const SavedRows *sv = nullptr) {
     const int kmax = std::max(Kw, Kr);
     if (kmax > 2 * kWave || A < 1)
         return false;
     int64_t cost = 0;
+    if (sv)  // saving rows: the precomputed-gain form over the whole slot space
+        return A <= kMaxPrePassSlots && save_fits(*sv, T) &&
+               plan_layout(B, H, A, A, C, kmax, elem, n_cu, T, false, true, out, &cost, sv);
     if (plan_layout(B, H, A, A, C, kmax, elem, n_cu, T, true, true, out, &cost))
         return true;
     // Too wide for one resident slice: split the slot space into the fewest
@@ -1279,8 +1297,22 @@ static int layout_override(const SegmentJob &job, Plan *p, const char **why) {
 }
 
 // The layout a launch of this job uses: the override, else the planner's
-// choice for the job's B, H, dtype and this device's CU count.
+// choice for the job's B, H, dtype and this device's CU count. A job that
+// saves rows takes the override only where it can save them.
 static bool pick_plan(const SegmentJob &job, Plan *p, const char **why) {
+    if (job.save.w) {
+        const SavedRows &sv = job.save;
+        const int forced = layout_override(job, p, why);
+        if (forced > 0 && p->pre && p->tp == 1 && job.A <= kMaxPrePassSlots && save_fits(sv, job.T) &&
+            save_layout_ok(&sv, p->vec, p->epp, p->np, p->cs, job.C))
+            return true;
+        if (!make_plan(job.B, job.H, job.A, job.C, job.Kw, job.Kr, dtype_bytes(job.dtype), cu_count(), job.T, p, &sv)) {
+            *why = "segment forward: no layout saves the backward's rows for this shape (see "
+                   "ramnet_segment_saved_bytes)";
+            return false;
+        }
+        return true;
+    }
     const int forced = layout_override(job, p, why);
     if (forced < 0)
         return false;
@@ -1316,6 +1348,11 @@ int segment_plan(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, i
     if (ranges)
         *ranges = p.nr;
     return 1;
+}
+
+bool segment_forward_can_save(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, const SavedRows &geo) {
+    Plan p{};
+    return make_plan(B, H, A, C, Kw, Kr, dtype_bytes(dtype), cu_count(), T, &p, &geo);
 }
 
 hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, const char **why) {

@@ -389,9 +389,10 @@ inline size_t scan_lds_bytes(int A, int vec, int epp, int np, int nw, int elem, 
 // without a barrier from the first chunk to the write-back.
 // RANGE (precomputed-gain form only): one slot range of a split slot space
 // (segment_scan_range_kernel); the whole space otherwise.
-template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE, bool RANGE>
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE, bool RANGE, bool SAVE = false>
 __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const ScanGeom &geo) {
     static_assert(PRE || !RANGE, "slot ranges need the precomputed-gain form");
+    static_assert(!SAVE || (PRE && !RANGE && FAST && VEC == 1), "rows are saved by whole-slice one-channel lanes");
     constexpr int NWT = NW + (PRE ? 0 : 1);  // waves of the workgroup
     constexpr int LPE = kWave / EPP;
     constexpr int CSW = LPE * VEC;
@@ -632,6 +633,28 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
     hi[5] = bit_mask<32>(lane);
     // LDS address of this lane's first channel in slot 0
     const uint32_t lrow = lds_addr(st) + static_cast<uint32_t>(cl) * 4;
+    // SAVE: each token's x - s of every write row and every read row go to
+    // the backward's slices (SavedRows), through buffer resources over the
+    // head's region: a byte offset per lane and pass (its channel and event
+    // slot) plus a scalar offset per token. The host guarantees that every
+    // lane's channel is below C and its event slot below kp. The region
+    // holds Tp tokens, so the tail chunk stores without a guard: a store
+    // under a branch would make the compiler assume fewer stores in flight
+    // on every path and wait for the chunk's stores before each deposit.
+    const SavedRows &sv = job.save;
+    const int64_t sv_head = SAVE ? static_cast<int64_t>(bh) * sv.n_sub * Tp * sv.kp * sv.csw : 0;
+    const int sv_bytes = SAVE ? sv.n_sub * Tp * sv.kp * sv.csw * 4 : 0;
+    [[maybe_unused]] const auto svw = __builtin_amdgcn_make_buffer_rsrc(SAVE ? sv.w + sv_head : nullptr, 0, sv_bytes, kBufWord3);
+    [[maybe_unused]] const auto svr = __builtin_amdgcn_make_buffer_rsrc(SAVE ? sv.r + sv_head : nullptr, 0, sv_bytes, kBufWord3);
+    [[maybe_unused]] int svo[NP] = {};
+    [[maybe_unused]] int sv_tok = 0;
+    if constexpr (SAVE) {
+        const int c = c0 + cl, lg = __builtin_ctz(static_cast<unsigned>(sv.csw));
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            svo[p] = (((c >> lg) * Tp * sv.kp + p * EPP + ev) * sv.csw + (c & (sv.csw - 1))) * 4;
+        sv_tok = sv.kp * sv.csw * 4;
+    }
     const Scalar *gx = static_cast<const Scalar *>(job.x) + static_cast<int64_t>(bh) * T * C;
     Scalar *gy = static_cast<Scalar *>(job.y) + static_cast<int64_t>(bh) * T * C;
     // Items past the end are clamped to the last item, so the threads that
@@ -808,11 +831,15 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 const float g = __int_as_float(rec[p][j].y);
-                FVec<VEC> o;
+                FVec<VEC> o, d;
 #pragma unroll
-                for (int v = 0; v < VEC; ++v)
-                    o.v[v] = fmaf(g, x_at(v, j) - s[p].v[v], s[p].v[v]);
+                for (int v = 0; v < VEC; ++v) {
+                    d.v[v] = x_at(v, j) - s[p].v[v];
+                    o.v[v] = fmaf(g, d.v[v], s[p].v[v]);
+                }
                 lds_store<VEC>(row(rec[p][j].x), o);
+                if constexpr (SAVE)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(d.v[0]), svw, svo[p], (t0 + j) * sv_tok, 0);
             }
 #pragma unroll
             for (int p = 0; p < NP; ++p)
@@ -824,6 +851,11 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
         // token
         float part[VEC][BFLY ? EPP : 1];
         auto reduce = [&](int j, const FVec<VEC> (&rv)[NP]) {
+            if constexpr (SAVE) {
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(rv[p].v[0]), svr, svo[p], (t0 + j) * sv_tok, 0);
+            }
             FVec<VEC> acc;
 #pragma unroll
             for (int v = 0; v < VEC; ++v)
@@ -974,10 +1006,14 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
             pre_deposit(fa);
             fm = flag_mask(fa.flag);
         }
+        // SAVE: one chunk body for every chunk. Around a choice between two
+        // bodies the compiler keeps an edge that skips both, and its memory
+        // waits then assume that none of a chunk's row stores are in flight:
+        // each deposit would wait for the whole chunk's stores.
         auto run = [&](int ci, uint64_t m) {
             Recs rc;
             stage_recs(priv, rc);
-            if (ci < n_full)
+            if (!SAVE && ci < n_full)
                 state_chunk(priv_x, ci * CH, Full{}, rc, m);
             else
                 state_chunk(priv_x, ci * CH, Tail{}, rc, m);
@@ -1059,10 +1095,10 @@ __device__ __forceinline__ void segment_scan_body(const SegmentJob &job, const S
     }
 }
 
-template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE, bool SAVE = false>
 __global__ __launch_bounds__(kWave * (NW + (PRE ? 0 : 1))) void segment_scan_kernel(const SegmentJob job,
                                                                                      const ScanGeom geo) {
-    segment_scan_body<Scalar, VEC, EPP, NP, NW, MA, FAST, PRE, false>(job, geo);
+    segment_scan_body<Scalar, VEC, EPP, NP, NW, MA, FAST, PRE, false, SAVE>(job, geo);
 }
 
 template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST>
@@ -1070,9 +1106,16 @@ __global__ __launch_bounds__(kWave * NW) void segment_scan_range_kernel(const Se
     segment_scan_body<Scalar, VEC, EPP, NP, NW, MA, FAST, true, true>(job, geo);
 }
 
-template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE>
+template<typename Scalar, int VEC, int EPP, int NP, int NW, bool MA, bool FAST, bool PRE, bool SAVE = false>
 hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t stream) {
     const unsigned blocks = static_cast<unsigned>(((geo.n_units + 7) / 8) * 8);
+    if constexpr (SAVE) {
+        hipLaunchKernelGGL((segment_scan_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST, true, true>), dim3(blocks),
+                           dim3(kWave * NW),
+                           scan_lds_bytes(geo.n_local, VEC, EPP, NP, NW, static_cast<int>(sizeof(Scalar)), true), stream,
+                           job, geo);
+        return hipGetLastError();
+    }
     if constexpr (PRE) {
         if (geo.n_local != job.A) {
             hipLaunchKernelGGL((segment_scan_range_kernel<Scalar, VEC, EPP, NP, NW, MA, FAST>), dim3(blocks),
@@ -1101,11 +1144,24 @@ hipError_t launch_scan(const SegmentJob &job, const ScanGeom &geo, hipStream_t s
 #define RAMNET_SCAN_PRE_LAYOUTS(X)                                                                   \
     X(1, 8, 1, 2) X(1, 8, 1, 4) X(1, 16, 1, 2) X(1, 16, 1, 4) X(1, 32, 1, 2) X(1, 64, 1, 2) X(1, 64, 2, 1)
 
+// A scan that saves rows (job.save.w set) runs a precomputed-gain layout
+// over the whole slot space with whole slices (FAST); the host checks this.
 template<typename Scalar>
 hipError_t scan_dispatch(const SegmentJob &job, const ScanGeom &geo, int vec, int epp, int np, int nw, bool pre,
                          hipStream_t stream) {
     const int cs = nw * (kWave / epp) * vec;
     const bool fast = job.C % cs == 0;
+    if (job.save.w != nullptr) {
+        if (!pre || !fast || vec != 1 || geo.n_local != job.A)
+            return hipErrorInvalidValue;
+#define RAMNET_SCAN_CASE_SAVE(V, E, N, W)                                                            \
+        if (V == 1 && epp == E && np == N && nw == W)                                                \
+            return job.mass_aware ? launch_scan<Scalar, 1, E, N, W, true, true, true, true>(job, geo, stream) \
+                                  : launch_scan<Scalar, 1, E, N, W, false, true, true, true>(job, geo, stream);
+        RAMNET_SCAN_PRE_LAYOUTS(RAMNET_SCAN_CASE_SAVE)
+#undef RAMNET_SCAN_CASE_SAVE
+        return hipErrorInvalidValue;
+    }
 #define RAMNET_SCAN_CASE(V, E, N, W, P)                                                              \
     if (pre == P && vec == V && epp == E && np == N && nw == W) {                                    \
         if (job.mass_aware)                                                                          \

@@ -85,6 +85,16 @@ SIGNATURES: dict[str, tuple[type, list]] = {
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
         _c_int, _c_float, _c_ptr, _c_i64, _c_ptr]),
     "ramnet_segment_backward_workspace_bytes": (_c_i64, [_c_i64] * 7),
+    "ramnet_segment_saved_bytes": (_c_i64, [_c_i64] * 7 + [_c_int]),
+    "ramnet_topk_segment_forward_save": (_c_int, [
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_float, _c_ptr, _c_i64, _c_ptr, _c_i64,
+        _c_ptr]),
+    "ramnet_segment_backward_saved_workspace_bytes": (_c_i64, [_c_i64] * 7),
+    "ramnet_topk_segment_backward_saved": (_c_int, [
+        _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_int, _c_float, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
     "ramnet_segment_plan": (_c_int, [
         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int),
         ctypes.POINTER(_c_int)]),
@@ -153,6 +163,21 @@ def segment_workspace_bytes(B: int, H: int, T: int, A: int, C: int, w_top_k: int
 def segment_backward_workspace_bytes(B: int, H: int, T: int, A: int, C: int, w_top_k: int, r_top_k: int) -> int:
     """Device workspace (bytes) of the segment backward; -1 for shapes it does not take."""
     return int(lib().ramnet_segment_backward_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k))
+
+
+def segment_saved_bytes(B: int, H: int, T: int, A: int, C: int, w_top_k: int, r_top_k: int,
+                        dtype: torch.dtype) -> int:
+    """Bytes of the rows a training forward saves for its backward
+    (ramnet_topk_segment_forward_save); -1 where that pair does not apply."""
+    if dtype not in DTYPE_CODES:
+        return -1
+    return int(lib().ramnet_segment_saved_bytes(B, H, T, A, C, w_top_k, r_top_k, DTYPE_CODES[dtype]))
+
+
+def segment_backward_saved_workspace_bytes(B: int, H: int, T: int, A: int, C: int, w_top_k: int,
+                                           r_top_k: int) -> int:
+    """Device workspace (bytes) of the segment backward that takes saved rows."""
+    return int(lib().ramnet_segment_backward_saved_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -402,6 +402,145 @@ def _segment_backward(ctx, D_y, D_slot, D_mass):
 topk_segment_forward.register_autograd(_segment_backward, setup_context=_segment_setup)
 
 
+# --------------------------------------------------------------------------
+# training pair with saved rows (no reference counterpart: the reference's
+# backward reconstructs the forward). Same results as topk_segment_forward /
+# topk_segment_backward; the forward also keeps, per event, the row its
+# backward would otherwise recompute.
+
+def _saved_bytes(op: str, B: int, H: int, T: int, A: int, C: int, w_top_k: int, r_top_k: int,
+                 dtype: torch.dtype) -> int:
+    n = nat.segment_saved_bytes(B, H, T, A, C, w_top_k, r_top_k, dtype)
+    if n < 0:
+        raise RuntimeError(f"{op}: no saved-row form for this shape (A={A}, C={C}, top_k=({w_top_k}, {r_top_k})); "
+                           "use topk_segment_forward")
+    return n
+
+
+@torch.library.custom_op(f"{_NS}::topk_segment_forward_saved", mutates_args=(), device_types="cuda")
+def topk_segment_forward_saved(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, init_slot: Tensor,
+                               init_mass: Tensor, mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool,
+                               eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """``topk_segment_forward`` that also returns ``saved`` (uint8): the scan
+    records and, per event, x - s before each write and the row of each
+    read, which ``topk_segment_backward_saved`` takes instead of replaying
+    the forward. Raises RuntimeError where
+    ``ramnet_ops._native.segment_saved_bytes`` is -1."""
+    op = "topk_segment_forward_saved"
+    _require_gpu(op, addr_idx, addr_val, x, gamma, init_slot, init_mass, mask)
+    B, H, T, C, A = _check_segment(op, addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k)
+    x, gamma, mask = _segment_args(x, gamma, mask)
+    nbytes = _saved_bytes(op, B, H, T, A, C, w_top_k, r_top_k, x.dtype)
+    addr_idx = addr_idx.to(torch.int32).contiguous()
+    addr_val = addr_val.to(torch.float32).contiguous()
+    init_slot = init_slot.to(torch.float32).contiguous()
+    init_mass = init_mass.to(torch.float32).contiguous()
+    slot = torch.empty_like(init_slot)
+    mass = torch.empty_like(init_mass)
+    y = torch.empty_like(x)
+    ws = _workspace(x, B, H, T, A, C, w_top_k, r_top_k)
+    saved = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        nat.call("ramnet_topk_segment_forward_save", addr_idx.data_ptr(), addr_val.data_ptr(), x.data_ptr(),
+                 gamma.data_ptr(), _code(x), nat.ptr(mask), init_slot.data_ptr(), init_mass.data_ptr(),
+                 slot.data_ptr(), mass.data_ptr(), y.data_ptr(), B, H, T, A, C, w_top_k, r_top_k, int(mass_aware),
+                 float(eps), ws.data_ptr(), ws.numel(), saved.data_ptr(), saved.numel(), nat.stream_of(x))
+    return y, slot, mass, saved
+
+
+@topk_segment_forward_saved.register_fake
+def _(addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps):
+    B, H, T, C = x.shape
+    A = init_slot.shape[2]
+    nbytes = _saved_bytes("topk_segment_forward_saved", B, H, T, A, C, w_top_k, r_top_k, x.dtype)
+    return (x.new_empty(x.shape), init_slot.new_empty(init_slot.shape, dtype=torch.float32),
+            init_mass.new_empty(init_mass.shape, dtype=torch.float32), x.new_empty((nbytes,), dtype=torch.uint8))
+
+
+@torch.library.custom_op(f"{_NS}::topk_segment_backward_saved", mutates_args=(), device_types="cuda")
+def topk_segment_backward_saved(addr_val: Tensor, x: Tensor, gamma: Tensor, init_slot: Tensor, init_mass: Tensor,
+                                saved: Tensor, D_y: Tensor, D_post_slot: Tensor | None, D_post_mass: Tensor | None,
+                                w_top_k: int, r_top_k: int, mass_aware: bool,
+                                eps: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of ``topk_segment_forward_saved`` from its ``saved`` rows;
+    outputs as ``topk_segment_backward``."""
+    op = "topk_segment_backward_saved"
+    _require_given(op, addr_val=addr_val, x=x, gamma=gamma, init_slot=init_slot, init_mass=init_mass, saved=saved,
+                   D_y=D_y)
+    _require_gpu(op, addr_val, x, gamma, init_slot, init_mass, saved, D_y, D_post_slot, D_post_mass)
+    B, H, T, C = _dims(op, "x", x, 4)
+    A = _dims(op, "init_slot", init_slot, 4)[2]
+    K = w_top_k + r_top_k
+    _check_shapes(op, addr_val=(addr_val, (B, H, K, T)), gamma=(gamma, (B, H, T)), init_slot=(init_slot, (B, H, A, C)),
+                  init_mass=(init_mass, (B, H, A)), D_y=(D_y, (B, H, T, C)), D_post_slot=(D_post_slot, (B, H, A, C)),
+                  D_post_mass=(D_post_mass, (B, H, A)))
+    x, gamma, _ = _segment_args(x, gamma, None)
+    nbytes = _saved_bytes(op, B, H, T, A, C, w_top_k, r_top_k, x.dtype)
+    if saved.dtype != torch.uint8 or saved.numel() < nbytes or not saved.is_contiguous():
+        raise RuntimeError(f"{op}: saved must be the contiguous uint8 tensor of topk_segment_forward_saved")
+    addr_val = addr_val.to(torch.float32).contiguous()
+    init_slot = init_slot.to(torch.float32).contiguous()
+    init_mass = init_mass.to(torch.float32).contiguous()
+    D_y = D_y.to(dtype=x.dtype).contiguous()
+    if D_post_slot is not None:
+        D_post_slot = D_post_slot.to(torch.float32).contiguous()
+    if D_post_mass is not None:
+        D_post_mass = D_post_mass.to(torch.float32).contiguous()
+    f32 = dict(dtype=torch.float32, device=x.device)
+    D_addr = torch.empty((B, H, K, T), **f32)
+    D_x = torch.empty((B, H, T, C), **f32)
+    D_gamma = torch.empty((B, H, T), **f32)
+    D_slot = torch.empty_like(init_slot)
+    D_mass = torch.empty_like(init_mass)
+    ws = torch.empty(max(1, nat.segment_backward_saved_workspace_bytes(B, H, T, A, C, w_top_k, r_top_k)),
+                     dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        nat.call("ramnet_topk_segment_backward_saved", addr_val.data_ptr(), x.data_ptr(), gamma.data_ptr(), _code(x),
+                 init_slot.data_ptr(), init_mass.data_ptr(), D_y.data_ptr(), nat.ptr(D_post_slot),
+                 nat.ptr(D_post_mass), D_addr.data_ptr(), D_x.data_ptr(), D_gamma.data_ptr(), D_slot.data_ptr(),
+                 D_mass.data_ptr(), B, H, T, A, C, w_top_k, r_top_k, int(mass_aware), float(eps), saved.data_ptr(),
+                 saved.numel(), ws.data_ptr(), ws.numel(), nat.stream_of(x))
+    return D_addr, D_x, D_gamma, D_slot, D_mass
+
+
+@topk_segment_backward_saved.register_fake
+def _(addr_val, x, gamma, init_slot, init_mass, saved, D_y, D_post_slot, D_post_mass, w_top_k, r_top_k, mass_aware,
+      eps):
+    B, H, T, C = x.shape
+    f32 = torch.float32
+    return (x.new_empty((B, H, w_top_k + r_top_k, T), dtype=f32), x.new_empty(x.shape, dtype=f32),
+            x.new_empty((B, H, T), dtype=f32), init_slot.new_empty(init_slot.shape, dtype=f32),
+            init_mass.new_empty(init_mass.shape, dtype=f32))
+
+
+def _segment_saved_setup(ctx, inputs, output):
+    addr_idx, addr_val, x, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps = inputs
+    ctx.args = (w_top_k, r_top_k, bool(mass_aware), float(eps))
+    ctx.dtypes = (x.dtype, gamma.dtype, init_slot.dtype, init_mass.dtype)
+    ctx.save_for_backward(addr_val, x, gamma, init_slot, init_mass, output[3])  # saved: uint8, no gradient
+    ctx.set_materialize_grads(False)
+
+
+def _segment_saved_backward(ctx, D_y, D_slot, D_mass, D_saved):
+    addr_val, x, gamma, init_slot, init_mass, saved = ctx.saved_tensors
+    w_top_k, r_top_k, mass_aware, eps = ctx.args
+    x_dt, g_dt, s_dt, m_dt = ctx.dtypes
+    if D_y is None:
+        D_y = torch.zeros_like(x)
+    D_addr, D_x, D_gamma, D_s, D_m = topk_segment_backward_saved(addr_val, x, gamma, init_slot, init_mass, saved, D_y,
+                                                                 D_slot, D_mass, w_top_k, r_top_k, mass_aware, eps)
+    need = ctx.needs_input_grad
+    return (None,
+            D_addr if need[1] else None,
+            D_x.to(x_dt) if need[2] else None,
+            D_gamma.to(g_dt) if need[3] else None,
+            D_s.to(s_dt) if need[4] else None,
+            D_m.to(m_dt) if need[5] else None) + (None,) * 5
+
+
+topk_segment_forward_saved.register_autograd(_segment_saved_backward, setup_context=_segment_saved_setup)
+
+
 @torch.library.custom_op(f"{_NS}::topk_segment_forward_", mutates_args=("slot", "mass"), device_types="cuda")
 def topk_segment_forward_(addr_idx: Tensor, addr_val: Tensor, x: Tensor, gamma: Tensor, slot: Tensor, mass: Tensor,
                           mask: Tensor | None, w_top_k: int, r_top_k: int, mass_aware: bool, eps: float) -> Tensor:

@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import torch
 
+from .. import _native as nat
 from . import _ops
 from ._cuda_config import ADDRESS_LIMIT, check_int_capacity
 
@@ -123,9 +124,16 @@ def _cuda_ram_attn(
         assert init_slot.is_contiguous() and init_mass.is_contiguous(), "Expected contiguous inplace state."
 
     if requires_grad:
-        # the differentiable composition (reference: cuda_impl.py:252-271)
+        # the differentiable composition (reference: cuda_impl.py:252-271).
+        # Where the shape allows it, the segment forward keeps the rows its
+        # backward needs (topk_segment_forward_saved), so the backward runs
+        # one pass over the sequence instead of replaying the forward first.
         addr_idx, addr_val = torch.ops.ramnet_ops.topk_addr_forward(
             w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re, r_re)
+        if nat.segment_saved_bytes(B, H, T, A, C, w_top_k, r_top_k, xs.dtype) >= 0:
+            ys, post_slot, post_mass, _ = torch.ops.ramnet_ops.topk_segment_forward_saved(
+                addr_idx, addr_val, xs, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps)
+            return ys, post_slot, post_mass
         return torch.ops.ramnet_ops.topk_segment_forward(
             addr_idx, addr_val, xs, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps)
 
