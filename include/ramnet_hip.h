@@ -208,11 +208,12 @@ int64_t ramnet_segment_backward_workspace_bytes(int64_t B, int64_t H, int64_t T,
  * ramnet_topk_segment_forward and ramnet_topk_segment_backward
  * (ram_attn_bind.cpp:65-82) on the same inputs, to fp32 rounding. For
  * training callers with memory to spare: the saved buffer holds the scan
- * records plus two fp32 arrays of B*H*T_pad*kp*C*4 bytes (x - s before each
- * write, the row of each read; kp = max(Kw, Kr) rounded up to the backward's
- * event slots, T_pad = T rounded up to 32): 4.4 GB at B=8, H=16, T=4096,
- * C=128, K=8. One backward pass over the sequence then replaces the
- * backward's replay of the forward.
+ * records, the backward's per-event mass records (16 bytes per event), and
+ * two fp32 arrays of B*H*T_pad*kp*C*4 bytes (x - s before each write, the
+ * row of each read; kp = max(Kw, Kr) rounded up to the backward's event
+ * slots, T_pad = T rounded up to 32): 4.5 GB at B=8, H=16, T=4096, C=128,
+ * K=8. One backward pass over the sequence, with no replay of the mass
+ * pre-pass, then replaces the backward's replay of the forward.
  *
  * ramnet_segment_saved_bytes: bytes of the saved buffer, or -1 where the pair
  * does not apply (the forward must run a one-token precomputed-gain scan

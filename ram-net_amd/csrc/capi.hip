@@ -577,10 +577,16 @@ int ramnet_topk_segment_backward(const int32_t *addr_idx, const float *addr_val,
 }
 
 // ---- training pair with saved rows. The saved buffer holds the scan
-// records, then x - s of every write row and every read row, in the
-// backward's channel slices (SavedRows), each part 256-byte aligned.
+// records, the backward's per-event records (MassAux: where its
+// record-keeping pre-pass holds the slot space in one piece), then x - s of
+// every write row and every read row in the backward's channel slices
+// (SavedRows), each part 256-byte aligned.
+struct SavedParts {
+    int64_t rec, aux_w, aux_r, rows;
+    int64_t total() const { return rec + aux_w + aux_r + 2 * rows; }
+};
 static bool saved_layout(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t Kw, int64_t Kr, int dtype,
-                         ramnet::SavedRows *geo, int64_t *rec_bytes, int64_t *row_bytes) {
+                         ramnet::SavedRows *geo, SavedParts *parts) {
     if (B <= 0 || H <= 0 || T <= 0 || A <= 0 || A >= kAddressLimit || C <= 0 || Kw <= 0 || Kr <= 0 || Kw > A ||
         Kr > A || !valid_dtype(dtype) ||
         !fits_int({B * H * A * C, B * H * (A + 2), B * H * T * C, B * H * (T + ramnet::kScanPad) * (Kw + Kr)}))
@@ -592,16 +598,29 @@ static bool saved_layout(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, 
                                           static_cast<int>(A), static_cast<int>(C), static_cast<int>(Kw),
                                           static_cast<int>(Kr), dtype, *geo))
         return false;
-    *rec_bytes = (ramnet::scan_record_bytes(B, H, T, Kw, Kr) + 255) / 256 * 256;
-    *row_bytes = (B * H * geo->n_sub * ramnet::scan_t_pad64(T) * geo->kp * geo->csw * 4 + 255) / 256 * 256;
+    auto al = [](int64_t n) { return (n + 255) / 256 * 256; };
+    const bool aux = ramnet::segment_saved_aux(static_cast<int>(A));
+    parts->rec = al(ramnet::scan_record_bytes(B, H, T, Kw, Kr));
+    parts->aux_w = aux ? al(B * H * T * Kw * 16) : 0;
+    parts->aux_r = aux ? al(B * H * T * Kr * 16) : 0;
+    parts->rows = al(B * H * geo->n_sub * ramnet::scan_t_pad64(T) * geo->kp * geo->csw * 4);
     return true;
+}
+
+// The parts of a saved buffer at `base`.
+static void saved_pointers(char *base, const SavedParts &parts, ramnet::SavedRows *geo) {
+    char *aw = base + parts.rec, *ar = aw + parts.aux_w, *rw = ar + parts.aux_r;
+    geo->aux = parts.aux_w ? ramnet::MassAux{reinterpret_cast<int4 *>(aw), reinterpret_cast<int4 *>(ar)}
+                           : ramnet::MassAux{};
+    geo->w = reinterpret_cast<float *>(rw);
+    geo->r = reinterpret_cast<float *>(rw + parts.rows);
 }
 
 int64_t ramnet_segment_saved_bytes(int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int64_t w_top_k,
                                    int64_t r_top_k, int dtype) {
     ramnet::SavedRows geo{};
-    int64_t rec = 0, rows = 0;
-    return saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &rec, &rows) ? rec + 2 * rows : -1;
+    SavedParts parts{};
+    return saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &parts) ? parts.total() : -1;
 }
 
 int ramnet_topk_segment_forward_save(const int32_t *addr_idx, const float *addr_val, const void *x,
@@ -614,10 +633,10 @@ int ramnet_topk_segment_forward_save(const int32_t *addr_idx, const float *addr_
                                 r_top_k, eps, workspace, workspace_bytes))
         return rc;
     ramnet::SavedRows geo{};
-    int64_t rec = 0, rows = 0;
-    RAMNET_REQUIRE(saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &rec, &rows),
+    SavedParts parts{};
+    RAMNET_REQUIRE(saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &parts),
                    "topk_segment_forward_save: no saved-row form for this shape (ramnet_segment_saved_bytes < 0)");
-    RAMNET_REQUIRE(saved && saved_bytes >= rec + 2 * rows, "saved buffer too small: see ramnet_segment_saved_bytes");
+    RAMNET_REQUIRE(saved && saved_bytes >= parts.total(), "saved buffer too small: see ramnet_segment_saved_bytes");
     RAMNET_REQUIRE(addr_idx && addr_val, "null tensor pointer");
     ramnet::SegmentJob job = make_segment_job(x, dtype, init_slot, init_mass, slot_out, mass_out, y, B, H, T, A, C,
                                               w_top_k, r_top_k, mass_aware, eps, workspace);
@@ -625,8 +644,7 @@ int ramnet_topk_segment_forward_save(const int32_t *addr_idx, const float *addr_
     job.wrec = reinterpret_cast<const ramnet::WriteRec *>(sv);
     job.rrec = reinterpret_cast<const ramnet::ReadRec *>(sv + B * H * ramnet::scan_t_pad64(T) * w_top_k *
                                                                static_cast<int64_t>(sizeof(ramnet::WriteRec)));
-    geo.w = reinterpret_cast<float *>(sv + rec);
-    geo.r = reinterpret_cast<float *>(sv + rec + rows);
+    saved_pointers(sv, parts, &geo);
     job.save = geo;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const char *why = nullptr;
@@ -657,10 +675,10 @@ int ramnet_topk_segment_backward_saved(const float *addr_val, const void *x, con
                                 T, A, C, w_top_k, r_top_k, eps, workspace, workspace_bytes, need < 0 ? 0 : need))
         return rc;
     ramnet::SavedRows geo{};
-    int64_t rec = 0, rows = 0;
-    RAMNET_REQUIRE(need >= 0 && saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &rec, &rows),
+    SavedParts parts{};
+    RAMNET_REQUIRE(need >= 0 && saved_layout(B, H, T, A, C, w_top_k, r_top_k, dtype, &geo, &parts),
                    "topk_segment_backward_saved: no saved-row form for this shape (ramnet_segment_saved_bytes < 0)");
-    RAMNET_REQUIRE(saved && saved_bytes >= rec + 2 * rows, "saved buffer too small: see ramnet_segment_saved_bytes");
+    RAMNET_REQUIRE(saved && saved_bytes >= parts.total(), "saved buffer too small: see ramnet_segment_saved_bytes");
     RAMNET_REQUIRE(workspace_bytes >= need && workspace,
                    "workspace too small: see ramnet_segment_backward_saved_workspace_bytes");
     RAMNET_REQUIRE(addr_val && grad_y && grad_addr_val && grad_gamma, "null tensor pointer");
@@ -684,9 +702,13 @@ int ramnet_topk_segment_backward_saved(const float *addr_val, const void *x, con
     ramnet::segment_backward_layout(static_cast<int>(B), static_cast<int>(H), static_cast<int>(T), static_cast<int>(A),
                                     static_cast<int>(C), static_cast<int>(w_top_k), static_cast<int>(r_top_k),
                                     static_cast<char *>(workspace), &job, true);
-    const char *sv = static_cast<const char *>(saved);
-    job.delta = reinterpret_cast<float *>(const_cast<char *>(sv) + rec);
-    job.saved_r = reinterpret_cast<const float *>(sv + rec + rows);
+    saved_pointers(static_cast<char *>(const_cast<void *>(saved)), parts, &geo);
+    job.delta = geo.w;
+    job.saved_r = geo.r;
+    if (geo.aux.wev) {
+        job.aux = geo.aux;
+        job.aux_saved = 1;
+    }
     const char *why = nullptr;
     const hipError_t err = ramnet::launch_segment_backward(job, static_cast<hipStream_t>(stream), &why);
     return finish(err, why, "topk_segment_backward_saved launch");

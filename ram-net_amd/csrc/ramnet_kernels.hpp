@@ -111,6 +111,15 @@ struct AddrBwdJob {
     float sign;
 };
 
+// Per-event forward quantities of the segment backward, written by the mass
+// pre-pass in its record-keeping mode. Token-major: (B*H, T, K).
+struct MassAux {
+    int4 *wev;   // (B*H, T, Kw) {slot, or -2 for a no-op; gain g = w / (m + eps); effective weight of
+                 //  the read of the same slot in this token, or 0; slot mass before the write} (floats as bits)
+    int4 *rev;   // (B*H, T, Kr) {slot, or -1 for a no-op; effective read weight; post-write mass of
+                 //  the slot; 0} (floats as bits)
+};
+
 // Rows a training forward saves for the segment backward, laid out in the
 // backward's channel slices: (B*H*n_sub, T_pad, kp, csw) floats each, n_sub
 // slices of csw channels (a power of two), kp padded event slots per token,
@@ -119,6 +128,9 @@ struct SavedRows {
     float *w;  // per write event: x_t - s before the write; null: nothing saved
     float *r;  // per read event: the row read, after the token's writes
     int n_sub, kp, csw;
+    // the backward's per-event records, written by the forward's mass
+    // pre-pass alongside the gains (null: the backward replays it)
+    MassAux aux;
 };
 
 // Time-sequential gated sparse update + top-K read over a whole sequence.
@@ -147,14 +159,6 @@ struct SegmentJob {
     float eps;
 };
 
-// Per-event forward quantities of the segment backward, written by the mass
-// pre-pass in its record-keeping mode. Token-major: (B*H, T, K).
-struct MassAux {
-    int4 *wev;   // (B*H, T, Kw) {slot, or -2 for a no-op; gain g = w / (m + eps); effective weight of
-                 //  the read of the same slot in this token, or 0; slot mass before the write} (floats as bits)
-    int4 *rev;   // (B*H, T, Kr) {slot, or -1 for a no-op; effective read weight; post-write mass of
-                 //  the slot; 0} (floats as bits)
-};
 
 // Segment backward (gradients of ramnet_topk_segment_forward).
 struct SegmentBwdJob {
@@ -172,6 +176,7 @@ struct SegmentBwdJob {
     float *grad_init_mass;    // (B, H, A)
     float *delta;             // (B*H*n_sub, T_pad, KP, CSW) x - s before each write (KP: padded event count)
     const float *saved_r;     // same layout: the rows read, saved by the forward (then delta too); else null
+    int aux_saved;            // 1: `aux` was written by the forward (no replay here)
     float *dr_part;           // (n_sub, B*H, T_pad, KP) per-slice read dot products
     float *dg_part;           // (n_sub, B*H, T_pad, KP) per-slice gain gradients
     float *dr_sum;            // (B*H, T, Kr) read dot products d_j
@@ -257,6 +262,9 @@ bool segment_saved_slices(int A, int C, int Kw, int Kr, SavedRows *geo);
 // current device (a one-token precomputed-gain scan over the whole slot
 // space, with whole channel slices).
 bool segment_forward_can_save(int B, int H, int T, int A, int C, int Kw, int Kr, int dtype, const SavedRows &geo);
+// Whether a saving forward also keeps the backward's per-event records
+// (MassAux): the record-keeping pre-pass holds the slot space in one piece.
+bool segment_saved_aux(int A);
 hipError_t launch_segment_backward(const SegmentBwdJob &job, hipStream_t stream, const char **why);
 
 }  // namespace ramnet

@@ -1115,11 +1115,13 @@ hipError_t launch_segment_backward(const SegmentBwdJob &job, hipStream_t stream,
                            job.grad_init_mass, job.grad_mass, ns);
         return hipGetLastError();
     }
-    SegmentJob mj = fj;
-    mj.mass_out = job.mass_scratch;
-    hipError_t err = launch_mass_replay(mj, job.aux, job.maps, job.maps_bytes, stream);
-    if (err != hipSuccess)
-        return err;
+    if (!job.aux_saved) {
+        SegmentJob mj = fj;
+        mj.mass_out = job.mass_scratch;
+        const hipError_t err = launch_mass_replay(mj, job.aux, job.maps, job.maps_bytes, stream);
+        if (err != hipSuccess)
+            return err;
+    }
     switch (fj.dtype) {
         case kF32: return launch_typed<float>(job, p, stream);
         case kF16: return launch_typed<_Float16>(job, p, stream);

@@ -624,9 +624,10 @@ __global__ __launch_bounds__(256) void mass_chunk_scan_kernel(const SegmentJob j
 }
 
 // Step 3: one wave per NU (b, h) units of one chunk, from m_start (the maps
-// after step 2, or the initial mass when there is one chunk). With AUX the
-// records stay as they are and the per-event quantities go to `aux` instead
-// (the forward replay of the segment backward). NU > 1 (at most 32 / NU
+// after step 2, or the initial mass when there is one chunk). AUX = 0: the
+// gain records; AUX = 1: the per-event quantities of `aux` instead (the
+// forward replay of the segment backward); AUX = 2: both (a forward that
+// saves them for its backward). NU > 1 (at most 32 / NU
 // events per token): unit u takes lanes [u * 64 / NU, (u + 1) * 64 / NU),
 // so every lane of a record load or gain store serves an event; the units
 // past the last (b, h) repeat it (same records, same values stored).
@@ -635,7 +636,7 @@ __global__ __launch_bounds__(256) void mass_chunk_scan_kernel(const SegmentJob j
 // Each token's reads post the token under their slots in an LDS tag table;
 // the next token's writes look their slots up. The first token of a chunk
 // (whose predecessor another chunk replays) is flagged.
-template<bool MA, int MP, bool AUX = false, int NU = 1, bool FL = false>
+template<bool MA, int MP, int AUX = 0, int NU = 1, bool FL = false>
 __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob job, int t_pad, int chunk_len,
                                                             const float2 *starts, const MassAux aux) {
     static_assert(NU == 1 || (MP == 1 && !AUX), "several units per wave: one pass of events, no AUX");
@@ -694,7 +695,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
     const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad;
     // gain records of this head (not written in the record-keeping mode)
     const int ek = max(Kw, Kr);
-    GainRec *gg = AUX ? nullptr : job.gain + static_cast<int64_t>(bh) * ek * t_pad;
+    GainRec *gg = AUX == 1 ? nullptr : job.gain + static_cast<int64_t>(bh) * ek * t_pad;
     const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
     int *gfl = FL ? job.flags + static_cast<int64_t>(bh) * t_pad : nullptr;
     auto run = [&](int t0, const MassRecs<MP, CH> &c) {
@@ -772,12 +773,13 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
                     re[p] = MA ? rr[p] * mm[p] * scale : rr[p];
-                    if constexpr (AUX) {
+                    if constexpr (AUX != 0) {
                         if (!wlane && ln.on[p] && live) {
                             const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kr + ln.ev[p];
                             aux.rev[o] = make_int4(rb[p], __float_as_int(re[p]), __float_as_int(mm[p]), 0);
                         }
-                    } else {
+                    }
+                    if constexpr (AUX != 1) {
                         // every event below max(Kw, Kr) gets a record (past Kw
                         // the no-op write: slot -2, gain 0; past Kr the no-op
                         // read: slot -1, weight 0); write lanes store its first
@@ -926,7 +928,7 @@ size_t mass_lds_bytes(int A, bool aux, int nu = 1, bool fl = false) {
 
 // The replay kernel with NU units per wave: (b, h) units of a chunk in
 // groups of NU.
-template<bool MA, int MP, bool AUX, int NU>
+template<bool MA, int MP, int AUX, int NU>
 void launch_replay_units(const SegmentJob &job, int t_pad, int len, int nck, const float2 *starts, const MassAux &aux,
                          hipStream_t stream) {
     const unsigned groups = static_cast<unsigned>((job.B * job.H + NU - 1) / NU);
@@ -935,12 +937,12 @@ void launch_replay_units(const SegmentJob &job, int t_pad, int len, int nck, con
     if constexpr (!AUX) {
         if (fl) {
             hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX, NU, true>), grid, dim3(kWave),
-                               mass_lds_bytes(job.A, AUX, NU, true), stream, job, t_pad, len, starts, aux);
+                               mass_lds_bytes(job.A, false, NU, true), stream, job, t_pad, len, starts, aux);
             return;
         }
     }
-    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX, NU>), grid, dim3(kWave), mass_lds_bytes(job.A, AUX, NU), stream,
-                       job, t_pad, len, starts, aux);
+    hipLaunchKernelGGL((segment_mass_kernel<MA, MP, AUX, NU>), grid, dim3(kWave), mass_lds_bytes(job.A, AUX != 0, NU),
+                       stream, job, t_pad, len, starts, aux);
 }
 
 // Units per replay wave: four when a token has at most 8 events and the
@@ -948,7 +950,7 @@ void launch_replay_units(const SegmentJob &job, int t_pad, int len, int nck, con
 // MI355X: config 2 (K = 8) segment stage 0.762 -> 0.755 ms with four units;
 // config 4 (K = 16) 1.420 -> 1.433 ms with two (so one there), and both
 // slower with the time chunks halved to keep the wave count.
-template<bool MA, int MP, bool AUX>
+template<bool MA, int MP, int AUX>
 void launch_mass_replay_nu(const SegmentJob &job, int t_pad, int len, int nck, const float2 *starts,
                            const MassAux &aux, hipStream_t stream) {
     if constexpr (MP == 1 && !AUX) {
@@ -960,7 +962,7 @@ void launch_mass_replay_nu(const SegmentJob &job, int t_pad, int len, int nck, c
 
 // `maps` is scratch for the chunk maps (maps_bytes of it); the final masses
 // go to job.mass_out.
-template<bool MA, int MP, bool AUX>
+template<bool MA, int MP, int AUX>
 hipError_t launch_mass_pass_mp(const SegmentJob &job, int t_pad, int n_cu, void *maps_buf, size_t maps_bytes,
                                const MassAux &aux, hipStream_t stream) {
     int len = 0;
@@ -1184,7 +1186,7 @@ hipError_t launch_mass_ranges(const SegmentJob &job, int t_pad, int64_t max_al, 
     return hipGetLastError();
 }
 
-template<bool MA, bool AUX>
+template<bool MA, int AUX>
 hipError_t launch_mass_pass(const SegmentJob &job, int t_pad, int n_cu, void *maps, size_t maps_bytes,
                             const MassAux &aux, hipStream_t stream) {
     const int kmax = std::max(job.Kw, job.Kr);
@@ -1220,9 +1222,11 @@ hipError_t launch_mass_replay(const SegmentJob &job, const MassAux &aux, void *m
     if (job.A > kMaxAuxSlots)
         return launch_mass_ranges<true>(job, t_pad, kMaxAuxSlots, aux, stream);
     const int n = kReplayChunkFactor * cu_count();
-    return job.mass_aware ? launch_mass_pass<true, true>(job, t_pad, n, maps, maps_bytes, aux, stream)
-                          : launch_mass_pass<false, true>(job, t_pad, n, maps, maps_bytes, aux, stream);
+    return job.mass_aware ? launch_mass_pass<true, 1>(job, t_pad, n, maps, maps_bytes, aux, stream)
+                          : launch_mass_pass<false, 1>(job, t_pad, n, maps, maps_bytes, aux, stream);
 }
+
+bool segment_saved_aux(int A) { return A <= kMaxAuxSlots; }
 
 template<typename Scalar>
 hipError_t launch_pack(const PackJob &job, unsigned blocks, int t_pad, hipStream_t stream) {
@@ -1408,8 +1412,14 @@ hipError_t launch_segment_forward(const SegmentJob &job, hipStream_t stream, con
             const size_t y_bytes = static_cast<size_t>(job.B) * job.H * job.T * job.C * dtype_bytes(job.dtype);
             const MassAux none{};
             const int n = kReplayChunkFactor * cu_count();
-            err = job.mass_aware ? launch_mass_pass<true, false>(pj, geo.t_pad, n, job.y, y_bytes, none, stream)
-                                 : launch_mass_pass<false, false>(pj, geo.t_pad, n, job.y, y_bytes, none, stream);
+            if (job.save.w && job.save.aux.wev) {
+                // a saving forward also keeps the backward's per-event records
+                err = job.mass_aware ? launch_mass_pass<true, 2>(pj, geo.t_pad, n, job.y, y_bytes, job.save.aux, stream)
+                                     : launch_mass_pass<false, 2>(pj, geo.t_pad, n, job.y, y_bytes, job.save.aux, stream);
+            } else {
+                err = job.mass_aware ? launch_mass_pass<true, 0>(pj, geo.t_pad, n, job.y, y_bytes, none, stream)
+                                     : launch_mass_pass<false, 0>(pj, geo.t_pad, n, job.y, y_bytes, none, stream);
+            }
         }
         if (err != hipSuccess)
             return err;

@@ -238,9 +238,10 @@ def test_segment_workspace_query():
 
 
 def test_saved_pair_sizes():
-    """``ramnet_segment_saved_bytes``: the scan records plus two fp32 rows per
-    padded event slot (x - s of each write, the row of each read), each part
-    256-byte aligned, in the backward's channel slices; -1 outside the
+    """``ramnet_segment_saved_bytes``: the scan records, the backward's
+    per-event records (16 bytes per event), and two fp32 rows per
+    padded event slot (x - s of each write, the row of each read) in the
+    backward's channel slices, each part 256-byte aligned; -1 outside the
     pair's envelope. The saved backward's workspace holds everything the
     recompute backward's does but the records and the rows."""
     from ramnet_ops import _native as nat
@@ -248,12 +249,13 @@ def test_saved_pair_sizes():
     B, H, T, A, C, K = 8, 16, 4096, 1024, 128, 8
     t_pad = (T + 31) // 32 * 32
     rec = al(B * H * t_pad * (K * 16 + K * 8))
+    aux = 2 * al(B * H * T * K * 16)
     rows = al(B * H * t_pad * K * C * 4)  # 8 event slots, 16 slices of 8 channels, padded tokens
     for dtype in (torch.float32, torch.float16, torch.bfloat16):
-        assert nat.segment_saved_bytes(B, H, T, A, C, K, K, dtype) == rec + 2 * rows
+        assert nat.segment_saved_bytes(B, H, T, A, C, K, K, dtype) == rec + aux + 2 * rows
     # top-k 5 pads to 8 event slots
     assert nat.segment_saved_bytes(1, 2, 40, 64, 32, 5, 5, torch.float32) == \
-        al(2 * 64 * (5 * 16 + 5 * 8)) + 2 * al(2 * 64 * 8 * 32 * 4)
+        al(2 * 64 * (5 * 16 + 5 * 8)) + 2 * al(2 * 40 * 5 * 16) + 2 * al(2 * 64 * 8 * 32 * 4)
     assert nat.segment_saved_bytes(1, 2, 16, 64, 24, 8, 8, torch.float32) == -1  # no whole forward slices
     assert nat.segment_saved_bytes(1, 1, 13, 256, 16, 100, 70, torch.float32) == -1  # two event passes
     assert nat.segment_saved_bytes(1, 2, 16, 65536, 32, 8, 8, torch.float32) == -1  # slot ranges
