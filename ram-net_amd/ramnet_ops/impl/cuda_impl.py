@@ -128,9 +128,12 @@ def _cuda_ram_attn(
         # Where the shape allows it, the segment forward keeps the rows its
         # backward needs (topk_segment_forward_saved), so the backward runs
         # one pass over the sequence instead of replaying the forward first.
+        # Graphs traced by torch.compile keep the reference-shaped ops: the
+        # size query is a native call the tracer does not follow.
         addr_idx, addr_val = torch.ops.ramnet_ops.topk_addr_forward(
             w_addr, r_addr, embed_num, A, position_ids, w_top_k, r_top_k, w_re, r_re)
-        if nat.segment_saved_bytes(B, H, T, A, C, w_top_k, r_top_k, xs.dtype) >= 0:
+        if not torch.compiler.is_compiling() and \
+                nat.segment_saved_bytes(B, H, T, A, C, w_top_k, r_top_k, xs.dtype) >= 0:
             ys, post_slot, post_mass, _ = torch.ops.ramnet_ops.topk_segment_forward_saved(
                 addr_idx, addr_val, xs, gamma, init_slot, init_mass, mask, w_top_k, r_top_k, mass_aware, eps)
             return ys, post_slot, post_mass
