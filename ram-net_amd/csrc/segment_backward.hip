@@ -125,19 +125,6 @@ __device__ __forceinline__ uint32_t raw_load(const Scalar *p) {
         return *reinterpret_cast<const uint16_t *>(p);
 }
 
-template<int VEC>
-__device__ __forceinline__ void raw_load_vec(const float *p, uint32_t *out) {
-    if constexpr (VEC == 4) {
-        const uint4 t = *reinterpret_cast<const uint4 *>(p);
-        out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
-    } else if constexpr (VEC == 2) {
-        const uint2 t = *reinterpret_cast<const uint2 *>(p);
-        out[0] = t.x; out[1] = t.y;
-    } else {
-        out[0] = *reinterpret_cast<const uint32_t *>(p);
-    }
-}
-
 // SAVED: the forward saved the rows x - s and the read rows (job.delta,
 // job.saved_r), so the forward pass over t is skipped and the backward pass
 // also forms the read dot products d_j from the saved read rows.
@@ -199,8 +186,20 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
     float *drp = job.dr_part + (static_cast<int64_t>(sub) * BH + bh) * t_pad * KP;
     float *dgp = job.dg_part + (static_cast<int64_t>(sub) * BH + bh) * t_pad * KP;
     // the rows x - s: (unit, T_pad, KP, CSW), the forward's padded token count
-    float *dlt = job.delta + static_cast<int64_t>(unit) * scan_t_pad(T) * KP * CSW + e * CSW + q * VEC;  // + (t * KP + p * EPP) * CSW
-    const float *dlr = SAVED ? job.saved_r + (dlt - job.delta) : nullptr;  // saved read rows, same layout
+    // the rows x - s: (unit, T_pad, KP, CSW), the forward's padded token count
+    const int64_t unit_rows = static_cast<int64_t>(unit) * scan_t_pad(T) * KP * CSW;
+    float *dlt = job.delta + unit_rows + e * CSW + q * VEC;  // + (t * KP + p * EPP) * CSW
+    // They are read back through buffer resources over the unit's rows: a
+    // byte offset per lane and pass, and the token's as a scalar offset, so
+    // the loads need no per-lane address arithmetic.
+    const int unit_bytes = scan_t_pad(T) * KP * CSW * 4;
+    const auto rsd = __builtin_amdgcn_make_buffer_rsrc(job.delta + unit_rows, 0, unit_bytes, kBufWord3);
+    [[maybe_unused]] const auto rsr = __builtin_amdgcn_make_buffer_rsrc(
+        SAVED ? const_cast<float *>(job.saved_r) + unit_rows : nullptr, 0, SAVED ? unit_bytes : 0, kBufWord3);
+    int svo[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+        svo[p] = ((p * EPP + e) * CSW + q * VEC) * 4;
 
     struct Pre {
         int4 w[RPL];
@@ -463,16 +462,26 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
             uint32_t v[CH][NP * VEC];
             uint32_t r[NSR][NP * VEC];
         };
+        auto buf_vec = [&](__amdgpu_buffer_rsrc_t rs, int vo, int so, uint32_t *out) {
+            if constexpr (VEC == 4) {
+                const auto q4 = __builtin_amdgcn_raw_buffer_load_b128(rs, vo, so, 0);
+                out[0] = q4[0]; out[1] = q4[1]; out[2] = q4[2]; out[3] = q4[3];
+            } else if constexpr (VEC == 2) {
+                const auto q2 = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, so, 0);
+                out[0] = q2[0]; out[1] = q2[1];
+            } else {
+                out[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo, so, 0);
+            }
+        };
         auto load_saved = [&](int ci, Saved &sv) {
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
-                const int t = token(ci, j, Tag{});
+                const int so = __builtin_amdgcn_readfirstlane(token(ci, j, Tag{})) * (KP * CSW * 4);
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    const int64_t o = (static_cast<int64_t>(t) * KP + p * EPP) * CSW;
-                    raw_load_vec<VEC>(dlt + o, sv.v[j] + p * VEC);
+                    buf_vec(rsd, svo[p], so, sv.v[j] + p * VEC);
                     if constexpr (SAVED)
-                        raw_load_vec<VEC>(dlr + o, sv.r[j] + p * VEC);
+                        buf_vec(rsr, svo[p], so, sv.r[j] + p * VEC);
                 }
             }
         };
