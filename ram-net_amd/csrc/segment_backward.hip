@@ -212,23 +212,30 @@ __global__ __launch_bounds__(kWave) void segment_bwd_scan_kernel(const SegmentBw
         const int t = decltype(fwd_tag)::value ? ci * CH + j : T - 1 - ci * CH - j;
         return min(max(t, 0), T - 1);
     };
+    // Offsets within the head are 32-bit (T * K and T * C fit an int: the
+    // host checks B * H * T * C and B * H * T_pad * (Kw + Kr)), from bases
+    // per head, so a load costs no 64-bit index arithmetic.
+    const int4 *wev_h = job.aux.wev + static_cast<int64_t>(bh) * T * Kw;
+    const int2 *rev_h = rev2 + 2 * static_cast<int64_t>(bh) * T * Kr;
+    const Scalar *dy_h = dys + static_cast<int64_t>(bh) * T * C;
+    const Scalar *x_h = xs + static_cast<int64_t>(bh) * T * C;
     auto prefetch = [&](int ci, Pre &pf, auto fwd_tag) {
 #pragma unroll
         for (int i = 0; i < RPL; ++i) {
             const int idx = min(lane + kWave * i, NREC - 1);
             const int k = idx % KP;
-            const int64_t tb = static_cast<int64_t>(bh) * T + token(ci, idx / KP, fwd_tag);
-            pf.w[i] = job.aux.wev[tb * Kw + min(k, Kw - 1)];
-            pf.r[i] = rev2[2 * (tb * Kr + min(k, Kr - 1))];
+            const int t = token(ci, idx / KP, fwd_tag);
+            pf.w[i] = wev_h[static_cast<uint32_t>(t * Kw + min(k, Kw - 1))];
+            pf.r[i] = rev_h[2u * static_cast<uint32_t>(t * Kr + min(k, Kr - 1))];
         }
 #pragma unroll
         for (int i = 0; i < XPL; ++i) {
             const int idx = min(lane + kWave * i, NXE - 1);
             const int c = min(sub * CSW + idx % CSW, C - 1);
-            const int64_t tb = static_cast<int64_t>(bh) * T + token(ci, idx / CSW, fwd_tag);
-            pf.dy[i] = raw_load(dys + tb * C + c);
+            const uint32_t o = static_cast<uint32_t>(token(ci, idx / CSW, fwd_tag) * C + c);
+            pf.dy[i] = raw_load(dy_h + o);
             if constexpr (decltype(fwd_tag)::value)
-                pf.x[i] = raw_load(xs + tb * C + c);
+                pf.x[i] = raw_load(x_h + o);
         }
     };
     auto stage = [&](const Pre &pf, auto fwd_tag) {
