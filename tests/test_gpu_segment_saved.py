@@ -188,3 +188,46 @@ def test_config2_full_size_saved_pair_heads():
     mine = (gval[:, :, :K], gval[:, :, K:], sel(got[1]), sel(got[2]), sel(got[3]), sel(got[4]))
     for name, a, b in zip(names, mine, ref):
         _check(name, a, torch.as_tensor(b), 1e-5)
+
+
+def test_config4_full_size_saved_pair_heads():
+    """Config 4 at full size through the saved pair (B=4, H=8, T=8192, U=3,
+    P=16 -> A=4096, K=16, bf16): the 16-event saving scan and the saved
+    backward with two channels per lane, two heads against the fp64
+    state-reconstruction oracle."""
+    from ram_cases import projected_logits
+    ops, nat = _ops(), _nat()
+    B, H, U, P, T, C, K, E = 4, 8, 3, 16, 8192, 128, 16, 4
+    A = P ** U
+    assert nat.segment_saved_bytes(B, H, T, A, C, K, K, BF16) > 0
+    print("config 4 full-size saved pair", flush=True)
+    w, r = projected_logits(B, H, U, P, T, 128, seed=4, dtype=torch.float32)
+    w, r = w.to(torch.bfloat16), r.to(torch.bfloat16)
+    g = torch.Generator().manual_seed(43)
+    x = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16)
+    gamma = torch.sigmoid(torch.randn(B, H, T, generator=g)).to(torch.bfloat16)
+    pos = torch.arange(T).view(1, T).expand(B, T)
+    Dy = torch.randn(B, H, T, C, generator=g).to(torch.bfloat16)
+    slot0 = torch.zeros(B, H, A, C)
+    mass0 = torch.full((B, H, A), 1.0 / A)
+    idx, val = ops.topk_addr_forward(w.to(DEV), r.to(DEV), E, A, pos.to(DEV), K, K, 0.0, 0.0)
+    _, _, _, saved = ops.topk_segment_forward_saved(idx, val, x.to(DEV), gamma.to(DEV), slot0.to(DEV), mass0.to(DEV),
+                                                    None, K, K, False, 1e-12)
+    got = ops.topk_segment_backward_saved(val, x.to(DEV), gamma.to(DEV), slot0.to(DEV), mass0.to(DEV), saved,
+                                          Dy.to(DEV), None, None, K, K, False, 1e-12)
+    torch.cuda.synchronize()
+    del saved
+    got = [t.cpu() for t in got]
+    idx_c, val_c = idx.cpu(), val.cpu()
+    heads = ((0, 0), (3, 7))
+    sel = lambda t: torch.stack([t[b, h] for b, h in heads]).unsqueeze(1)  # (2, 1, ...)
+    local = torch.stack([idx_c[b, h] - (b * H + h) * A for b, h in heads]).unsqueeze(1)
+    vsel = sel(val_c)
+    ref = oracle.sparse_gsu_backward_f64(local[:, :, :K], vsel[:, :, :K], local[:, :, K:], -vsel[:, :, K:],
+                                         sel(x).double(), sel(gamma).double(), sel(slot0), sel(mass0),
+                                         sel(Dy).double(), None, None, None, False, 1e-12, encoded=False)
+    gval = sel(got[0])
+    names = ("D_w", "D_r", "D_x", "D_gamma", "D_init_slot", "D_init_mass")
+    mine = (gval[:, :, :K], gval[:, :, K:], sel(got[1]), sel(got[2]), sel(got[3]), sel(got[4]))
+    for name, a, b in zip(names, mine, ref):
+        _check(name, a, torch.as_tensor(b), 1e-5)
