@@ -360,9 +360,13 @@ hipError_t launch_typed(const AddrJob &job, hipStream_t stream, const char **why
 // logits of a digit are read coalesced across the lanes' consecutive t,
 // once into registers when P <= PR, else in three passes (max, sum,
 // gradient). KM > 0 keeps the K terms in registers; KM = 0 streams them for
-// any K.
-template<typename Scalar, int KM, int PR>
+// any K. BUF (P == PR, and every lane's offsets from the wave's first lane
+// fit in 31 bits): the logits and their gradients go through buffer
+// resources based at the wave's first lane, with 32-bit lane offsets, so the
+// 2 * U * P per-lane addresses are not kept in (spilled) scalar registers.
+template<typename Scalar, int KM, int PR, bool BUF = false>
 __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJob job) {
+    static_assert(!BUF || PR > 0, "buffer resources: the logits held in registers");
     const int T = job.T, H = job.H, A = job.A, P = job.P, U = job.U, K = job.K;
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (gid >= static_cast<int64_t>(job.B) * H * T)
@@ -421,13 +425,42 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
     const float dsoft = (1.f - re) * dsum;
     const Scalar *xp = static_cast<const Scalar *>(job.addr) + bh * U * P * static_cast<int64_t>(T) + t;
     Scalar *gp = static_cast<Scalar *>(job.grad_addr) + bh * U * P * static_cast<int64_t>(T) + t;
+    // BUF: resources based at the first active lane's logit and gradient
+    // (later lanes are at equal or higher addresses, within 2 * U * P * T
+    // elements: a wave spans at most two (b, h) rows). readfirstlane returns
+    // a signed int: each half is widened through uint32_t.
+    auto first_of = [](uint64_t mine) {
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(mine >> 32)));
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(mine)));
+        return (static_cast<uint64_t>(hi) << 32) | lo;
+    };
+    const uint64_t xmine = reinterpret_cast<uint64_t>(xp), gmine = reinterpret_cast<uint64_t>(gp);
+    const uint64_t xfirst = BUF ? first_of(xmine) : xmine, gfirst = BUF ? first_of(gmine) : gmine;
+    [[maybe_unused]] const auto xrs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(xfirst), 0, 0x7fffffff, kBufWord3);
+    [[maybe_unused]] const auto grs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(gfirst), 0, 0x7fffffff, kBufWord3);
+    [[maybe_unused]] const int xoff = static_cast<int>(xmine - xfirst), goff = static_cast<int>(gmine - gfirst);
+    [[maybe_unused]] const int step = T * static_cast<int>(sizeof(Scalar));
     int stride = 1;
     for (int u = 0; u < U; ++u, stride *= P) {
         const Scalar *xu = xp + static_cast<int64_t>(u) * P * T;
         Scalar *gu = gp + static_cast<int64_t>(u) * P * T;
         float xr[PR > 0 ? PR : 1];  // the digit's logits, then their exponentials
         float mx = -__builtin_huge_valf();
-        if constexpr (PR > 0) {
+        if constexpr (BUF) {
+#pragma unroll
+            for (int q = 0; q < PR; ++q) {
+                const int o = xoff + (u * PR + q) * step;
+                uint32_t bits;
+                if constexpr (sizeof(Scalar) == 2)
+                    bits = __builtin_amdgcn_raw_buffer_load_b16(xrs, o, 0, 0);
+                else
+                    bits = __builtin_amdgcn_raw_buffer_load_b32(xrs, o, 0, 0);
+                xr[q] = bits_f32<Scalar>(bits);
+                mx = fmaxf(mx, xr[q]);
+            }
+        } else if constexpr (PR > 0) {
 #pragma unroll
             for (int q = 0; q < PR; ++q) {
                 xr[q] = load_f32(xu + static_cast<int64_t>(q < P ? q : P - 1) * T);
@@ -468,7 +501,20 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
             }
             return g;
         };
-        if constexpr (PR > 0) {
+        if constexpr (BUF) {
+#pragma unroll
+            for (int q = 0; q < PR; ++q) {
+                const int o = goff + (u * PR + q) * step;
+                const float v = grad_of(q) - xr[q] * scale;
+                if constexpr (sizeof(Scalar) == 4)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), grs, o, 0, 0);
+                else if constexpr (__is_same(Scalar, bf16_t))
+                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), grs, o, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v)), grs, o,
+                                                          0, 0);
+            }
+        } else if constexpr (PR > 0) {
             if (P == PR) {  // the common case: stores without a branch each
 #pragma unroll
                 for (int q = 0; q < PR; ++q)
@@ -494,9 +540,16 @@ hipError_t launch_backward_typed(const AddrBwdJob &job, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((n + 255) / 256)), blk(256);
     // a digit's logits fit in registers up to P = 32; P = 16 has its own
     // instance, whose stores need no per-logit branch
+    // offsets from a wave's first lane stay below 2 * U * P * T elements
+    const bool buf = 2 * static_cast<int64_t>(job.U) * job.P * job.T * static_cast<int64_t>(sizeof(T)) + 256 <=
+                     0x7fffffff;
 #define RAMNET_ADDR_BWD(KM)                                                                          \
     do {                                                                                             \
-        if (job.P == 16)                                                                             \
+        if (job.P == 16 && buf)                                                                      \
+            hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 16, true>), grid, blk, 0, stream, job); \
+        else if (job.P == 32 && buf)                                                                 \
+            hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 32, true>), grid, blk, 0, stream, job); \
+        else if (job.P == 16)                                                                        \
             hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 16>), grid, blk, 0, stream, job);   \
         else if (job.P <= 32)                                                                        \
             hipLaunchKernelGGL((topk_addr_backward_kernel<T, KM, 32>), grid, blk, 0, stream, job);   \

@@ -174,3 +174,39 @@ def test_extreme_logit_gradients(golden, top_k, re_norm):
     _, rgrad = _reference(src, 0, positions, top_k, re_norm, True, up, idx=idx.cpu())
     assert bool(torch.isfinite(grad).all())
     assert oracle.rel_err(grad.cpu().double(), rgrad) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_logit_address_high_bit(dtype):
+    """The decoder backward bases its buffer resources at each wave's first
+    logit and gradient address: logits and gradients whose addresses have bit
+    31 of the low word set, and clear, give the same bits as plain
+    allocations (the widening of a signed low word would turn such an address
+    into a wild one)."""
+    from ramnet_ops import _native as nat
+    ops = _ops()
+    B, H, U, P, T, K, E = 2, 4, 2, 32, 200, 8, 2
+    A = P ** U
+    g = torch.Generator().manual_seed(37)
+    addr = torch.randn(B, H, U, P, T, generator=g).to(dtype).to(DEV)
+    pos = torch.randint(0, 1000, (B, T), generator=g).to(DEV)
+    idx, val = ops.topk_addr_single_forward(addr, E, A, pos, K, 0.5, False, True)
+    dval = torch.randn(B, H, K, T, generator=g).to(DEV)
+    ref = ops.topk_addr_single_backward(idx, val, addr, dval, E, pos, K, 0.5, False, [B, H, U, P, A, T], dtype)
+    pos32 = pos.to(torch.int32).contiguous()
+    nbytes = addr.numel() * addr.element_size()
+    pool = torch.empty((1 << 31) + (1 << 23), dtype=torch.uint8, device=DEV)
+    base = pool.data_ptr()
+    for bit in (True, False):
+        offs = [o for o in range(0, pool.numel() - nbytes, 1 << 20) if bool((base + o) & (1 << 31)) == bit]
+        xo, go = offs[0], offs[-1]
+        print(f"logits at {base + xo:#x}, gradient at {base + go:#x} (bit 31 {'set' if bit else 'clear'})", flush=True)
+        x_view = pool[xo:xo + nbytes].view(dtype).view(B, H, U, P, T)
+        g_view = pool[go:go + nbytes].view(dtype).view(B, H, U, P, T)
+        x_view.copy_(addr)
+        nat.call("ramnet_topk_addr_single_backward", idx.data_ptr(), val.data_ptr(), x_view.data_ptr(),
+                 dval.data_ptr(), nat.DTYPE_CODES[dtype], B, H, U, P, T, E, A, pos32.data_ptr(), K, 0.5,
+                 0, g_view.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(g_view, ref)
+    del pool
