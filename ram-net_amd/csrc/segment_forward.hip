@@ -673,12 +673,14 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
         if (lane < 2)
             mv[lane - 2] = 1.f;
     }
-    // AUX: per slot, the token whose read last posted there and its weight
-    int *rtag = reinterpret_cast<int *>(lds + A + 2);
-    float *rval = lds + 2 * A + 2;
+    // AUX: per slot of unit v, the token whose read last posted there and its
+    // weight (tables of A after the NU units' masses)
+    int *rtag = reinterpret_cast<int *>(lds + NU * (A + 2)) + unit * A;
+    float *rval = lds + NU * (A + 2) + NU * A + unit * A;
     if constexpr (AUX) {
-        for (int a = lane; a < A; a += kWave)
-            rtag[a] = -1;
+        int *rtags = reinterpret_cast<int *>(lds + NU * (A + 2));
+        for (int a = lane; a < NU * A; a += kWave)
+            rtags[a] = -1;
     }
     // FL: unit v's tags at ftag + v * (A + 3) + 3: [-2] where no-op writes
     // look (never posted), [-1] where no-op reads post ([-3] unused)
@@ -792,7 +794,11 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 if constexpr (AUX) {
                     // each write's record carries the effective weight of the read of
                     // the same slot in this token (0 if none): the reads post
-                    // (token, weight) under their slots, then the writes look up theirs
+                    // (token, weight) under their slots, then the writes look up theirs.
+                    // Other lanes post what a lane looks up: the barriers keep the
+                    // compiler from moving the lookups above the posts (or this
+                    // token's posts above the previous token's lookups).
+                    __builtin_amdgcn_wave_barrier();
 #pragma unroll
                     for (int p = 0; p < MP; ++p) {
                         if (!wlane && rb[p] >= 0) {
@@ -800,6 +806,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                             rval[rb[p]] = re[p];
                         }
                     }
+                    __builtin_amdgcn_wave_barrier();
                     float rmatch[MP];
 #pragma unroll
                     for (int p = 0; p < MP; ++p) {
@@ -922,7 +929,7 @@ int mass_chunks(const SegmentJob &job, size_t scratch_bytes, int n_cu, int *chun
 // LDS of the replay kernel: the masses of its NU units (and with AUX the
 // read tag table, with FL the flag tag tables).
 size_t mass_lds_bytes(int A, bool aux, int nu = 1, bool fl = false) {
-    return static_cast<size_t>(A + 2) * 4 * nu + (aux ? static_cast<size_t>(A) * 8 : 0) +
+    return static_cast<size_t>(A + 2) * 4 * nu + (aux ? static_cast<size_t>(A) * 8 * nu : 0) +
            (fl ? static_cast<size_t>(A + 3) * 4 * nu : 0);
 }
 
@@ -946,7 +953,8 @@ void launch_replay_units(const SegmentJob &job, int t_pad, int len, int nck, con
 }
 
 // Units per replay wave: four when a token has at most 8 events and the
-// four units' masses take at most 64 KB of LDS, else one. Measured on
+// four units' masses take at most 64 KB of LDS, else one (the record-keeping
+// modes, bound by their record stores, measured no faster with four). Measured on
 // MI355X: config 2 (K = 8) segment stage 0.762 -> 0.755 ms with four units;
 // config 4 (K = 16) 1.420 -> 1.433 ms with two (so one there), and both
 // slower with the time chunks halved to keep the wave count.
