@@ -105,6 +105,12 @@ bool bwd_plan(int A, int C, int Kw, int Kr, BwdPlan *p) {
     return false;
 }
 
+// 1 / d as v_rcp_f32 refined by one Newton step.
+__device__ __forceinline__ float recip_nr(float d) {
+    const float r = __builtin_amdgcn_rcpf(d);
+    return fmaf(r, fmaf(-d, r, 1.f), r);
+}
+
 // Sum over the lanes whose indices differ only in bits LO .. HI/2 (powers of
 // two): a butterfly of DPP and permlane exchanges, with no LDS traffic.
 template<int LO, int HI>
@@ -894,17 +900,24 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
                 if (wlane && on[p] && k.ev[p].x >= 0) {
                     const float w = k.v[p], m = __int_as_float(k.ev[p].w), Dg = k.dd[p];
                     const float g = __int_as_float(k.ev[p].y);
-                    const float al = gsu_alpha(w, gm);
+                    // alpha in the stable form of gsu_alpha, with one
+                    // exponential q = e^-|gamma| and reciprocals of its
+                    // denominator dn and of m' + eps (each v_rcp_f32 and a
+                    // Newton step)
+                    const bool gpos = gm >= 0.f;
+                    const float qd = expf(gpos ? -gm : gm);
+                    const float cw = 1.f - w;
+                    const float dn = gpos ? fmaf(qd, cw, w) : fmaf(qd, w, cw);
+                    const float rdn = recip_nr(dn);
+                    const float al = (gpos ? cw * qd : cw) * rdn;
                     const float den = fmaf(al, m, w) + eps;
-                    const float q0 = Dg * g / den;
+                    const float rden = recip_nr(den);
+                    const float q0 = Dg * g * rden;
                     const int a = k.ev[p].x;
                     if constexpr (REPLAY) {
                         const float dtot = dm[a] - q0;
-                        const float qd = expf(-fabsf(gm));
-                        const float cw = 1.f - w;
-                        const float dn = gm >= 0.f ? fmaf(qd, cw, w) : fmaf(qd, w, cw);
-                        const float t2 = qd / (dn * dn);
-                        dw[p] = Dg / den + dtot * fmaf(-m, t2, 1.f);
+                        const float t2 = qd * rdn * rdn;
+                        dw[p] = Dg * rden + dtot * fmaf(-m, t2, 1.f);
                         dgam = fmaf(-dtot * m, cw * w * t2, dgam);
                         dm[a] = dtot * al;
                     } else {
