@@ -111,6 +111,12 @@ __device__ __forceinline__ float recip_nr(float d) {
     return fmaf(r, fmaf(-d, r, 1.f), r);
 }
 
+// v where the mask is all ones, +0 where it is zero (also for a v that is
+// not finite); an integer AND, which the compiler does not turn into a branch
+__device__ __forceinline__ float keep_if(float v, uint32_t mask) {
+    return __uint_as_float(__float_as_uint(v) & mask);
+}
+
 // Sum over the lanes whose indices differ only in bits LO .. HI/2 (powers of
 // two): a butterfly of DPP and permlane exchanges, with no LDS traffic.
 template<int LO, int HI>
@@ -764,9 +770,14 @@ struct MassTok {
                    // read: {slot, effective weight, post-write mass, 0})
     float v[MP];   // write: w; read: the stored (negated) weight
     float dd[MP];  // write: Dg; read: d_j
-    uint32_t gam;  // gamma_t bits
 };
 
+// The token body is branch-free: every quantity that does not depend on the
+// slot values (alpha, the reciprocals, the read-side sums) is computed for
+// all lanes, and an event that is off acts on its kind's no-op slot (-2 for
+// writes, -1 for reads), so the only dependent chain from token to token is
+// the slot's LDS read-modify-write, and the scheduler can overlap the rest of
+// neighbouring tokens with it. The no-op slots' values are never used.
 template<typename Scalar, bool MA, int MP, bool REPLAY>
 __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBwdJob job, float2 *maps,
                                                                 int chunk_len) {
@@ -806,29 +817,50 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
     const int4 *evp = wlane ? job.aux.wev : job.aux.rev;
     const float *ddp = wlane ? job.dg_sum : job.dr_sum;
     const int kl = wlane ? Kw : Kr, koff = wlane ? 0 : Kw;
+    // per-lane bases of this head's records, Dg / d sums and weights; a
+    // token adds t * kl records (t * 1 weights). Loads a lane does not use
+    // repeat write lane hl's addresses (same cache lines, no extra traffic):
+    // without mass-aware reads, the chunk maps use only the write events and
+    // the replay's read lanes only the records and d sums.
+    const bool rd_rec = MA || REPLAY, rd_val = MA;
+    const int hw = wlane || rd_rec ? 0 : 1;  // 1: this read lane loads write lane hl's records
+    const int hv = wlane || rd_val ? 0 : 1;  // 1: ... and its weights
+    const int64_t head = static_cast<int64_t>(bh) * T;
+    const int klr = hw ? Kw : kl;
+    const int4 *ev_l[MP];
+    const float *dd_l[MP], *v_l[MP];
+#pragma unroll
+    for (int p = 0; p < MP; ++p) {
+        const int ecw = min(p * 32 + hl, Kw - 1);
+        ev_l[p] = (hw ? job.aux.wev : evp) + head * klr + (hw ? ecw : ec[p]);
+        dd_l[p] = (hw ? job.dg_sum : ddp) + head * klr + (hw ? ecw : ec[p]);
+        v_l[p] = val + static_cast<int64_t>(hv ? ecw : koff + ec[p]) * T;
+    }
 
     auto load_tok = [&](int t, MassTok<MP> &k) {
-        const int64_t tb = static_cast<int64_t>(bh) * T + t;
+        const uint32_t tk = static_cast<uint32_t>(t) * static_cast<uint32_t>(klr);
 #pragma unroll
         for (int p = 0; p < MP; ++p) {
-            const int64_t o = tb * kl + ec[p];
-            k.ev[p] = evp[o];
-            k.v[p] = val[static_cast<int64_t>(koff + ec[p]) * T + t];
-            k.dd[p] = ddp[o];
+            k.ev[p] = ev_l[p][tk];
+            k.v[p] = v_l[p][t];
+            k.dd[p] = dd_l[p][tk];
         }
-        k.gam = raw_load(gs + t);
     };
-
     const int t_begin = ck * chunk_len, t_end = min(T, t_begin + chunk_len);
     const int n = t_end - t_begin;
-    MassTok<MP> cur[CH], nxt[CH];
-#pragma unroll
-    for (int j = 0; j < CH; ++j)
-        load_tok(max(t_end - 1 - j, t_begin), cur[j]);
     const int nc = (n + CH - 1) / CH;
+    // group ci's tokens t_end - 1 - ci * CH - j, j < CH (clamped to the
+    // chunk); gamma of token j in lane j: the exponential of every token of
+    // a group is one vector operation, read back per token as a scalar
+    auto tok_t = [&](int ci, int j) { return max(t_end - 1 - ci * CH - j, t_begin); };
+    auto load_group = [&](int ci, MassTok<MP> (&k)[CH], uint32_t &graw) {
+#pragma unroll
+        for (int j = 0; j < CH; ++j)
+            load_tok(tok_t(ci, j), k[j]);
+        graw = raw_load(gs + tok_t(ci, lane % CH));
+    };
     // REPLAY: the chunk's gradients per lane (event) and of gamma, stored as
     // runs of consecutive tokens once the chunk is done
-    float outv[CH][MP], outg[CH];
     auto store_run = [&](float *row, int t_hi, const float *vals, int stride) {
         const int t_lo = t_hi - (CH - 1);
         if (t_lo >= t_begin && (t_lo & 3) == 0 && (T & 3) == 0) {
@@ -844,27 +876,36 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
                     row[t_hi - j] = vals[j * stride];
         }
     };
-    for (int ci = 0; ci < nc; ++ci) {
-#pragma unroll
-        for (int j = 0; j < CH; ++j)
-            load_tok(max(t_end - 1 - (ci + 1) * CH - j, t_begin), nxt[j]);
+    auto group = [&](int ci, const MassTok<MP> (&cur)[CH], uint32_t graw) {
+        float outv[CH][MP], outg[CH];
+        // tokens past the chunk's start (the last group's tail) repeat
+        // t_begin's loads; they act on the no-op slots only
+        const int left = n - ci * CH;
+        const float gmv = half_bits_to_f<Scalar>(graw);
+        const float qdv = expf(-fabsf(gmv));
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
-            const int t = t_end - 1 - ci * CH - j;
-            if (t < t_begin)
-                break;
+            const bool tok = j < left;
             const MassTok<MP> &k = cur[j];
+            // every field of the record counts as used, so that it stays one
+            // 16-byte load: a group's loads then fit the memory counter's 63
+            // (3 per token and event, 16 tokens, and gamma), and the wait for
+            // this group does not take in the next group's first loads
+#pragma unroll
+            for (int p = 0; p < MP; ++p)
+                asm volatile("" ::"v"(k.ev[p].z));
             // reads of token t (they follow its writes in the forward)
             float dr[MP];
             if constexpr (MA) {
                 float sr = 0.f, srm = 0.f, sdm = 0.f;
+                bool a_on[MP];
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
-                    const bool a_on = !wlane && on[p] && k.ev[p].x >= 0;
-                    const float rho = a_on ? -k.v[p] : 0.f;
+                    a_on[p] = tok && !wlane && on[p] && k.ev[p].x >= 0;
+                    const float rho = a_on[p] ? -k.v[p] : 0.f;
                     sr += rho;
                     srm = fmaf(rho, __int_as_float(k.ev[p].z), srm);
-                    sdm = fmaf(rho * __int_as_float(k.ev[p].z), a_on ? k.dd[p] : 0.f, sdm);
+                    sdm = fmaf(rho * __int_as_float(k.ev[p].z), a_on[p] ? k.dd[p] : 0.f, sdm);
                 }
                 sr = xor_sum<1, 32>(sr);
                 srm = xor_sum<1, 32>(srm);
@@ -873,57 +914,56 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
                 const float c = sr * inv, Q = sdm * inv;
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
-                    const bool a_on = !wlane && on[p] && k.ev[p].x >= 0;
+                    const uint32_t am = a_on[p] ? ~0u : 0u;
                     const float diff = k.dd[p] - Q;
-                    dr[p] = a_on ? fmaf(c * __int_as_float(k.ev[p].z), diff, Q) : 0.f;
-                    if (a_on) {
-                        const float kap = -c * k.v[p] * diff;
-                        if constexpr (REPLAY)
-                            dm[k.ev[p].x] += kap;
-                        else
-                            mp[k.ev[p].x].y += kap;
-                    }
+                    dr[p] = keep_if(fmaf(c * __int_as_float(k.ev[p].z), diff, Q), am);
+                    const float kap = keep_if(-c * k.v[p] * diff, am);
+                    const int s = a_on[p] ? k.ev[p].x : -1;
+                    if constexpr (REPLAY)
+                        dm[s] += kap;
+                    else
+                        mp[s].y += kap;
                 }
-                __syncthreads();
+                // the write lanes' reads of this token's slots come after
+                // the read lanes' updates (other lanes, same slots)
+                __builtin_amdgcn_wave_barrier();
             } else {
 #pragma unroll
                 for (int p = 0; p < MP; ++p)
-                    dr[p] = (!wlane && on[p] && k.ev[p].x >= 0) ? k.dd[p] : 0.f;
+                    dr[p] = keep_if(k.dd[p], tok && !wlane && on[p] && k.ev[p].x >= 0 ? ~0u : 0u);
             }
-            // writes of token t
+            // writes of token t: alpha in the stable form of gsu_alpha, with
+            // q = e^-|gamma| and reciprocals of its denominator dn and of
+            // m' + eps (each v_rcp_f32 and a Newton step)
             float dgam = 0.f;
             float dw[MP];
-            const float gm = half_bits_to_f<Scalar>(k.gam);
+            const float gm = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gmv), j));
+            const float qd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qdv), j));
+            const bool gpos = gm >= 0.f;
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
-                dw[p] = 0.f;
-                if (wlane && on[p] && k.ev[p].x >= 0) {
-                    const float w = k.v[p], m = __int_as_float(k.ev[p].w), Dg = k.dd[p];
-                    const float g = __int_as_float(k.ev[p].y);
-                    // alpha in the stable form of gsu_alpha, with one
-                    // exponential q = e^-|gamma| and reciprocals of its
-                    // denominator dn and of m' + eps (each v_rcp_f32 and a
-                    // Newton step)
-                    const bool gpos = gm >= 0.f;
-                    const float qd = expf(gpos ? -gm : gm);
-                    const float cw = 1.f - w;
-                    const float dn = gpos ? fmaf(qd, cw, w) : fmaf(qd, w, cw);
-                    const float rdn = recip_nr(dn);
-                    const float al = (gpos ? cw * qd : cw) * rdn;
-                    const float den = fmaf(al, m, w) + eps;
-                    const float rden = recip_nr(den);
-                    const float q0 = Dg * g * rden;
-                    const int a = k.ev[p].x;
-                    if constexpr (REPLAY) {
-                        const float dtot = dm[a] - q0;
-                        const float t2 = qd * rdn * rdn;
-                        dw[p] = Dg * rden + dtot * fmaf(-m, t2, 1.f);
-                        dgam = fmaf(-dtot * m, cw * w * t2, dgam);
-                        dm[a] = dtot * al;
-                    } else {
-                        const float2 ab = mp[a];
-                        mp[a] = make_float2(al * ab.x, al * (ab.y - q0));
-                    }
+                const bool act = tok && wlane && on[p] && k.ev[p].x >= 0;
+                const float w = k.v[p], m = __int_as_float(k.ev[p].w), Dg = k.dd[p];
+                const float g = __int_as_float(k.ev[p].y);
+                const float cw = 1.f - w;
+                const float dn = gpos ? fmaf(qd, cw, w) : fmaf(qd, w, cw);
+                const float rdn = recip_nr(dn);
+                const float al = (gpos ? cw * qd : cw) * rdn;
+                const float den = fmaf(al, m, w) + eps;
+                const float rden = recip_nr(den);
+                const float q0 = Dg * g * rden;
+                const int s = act ? k.ev[p].x : -2;
+                if constexpr (REPLAY) {
+                    const uint32_t am = act ? ~0u : 0u;
+                    const float dtot = dm[s] - q0;
+                    dm[s] = dtot * al;
+                    const float t2 = qd * rdn * rdn;
+                    dw[p] = keep_if(fmaf(dtot, fmaf(-m, t2, 1.f), Dg * rden), am);
+                    dgam = fmaf(keep_if(-dtot * m, am), keep_if(cw * w * t2, am), dgam);
+                } else {
+                    const float2 ab = mp[s];
+                    mp[s] = make_float2(al * ab.x, al * (ab.y - q0));
+                    dw[p] = 0.f;
                 }
             }
             if constexpr (REPLAY) {
@@ -932,8 +972,6 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
                 for (int p = 0; p < MP; ++p)
                     outv[j][p] = wlane ? dw[p] : dr[p];
             }
-            if constexpr (MA)
-                __syncthreads();
         }
         if constexpr (REPLAY) {
             const int t_hi = t_end - 1 - ci * CH;
@@ -944,10 +982,25 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
                 if (on[p])
                     store_run(gval + static_cast<int64_t>(koff + p * 32 + hl) * T, t_hi, &outv[0][p], MP);
         }
-#pragma unroll
-        for (int j = 0; j < CH; ++j)
-            cur[j] = nxt[j];
+    };
+    // two groups per iteration with swapped buffers: a copy of registers
+    // with loads pending would wait for every outstanding load
+    MassTok<MP> ka[CH], kb[CH];
+    uint32_t ga, gb;
+    load_group(0, ka, ga);
+    int ci = 0;
+    for (; ci + 1 < nc; ci += 2) {
+        load_group(ci + 1, kb, gb);
+        __builtin_amdgcn_sched_barrier(0);
+        group(ci, ka, ga);
+        __builtin_amdgcn_sched_barrier(0);
+        load_group(min(ci + 2, nc - 1), ka, ga);
+        __builtin_amdgcn_sched_barrier(0);
+        group(ci + 1, kb, gb);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    if (ci < nc)
+        group(ci, ka, ga);
     __syncthreads();
     if constexpr (REPLAY) {
         if (nck == 1) {
