@@ -901,7 +901,7 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
                 bool a_on[MP];
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
-                    a_on[p] = tok && !wlane && on[p] && k.ev[p].x >= 0;
+                    a_on[p] = tok & !wlane & on[p] & (k.ev[p].x >= 0);
                     const float rho = a_on[p] ? -k.v[p] : 0.f;
                     sr += rho;
                     srm = fmaf(rho, __int_as_float(k.ev[p].z), srm);
@@ -930,7 +930,7 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
             } else {
 #pragma unroll
                 for (int p = 0; p < MP; ++p)
-                    dr[p] = keep_if(k.dd[p], tok && !wlane && on[p] && k.ev[p].x >= 0 ? ~0u : 0u);
+                    dr[p] = keep_if(k.dd[p], tok & !wlane & on[p] & (k.ev[p].x >= 0) ? ~0u : 0u);
             }
             // writes of token t: alpha in the stable form of gsu_alpha, with
             // q = e^-|gamma| and reciprocals of its denominator dn and of
@@ -942,7 +942,9 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
             const bool gpos = gm >= 0.f;
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
-                const bool act = tok && wlane && on[p] && k.ev[p].x >= 0;
+                // (bitwise: a short-circuit test of a lane condition becomes
+                // an exec-mask region, which the scheduler does not cross)
+                const bool act = tok & wlane & on[p] & (k.ev[p].x >= 0);
                 const float w = k.v[p], m = __int_as_float(k.ev[p].w), Dg = k.dd[p];
                 const float g = __int_as_float(k.ev[p].y);
                 const float cw = 1.f - w;
@@ -1025,10 +1027,20 @@ __global__ __launch_bounds__(256) void segment_bwd_mass_scan_kernel(const Segmen
     const int a = static_cast<int>(i - bh * A);
     float D = job.grad_mass ? job.grad_mass[i] : 0.f;
     float2 *mp = maps + bh * nck * A + a;
-    for (int c = nck - 1; c >= 0; --c) {
-        const float2 ab = mp[static_cast<int64_t>(c) * A];
-        mp[static_cast<int64_t>(c) * A] = make_float2(D, 0.f);
-        D = fmaf(ab.x, D, ab.y);
+    // eight chunks' maps loaded before their stores (a store could alias a
+    // later load as far as the compiler knows)
+    for (int c0 = nck - 1; c0 >= 0; c0 -= 8) {
+        float2 ab[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            ab[j] = mp[static_cast<int64_t>(max(c0 - j, 0)) * A];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (c0 - j >= 0) {
+                mp[static_cast<int64_t>(c0 - j) * A] = make_float2(D, 0.f);
+                D = fmaf(ab[j].x, D, ab[j].y);
+            }
+        }
     }
     job.grad_init_mass[i] = D;
 }

@@ -567,7 +567,9 @@ __global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob 
         for (int j = 0; j < CH; ++j) {
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
-                const bool act = wlane && ln.on[p] && t_begin + ci * CH + j < t_end;
+                // (bitwise: a short-circuit test of a lane condition becomes
+                // an exec-mask region, which the scheduler does not cross)
+                const bool act = wlane & ln.on[p] & (t_begin + ci * CH + j < t_end);
                 const int a = act ? c.w[p][j].x : -2;
                 const float w = act ? __int_as_float(c.w[p][j].y) : 0.f;
                 const float al = act ? __int_as_float(c.w[p][j].z) : 1.f;
@@ -576,23 +578,33 @@ __global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob 
             }
         }
     };
-    // two chunks per iteration with swapped buffers: a copy of registers
-    // with loads pending would wait for every outstanding load
-    MassRecs<MP, CH> ca, cb;
-    mass_fetch<true>(ln, gw, gr, t_pad, t_begin, ca);
-    int ci = 0;
-    for (; ci + 1 < nc; ci += 2) {
-        mass_fetch<true>(ln, gw, gr, t_pad, t_begin + (ci + 1) * CH, cb);
+    // a ring of three fetch buffers, two fetches ahead of the mass chain
+    // (at config 2 the grid leaves half the SIMDs without a wave, so no
+    // other wave covers the loads' latency); rotating in an unrolled loop,
+    // as a copy of registers with loads pending would wait for every
+    // outstanding load. Fetches past the last repeat it.
+    auto at = [&](int i) { return t_begin + max(min(i, nc - 1), 0) * CH; };
+    MassRecs<MP, CH> ca, cb, cc;
+    mass_fetch<true>(ln, gw, gr, t_pad, at(0), ca);
+    mass_fetch<true>(ln, gw, gr, t_pad, at(1), cb);
+    for (int ci = 0; ci < nc; ci += 3) {
+        mass_fetch<true>(ln, gw, gr, t_pad, at(ci + 2), cc);
         __builtin_amdgcn_sched_barrier(0);
         run(ci, ca);
         __builtin_amdgcn_sched_barrier(0);
-        mass_fetch<true>(ln, gw, gr, t_pad, t_begin + min(ci + 2, nc - 1) * CH, ca);
+        if (ci + 1 >= nc)
+            break;
+        mass_fetch<true>(ln, gw, gr, t_pad, at(ci + 3), ca);
         __builtin_amdgcn_sched_barrier(0);
         run(ci + 1, cb);
         __builtin_amdgcn_sched_barrier(0);
+        if (ci + 2 >= nc)
+            break;
+        mass_fetch<true>(ln, gw, gr, t_pad, at(ci + 4), cb);
+        __builtin_amdgcn_sched_barrier(0);
+        run(ci + 2, cc);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    if (ci < nc)
-        run(ci, ca);
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < NU; ++v) {
@@ -615,10 +627,21 @@ __global__ __launch_bounds__(256) void mass_chunk_scan_kernel(const SegmentJob j
     const int a = static_cast<int>(i - bh * A);
     float m = job.init_mass[i];
     float2 *mp = maps + bh * nck * A + a;
-    for (int c = 0; c < nck; ++c) {
-        const float2 ab = mp[static_cast<int64_t>(c) * A];
-        mp[static_cast<int64_t>(c) * A] = make_float2(m, 0.f);
-        m = fmaf(ab.x, m, ab.y);
+    // eight chunks' maps loaded before their stores (a store could alias a
+    // later load as far as the compiler knows, so one at a time each load
+    // would wait for the store before it)
+    for (int c0 = 0; c0 < nck; c0 += 8) {
+        float2 ab[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            ab[j] = mp[static_cast<int64_t>(min(c0 + j, nck - 1)) * A];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (c0 + j < nck) {
+                mp[static_cast<int64_t>(c0 + j) * A] = make_float2(m, 0.f);
+                m = fmaf(ab[j].x, m, ab[j].y);
+            }
+        }
     }
     job.mass_out[i] = m;
 }
@@ -705,7 +728,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
         // (compared once the chunk is done, off the mass chain)
         int tgv[CH][MP];
         auto wev = [&](int p, int j, int &a, float &w, float &al) {
-            const bool act = wlane && ln.act[p] && t0 + j < t_end;
+            const bool act = wlane & ln.act[p] & (t0 + j < t_end);  // bitwise: no exec-mask region
             a = act ? c.w[p][j].x : -2;
             w = act ? __int_as_float(c.w[p][j].y) : 0.f;
             al = act ? __int_as_float(c.w[p][j].z) : 1.f;
@@ -716,7 +739,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
             int rb[MP];
 #pragma unroll
             for (int p = 0; p < MP; ++p) {
-                const bool act = !wlane && ln.act[p] && live;
+                const bool act = !wlane & ln.act[p] & live;
                 rb[p] = act ? c.r[p][j].x : -1;
             }
             if constexpr (FL) {
@@ -755,7 +778,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 float sr = 0.f, srm = 0.f;
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
-                    const bool act = !wlane && ln.act[p] && live;
+                    const bool act = !wlane & ln.act[p] & live;
                     rr[p] = act ? __int_as_float(c.r[p][j].y) : 0.f;
                     mm[p] = 0.f;
                     if constexpr (MA || AUX) {
@@ -873,20 +896,29 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
         }
     };
     const int nc = (t_end - t_begin + CH - 1) / CH;
-    // the next chunk's loads stay ahead of this chunk's mass chain; two
-    // chunks per iteration with swapped buffers (no copy of pending loads)
-    MassRecs<MP, CH> ca, cb;
-    mass_fetch<false>(ln, gw, gr, t_pad, t_begin, ca);
-    for (int ci = 0; ci < nc; ci += 2) {
-        mass_fetch<false>(ln, gw, gr, t_pad, t_begin + min(ci + 1, nc - 1) * CH, cb);
+    // the loads stay two fetches ahead of the mass chain: a ring of three
+    // buffers rotating in an unrolled loop (no copy of pending loads);
+    // fetches past the last repeat it
+    auto at = [&](int i) { return t_begin + max(min(i, nc - 1), 0) * CH; };
+    MassRecs<MP, CH> ca, cb, cc;
+    mass_fetch<false>(ln, gw, gr, t_pad, at(0), ca);
+    mass_fetch<false>(ln, gw, gr, t_pad, at(1), cb);
+    for (int ci = 0; ci < nc; ci += 3) {
+        mass_fetch<false>(ln, gw, gr, t_pad, at(ci + 2), cc);
         __builtin_amdgcn_sched_barrier(0);
         run(t_begin + ci * CH, ca);
         __builtin_amdgcn_sched_barrier(0);
         if (ci + 1 >= nc)
             break;
-        mass_fetch<false>(ln, gw, gr, t_pad, t_begin + min(ci + 2, nc - 1) * CH, ca);
+        mass_fetch<false>(ln, gw, gr, t_pad, at(ci + 3), ca);
         __builtin_amdgcn_sched_barrier(0);
         run(t_begin + (ci + 1) * CH, cb);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ci + 2 >= nc)
+            break;
+        mass_fetch<false>(ln, gw, gr, t_pad, at(ci + 4), cb);
+        __builtin_amdgcn_sched_barrier(0);
+        run(t_begin + (ci + 2) * CH, cc);
         __builtin_amdgcn_sched_barrier(0);
     }
     if (!starts) {
