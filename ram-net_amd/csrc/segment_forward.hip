@@ -370,8 +370,13 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
     const int tl = t < T ? t : T - 1;
     const int32_t *ip = job.addr_idx + static_cast<int64_t>(bh) * Kt * T;
     const float *vp = job.addr_val + static_cast<int64_t>(bh) * Kt * T;
-    const uint8_t *mrow = job.mask ? job.mask + static_cast<int64_t>(b) * T : nullptr;
-    auto unmasked = [&](int tt) { return *(mrow ? mrow + tt : &kScanAllValid) != 0; };
+    // Conditions below are bitwise: a short-circuit test of a lane value
+    // becomes an exec-mask region (scalar instructions, and a boundary the
+    // scheduler does not cross). Without a mask, the mask loads read bytes
+    // of this head's indices instead (always in bounds) and are ignored.
+    const bool has_mask = job.mask != nullptr;
+    const uint8_t *mrow = has_mask ? job.mask + static_cast<int64_t>(b) * T : reinterpret_cast<const uint8_t *>(ip);
+    auto unmasked = [&](int tt) { return !has_mask | (mrow[tt] != 0); };
     // this token's events (write events 0..Kw-1, then read events), clamped
     int ia[2 * KE];
     float va[2 * KE];
@@ -388,7 +393,7 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
 #pragma unroll
     for (int d = 1; d <= 3; ++d) {
         const int tq = tl - d > 0 ? tl - d : 0;
-        pon[d - 1] = t < T && t >= d && unmasked(tq);
+        pon[d - 1] = (t < T) & (t >= d) & unmasked(tq);
 #pragma unroll
         for (int e = 0; e < KE; ++e) {
             const int k = min(e, Kw - 1);
@@ -397,25 +402,29 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
         }
     }
     const float g = load_f32(static_cast<const Scalar *>(job.gamma) + static_cast<int64_t>(bh) * T + tl);
-    const bool live = t < T && unmasked(tl);
+    const bool live = (t < T) & unmasked(tl);
     const int base = bh * A;
-    // slot written by event e (or -1): in range, with a nonzero weight
-    auto wslot = [&](int a, float v) {
+    // slot written by event e (or `none`): in range, with a nonzero weight
+    auto wslot = [&](bool on, int a, float v, int none) {
         const int o = a - base;
-        return static_cast<unsigned>(o) < static_cast<unsigned>(A) && v != 0.f ? o : -1;
+        return (on & (static_cast<unsigned>(o) < static_cast<unsigned>(A)) & (v != 0.f)) ? o : none;
     };
+    // this token's write slots (-1: none) and, per token before, whether one
+    // of them is written there too (its none, -2, never matches)
+    int mine[KE];
+#pragma unroll
+    for (int j = 0; j < KE; ++j)
+        mine[j] = wslot((j < Kw) & live, ia[j], va[j], -1);
     int ov = 0;
 #pragma unroll
     for (int d = 0; d < 3; ++d) {
         bool hit = false;
 #pragma unroll
         for (int i = 0; i < KE; ++i) {
-            const int x = i < Kw && pon[d] ? wslot(pa[d][i], pv[d][i]) : -1;
+            const int x = wslot((i < Kw) & pon[d], pa[d][i], pv[d][i], -2);
 #pragma unroll
-            for (int j = 0; j < KE; ++j) {
-                const int y = j < Kw && live ? wslot(ia[j], va[j]) : -1;
-                hit = hit || (x >= 0 && x == y);
-            }
+            for (int j = 0; j < KE; ++j)
+                hit |= x == mine[j];
         }
         ov |= hit ? 1 << d : 0;
     }
@@ -425,11 +434,10 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
         if (e < Kw) {
             const int a = ia[e] - base;
             const float v = va[e];
-            const bool act = live && static_cast<unsigned>(a) < static_cast<unsigned>(A) && v != 0.f;
-            WriteRec rec{-2, 0.f, 1.f, overlap};
-            if (act)
-                rec = WriteRec{a, v, gsu_alpha(v, g), overlap};
-            job.wrec[(static_cast<int64_t>(bh) * Kw + e) * t_pad + t] = rec;
+            const bool act = live & (static_cast<unsigned>(a) < static_cast<unsigned>(A)) & (v != 0.f);
+            const float al = gsu_alpha(v, g);
+            job.wrec[(static_cast<int64_t>(bh) * Kw + e) * t_pad + t] =
+                WriteRec{act ? a : -2, act ? v : 0.f, act ? al : 1.f, overlap};
         }
     }
 #pragma unroll
@@ -437,8 +445,8 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
         if (e < Kr) {
             const int a = ia[KE + e] - base;
             const float r = -va[KE + e];  // reads were stored negated
-            const bool act = live && static_cast<unsigned>(a) < static_cast<unsigned>(A) && r != 0.f;
-            job.rrec[(static_cast<int64_t>(bh) * Kr + e) * t_pad + t] = act ? ReadRec{a, r} : ReadRec{-1, 0.f};
+            const bool act = live & (static_cast<unsigned>(a) < static_cast<unsigned>(A)) & (r != 0.f);
+            job.rrec[(static_cast<int64_t>(bh) * Kr + e) * t_pad + t] = ReadRec{act ? a : -1, act ? r : 0.f};
         }
     }
 }

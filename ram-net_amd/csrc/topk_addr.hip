@@ -32,7 +32,15 @@ namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
-__device__ const uint8_t kAddrAllValid = 1;
+// Whether token tl of batch row b is unmasked. Without a mask the load reads
+// a byte of this row's position ids instead (always in bounds) and is
+// ignored: a load that is always made needs no branch.
+__device__ __forceinline__ bool addr_unmasked(const AddrJob &job, int b, int tl) {
+    const bool has = job.mask != nullptr;
+    const uint8_t *row = has ? job.mask + static_cast<int64_t>(b) * job.T
+                             : reinterpret_cast<const uint8_t *>(job.position_ids + static_cast<int64_t>(b) * job.T);
+    return !has | (row[tl] != 0);
+}
 
 // Record mode output of one address (source 0 = writes, 1 = reads). `get(k,
 // c, v)` yields the k-th selected content slot and its weight. Events of
@@ -45,8 +53,9 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
                                               bool inactive, Get get, int K, int shift, int overlap) {
     const int T = job.T, A = job.A;
     const int Tp = scan_t_pad(T);
-    const uint8_t *mp = job.mask ? job.mask + static_cast<int64_t>(b) * T + tl : &kAddrAllValid;
-    const bool live = t < T && *mp != 0 && !inactive;
+    // (conditions are bitwise: a short-circuit test of a lane value becomes
+    // an exec-mask region, scalar instructions and a scheduling boundary)
+    const bool live = (t < T) & addr_unmasked(job, b, tl) & !inactive;
     const float g = which == 0 ? load_f32(static_cast<const Scalar *>(job.gamma) + bh * T + tl) : 0.f;
     auto one = [&](int k) {
         int c;
@@ -54,7 +63,7 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
         get(k, c, v);
         int o = c - shift;
         o = o < 0 ? o + A : o;
-        const bool act = live && v != 0.f;
+        const bool act = live & (v != 0.f);
         if (which == 0) {
             WriteRec rec{-2, 0.f, 1.f, __int_as_float(overlap)};
             if (act)
@@ -132,15 +141,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
     const bool inactive = !found;
 
     const int K = src.top_k;
-    float lse = 0.f;
-    if (src.re_norm != 0.f && !inactive && mv[0] > kNegInf) {
-        float sum = 0.f;
+    // log-sum-exp of the selected scores, computed on every lane and kept
+    // where it applies (no divergent branch)
+    float sum = 0.f;
 #pragma unroll
-        for (int k = KM - 1; k >= 0; --k)
-            if (k < K)
-                sum += expf(mv[k] - mv[0]);
-        lse = mv[0] + log_sum(sum);
-    }
+    for (int k = KM - 1; k >= 0; --k)
+        if (k < K)
+            sum += expf(mv[k] - mv[0]);
+    const bool norm = (src.re_norm != 0.f) & !inactive & (mv[0] > kNegInf);
+    const float lse = norm ? mv[0] + log_sum(sum) : 0.f;
     const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + tl], A) : 0;
     if (rec_mode) {
         // Overlap flags of the write address, bit d - 1 for d = 1, 2, 3:
@@ -151,14 +160,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
         // may have been written within its group.
         int overlap = 0;
         if (blockIdx.y == 0) {
-            const uint8_t *mp = job.mask ? job.mask + static_cast<int64_t>(b) * T + tl : &kAddrAllValid;
-            const bool live = t < T && *mp != 0 && !inactive;
-            int mine[KM];
+            const bool live = (t < T) & addr_unmasked(job, b, tl) & !inactive;
+            // this token's write slots (-1: none); the tokens before post
+            // theirs with -2 for none, which never matches
+            int mine[KM], post[KM];
 #pragma unroll
             for (int k = 0; k < KM; ++k) {
                 int o = mi[k] - shift;
                 o = o < 0 ? o + A : o;
-                mine[k] = live && k < K ? o : -1;
+                const bool on = live & (k < K);
+                mine[k] = on ? o : -1;
+                post[k] = on ? o : -2;
             }
             const int wl = static_cast<int>(threadIdx.x & (kWave - 1));
 #pragma unroll
@@ -166,15 +178,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                 int prev[KM];
 #pragma unroll
                 for (int k = 0; k < KM; ++k)
-                    prev[k] = __shfl_up(mine[k], d);
+                    prev[k] = __shfl_up(post[k], d);
                 bool hit = false;
 #pragma unroll
                 for (int k = 0; k < KM; ++k)
 #pragma unroll
                     for (int k2 = 0; k2 < KM; ++k2)
-                        hit = hit || (mine[k] >= 0 && mine[k] == prev[k2]);
-                if (t >= d && (hit || wl < d))
-                    overlap |= 1 << (d - 1);
+                        hit |= mine[k] == prev[k2];
+                overlap |= (t >= d) & (hit | (wl < d)) ? 1 << (d - 1) : 0;
             }
         }
         write_records<Scalar, KM>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
