@@ -930,7 +930,7 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
             } else {
 #pragma unroll
                 for (int p = 0; p < MP; ++p)
-                    dr[p] = keep_if(k.dd[p], tok & !wlane & on[p] & (k.ev[p].x >= 0) ? ~0u : 0u);
+                    dr[p] = keep_if(k.dd[p], (tok & !wlane & on[p] & (k.ev[p].x >= 0)) ? ~0u : 0u);
             }
             // writes of token t: alpha in the stable form of gsu_alpha, with
             // q = e^-|gamma| and reciprocals of its denominator dn and of

@@ -435,9 +435,11 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
             const int a = ia[e] - base;
             const float v = va[e];
             const bool act = live & (static_cast<unsigned>(a) < static_cast<unsigned>(A)) & (v != 0.f);
-            const float al = gsu_alpha(v, g);
-            job.wrec[(static_cast<int64_t>(bh) * Kw + e) * t_pad + t] =
-                WriteRec{act ? a : -2, act ? v : 0.f, act ? al : 1.f, overlap};
+            // alpha kept through an opaque bit mask (a select of the quotient
+            // would be turned back into a branch around the division)
+            const uint32_t m = opaque(act ? ~0u : 0u);
+            const float al = __uint_as_float((__float_as_uint(gsu_alpha(v, g)) & m) | (__float_as_uint(1.f) & ~m));
+            job.wrec[(static_cast<int64_t>(bh) * Kw + e) * t_pad + t] = WriteRec{act ? a : -2, act ? v : 0.f, al, overlap};
         }
     }
 #pragma unroll
@@ -807,7 +809,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 for (int p = 0; p < MP; ++p) {
                     re[p] = MA ? rr[p] * mm[p] * scale : rr[p];
                     if constexpr (AUX != 0) {
-                        if (!wlane && ln.on[p] && live) {
+                        if (!wlane & ln.on[p] & live) {
                             const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kr + ln.ev[p];
                             aux.rev[o] = make_int4(rb[p], __float_as_int(re[p]), __float_as_int(mm[p]), 0);
                         }
@@ -832,7 +834,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                     __builtin_amdgcn_wave_barrier();
 #pragma unroll
                     for (int p = 0; p < MP; ++p) {
-                        if (!wlane && rb[p] >= 0) {
+                        if (!wlane & (rb[p] >= 0)) {
                             rtag[rb[p]] = t;
                             rval[rb[p]] = re[p];
                         }
@@ -841,13 +843,17 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                     float rmatch[MP];
 #pragma unroll
                     for (int p = 0; p < MP; ++p) {
+                        // (bitwise, both tables read on every lane: a
+                        // short-circuit LDS read would be an exec-mask region
+                        // waiting on its own load)
                         const int sl = a[p] < 0 ? 0 : a[p];
-                        const bool hit = wlane && a[p] >= 0 && rtag[sl] == t;
-                        rmatch[p] = hit ? rval[sl] : 0.f;
+                        const bool hit = wlane & (a[p] >= 0) & (rtag[sl] == t);
+                        const float rv = rval[sl];
+                        rmatch[p] = hit ? rv : 0.f;
                     }
 #pragma unroll
                     for (int p = 0; p < MP; ++p) {
-                        if (wlane && ln.on[p] && live) {
+                        if (wlane & ln.on[p] & live) {
                             const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kw + ln.ev[p];
                             aux.wev[o] = make_int4(a[p], __float_as_int(gn[p]), __float_as_int(rmatch[p]),
                                                    __float_as_int(m[p]));
@@ -893,7 +899,7 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                 bool hit = false;
 #pragma unroll
                 for (int p = 0; p < MP; ++p)
-                    hit = hit || (wlane && ln.on[p] && tgv[j][p] == t0 + j - 1);
+                    hit |= wlane & ln.on[p] & (tgv[j][p] == t0 + j - 1);
                 const uint64_t hb = __ballot(hit);
                 const bool unit_hit = ((hb >> ubase) & ((1ull << HALF) - 1)) != 0;
                 const bool first = t0 + j == t_begin && t_begin > 0;

@@ -65,10 +65,12 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
         o = o < 0 ? o + A : o;
         const bool act = live & (v != 0.f);
         if (which == 0) {
-            WriteRec rec{-2, 0.f, 1.f, __int_as_float(overlap)};
-            if (act)
-                rec = WriteRec{o, v, gsu_alpha(v, g), __int_as_float(overlap)};
-            job.wrec[(bh * K + k) * Tp + t] = rec;
+            // alpha on every lane, kept through an opaque bit mask (a select
+            // of the quotient would be turned back into a branch around the
+            // division)
+            const uint32_t m = opaque(act ? ~0u : 0u);
+            const float al = __uint_as_float((__float_as_uint(gsu_alpha(v, g)) & m) | (__float_as_uint(1.f) & ~m));
+            job.wrec[(bh * K + k) * Tp + t] = WriteRec{act ? o : -2, act ? v : 0.f, al, __int_as_float(overlap)};
         } else {
             job.rrec[(bh * K + k) * Tp + t] = act ? ReadRec{o, v} : ReadRec{-1, 0.f};
         }
@@ -185,7 +187,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
 #pragma unroll
                     for (int k2 = 0; k2 < KM; ++k2)
                         hit |= mine[k] == prev[k2];
-                overlap |= (t >= d) & (hit | (wl < d)) ? 1 << (d - 1) : 0;
+                overlap |= ((t >= d) & (hit | (wl < d))) ? 1 << (d - 1) : 0;
             }
         }
         write_records<Scalar, KM>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
@@ -421,16 +423,21 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
             vsum += weight(k);
         }
     }
-    const bool renorm = re != 0.f && vsum > 0.f;
+    // (conditions bitwise and corrections selected, not branched on: a
+    // lane-dependent branch is an exec-mask region)
+    const bool renorm = (re != 0.f) & (vsum > 0.f);
     auto dk = [&](int k) {  // the re-normalised D_k (streaming form)
         const float d = dscore(k);
         return renorm ? d - re * (weight(k) / vsum) * dsum : d;
     };
     if constexpr (KM > 0) {
-        if (renorm) {
 #pragma unroll
-            for (int k = 0; k < KM; ++k)
-                D[k] = k < K ? D[k] - re * (wk[k] / vsum) * dsum : 0.f;
+        for (int k = 0; k < KM; ++k) {
+            // (a bit select through an opaque mask: a select of the quotient
+            // would be turned back into a branch around the division)
+            const float dr = D[k] - re * (wk[k] / vsum) * dsum;
+            const uint32_t m = opaque((renorm & (k < K)) ? ~0u : 0u);
+            D[k] = __uint_as_float((__float_as_uint(dr) & m) | (__float_as_uint(D[k]) & ~m));
         }
     }
     const float dsoft = (1.f - re) * dsum;
@@ -486,7 +493,8 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
         if constexpr (PR > 0) {
 #pragma unroll
             for (int q = 0; q < PR; ++q) {
-                xr[q] = live && q < P ? expf(xr[q] - mx) : 0.f;
+                const float e = expf(xr[q] - mx);
+                xr[q] = (live & (q < P)) ? e : 0.f;
                 se += xr[q];
             }
         } else {
@@ -496,9 +504,18 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
         const float scale = live ? dsoft / se : 0.f;
         int du[KM > 0 ? KM : 1];
         if constexpr (KM > 0) {
+            // digit u of each content index: shifts when P is a power of two
+            // (a uniform branch), else integer division
+            if ((P & (P - 1)) == 0) {
+                const int sh = u * __builtin_ctz(static_cast<unsigned>(P));
 #pragma unroll
-            for (int k = 0; k < KM; ++k)
-                du[k] = c[k] < 0 ? -1 : (c[k] / stride) % P;
+                for (int k = 0; k < KM; ++k)
+                    du[k] = c[k] < 0 ? -1 : (c[k] >> sh) & (P - 1);
+            } else {
+#pragma unroll
+                for (int k = 0; k < KM; ++k)
+                    du[k] = c[k] < 0 ? -1 : (c[k] / stride) % P;
+            }
         }
         auto grad_of = [&](int q) {
             float g = 0.f;
