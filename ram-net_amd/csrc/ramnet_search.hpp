@@ -515,10 +515,13 @@ __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int 
         const int pi = __shfl(ci, g0 + ii);
         const float qv = __shfl(dv, g0 + jj);
         const int qi = __shfl(di, g0 + jj);
-        const bool ok = si_ >= 0 && pi >= 0 && qi >= 0;
-        uint64_t ck = ok ? (static_cast<uint64_t>(ord32(__float_as_uint(pv + qv))) << 32) |
-                               (0xFFFFFFFFu - static_cast<uint32_t>(pi + stride * qi))
-                         : uint64_t(0);
+        // (bitwise tests and a select: a short-circuit test of the shuffled
+        // values would put the key's computation in an exec-mask region,
+        // which the scheduler does not cross)
+        const bool ok = (si_ >= 0) & (pi >= 0) & (qi >= 0);
+        const uint64_t key = (static_cast<uint64_t>(ord32(__float_as_uint(pv + qv))) << 32) |
+                             (0xFFFFFFFFu - static_cast<uint32_t>(pi + stride * qi));
+        uint64_t ck = ok ? key : uint64_t(0);
         group_sort_desc<GW>(ck, li);
         cv = __uint_as_float(unord32(static_cast<uint32_t>(ck >> 32)));
         ci = ck != 0 ? static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck)) : -1;
@@ -543,7 +546,7 @@ __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int 
         group_digit_unkey<T>(kb, xsb, db);
         const float mxa = group_first<GW>(xsa);
         const float mxb = two ? group_first<GW>(xsb) : kNegInfF;
-        inactive = inactive || !(mxa > kNegInfF) || (two && !(mxb > kNegInfF));
+        inactive = inactive | !(mxa > kNegInfF) | (two & !(mxb > kNegInfF));
         const float ea = li < P ? __builtin_amdgcn_exp2f((xa - mxa) * kLog2e) : 0.f;
         const float eb = li < P ? __builtin_amdgcn_exp2f((xb - mxb) * kLog2e) : 0.f;
         const float lsa = log_sum(group_sum<GW>(ea));
@@ -566,7 +569,7 @@ __device__ bool group_search(const GroupLogits<T> &lg, int U, int P, int K, int 
     }
     const bool keep = li < K;
     out_v = keep ? cv : kNegInfF;
-    out_i = keep && ci >= 0 ? ci : kNoIdx;
+    out_i = (keep & (ci >= 0)) ? ci : kNoIdx;
     return inactive;
 }
 
