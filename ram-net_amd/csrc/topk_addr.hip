@@ -493,7 +493,9 @@ __global__ __launch_bounds__(256) void topk_addr_backward_kernel(const AddrBwdJo
         if constexpr (PR > 0) {
 #pragma unroll
             for (int q = 0; q < PR; ++q) {
-                const float e = expf(xr[q] - mx);
+                // exp2 of a prescaled argument (one transcendental
+                // instruction), as the forward's log-sum-exp takes it
+                const float e = __builtin_amdgcn_exp2f((xr[q] - mx) * 1.4426950408889634f);
                 xr[q] = (live & (q < P)) ? e : 0.f;
                 se += xr[q];
             }
