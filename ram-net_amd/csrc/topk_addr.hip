@@ -57,6 +57,10 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
     // an exec-mask region, scalar instructions and a scheduling boundary)
     const bool live = (t < T) & addr_unmasked(job, b, tl) & !inactive;
     const float g = which == 0 ? load_f32(static_cast<const Scalar *>(job.gamma) + bh * T + tl) : 0.f;
+    // this lane's record of event 0; event k is k * Tp records further (a
+    // uniform 32-bit step, not a 64-bit index product per event)
+    WriteRec *wr0 = job.wrec + bh * K * Tp + t;
+    ReadRec *rr0 = job.rrec + bh * K * Tp + t;
     auto one = [&](int k) {
         int c;
         float v;
@@ -70,9 +74,9 @@ __device__ __forceinline__ void write_records(const AddrJob &job, int which, int
             // division)
             const uint32_t m = opaque(act ? ~0u : 0u);
             const float al = __uint_as_float((__float_as_uint(gsu_alpha(v, g)) & m) | (__float_as_uint(1.f) & ~m));
-            job.wrec[(bh * K + k) * Tp + t] = WriteRec{act ? o : -2, act ? v : 0.f, al, __int_as_float(overlap)};
+            wr0[static_cast<uint32_t>(k * Tp)] = WriteRec{act ? o : -2, act ? v : 0.f, al, __int_as_float(overlap)};
         } else {
-            job.rrec[(bh * K + k) * Tp + t] = act ? ReadRec{o, v} : ReadRec{-1, 0.f};
+            rr0[static_cast<uint32_t>(k * Tp)] = act ? ReadRec{o, v} : ReadRec{-1, 0.f};
         }
     };
     if constexpr (KM > 0) {
@@ -145,11 +149,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
     const int K = src.top_k;
     // log-sum-exp of the selected scores, computed on every lane and kept
     // where it applies (no divergent branch)
+    // (exponentials as exp2 of a prescaled argument, one transcendental
+    // instruction each, as the digits' log-sum-exps take them)
+    constexpr float kLog2e = 1.4426950408889634f;
     float sum = 0.f;
 #pragma unroll
     for (int k = KM - 1; k >= 0; --k)
         if (k < K)
-            sum += expf(mv[k] - mv[0]);
+            sum += __builtin_amdgcn_exp2f((mv[k] - mv[0]) * kLog2e);
     const bool norm = (src.re_norm != 0.f) & !inactive & (mv[0] > kNegInf);
     const float lse = norm ? mv[0] + log_sum(sum) : 0.f;
     const int shift = h < job.embed_num ? pos_mod(job.position_ids[static_cast<int64_t>(b) * T + tl], A) : 0;
@@ -192,21 +199,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
         }
         write_records<Scalar, KM>(job, blockIdx.y, bh, b, t, tl, inactive, [&](int k, int &c, float &v) {
             c = mi[k];
-            v = expf(mv[k] - src.re_norm * lse);
+            v = __builtin_amdgcn_exp2f((mv[k] - src.re_norm * lse) * kLog2e);
         }, K, shift, overlap);
         return;
     }
     const int idx_base = (job.encode_batch_idx ? static_cast<int>(bh) : h) * A;
     const int64_t row0 = (bh * job.k_total + src.k_off) * static_cast<int64_t>(T) + t;
+    int *ip = job.idx_out + row0;  // event k at k * T (a uniform 32-bit step)
+    float *vp = job.val_out + row0;
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
         if (k < K) {
             const int c = inactive ? k : mi[k];
-            const float val = inactive ? 0.f : expf(mv[k] - src.re_norm * lse);
+            const float val = inactive ? 0.f : __builtin_amdgcn_exp2f((mv[k] - src.re_norm * lse) * kLog2e);
             int o = c - shift;
             o = o < 0 ? o + A : o;
-            job.idx_out[row0 + static_cast<int64_t>(k) * T] = idx_base + o;
-            job.val_out[row0 + static_cast<int64_t>(k) * T] = src.sign * val;
+            ip[static_cast<uint32_t>(k * T)] = idx_base + o;
+            vp[static_cast<uint32_t>(k * T)] = src.sign * val;
         }
     }
 }
