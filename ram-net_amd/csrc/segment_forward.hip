@@ -382,9 +382,10 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
     float va[2 * KE];
 #pragma unroll
     for (int e = 0; e < 2 * KE; ++e) {
+        // (offsets within the head fit 32 bits: the host checks B * H * T * (Kw + Kr))
         const int k = e < KE ? min(e, Kw - 1) : Kw + min(e - KE, Kr - 1);
-        ia[e] = ip[static_cast<int64_t>(k) * T + tl];
-        va[e] = vp[static_cast<int64_t>(k) * T + tl];
+        ia[e] = ip[static_cast<uint32_t>(k * T + tl)];
+        va[e] = vp[static_cast<uint32_t>(k * T + tl)];
     }
     // the write slots of tokens t - 1, t - 2, t - 3 (clamped to token 0)
     int pa[3][KE];
@@ -397,8 +398,8 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
 #pragma unroll
         for (int e = 0; e < KE; ++e) {
             const int k = min(e, Kw - 1);
-            pa[d - 1][e] = ip[static_cast<int64_t>(k) * T + tq];
-            pv[d - 1][e] = vp[static_cast<int64_t>(k) * T + tq];
+            pa[d - 1][e] = ip[static_cast<uint32_t>(k * T + tq)];
+            pv[d - 1][e] = vp[static_cast<uint32_t>(k * T + tq)];
         }
     }
     const float g = load_f32(static_cast<const Scalar *>(job.gamma) + static_cast<int64_t>(bh) * T + tl);
@@ -429,6 +430,9 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
         ov |= hit ? 1 << d : 0;
     }
     const float overlap = __int_as_float(ov);
+    // this thread's records of event 0; event e is e * t_pad records further
+    WriteRec *wr0 = job.wrec + static_cast<int64_t>(bh) * Kw * t_pad + t;
+    ReadRec *rr0 = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad + t;
 #pragma unroll
     for (int e = 0; e < KE; ++e) {
         if (e < Kw) {
@@ -439,7 +443,7 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
             // would be turned back into a branch around the division)
             const uint32_t m = opaque(act ? ~0u : 0u);
             const float al = __uint_as_float((__float_as_uint(gsu_alpha(v, g)) & m) | (__float_as_uint(1.f) & ~m));
-            job.wrec[(static_cast<int64_t>(bh) * Kw + e) * t_pad + t] = WriteRec{act ? a : -2, act ? v : 0.f, al, overlap};
+            wr0[static_cast<uint32_t>(e * t_pad)] = WriteRec{act ? a : -2, act ? v : 0.f, al, overlap};
         }
     }
 #pragma unroll
@@ -448,7 +452,7 @@ __global__ __launch_bounds__(256) void pack_token_records_kernel(const PackJob j
             const int a = ia[KE + e] - base;
             const float r = -va[KE + e];  // reads were stored negated
             const bool act = live & (static_cast<unsigned>(a) < static_cast<unsigned>(A)) & (r != 0.f);
-            job.rrec[(static_cast<int64_t>(bh) * Kr + e) * t_pad + t] = ReadRec{act ? a : -1, act ? r : 0.f};
+            rr0[static_cast<uint32_t>(e * t_pad)] = ReadRec{act ? a : -1, act ? r : 0.f};
         }
     }
 }
