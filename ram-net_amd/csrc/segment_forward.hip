@@ -530,14 +530,22 @@ template<bool WONLY, int MP, int CH, int HALF>
 __device__ __forceinline__ void mass_fetch(const MassLanes<MP, HALF> &ln, const WriteRec *gw, const ReadRec *gr, int t_pad,
                                            int t0, MassRecs<MP, CH> &c) {
 #pragma unroll
-    for (int p = 0; p < MP; ++p)
+    for (int p = 0; p < MP; ++p) {
+        if constexpr (WONLY) {
+            // the chunk's groups start at multiples of CH from a multiple of
+            // 16 and end by roundup(T, 8) <= t_pad: no clamp, so the tokens
+            // are immediate offsets from one address per group
+            const int4 *pw0 = reinterpret_cast<const int4 *>(gw + static_cast<int64_t>(ln.evw[p]) * t_pad + t0);
+#pragma unroll
+            for (int j = 0; j < CH; ++j)
+                c.w[p][j] = pw0[j];
+            continue;
+        }
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
             const int t = min(t0 + j, t_pad - 1);
             const WriteRec *pw = gw + static_cast<int64_t>(ln.evw[p]) * t_pad + t;
-            if constexpr (WONLY) {
-                c.w[p][j] = *reinterpret_cast<const int4 *>(pw);
-            } else {
+            {
                 const ReadRec *pr = gr + static_cast<int64_t>(ln.evr[p]) * t_pad + (t & ~1);
                 const int4 q = *reinterpret_cast<const int4 *>(ln.wl ? static_cast<const void *>(pw)
                                                                      : static_cast<const void *>(pr));
@@ -545,6 +553,7 @@ __device__ __forceinline__ void mass_fetch(const MassLanes<MP, HALF> &ln, const 
                 c.r[p][j] = (t & 1) ? make_int2(q.z, q.w) : make_int2(q.x, q.y);
             }
         }
+    }
 }
 
 // Step 1: one wave per NU (b, h) units of one chunk (NU > 1: lanes as in
@@ -576,21 +585,32 @@ __global__ __launch_bounds__(kWave) void mass_chunk_map_kernel(const SegmentJob 
     const ReadRec *gr = job.rrec + static_cast<int64_t>(bh) * Kr * t_pad;
     const int t_begin = ck * chunk_len, t_end = min(job.T, t_begin + chunk_len);
     const int nc = (t_end - t_begin + CH - 1) / CH;
+    // Every lane of a unit holds a write record here: the read lanes and
+    // the lanes past Kw hold a copy of one of the write lanes', so they read
+    // and write the same map with the same values in the same instruction,
+    // which changes nothing. Only tokens past the chunk's end (its last
+    // group) act on the no-op slot.
     auto run = [&](int ci, const MassRecs<MP, CH> &c) {
+        auto step = [&](auto tail_tag) {
+            constexpr bool TL = decltype(tail_tag)::value;
+            const int left = t_end - (t_begin + ci * CH);
 #pragma unroll
-        for (int j = 0; j < CH; ++j) {
+            for (int j = 0; j < CH; ++j) {
 #pragma unroll
-            for (int p = 0; p < MP; ++p) {
-                // (bitwise: a short-circuit test of a lane condition becomes
-                // an exec-mask region, which the scheduler does not cross)
-                const bool act = wlane & ln.on[p] & (t_begin + ci * CH + j < t_end);
-                const int a = act ? c.w[p][j].x : -2;
-                const float w = act ? __int_as_float(c.w[p][j].y) : 0.f;
-                const float al = act ? __int_as_float(c.w[p][j].z) : 1.f;
-                const float2 m = mp[a];
-                mp[a] = make_float2(al * m.x, fmaf(al, m.y, w));
+                for (int p = 0; p < MP; ++p) {
+                    const bool act = !TL || j < left;
+                    const int a = act ? c.w[p][j].x : -2;
+                    const float w = act ? __int_as_float(c.w[p][j].y) : 0.f;
+                    const float al = act ? __int_as_float(c.w[p][j].z) : 1.f;
+                    const float2 m = mp[a];
+                    mp[a] = make_float2(al * m.x, fmaf(al, m.y, w));
+                }
             }
-        }
+        };
+        if (t_begin + (ci + 1) * CH <= t_end)
+            step(std::false_type{});
+        else
+            step(std::true_type{});
     };
     // a ring of three fetch buffers, two fetches ahead of the mass chain
     // (at config 2 the grid leaves half the SIMDs without a wave, so no
