@@ -832,12 +832,6 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
 #pragma unroll
                 for (int p = 0; p < MP; ++p) {
                     re[p] = MA ? rr[p] * mm[p] * scale : rr[p];
-                    if constexpr (AUX != 0) {
-                        if (!wlane & ln.on[p] & live) {
-                            const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kr + ln.ev[p];
-                            aux.rev[o] = make_int4(rb[p], __float_as_int(re[p]), __float_as_int(mm[p]), 0);
-                        }
-                    }
                     if constexpr (AUX != 1) {
                         // every event below max(Kw, Kr) gets a record (past Kw
                         // the no-op write: slot -2, gain 0; past Kr the no-op
@@ -875,13 +869,17 @@ __global__ __launch_bounds__(kWave) void segment_mass_kernel(const SegmentJob jo
                         const float rv = rval[sl];
                         rmatch[p] = hit ? rv : 0.f;
                     }
+                    // one store per event for both halves: the write lanes' record
+                    // into wev, the read lanes' into rev
 #pragma unroll
                     for (int p = 0; p < MP; ++p) {
-                        if (wlane & ln.on[p] & live) {
-                            const int64_t o = (static_cast<int64_t>(bh) * job.T + t) * Kw + ln.ev[p];
-                            aux.wev[o] = make_int4(a[p], __float_as_int(gn[p]), __float_as_int(rmatch[p]),
-                                                   __float_as_int(m[p]));
-                        }
+                        const int64_t tb = static_cast<int64_t>(bh) * job.T + t;
+                        int4 *dst = wlane ? aux.wev + tb * Kw + ln.ev[p] : aux.rev + tb * Kr + ln.ev[p];
+                        const int4 rec = wlane ? make_int4(a[p], __float_as_int(gn[p]), __float_as_int(rmatch[p]),
+                                                           __float_as_int(m[p]))
+                                               : make_int4(rb[p], __float_as_int(re[p]), __float_as_int(mm[p]), 0);
+                        if (ln.on[p] & live)
+                            *dst = rec;
                     }
                 }
             }
