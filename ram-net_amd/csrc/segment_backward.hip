@@ -944,7 +944,11 @@ __global__ __launch_bounds__(kWave) void segment_bwd_mass_kernel(const SegmentBw
             for (int p = 0; p < MP; ++p) {
                 // (bitwise: a short-circuit test of a lane condition becomes
                 // an exec-mask region, which the scheduler does not cross)
-                const bool act = tok & wlane & on[p] & (k.ev[p].x >= 0);
+                // (the chunk maps without mass-aware reads: every lane holds a
+                // write record, the read lanes and the lanes past Kw a copy of
+                // a write lane's, whose update they repeat in the same
+                // instruction; no-op records name slot -2 themselves)
+                const bool act = (!REPLAY && !MA) ? tok : tok & wlane & on[p] & (k.ev[p].x >= 0);
                 const float w = k.v[p], m = __int_as_float(k.ev[p].w), Dg = k.dd[p];
                 const float g = __int_as_float(k.ev[p].y);
                 const float cw = 1.f - w;
